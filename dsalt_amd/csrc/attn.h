@@ -1,0 +1,51 @@
+// Internal launch interface of the attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/dsalt_amd.h"
+
+namespace dsalt {
+
+struct AttnParams {
+    int total_len, num_seqs, max_seqlen, n_heads, n_kv_heads, head_dim, k_lmk;
+    int n_sets, block_size;  // block_size 0 in the global variant
+    int dtype;
+    int n_tiles;             // 64-row tiles per sequence, ceil(max_seqlen / 64)
+    float scale;
+    const void* q;
+    int64_t q_st, q_sh;
+    const void* k;
+    int64_t k_st, k_sh;
+    const void* v;
+    int64_t v_st, v_sh;
+    const void* o;           // forward: output; backward: saved output
+    int64_t o_st, o_sh;
+    const void* dout;
+    int64_t do_st, do_sh;
+    const float* lse;        // [T, H]
+    float* lse_out;
+    const int32_t* w;
+    const int32_t* cu;
+    const int32_t* lmk;      // [H, S, n_sets, K]
+    const float* lbias;      // same shape or null
+    void* dq;
+    void* dk;
+    void* dv;
+    float* d_bias;
+    // backward workspace
+    float* delta;            // [T, H]
+    int* tile_minlo;         // [S, ceil(max_seqlen/16)] min window start of 16-row tiles
+    int* seq_wmax;           // [S] max clamped window per sequence
+    float* part_k;           // [n_chunks, H, S, K, D] landmark dK partials
+    float* part_v;           // [n_chunks, H, S, K, D]
+    float* part_b;           // [n_chunks, H, S, K]
+    int n_chunks;            // row chunks of the landmark backward
+};
+
+hipError_t fwd_launch(const AttnParams& p, hipStream_t stream);
+size_t bwd_workspace(const AttnParams& p);
+hipError_t bwd_launch(AttnParams p, void* ws, hipStream_t stream);
+
+}  // namespace dsalt

@@ -1,0 +1,277 @@
+// DSALT attention forward for gfx950.
+//
+// Replaces _dsalt_fwd_kernel (dsalt/kernels/dsalt_triton_attn.py:27-169).
+// One 256-thread block (4 waves) owns 64 query rows of one (head, sequence);
+// wave w owns rows 16w..16w+15 and each lane one query row (column of the
+// transposed score tile S^T = K Q^T).  The block walks the union of its rows'
+// windows [min_i lo_i, max_i i] in BN-key chunks staged in LDS (K row-major,
+// V transposed, double-buffered), then the landmark slots of its set in the
+// same buffers.  Masks are folded into the MFMA accumulator initialisation
+// (0 or -inf, or bias/scale for landmarks); 16-key subtiles outside a wave's
+// own range are skipped.  Landmarks arrive sorted, so the landmarks visible to
+// row i are exactly the first cnt_i = #{p < i - w_i + 1} slots -- a landmark
+// inside the window is never counted twice.  Online softmax in base 2 with a
+// lazy rescale (the running max only moves when a row max grows by more than
+// 2^8), P rounded to the input dtype before P V as in the reference (:115,:147).
+#include "attn.h"
+#include "tiles.h"
+
+namespace dsalt {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kBM = 64;
+
+template <typename T, int D> struct FwdShape;
+template <> struct FwdShape<bf16, 64> { static constexpr int BN = 64; };
+template <> struct FwdShape<bf16, 128> { static constexpr int BN = 32; };
+template <> struct FwdShape<f16, 64> { static constexpr int BN = 64; };
+template <> struct FwdShape<f16, 128> { static constexpr int BN = 32; };
+template <> struct FwdShape<float, 64> { static constexpr int BN = 32; };
+template <> struct FwdShape<float, 128> { static constexpr int BN = 16; };
+
+// Per-lane row bounds shared by the forward and dq kernels.
+struct RowInfo {
+    int i;       // sequence-relative row
+    bool valid;  // i < len
+    int lo, hi;  // window [lo, hi], or lo = INT_MAX, hi = -1 for padding rows
+    int cnt;     // visible landmark slots
+};
+
+__device__ __forceinline__ int lower_bound_lds(const int* a, int n, int x) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        int mid = (lo + hi) >> 1;
+        if (a[mid] < x) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
+    constexpr int BN = FwdShape<T, D>::BN;
+    constexpr int NST = BN / 16;
+    typedef Tile<T, D, BN> KT;
+    __shared__ __attribute__((aligned(16))) T Ks[2][BN * KT::RS];
+    __shared__ __attribute__((aligned(16))) T Vt[2][D * KT::TS];
+    __shared__ int lpos[kMaxLandmarks];
+    __shared__ float lb[kMaxLandmarks + 64];
+    __shared__ int red[4][3];
+    __shared__ int nvalid_s;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
+    const int total = p.n_heads * p.num_seqs * p.n_tiles;
+    const int L = xcd_swizzle(blockIdx.x, total);
+    const int t = L % p.n_tiles;
+    const int s = (L / p.n_tiles) % p.num_seqs;
+    const int h = L / (p.n_tiles * p.num_seqs);
+    const int st = p.cu[s];
+    const int len = max(0, min(min(p.cu[s + 1], p.total_len) - st, p.max_seqlen));
+    const int r0 = t * kBM;
+    if (r0 >= len) return;
+    const int kvh = h / (p.n_heads / p.n_kv_heads);
+    const int set = p.block_size ? r0 / p.block_size : 0;
+    const int K = p.k_lmk;
+    const int64_t set_off = (((int64_t)h * p.num_seqs + s) * p.n_sets + set) * K;
+    const float c2 = p.scale * kLog2e;
+    const float inv_scale = 1.0f / p.scale;
+
+    if (tid == 0) nvalid_s = 0;
+    __syncthreads();
+    for (int i = tid; i < K; i += 256) {
+        int v = p.lmk[set_off + i];
+        lpos[i] = v;
+        if (v >= 0 && (i + 1 == K || p.lmk[set_off + i + 1] < 0)) nvalid_s = i + 1;
+    }
+    for (int i = tid; i < K + 64; i += 256) lb[i] = (i < K && p.lbias) ? p.lbias[set_off + i] * inv_scale : 0.f;
+    __syncthreads();
+    const int nvalid = nvalid_s;
+
+    // rows of this lane
+    RowInfo ri;
+    ri.i = r0 + wave * 16 + (lane & 15);
+    ri.valid = ri.i < len;
+    if (ri.valid) {
+        int wi = max(p.w[st + ri.i], 1);
+        ri.lo = max(ri.i - wi + 1, 0);
+        ri.hi = ri.i;
+        ri.cnt = lower_bound_lds(lpos, nvalid, ri.lo);
+    } else {
+        ri.lo = 0x7fffffff;
+        ri.hi = -1;
+        ri.cnt = 0;
+    }
+    const int wlo = min16(ri.lo), whi = max16(ri.hi);
+    const int wLmax = max16(ri.lo), wHmin = min16(ri.hi);
+    const int wcmax = max16(ri.cnt), wcmin = min16(ri.valid ? ri.cnt : 0);
+    if (lane == 0) {
+        red[wave][0] = wlo;
+        red[wave][1] = whi;
+        red[wave][2] = wcmax;
+    }
+    __syncthreads();
+    int blo = red[0][0], bhi = red[0][1], bcm = red[0][2];
+    for (int w2 = 1; w2 < 4; ++w2) {
+        blo = min(blo, red[w2][0]);
+        bhi = max(bhi, red[w2][1]);
+        bcm = max(bcm, red[w2][2]);
+    }
+    const int cs = (blo / BN) * BN;
+    const int nband = (bhi - cs) / BN + 1;
+    const int nchunks = nband + ceil_div(bcm, BN);
+
+    RowReg<T, D> qr;
+    qr.load(ri.valid ? (const T*)p.q + (int64_t)(st + ri.i) * p.q_st + (int64_t)h * p.q_sh : nullptr, g);
+
+    const T* kbase = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)kvh * p.k_sh;
+    const T* vbase = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)kvh * p.v_sh;
+    auto krow = [&](int c, int rr) -> const T* {
+        if (c < nband) {
+            int j = cs + c * BN + rr;
+            return j <= bhi ? kbase + (int64_t)j * p.k_st : nullptr;
+        }
+        int sl = (c - nband) * BN + rr;
+        int pos = sl < bcm ? lpos[sl] : -1;
+        return (pos >= 0 && pos < len) ? kbase + (int64_t)pos * p.k_st : nullptr;
+    };
+    auto vrow = [&](int c, int rr) -> const T* {
+        if (c < nband) {
+            int j = cs + c * BN + rr;
+            return j <= bhi ? vbase + (int64_t)j * p.v_st : nullptr;
+        }
+        int sl = (c - nband) * BN + rr;
+        int pos = sl < bcm ? lpos[sl] : -1;
+        return (pos >= 0 && pos < len) ? vbase + (int64_t)pos * p.v_st : nullptr;
+    };
+
+    KT kt, vt;
+    kt.load(tid, [&](int rr) { return krow(0, rr); });
+    vt.load(tid, [&](int rr) { return vrow(0, rr); });
+    kt.store_rows(Ks[0], tid);
+    vt.store_cols(Vt[0], tid);
+    __syncthreads();
+
+    floatx4 acc[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+    const float thr = 8.0f / c2;
+    const float NEG = -INFINITY;
+
+    for (int c = 0; c < nchunks; ++c) {
+        const int buf = c & 1;
+        if (c + 1 < nchunks) {
+            kt.load(tid, [&](int rr) { return krow(c + 1, rr); });
+            vt.load(tid, [&](int rr) { return vrow(c + 1, rr); });
+        }
+        const bool band = c < nband;
+        const int base = band ? cs + c * BN : (c - nband) * BN;
+        floatx4 S[NST];
+        bool act[NST];
+#pragma unroll
+        for (int stt = 0; stt < NST; ++stt) {
+            const int a = base + stt * 16;
+            act[stt] = band ? (a <= whi && a + 15 >= wlo) : (a < wcmax);
+            if (!act[stt]) {
+                S[stt] = floatx4{NEG, NEG, NEG, NEG};
+                continue;
+            }
+            floatx4 ci;
+            if (band) {
+                if (a >= wLmax && a + 15 <= wHmin) {
+                    ci = floatx4{0.f, 0.f, 0.f, 0.f};
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        int j = a + 4 * g + r;
+                        ci[r] = (j >= ri.lo && j <= ri.hi) ? 0.f : NEG;
+                    }
+                }
+            } else {
+                const bool full = a + 15 < wcmin;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    int sl = a + 4 * g + r;
+                    ci[r] = (full || sl < ri.cnt) ? lb[sl] : NEG;
+                }
+            }
+            S[stt] = dot_rows<T, D>(Ks[buf], KT::RS, stt * 16, lane, qr, ci);
+        }
+        // online softmax over the chunk
+        float mx = NEG;
+#pragma unroll
+        for (int stt = 0; stt < NST; ++stt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, S[stt][r]);
+        mx = max_g4(mx);
+        const float mnew = fmaxf(m_run, mx);
+        if (__any(mnew > m_run + thr)) {
+            const float alpha = m_run == NEG ? 0.f : __builtin_amdgcn_exp2f((m_run - mnew) * c2);
+#pragma unroll
+            for (int dt = 0; dt < D / 16; ++dt) acc[dt] *= alpha;
+            l_run *= alpha;
+            m_run = mnew;
+        }
+        const float msc = m_run == NEG ? 0.f : m_run * c2;
+#pragma unroll
+        for (int stt = 0; stt < NST; ++stt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float e = __builtin_amdgcn_exp2f(S[stt][r] * c2 - msc);
+                S[stt][r] = e;
+                l_run += e;
+            }
+        if constexpr (sizeof(T) == 2) {
+#pragma unroll
+            for (int hp = 0; hp < NST / 2; ++hp)
+                if (act[2 * hp] || act[2 * hp + 1])
+                    acc_cols<T, D>(Vt[buf], KT::TS, hp * 32, lane, S[2 * hp], S[2 * hp + 1], acc);
+        } else {
+#pragma unroll
+            for (int stt = 0; stt < NST; ++stt)
+                if (act[stt]) acc_cols32<D>((const float*)Vt[buf], KT::TS, stt * 16, lane, S[stt], acc);
+        }
+        if (c + 1 < nchunks) {
+            kt.store_rows(Ks[buf ^ 1], tid);
+            vt.store_cols(Vt[buf ^ 1], tid);
+        }
+        __syncthreads();
+    }
+
+    const float l_tot = sum_g4(l_run);
+    if (ri.valid) {
+        const float inv = 1.0f / l_tot;
+        T* orow = (T*)p.o + (int64_t)(st + ri.i) * p.o_st + (int64_t)h * p.o_sh;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) {
+            T ov[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ov[r] = from_float<T>(acc[dt][r] * inv);
+            if constexpr (sizeof(T) == 2) {
+                *(uint2*)(orow + dt * 16 + 4 * g) = *(const uint2*)ov;
+            } else {
+                *(floatx4*)(orow + dt * 16 + 4 * g) = *(const floatx4*)ov;
+            }
+        }
+        if (g == 0) p.lse_out[(int64_t)(st + ri.i) * p.n_heads + h] = m_run * p.scale + __logf(l_tot);
+    }
+}
+
+template <typename T>
+static hipError_t fwd_dispatch(const AttnParams& p, hipStream_t stream) {
+    const int total = p.n_heads * p.num_seqs * p.n_tiles;
+    if (total == 0) return hipSuccess;
+    if (p.head_dim == 64)
+        hipLaunchKernelGGL((fwd_kernel<T, 64>), dim3(total), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((fwd_kernel<T, 128>), dim3(total), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t fwd_launch(const AttnParams& p, hipStream_t stream) {
+    if (p.dtype == DSALT_DTYPE_BF16) return fwd_dispatch<bf16>(p, stream);
+    if (p.dtype == DSALT_DTYPE_F16) return fwd_dispatch<f16>(p, stream);
+    return fwd_dispatch<float>(p, stream);
+}
+
+}  // namespace dsalt

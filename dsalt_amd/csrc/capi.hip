@@ -1,0 +1,298 @@
+// C ABI of the DSALT library: argument validation, workspace sizing and
+// dispatch to the selection / forward / backward launchers.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "attn.h"
+#include "select.h"
+#include "common.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return DSALT_OK;
+    return fail(DSALT_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+size_t esize(int dtype) { return dtype == DSALT_DTYPE_F32 ? 4 : 2; }
+
+int n_sets_of(const dsalt_problem& p) {
+    if (p.select_mode == DSALT_SELECT_GLOBAL) return 1;
+    return (p.max_seqlen + p.block_size - 1) / p.block_size;
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+int check_problem(const dsalt_problem& p, bool attention) {
+    if (p.total_len < 0 || p.num_seqs < 1) return fail(DSALT_ERR_INVALID, "total_len must be >= 0 and num_seqs >= 1");
+    if (p.max_seqlen < 1 || (int64_t)p.max_seqlen > (int64_t)p.total_len + (p.total_len == 0))
+        return fail(DSALT_ERR_INVALID, "max_seqlen %d outside [1, total_len=%d]", p.max_seqlen, p.total_len);
+    if (p.n_heads < 1 || p.n_kv_heads < 1 || p.n_heads % p.n_kv_heads)
+        return fail(DSALT_ERR_INVALID, "n_heads (%d) must be a positive multiple of n_kv_heads (%d)", p.n_heads,
+                    p.n_kv_heads);
+    if (p.head_dim != 64 && p.head_dim != 128)
+        return fail(DSALT_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", p.head_dim);
+    if (p.k_lmk < 0 || p.k_lmk > dsalt::kMaxLandmarks)
+        return fail(DSALT_ERR_INVALID, "k_lmk %d outside [0, %d]", p.k_lmk, dsalt::kMaxLandmarks);
+    if (p.select_mode != DSALT_SELECT_GLOBAL && p.select_mode != DSALT_SELECT_BLOCK)
+        return fail(DSALT_ERR_INVALID, "unknown select_mode %d", p.select_mode);
+    if (p.select_mode == DSALT_SELECT_BLOCK && (p.block_size < 64 || p.block_size % 64))
+        return fail(DSALT_ERR_INVALID, "block_size %d must be a positive multiple of 64", p.block_size);
+    if (p.dtype != DSALT_DTYPE_F32 && p.dtype != DSALT_DTYPE_BF16 && p.dtype != DSALT_DTYPE_F16)
+        return fail(DSALT_ERR_INVALID, "unknown dtype %d", p.dtype);
+    (void)attention;
+    return DSALT_OK;
+}
+
+int check_rows(const void* ptr, int64_t st, int64_t sh, int dtype, const char* name) {
+    if (!ptr) return fail(DSALT_ERR_INVALID, "%s is null", name);
+    if (!aligned16(ptr)) return fail(DSALT_ERR_INVALID, "%s must be 16-byte aligned", name);
+    size_t es = esize(dtype);
+    if ((st * (int64_t)es) % 16 || (sh * (int64_t)es) % 16 || st <= 0 || sh < 0)
+        return fail(DSALT_ERR_INVALID, "%s strides (%lld, %lld) must be positive multiples of 16 bytes", name,
+                    (long long)st, (long long)sh);
+    return DSALT_OK;
+}
+
+dsalt::SelectParams select_params(const dsalt_select_args* a) {
+    dsalt::SelectParams p;
+    const dsalt_problem& q = a->p;
+    p.total_len = q.total_len;
+    p.num_seqs = q.num_seqs;
+    p.max_seqlen = q.max_seqlen;
+    p.n_heads = q.n_heads;
+    p.n_kv_heads = q.n_kv_heads;
+    p.head_dim = q.head_dim;
+    p.k_lmk = q.k_lmk;
+    p.select_mode = q.select_mode;
+    p.block_size = q.block_size;
+    p.dtype = q.dtype;
+    p.hidden = a->hidden;
+    p.stats_scope = a->stats_scope;
+    p.n_sets = n_sets_of(q);
+    p.h = a->h;
+    p.h_stride_t = a->h_stride_t;
+    p.v = a->v;
+    p.v_stride_t = a->v_stride_t;
+    p.v_stride_h = a->v_stride_h;
+    p.alpha = a->alpha;
+    p.w = a->w;
+    p.cu = a->cu_seqlens;
+    p.lmk_idx = a->lmk_idx;
+    p.z_x = a->z_x;
+    p.z_v = a->z_v;
+    p.scores = a->scores;
+    return p;
+}
+
+int check_select(const dsalt_select_args* a) {
+    if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
+    int rc = check_problem(a->p, false);
+    if (rc) return rc;
+    size_t es = esize(a->p.dtype);
+    if (a->hidden <= 0 || (a->hidden * es) % 16)
+        return fail(DSALT_ERR_INVALID, "hidden %d must be a positive multiple of 16 bytes", a->hidden);
+    if (a->stats_scope != DSALT_STATS_PACKED && a->stats_scope != DSALT_STATS_SEQUENCE)
+        return fail(DSALT_ERR_INVALID, "unknown stats_scope %d", a->stats_scope);
+    if ((rc = check_rows(a->h, a->h_stride_t, 0, a->p.dtype, "h"))) return rc;
+    if ((rc = check_rows(a->v, a->v_stride_t, a->v_stride_h, a->p.dtype, "v"))) return rc;
+    if (!a->alpha || !a->w || !a->cu_seqlens || (a->p.k_lmk > 0 && !a->lmk_idx))
+        return fail(DSALT_ERR_INVALID, "alpha, w, cu_seqlens and lmk_idx are required");
+    if (a->p.select_mode == DSALT_SELECT_BLOCK && (a->z_x || a->z_v || a->scores))
+        return fail(DSALT_ERR_INVALID, "z_x / z_v / scores are outputs of the global variant only");
+    return DSALT_OK;
+}
+
+dsalt::AttnParams attn_common(const dsalt_problem& q, float scale) {
+    dsalt::AttnParams p = {};
+    p.total_len = q.total_len;
+    p.num_seqs = q.num_seqs;
+    p.max_seqlen = q.max_seqlen;
+    p.n_heads = q.n_heads;
+    p.n_kv_heads = q.n_kv_heads;
+    p.head_dim = q.head_dim;
+    p.k_lmk = q.k_lmk;
+    p.n_sets = n_sets_of(q);
+    p.block_size = q.select_mode == DSALT_SELECT_BLOCK ? q.block_size : 0;
+    p.dtype = q.dtype;
+    p.n_tiles = (q.max_seqlen + 63) / 64;
+    p.scale = scale;
+    return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsalt_abi_version(void) { return DSALT_ABI_VERSION; }
+
+const char* dsalt_last_error(void) { return g_err.c_str(); }
+
+size_t dsalt_select_workspace_bytes(const dsalt_select_args* a) {
+    if (check_select(a)) return 0;
+    return dsalt::select_workspace(select_params(a));
+}
+
+int dsalt_select_with_border_cap(const dsalt_select_args* a, dsalt_stream_t stream, int border_cap) {
+    int rc = check_select(a);
+    if (rc) return rc;
+    dsalt::SelectParams p = select_params(a);
+    size_t need = dsalt::select_workspace(p);
+    if (!a->workspace || a->workspace_bytes < need)
+        return fail(DSALT_ERR_WORKSPACE, "selection needs %zu workspace bytes, got %zu", need, a->workspace_bytes);
+    if (border_cap < 1) return fail(DSALT_ERR_INVALID, "border_cap must be >= 1");
+    return hip_status(dsalt::select_launch(p, a->workspace, (hipStream_t)stream, border_cap), "dsalt_select");
+}
+
+int dsalt_select(const dsalt_select_args* a, dsalt_stream_t stream) {
+    return dsalt_select_with_border_cap(a, stream, 1 << 30);
+}
+
+size_t dsalt_fwd_workspace_bytes(const dsalt_fwd_args* a) {
+    (void)a;
+    return 0;
+}
+
+int dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream) {
+    if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
+    int rc = check_problem(a->p, true);
+    if (rc) return rc;
+    const int dt = a->p.dtype;
+    if ((rc = check_rows(a->q, a->q_stride_t, a->q_stride_h, dt, "q"))) return rc;
+    if ((rc = check_rows(a->k, a->k_stride_t, a->k_stride_h, dt, "k"))) return rc;
+    if ((rc = check_rows(a->v, a->v_stride_t, a->v_stride_h, dt, "v"))) return rc;
+    if ((rc = check_rows(a->out, a->o_stride_t, a->o_stride_h, dt, "out"))) return rc;
+    if (!a->w || !a->cu_seqlens || !a->lse || (a->p.k_lmk > 0 && !a->lmk_idx))
+        return fail(DSALT_ERR_INVALID, "w, cu_seqlens, lse and lmk_idx are required");
+    if (!(a->scale > 0.f)) return fail(DSALT_ERR_INVALID, "scale must be positive");
+    dsalt::AttnParams p = attn_common(a->p, a->scale);
+    p.q = a->q;
+    p.q_st = a->q_stride_t;
+    p.q_sh = a->q_stride_h;
+    p.k = a->k;
+    p.k_st = a->k_stride_t;
+    p.k_sh = a->k_stride_h;
+    p.v = a->v;
+    p.v_st = a->v_stride_t;
+    p.v_sh = a->v_stride_h;
+    p.o = a->out;
+    p.o_st = a->o_stride_t;
+    p.o_sh = a->o_stride_h;
+    p.lse_out = a->lse;
+    p.w = a->w;
+    p.cu = a->cu_seqlens;
+    p.lmk = a->lmk_idx;
+    p.lbias = a->lmk_bias;
+    return hip_status(dsalt::fwd_launch(p, (hipStream_t)stream), "dsalt_fwd");
+}
+
+static int bwd_params(const dsalt_bwd_args* a, dsalt::AttnParams* out) {
+    if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
+    int rc = check_problem(a->p, true);
+    if (rc) return rc;
+    if (a->p.select_mode != DSALT_SELECT_GLOBAL)
+        return fail(DSALT_ERR_UNSUPPORTED, "backward of the block-causal variant is not implemented");
+    if (a->p.n_kv_heads != a->p.n_heads)
+        return fail(DSALT_ERR_UNSUPPORTED, "backward needs n_kv_heads == n_heads (expand GQA heads first)");
+    const int dt = a->p.dtype;
+    if ((rc = check_rows(a->q, a->q_stride_t, a->q_stride_h, dt, "q"))) return rc;
+    if ((rc = check_rows(a->k, a->k_stride_t, a->k_stride_h, dt, "k"))) return rc;
+    if ((rc = check_rows(a->v, a->v_stride_t, a->v_stride_h, dt, "v"))) return rc;
+    if ((rc = check_rows(a->out, a->o_stride_t, a->o_stride_h, dt, "out"))) return rc;
+    if ((rc = check_rows(a->dout, a->do_stride_t, a->do_stride_h, dt, "dout"))) return rc;
+    if (!a->dq || !a->dk || !a->dv || !aligned16(a->dq) || !aligned16(a->dk) || !aligned16(a->dv))
+        return fail(DSALT_ERR_INVALID, "dq, dk, dv must be non-null and 16-byte aligned");
+    if (!a->w || !a->cu_seqlens || !a->lse || (a->p.k_lmk > 0 && !a->lmk_idx))
+        return fail(DSALT_ERR_INVALID, "w, cu_seqlens, lse and lmk_idx are required");
+    if (!(a->scale > 0.f)) return fail(DSALT_ERR_INVALID, "scale must be positive");
+    dsalt::AttnParams p = attn_common(a->p, a->scale);
+    p.q = a->q;
+    p.q_st = a->q_stride_t;
+    p.q_sh = a->q_stride_h;
+    p.k = a->k;
+    p.k_st = a->k_stride_t;
+    p.k_sh = a->k_stride_h;
+    p.v = a->v;
+    p.v_st = a->v_stride_t;
+    p.v_sh = a->v_stride_h;
+    p.o = a->out;
+    p.o_st = a->o_stride_t;
+    p.o_sh = a->o_stride_h;
+    p.dout = a->dout;
+    p.do_st = a->do_stride_t;
+    p.do_sh = a->do_stride_h;
+    p.lse = a->lse;
+    p.w = a->w;
+    p.cu = a->cu_seqlens;
+    p.lmk = a->lmk_idx;
+    p.lbias = a->lmk_bias;
+    p.dq = a->dq;
+    p.dk = a->dk;
+    p.dv = a->dv;
+    p.d_bias = a->d_bias;
+    *out = p;
+    return DSALT_OK;
+}
+
+size_t dsalt_bwd_workspace_bytes(const dsalt_bwd_args* a) {
+    dsalt::AttnParams p;
+    if (bwd_params(a, &p)) return 0;
+    return dsalt::bwd_workspace(p);
+}
+
+int dsalt_bwd(const dsalt_bwd_args* a, dsalt_stream_t stream) {
+    dsalt::AttnParams p;
+    int rc = bwd_params(a, &p);
+    if (rc) return rc;
+    size_t need = dsalt::bwd_workspace(p);
+    if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
+        return fail(DSALT_ERR_WORKSPACE, "backward needs %zu workspace bytes, got %zu", need, a->workspace_bytes);
+    return hip_status(dsalt::bwd_launch(p, a->workspace, (hipStream_t)stream), "dsalt_bwd");
+}
+
+int dsalt_gather_landmarks(const dsalt_gather_args* a, dsalt_stream_t stream) {
+    if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
+    int rc = check_problem(a->p, false);
+    if (rc) return rc;
+    const int dt = a->p.dtype;
+    if ((rc = check_rows(a->k, a->k_stride_t, a->k_stride_h, dt, "k"))) return rc;
+    if ((rc = check_rows(a->v, a->v_stride_t, a->v_stride_h, dt, "v"))) return rc;
+    if (!a->cu_seqlens || !a->lmk_idx || !a->lmk_k || !a->lmk_v || !aligned16(a->lmk_k) || !aligned16(a->lmk_v))
+        return fail(DSALT_ERR_INVALID, "cu_seqlens, lmk_idx, lmk_k, lmk_v are required (16-byte aligned)");
+    dsalt::GatherParams p;
+    p.total_len = a->p.total_len;
+    p.num_seqs = a->p.num_seqs;
+    p.n_heads = a->p.n_heads;
+    p.n_kv_heads = a->p.n_kv_heads;
+    p.head_dim = a->p.head_dim;
+    p.k_lmk = a->p.k_lmk;
+    p.n_sets = n_sets_of(a->p);
+    p.dtype = dt;
+    p.k = a->k;
+    p.k_stride_t = a->k_stride_t;
+    p.k_stride_h = a->k_stride_h;
+    p.v = a->v;
+    p.v_stride_t = a->v_stride_t;
+    p.v_stride_h = a->v_stride_h;
+    p.cu = a->cu_seqlens;
+    p.lmk_idx = a->lmk_idx;
+    p.lmk_k = a->lmk_k;
+    p.lmk_v = a->lmk_v;
+    return hip_status(dsalt::gather_launch(p, (hipStream_t)stream), "dsalt_gather_landmarks");
+}
+
+}  // extern "C"

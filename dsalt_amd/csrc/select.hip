@@ -1,0 +1,524 @@
+// Landmark selection for gfx950.
+//
+// Replaces hybrid_scores_per_head (dsalt/kernels/landmark_tokens_ker.py:19-61),
+// _compute_landmark_indices (dsalt/kernels/selectors.py:75-134) and the
+// block-causal _select (results/causal_landmark_check.py:82-113).
+//
+// Pipeline (all stream-ordered, no host sync):
+//   sel_norms   one wave per token: |h_t| and |v_{t,g}| (fp64 sums of squares,
+//               lane-strided 16-byte chunks + xor butterfly), rounded to fp32 and
+//               then to the input dtype.
+//   sel_sums    one 256-thread block per (range, signal): fp64 S1, S2 by 256
+//               strided partials and a halving tree.
+//   sel_stats   mean / unbiased std per scope, or per block-causal prefix by
+//               adding whole-block sums in block order.
+//   sel_z       (global) z = fp32((a - mean)/std) in fp64, optional API outputs.
+//   sel_topk    one 1024-thread block per landmark set: radix select on the
+//               64-bit key (order(score) << 32 | ~index) -- so ties go to the
+//               lower index -- 8 bits per pass until the boundary bin fits in
+//               LDS, then a bitonic sort of that bin; output ascending indices.
+// The arithmetic order above is the canonical one that the CPU oracle
+// restates; this file is compiled with -ffp-contract=off.
+#include "common.h"
+#include "select.h"
+
+namespace dsalt {
+
+constexpr int kSelThreads = 1024;
+constexpr int kSelWaves = kSelThreads / kWave;
+constexpr int kBorderCap = 2048;
+
+__device__ __forceinline__ int pow2ceil64(int n) {
+    int g = 1;
+    while (g < n && g < 64) g <<= 1;
+    return g;
+}
+
+// ------------------------------------------------------------------ norms
+template <typename T>
+__global__ __launch_bounds__(256) void sel_norms_kernel(SelectParams p, float* nx, float* nv) {
+    constexpr int VW = 16 / (int)sizeof(T);
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63;
+    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    const int hch = p.hidden / VW, gh = pow2ceil64(hch);
+    const int vch = p.head_dim / VW, gv = pow2ceil64(vch);
+    const int hpp = 64 / gv;  // value heads per pass
+    for (int t = (blockIdx.x * blockDim.x + threadIdx.x) >> 6; t < p.total_len; t += nwaves) {
+        // hidden-state norm
+        const T* hr = (const T*)p.h + (int64_t)t * p.h_stride_t;
+        double acc = 0.0;
+        if (lane < gh) {
+            for (int ch = lane; ch < hch; ch += gh) {
+                u4 raw = *(const u4*)(hr + ch * VW);
+                const T* e = (const T*)&raw;
+#pragma unroll
+                for (int i = 0; i < VW; ++i) {
+                    double x = (double)to_float(e[i]);
+                    acc = __dadd_rn(acc, __dmul_rn(x, x));
+                }
+            }
+        }
+        for (int off = gh >> 1; off >= 1; off >>= 1) acc = __dadd_rn(acc, wave_xor(acc, off));
+        if (lane == 0) nx[t] = round_norm<T>((float)canon_sqrt64(acc));
+        // value-vector norms, gv lanes per kv head
+        for (int g0 = 0; g0 < p.n_kv_heads; g0 += hpp) {
+            int g = g0 + lane / gv, sub = lane % gv;
+            double a2 = 0.0;
+            if (g < p.n_kv_heads && sub < vch) {
+                const T* vr = (const T*)p.v + (int64_t)t * p.v_stride_t + (int64_t)g * p.v_stride_h;
+                u4 raw = *(const u4*)(vr + sub * VW);
+                const T* e = (const T*)&raw;
+#pragma unroll
+                for (int i = 0; i < VW; ++i) {
+                    double x = (double)to_float(e[i]);
+                    a2 = __dadd_rn(a2, __dmul_rn(x, x));
+                }
+            }
+            for (int off = gv >> 1; off >= 1; off >>= 1) a2 = __dadd_rn(a2, wave_xor(a2, off));
+            if (sub == 0 && g < p.n_kv_heads)
+                nv[(int64_t)g * p.total_len + t] = round_norm<T>((float)canon_sqrt64(a2));
+        }
+    }
+}
+
+// ------------------------------------------------------------- statistics
+// Range r of signal sig: global/packed r=0 -> [0,T); global/sequence r=s ->
+// sequence s; block r = s*n_sets + b -> block b of sequence s.
+__device__ __forceinline__ void range_of(const SelectParams& p, int r, int& r0, int& r1) {
+    if (p.select_mode == DSALT_SELECT_GLOBAL) {
+        if (p.stats_scope == DSALT_STATS_PACKED) {
+            r0 = 0;
+            r1 = p.total_len;
+        } else {
+            r0 = p.cu[r];
+            r1 = min(p.cu[r + 1], p.total_len);
+        }
+    } else {
+        int s = r / p.n_sets, b = r % p.n_sets;
+        int st = p.cu[s], en = min(p.cu[s + 1], p.total_len);
+        r0 = min(st + b * p.block_size, en);
+        r1 = min(r0 + p.block_size, en);
+    }
+}
+
+__global__ __launch_bounds__(256) void sel_sums_kernel(SelectParams p, const float* nx, const float* nv,
+                                                       double* sums) {
+    __shared__ double a1[256], a2[256];
+    const int r = blockIdx.x, sig = blockIdx.y, t = threadIdx.x;
+    const float* x = sig == 0 ? nx : nv + (int64_t)(sig - 1) * p.total_len;
+    int r0, r1;
+    range_of(p, r, r0, r1);
+    double s1 = 0.0, s2 = 0.0;
+    for (int j = r0 + t; j < r1; j += 256) {
+        double v = (double)x[j];
+        s1 = __dadd_rn(s1, v);
+        s2 = __dadd_rn(s2, __dmul_rn(v, v));
+    }
+    a1[t] = s1;
+    a2[t] = s2;
+    __syncthreads();
+    for (int off = 128; off >= 1; off >>= 1) {
+        if (t < off) {
+            a1[t] = __dadd_rn(a1[t], a1[t + off]);
+            a2[t] = __dadd_rn(a2[t], a2[t + off]);
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        int nsig = 1 + p.n_kv_heads;
+        sums[((int64_t)r * nsig + sig) * 2 + 0] = a1[0];
+        sums[((int64_t)r * nsig + sig) * 2 + 1] = a2[0];
+    }
+}
+
+__device__ __forceinline__ void mean_std(double s1, double s2, int n, double& mean, double& sd) {
+    double m = __ddiv_rn(s1, (double)n);
+    double den = (double)(n - 1 > 1 ? n - 1 : 1);
+    double var = __ddiv_rn(__dadd_rn(s2, -__dmul_rn(__dmul_rn((double)n, m), m)), den);
+    if (!(var > 0.0)) var = 0.0;
+    double s = canon_sqrt64(var);
+    if (s < 1e-6) s = 1e-6;
+    mean = m;
+    sd = s;
+}
+
+// stats[(r * nsig + sig) * 2] = {mean, std}; r indexes ranges (global) or
+// (sequence, block) sets (block-causal, prefix over earlier blocks).
+__global__ void sel_stats_kernel(SelectParams p, const double* sums, double* stats, int nranges) {
+    const int nsig = 1 + p.n_kv_heads;
+    const int id = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p.select_mode == DSALT_SELECT_GLOBAL) {
+        if (id >= nranges * nsig) return;
+        int r = id / nsig;
+        int r0, r1;
+        range_of(p, r, r0, r1);
+        double m = 0.0, sd = 1.0;
+        if (r1 > r0) mean_std(sums[id * 2], sums[id * 2 + 1], r1 - r0, m, sd);
+        stats[id * 2] = m;
+        stats[id * 2 + 1] = sd;
+    } else {
+        if (id >= p.num_seqs * nsig) return;
+        int s = id / nsig, sig = id % nsig;
+        int len = min(p.cu[s + 1], p.total_len) - p.cu[s];
+        double p1 = 0.0, p2 = 0.0;
+        for (int b = 0; b < p.n_sets; ++b) {
+            int64_t o = ((int64_t)(s * p.n_sets + b) * nsig + sig) * 2;
+            int b0 = b * p.block_size;
+            double m = 0.0, sd = 1.0;
+            if (b0 >= 2 && b0 < len) mean_std(p1, p2, b0, m, sd);
+            stats[o] = m;
+            stats[o + 1] = sd;
+            if (b0 < len) {
+                p1 = __dadd_rn(p1, sums[o]);
+                p2 = __dadd_rn(p2, sums[o + 1]);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ float zscore(float a, double mean, double sd) {
+    return (float)__ddiv_rn(__dadd_rn((double)a, -mean), sd);
+}
+
+__device__ __forceinline__ float mix_score(float alpha, float zv, float zx) {
+    float t1 = __fmul_rn(alpha, zv);
+    float om = __fsub_rn(1.0f, alpha);
+    float t2 = __fmul_rn(om, zx);
+    float s = __fadd_rn(t1, t2);
+    return s == 0.0f ? 0.0f : s;
+}
+
+__device__ __forceinline__ uint32_t order_key(float s) {
+    uint32_t u = __float_as_uint(s);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// global variant: z per token (head-major zv for the selection), API outputs
+__global__ __launch_bounds__(256) void sel_z_kernel(SelectParams p, const float* nx, const float* nv,
+                                                    const double* stats, float* zx, float* zv) {
+    const int s = blockIdx.y;
+    const int nsig = 1 + p.n_kv_heads;
+    int st = p.cu[s], en = min(p.cu[s + 1], p.total_len);
+    int t = st + blockIdx.x * 256 + threadIdx.x;
+    if (t >= en) return;
+    int r = p.stats_scope == DSALT_STATS_PACKED ? 0 : s;
+    const double* sr = stats + (int64_t)r * nsig * 2;
+    float zxt = zscore(nx[t], sr[0], sr[1]);
+    zx[t] = zxt;
+    if (p.z_x) p.z_x[t] = zxt;
+    for (int g = 0; g < p.n_kv_heads; ++g) {
+        float z = zscore(nv[(int64_t)g * p.total_len + t], sr[2 * (g + 1)], sr[2 * (g + 1) + 1]);
+        zv[(int64_t)g * p.total_len + t] = z;
+        if (p.z_v) p.z_v[(int64_t)t * p.n_kv_heads + g] = z;
+    }
+    if (p.scores) {
+        int rep = p.n_heads / p.n_kv_heads;
+        for (int h = 0; h < p.n_heads; ++h)
+            p.scores[(int64_t)t * p.n_heads + h] = mix_score(p.alpha[h], zv[(int64_t)(h / rep) * p.total_len + t], zxt);
+    }
+}
+
+// ------------------------------------------------------------------ top-k
+struct TopkShared {
+    uint32_t hist[kSelWaves][256];
+    unsigned long long border[kBorderCap];
+    int sel[kMaxLandmarks];
+    uint32_t total;
+    int digit;
+    uint32_t above;
+    uint32_t nsure;
+    uint32_t nborder;
+};
+
+// key of candidate j_rel, or 0 when j_rel is not a candidate
+struct KeyFn {
+    const int32_t* w;
+    int total_len;
+    int st, rep_g, h;
+    float alpha;
+    bool block;
+    const float *zx, *zv, *nx, *nv;
+    double mx, sx, mv, sv;
+    __device__ __forceinline__ unsigned long long operator()(int j) const {
+        if (j < w[st + j]) return 0ull;
+        float zxj, zvj;
+        if (!block) {
+            zxj = zx[st + j];
+            zvj = zv[(int64_t)rep_g * total_len + st + j];
+        } else {
+            zxj = zscore(nx[st + j], mx, sx);
+            zvj = zscore(nv[(int64_t)rep_g * total_len + st + j], mv, sv);
+        }
+        uint32_t u = order_key(mix_score(alpha, zvj, zxj));
+        return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)j);
+    }
+};
+
+__device__ void bitonic_desc_u64(unsigned long long* a, int n, int tid) {
+    for (int size = 2; size <= n; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < (n >> 1); i += kSelThreads) {
+                int lo = (i / stride) * 2 * stride + (i % stride), hi = lo + stride;
+                bool desc = (lo & size) == 0;
+                unsigned long long x = a[lo], y = a[hi];
+                if ((x < y) == desc) {
+                    a[lo] = y;
+                    a[hi] = x;
+                }
+            }
+            __syncthreads();
+        }
+}
+
+__device__ void bitonic_asc_i32(int* a, int n, int tid) {
+    for (int size = 2; size <= n; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < (n >> 1); i += kSelThreads) {
+                int lo = (i / stride) * 2 * stride + (i % stride), hi = lo + stride;
+                bool asc = (lo & size) == 0;
+                int x = a[lo], y = a[hi];
+                if ((x > y) == asc) {
+                    a[lo] = y;
+                    a[hi] = x;
+                }
+            }
+            __syncthreads();
+        }
+}
+
+__global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, const float* zx, const float* zv,
+                                                               const float* nx, const float* nv,
+                                                               const double* stats, int border_cap) {
+    __shared__ TopkShared sh;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int set = blockIdx.x % p.n_sets;
+    const int s = (blockIdx.x / p.n_sets) % p.num_seqs;
+    const int h = blockIdx.x / (p.n_sets * p.num_seqs);
+    const int K = p.k_lmk;
+    int32_t* out = p.lmk_idx + (((int64_t)h * p.num_seqs + s) * p.n_sets + set) * K;
+    const int st = p.cu[s];
+    const int len = max(0, min(p.cu[s + 1], p.total_len) - st);
+    const bool block = p.select_mode == DSALT_SELECT_BLOCK;
+    int n = len;
+    KeyFn key;
+    key.w = p.w;
+    key.total_len = p.total_len;
+    key.st = st;
+    key.h = h;
+    key.rep_g = h / (p.n_heads / p.n_kv_heads);
+    key.alpha = p.alpha[h];
+    key.block = block;
+    key.zx = zx;
+    key.zv = zv;
+    key.nx = nx;
+    key.nv = nv;
+    if (block) {
+        int b0 = set * p.block_size;
+        if (b0 < 2 || b0 >= len) {
+            for (int i = tid; i < K; i += kSelThreads) out[i] = -1;
+            return;
+        }
+        n = b0;
+        const int nsig = 1 + p.n_kv_heads;
+        const double* sr = stats + (int64_t)(s * p.n_sets + set) * nsig * 2;
+        key.mx = sr[0];
+        key.sx = sr[1];
+        key.mv = sr[2 * (key.rep_g + 1)];
+        key.sv = sr[2 * (key.rep_g + 1) + 1];
+    }
+    const int cap = min(border_cap, kBorderCap);
+
+    unsigned long long prefix = 0ull;
+    int plen = 0;
+    uint32_t k_rem = (uint32_t)K;
+    bool all_sure = false;
+    for (;;) {
+        for (int i = tid; i < kSelWaves * 256; i += kSelThreads) (&sh.hist[0][0])[i] = 0u;
+        __syncthreads();
+        const int shift = 56 - plen;
+        for (int j = tid; j < n; j += kSelThreads) {
+            unsigned long long kj = key(j);
+            if (kj == 0ull) continue;
+            if (plen > 0 && (kj >> (64 - plen)) != prefix) continue;
+            atomicAdd(&sh.hist[wave][(uint32_t)(kj >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid < 256) {
+            uint32_t c = 0;
+            for (int w2 = 0; w2 < kSelWaves; ++w2) c += sh.hist[w2][tid];
+            sh.hist[0][tid] = c;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            uint32_t c0 = sh.hist[0][4 * lane], c1 = sh.hist[0][4 * lane + 1];
+            uint32_t c2 = sh.hist[0][4 * lane + 2], c3 = sh.hist[0][4 * lane + 3];
+            uint32_t loc = c0 + c1 + c2 + c3, suf = loc;
+            for (int off = 1; off < 64; off <<= 1) {
+                uint32_t o = __shfl_down(suf, off, 64);
+                if (lane + off < 64) suf += o;
+            }
+            uint32_t excl = suf - loc;  // bins >= 4*lane+4
+            if (plen == 0 && lane == 0) sh.total = suf;
+            uint32_t cs[4] = {c0, c1, c2, c3};
+            uint32_t above = excl;
+            for (int b = 3; b >= 0; --b) {
+                if (above < k_rem && above + cs[b] >= k_rem) {
+                    sh.digit = 4 * lane + b;
+                    sh.above = above;
+                }
+                above += cs[b];
+            }
+        }
+        __syncthreads();
+        if (plen == 0 && sh.total <= k_rem) {
+            all_sure = true;
+            break;
+        }
+        const int d = sh.digit;
+        const uint32_t above = sh.above;
+        const uint32_t inbin = sh.hist[0][d];
+        __syncthreads();
+        k_rem -= above;
+        prefix = (prefix << 8) | (unsigned long long)d;
+        plen += 8;
+        if ((int)inbin <= cap || plen == 64) break;
+    }
+
+    // collect: sure candidates (prefix above) and the boundary bin
+    if (tid == 0) {
+        sh.nsure = 0u;
+        sh.nborder = 0u;
+    }
+    __syncthreads();
+    for (int j = tid; j < n; j += kSelThreads) {
+        unsigned long long kj = key(j);
+        if (kj == 0ull) continue;
+        if (all_sure) {
+            sh.sel[atomicAdd(&sh.nsure, 1u)] = j;
+            continue;
+        }
+        unsigned long long top = kj >> (64 - plen);
+        if (top > prefix) sh.sel[atomicAdd(&sh.nsure, 1u)] = j;
+        else if (top == prefix) sh.border[atomicAdd(&sh.nborder, 1u)] = kj;
+    }
+    __syncthreads();
+    int nsel = (int)sh.nsure;
+    if (!all_sure) {
+        int nb = (int)sh.nborder, nb2 = 1;
+        while (nb2 < nb) nb2 <<= 1;
+        for (int i = nb + tid; i < nb2; i += kSelThreads) sh.border[i] = 0ull;
+        __syncthreads();
+        bitonic_desc_u64(sh.border, nb2, tid);
+        for (int i = tid; i < (int)k_rem; i += kSelThreads)
+            sh.sel[nsel + i] = (int)(0xffffffffu - (uint32_t)(sh.border[i] & 0xffffffffull));
+        nsel += (int)k_rem;
+        __syncthreads();
+    }
+    int ns2 = 1;
+    while (ns2 < nsel) ns2 <<= 1;
+    for (int i = nsel + tid; i < ns2; i += kSelThreads) sh.sel[i] = 0x7fffffff;
+    __syncthreads();
+    bitonic_asc_i32(sh.sel, ns2, tid);
+    for (int i = tid; i < K; i += kSelThreads) out[i] = i < nsel ? sh.sel[i] : -1;
+}
+
+// --------------------------------------------------------------- gather
+template <typename T>
+__global__ __launch_bounds__(256) void gather_kernel(GatherParams p) {
+    constexpr int VW = 16 / (int)sizeof(T);
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const int vpr = p.head_dim / VW;  // vectors per row
+    const int64_t nrows = (int64_t)p.n_heads * p.num_seqs * p.n_sets * p.k_lmk;
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= nrows * vpr) return;
+    const int c = (int)(id % vpr);
+    const int64_t row = id / vpr;
+    const int s = (int)((row / ((int64_t)p.n_sets * p.k_lmk)) % p.num_seqs);
+    const int h = (int)(row / ((int64_t)p.num_seqs * p.n_sets * p.k_lmk));
+    const int g = h / (p.n_heads / p.n_kv_heads);
+    const int pos = p.lmk_idx[row];
+    const int st = p.cu[s], len = max(0, min(p.cu[s + 1], p.total_len) - st);
+    u4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
+    if (pos >= 0 && pos < len) {
+        kv = *(const u4*)((const T*)p.k + (int64_t)(st + pos) * p.k_stride_t + (int64_t)g * p.k_stride_h + c * VW);
+        vv = *(const u4*)((const T*)p.v + (int64_t)(st + pos) * p.v_stride_t + (int64_t)g * p.v_stride_h + c * VW);
+    }
+    *(u4*)((T*)p.lmk_k + row * p.head_dim + c * VW) = kv;
+    *(u4*)((T*)p.lmk_v + row * p.head_dim + c * VW) = vv;
+}
+
+// ------------------------------------------------------------- launchers
+size_t select_workspace(const SelectParams& p) {
+    const int nsig = 1 + p.n_kv_heads;
+    const int nranges = p.select_mode == DSALT_SELECT_GLOBAL
+                            ? (p.stats_scope == DSALT_STATS_PACKED ? 1 : p.num_seqs)
+                            : p.num_seqs * p.n_sets;
+    size_t b = 0;
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    b += al(sizeof(float) * (size_t)p.total_len * nsig);           // norms
+    b += al(sizeof(double) * 2 * (size_t)nranges * nsig);          // sums
+    b += al(sizeof(double) * 2 * (size_t)nranges * nsig);          // stats
+    if (p.select_mode == DSALT_SELECT_GLOBAL)
+        b += al(sizeof(float) * (size_t)p.total_len * nsig);       // z
+    return b;
+}
+
+hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, int border_cap) {
+    const int nsig = 1 + p.n_kv_heads;
+    const int nranges = p.select_mode == DSALT_SELECT_GLOBAL
+                            ? (p.stats_scope == DSALT_STATS_PACKED ? 1 : p.num_seqs)
+                            : p.num_seqs * p.n_sets;
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    char* w = (char*)ws;
+    float* nx = (float*)w;
+    float* nv = nx + p.total_len;
+    w += al(sizeof(float) * (size_t)p.total_len * nsig);
+    double* sums = (double*)w;
+    w += al(sizeof(double) * 2 * (size_t)nranges * nsig);
+    double* stats = (double*)w;
+    w += al(sizeof(double) * 2 * (size_t)nranges * nsig);
+    float* zx = nullptr;
+    float* zv = nullptr;
+    if (p.select_mode == DSALT_SELECT_GLOBAL) {
+        zx = (float*)w;
+        zv = zx + p.total_len;
+    }
+    if (p.total_len > 0) {
+        int blocks = min(ceil_div(p.total_len, 4), 65536);
+        if (p.dtype == DSALT_DTYPE_BF16)
+            hipLaunchKernelGGL(sel_norms_kernel<bf16>, dim3(blocks), dim3(256), 0, stream, p, nx, nv);
+        else if (p.dtype == DSALT_DTYPE_F16)
+            hipLaunchKernelGGL(sel_norms_kernel<f16>, dim3(blocks), dim3(256), 0, stream, p, nx, nv);
+        else
+            hipLaunchKernelGGL(sel_norms_kernel<float>, dim3(blocks), dim3(256), 0, stream, p, nx, nv);
+        hipLaunchKernelGGL(sel_sums_kernel, dim3(nranges, nsig), dim3(256), 0, stream, p, nx, nv, sums);
+        int nst = p.select_mode == DSALT_SELECT_GLOBAL ? nranges * nsig : p.num_seqs * nsig;
+        hipLaunchKernelGGL(sel_stats_kernel, dim3(ceil_div(nst, 64)), dim3(64), 0, stream, p, sums, stats,
+                           nranges);
+        if (p.select_mode == DSALT_SELECT_GLOBAL)
+            hipLaunchKernelGGL(sel_z_kernel, dim3(ceil_div(p.max_seqlen, 256), p.num_seqs), dim3(256), 0,
+                               stream, p, nx, nv, stats, zx, zv);
+    }
+    int nsets_total = p.n_heads * p.num_seqs * p.n_sets;
+    if (nsets_total > 0 && p.k_lmk > 0)
+        hipLaunchKernelGGL(sel_topk_kernel, dim3(nsets_total), dim3(kSelThreads), 0, stream, p, zx, zv, nx,
+                           nv, stats, border_cap);
+    return hipGetLastError();
+}
+
+hipError_t gather_launch(const GatherParams& p, hipStream_t stream) {
+    const int vw = p.dtype == DSALT_DTYPE_F32 ? 4 : 8;
+    int64_t n = (int64_t)p.n_heads * p.num_seqs * p.n_sets * p.k_lmk * (p.head_dim / vw);
+    if (n == 0) return hipSuccess;
+    dim3 grid((unsigned)((n + 255) / 256));
+    if (p.dtype == DSALT_DTYPE_BF16)
+        hipLaunchKernelGGL(gather_kernel<bf16>, grid, dim3(256), 0, stream, p);
+    else if (p.dtype == DSALT_DTYPE_F16)
+        hipLaunchKernelGGL(gather_kernel<f16>, grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(gather_kernel<float>, grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace dsalt

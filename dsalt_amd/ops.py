@@ -1,0 +1,273 @@
+"""Torch-tensor wrappers over the C ABI: one function per library entry point.
+
+Tensors must live on a ROCm device; every call is enqueued on torch's current stream and
+allocates its outputs and workspace through torch's caching allocator.  There is no CPU
+path: CPU tensors or a missing library raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, SELECT_BLOCK, SELECT_GLOBAL, STATS_PACKED,
+                   STATS_SEQUENCE, BwdArgs, FwdArgs, GatherArgs, Problem, SelectArgs)
+
+_DT = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
+MAX_LANDMARKS = 512
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt not in _DT:
+        raise TypeError(f"dsalt_amd supports float32, bfloat16 and float16 tensors, got {dt}")
+    return _DT[dt]
+
+
+def _gpu(*ts: torch.Tensor) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError("dsalt_amd runs on the GPU only; got a tensor on " + str(t.device))
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError("all tensors must be on the same device")
+    return dev
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _rows3(t: torch.Tensor, name: str) -> torch.Tensor:
+    """[T, H, D] with unit stride along D (other strides free)."""
+    if t.dim() != 3:
+        raise ValueError(f"{name} must be [T, H, D], got shape {tuple(t.shape)}")
+    if t.stride(2) != 1:
+        t = t.contiguous()
+    return t
+
+
+def _max_seqlen(cu_seqlens: torch.Tensor, cu_list=None) -> int:
+    if cu_list is not None:
+        return max(1, max(int(cu_list[i + 1]) - int(cu_list[i]) for i in range(len(cu_list) - 1)))
+    lens = (cu_seqlens[1:] - cu_seqlens[:-1])
+    return max(1, int(lens.max().item()))  # one device-to-host sync, as the reference's .tolist()
+
+
+def n_sets(select_mode: int, max_seqlen: int, block_size: int) -> int:
+    return 1 if select_mode == SELECT_GLOBAL else -(-max_seqlen // block_size)
+
+
+def _problem(T, S, maxlen, H, G, D, K, mode, block_size, dtype) -> Problem:
+    return Problem(T, S, maxlen, H, G, D, K, mode, block_size if mode == SELECT_BLOCK else 0, dtype)
+
+
+def _workspace(nbytes: int, dev) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
+
+
+# --------------------------------------------------------------------- selection
+def select_landmarks(h: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, w: torch.Tensor,
+                     cu_seqlens: torch.Tensor, k_lmk: int, *, max_seqlen: int | None = None,
+                     select_mode: int = SELECT_GLOBAL, block_size: int = 512,
+                     stats_scope: int = STATS_PACKED, want_scores: bool = False,
+                     border_cap: int | None = None):
+    """Landmark indices [H, S, n_sets, k] (int32, ascending, -1 padded).
+
+    h [T, hidden], v [T, n_kv, D] (value vectors x W_V^T without bias), alpha [H] in (0,1),
+    w [T] integer windows, cu_seqlens [S+1].  With ``want_scores`` (global variant) also
+    returns z_x [T], z_v [T, n_kv] and scores [T, H] in fp32.
+    """
+    dev = _gpu(h, v, alpha, w, cu_seqlens)
+    if h.dim() != 2 or h.stride(1) != 1:
+        h = h.contiguous()
+    v = _rows3(v, "v")
+    dt = dtype_code(h.dtype)
+    if v.dtype != h.dtype:
+        raise TypeError("h and v must share a dtype")
+    T, hidden = h.shape
+    _, G, D = v.shape
+    H = alpha.shape[0]
+    S = cu_seqlens.shape[0] - 1
+    if v.shape[0] != T or w.shape[0] != T:
+        raise ValueError("h, v and w must have the same number of rows")
+    if not 0 <= k_lmk <= MAX_LANDMARKS:
+        raise ValueError(f"k_lmk must be in [0, {MAX_LANDMARKS}]")
+    maxlen = max_seqlen if max_seqlen is not None else _max_seqlen(cu_seqlens)
+    nset = n_sets(select_mode, maxlen, block_size)
+    alpha_c = alpha.detach().to(torch.float32).contiguous()
+    w_c = w.detach().to(torch.int32).contiguous()
+    cu_c = cu_seqlens.detach().to(torch.int32).contiguous()
+    idx = torch.empty((H, S, nset, k_lmk), dtype=torch.int32, device=dev)
+    zx = zv = sc = None
+    if want_scores:
+        zx = torch.empty(T, dtype=torch.float32, device=dev)
+        zv = torch.empty((T, G), dtype=torch.float32, device=dev)
+        sc = torch.empty((T, H), dtype=torch.float32, device=dev)
+    a = SelectArgs()
+    a.p = _problem(T, S, maxlen, H, G, D, k_lmk, select_mode, block_size, dt)
+    a.hidden, a.stats_scope = hidden, stats_scope
+    a.h, a.h_stride_t = h.data_ptr(), h.stride(0)
+    a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
+    a.alpha, a.w, a.cu_seqlens = alpha_c.data_ptr(), w_c.data_ptr(), cu_c.data_ptr()
+    a.lmk_idx = idx.data_ptr() if idx.numel() else None
+    a.z_x = zx.data_ptr() if zx is not None else None
+    a.z_v = zv.data_ptr() if zv is not None else None
+    a.scores = sc.data_ptr() if sc is not None else None
+    L = _lib.load()
+    need = L.dsalt_select_workspace_bytes(ctypes.byref(a))
+    if need == 0:
+        _lib.check("dsalt_select", L.dsalt_select(ctypes.byref(a), None))
+    ws = _workspace(need, dev)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    if border_cap is None:
+        rc = L.dsalt_select(ctypes.byref(a), _stream(dev))
+    else:
+        rc = L.dsalt_select_with_border_cap(ctypes.byref(a), _stream(dev), int(border_cap))
+    _lib.check("dsalt_select", rc)
+    if want_scores:
+        return idx, zx, zv, sc
+    return idx
+
+
+# ------------------------------------------------------------------------ forward
+def attention_forward(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias=None, *, scale=None,
+                      max_seqlen=None, select_mode=SELECT_GLOBAL, block_size=512):
+    """(out [T,H,D] in q.dtype, lse [T,H] fp32).  lmk_idx [H,S,n_sets,K] int32 ascending with
+    -1 padding at the end of each set (as select_landmarks returns)."""
+    dev = _gpu(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias)
+    q, k, v = _rows3(q, "q"), _rows3(k, "k"), _rows3(v, "v")
+    dt = dtype_code(q.dtype)
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("q, k and v must share a dtype")
+    T, H, D = q.shape
+    G = k.shape[1]
+    S = cu_seqlens.shape[0] - 1
+    maxlen = max_seqlen if max_seqlen is not None else _max_seqlen(cu_seqlens)
+    K = lmk_idx.shape[-1]
+    if lmk_idx.shape[:2] != (H, S) or lmk_idx.dim() != 4:
+        raise ValueError(f"lmk_idx must be [H, S, n_sets, K], got {tuple(lmk_idx.shape)}")
+    if lmk_idx.shape[2] != n_sets(select_mode, maxlen, block_size):
+        raise ValueError("lmk_idx n_sets does not match select_mode / block_size / max_seqlen")
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    w_c = w.detach().to(torch.int32).contiguous()
+    cu_c = cu_seqlens.detach().to(torch.int32).contiguous()
+    li = lmk_idx.to(torch.int32).contiguous()
+    lb = lmk_bias.detach().to(torch.float32).contiguous() if lmk_bias is not None else None
+    out = torch.empty((T, H, D), dtype=q.dtype, device=dev)
+    lse = torch.empty((T, H), dtype=torch.float32, device=dev)
+    a = FwdArgs()
+    a.p = _problem(T, S, maxlen, H, G, D, K, select_mode, block_size, dt)
+    a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
+    a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
+    a.w, a.cu_seqlens = w_c.data_ptr(), cu_c.data_ptr()
+    a.lmk_idx = li.data_ptr() if li.numel() else None
+    a.lmk_bias = lb.data_ptr() if lb is not None and lb.numel() else None
+    a.out, a.o_stride_t, a.o_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    a.lse, a.scale = lse.data_ptr(), scale
+    if T == 0:
+        return out, lse
+    L = _lib.load()
+    _lib.check("dsalt_fwd", L.dsalt_fwd(ctypes.byref(a), _stream(dev)))
+    return out, lse
+
+
+# ----------------------------------------------------------------------- backward
+def attention_backward(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias=None, *,
+                       scale=None, max_seqlen=None, want_dbias=True):
+    """(dq, dk, dv) in q.dtype, [T,H,D], and d_bias [H,S,1,K] fp32 (or None).
+    Global selection variant, n_kv_heads == n_heads."""
+    dev = _gpu(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias)
+    q, k, v, out, dout = (_rows3(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out"),
+                                                   (dout, "dout")))
+    dt = dtype_code(q.dtype)
+    if dout.dtype != q.dtype:
+        dout = dout.to(q.dtype)
+    T, H, D = q.shape
+    S = cu_seqlens.shape[0] - 1
+    maxlen = max_seqlen if max_seqlen is not None else _max_seqlen(cu_seqlens)
+    K = lmk_idx.shape[-1]
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    w_c = w.detach().to(torch.int32).contiguous()
+    cu_c = cu_seqlens.detach().to(torch.int32).contiguous()
+    li = lmk_idx.to(torch.int32).contiguous()
+    lb = lmk_bias.detach().to(torch.float32).contiguous() if lmk_bias is not None else None
+    lse = lse.detach().to(torch.float32).contiguous()
+    dq = torch.empty((T, H, D), dtype=q.dtype, device=dev)
+    dk = torch.empty((T, H, D), dtype=q.dtype, device=dev)
+    dv = torch.empty((T, H, D), dtype=q.dtype, device=dev)
+    db = torch.empty(tuple(lmk_idx.shape), dtype=torch.float32, device=dev) if want_dbias else None
+    a = BwdArgs()
+    a.p = _problem(T, S, maxlen, H, k.shape[1], D, K, SELECT_GLOBAL, 0, dt)
+    a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
+    a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
+    a.out, a.o_stride_t, a.o_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    a.dout, a.do_stride_t, a.do_stride_h = dout.data_ptr(), dout.stride(0), dout.stride(1)
+    a.lse, a.w, a.cu_seqlens = lse.data_ptr(), w_c.data_ptr(), cu_c.data_ptr()
+    a.lmk_idx = li.data_ptr() if li.numel() else None
+    a.lmk_bias = lb.data_ptr() if lb is not None and lb.numel() else None
+    a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    a.d_bias = db.data_ptr() if db is not None and db.numel() else None
+    a.scale = scale
+    if T == 0:
+        return dq.zero_(), dk.zero_(), dv.zero_(), db
+    L = _lib.load()
+    need = L.dsalt_bwd_workspace_bytes(ctypes.byref(a))
+    if need == 0:
+        _lib.check("dsalt_bwd", L.dsalt_bwd(ctypes.byref(a), None))
+    ws = _workspace(need, dev)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    _lib.check("dsalt_bwd", L.dsalt_bwd(ctypes.byref(a), _stream(dev)))
+    return dq, dk, dv, db
+
+
+# ------------------------------------------------------------------------- gather
+def gather_landmarks(k, v, cu_seqlens, lmk_idx, *, max_seqlen=None, select_mode=SELECT_GLOBAL,
+                     block_size=512, n_heads=None):
+    """(lmk_k, lmk_v) [H, S, n_sets, K, D]; rows of -1 slots are zero."""
+    dev = _gpu(k, v, cu_seqlens, lmk_idx)
+    k, v = _rows3(k, "k"), _rows3(v, "v")
+    dt = dtype_code(k.dtype)
+    T, G, D = k.shape
+    H = lmk_idx.shape[0] if n_heads is None else n_heads
+    S = cu_seqlens.shape[0] - 1
+    K = lmk_idx.shape[-1]
+    maxlen = max_seqlen if max_seqlen is not None else _max_seqlen(cu_seqlens)
+    li = lmk_idx.to(torch.int32).contiguous()
+    cu_c = cu_seqlens.detach().to(torch.int32).contiguous()
+    shape = tuple(lmk_idx.shape) + (D,)
+    lk = torch.empty(shape, dtype=k.dtype, device=dev)
+    lv = torch.empty(shape, dtype=k.dtype, device=dev)
+    a = GatherArgs()
+    a.p = _problem(T, S, maxlen, H, G, D, K, select_mode, block_size, dt)
+    a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
+    a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
+    a.cu_seqlens, a.lmk_idx = cu_c.data_ptr(), li.data_ptr()
+    a.lmk_k, a.lmk_v = lk.data_ptr(), lv.data_ptr()
+    if lk.numel() == 0:
+        return lk, lv
+    L = _lib.load()
+    _lib.check("dsalt_gather_landmarks", L.dsalt_gather_landmarks(ctypes.byref(a), _stream(dev)))
+    return lk, lv
+
+
+def sort_landmarks(idx: torch.Tensor, bias: torch.Tensor | None = None):
+    """Sort each set ascending with -1 last (the order the kernels require); returns
+    (sorted int32 indices, bias permuted the same way or None, permutation)."""
+    big = torch.iinfo(torch.int32).max
+    key = torch.where(idx < 0, torch.full_like(idx, big), idx).to(torch.int64)
+    srt, perm = key.sort(dim=-1)
+    out = torch.where(srt == big, torch.full_like(srt, -1), srt).to(torch.int32)
+    b = bias.gather(-1, perm) if bias is not None else None
+    return out, b, perm

@@ -1,0 +1,87 @@
+"""Seeded synthetic inputs for the operator workloads used by the benchmark and tests.
+
+Each workload is generated on the CPU with ``torch.Generator().manual_seed(seed)`` in
+float32 and then cast, so the bits handed to the GPU and to any CPU check are identical.
+Draw order: q, k, v, h, window normals, upstream gradient.
+Windows: ``w_i = clamp(round_half_even(sigmoid(z_i) * w_max), 16, w_max)``.
+Landmark score: alpha = 0.5 for every head (the same ranking as z(|v|) + z(|h|)).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass(frozen=True)
+class Workload:
+    name: str
+    batch: int
+    heads: int
+    seqlen: int
+    head_dim: int
+    hidden: int
+    dtype: torch.dtype
+    w_max: int
+    k_lmk: int
+    backward: bool
+    select_mode: str = "global"  # or "block"
+    block_size: int = 512
+    heavy_tails: bool = False    # v rows x lognormal(0,1), h rows x lognormal(0,0.5)
+    seed: int = 1000
+
+    @property
+    def total_len(self) -> int:
+        return self.batch * self.seqlen
+
+
+WORKLOADS = {
+    w.name: w
+    for w in [
+        # forward only, fp32, masked-SDPA size the CPU path handles in full
+        Workload("fwd_f32_h4_l2048", 1, 4, 2048, 64, 256, torch.float32, 128, 32, False, seed=1000),
+        # forward + backward, bf16, 4 packed sequences of 8192 (70M-class layer)
+        Workload("fwdbwd_bf16_b4_h8_l8192", 4, 8, 8192, 64, 512, torch.bfloat16, 256, 64, True, seed=1001),
+        # forward + backward, bf16, one 32K sequence, heavy-tailed norms
+        Workload("fwdbwd_bf16_h16_l32768", 1, 16, 32768, 64, 1024, torch.bfloat16, 512, 128, True,
+                 heavy_tails=True, seed=1002),
+        # forward (inference), bf16, 128K tokens, block-causal landmarks (512-query blocks)
+        Workload("fwd_bf16_h16_l131072_block", 1, 16, 131072, 128, 2048, torch.bfloat16, 512, 256, False,
+                 select_mode="block", block_size=512, seed=1003),
+    ]
+}
+
+
+def make_windows(z: torch.Tensor, w_max: int) -> torch.Tensor:
+    w = torch.round(torch.sigmoid(z) * w_max)
+    return w.clamp(16, w_max).to(torch.int32)
+
+
+def generate(wl: Workload, device="cpu", seqlen: int | None = None, heads: int | None = None):
+    """Inputs of a workload as a dict of tensors on ``device``.
+
+    ``seqlen`` / ``heads`` shrink the shape for tests while keeping the recipe.
+    Keys: q, k, v [T,H,D]; h [T,hidden]; w [T] int32; cu [S+1] int32; alpha [H] fp32;
+    dout [T,H,D] (backward workloads).
+    """
+    L = seqlen or wl.seqlen
+    H = heads or wl.heads
+    T = wl.batch * L
+    g = torch.Generator().manual_seed(wl.seed)
+    q = torch.randn(T, H, wl.head_dim, generator=g)
+    k = torch.randn(T, H, wl.head_dim, generator=g)
+    v = torch.randn(T, H, wl.head_dim, generator=g)
+    h = torch.randn(T, wl.hidden, generator=g)
+    zw = torch.randn(T, generator=g)
+    if wl.heavy_tails:
+        v = v * torch.exp(torch.randn(T, H, 1, generator=g))
+        h = h * torch.exp(0.5 * torch.randn(T, 1, generator=g))
+    out = dict(
+        q=q.to(wl.dtype), k=k.to(wl.dtype), v=v.to(wl.dtype), h=h.to(wl.dtype),
+        w=make_windows(zw, wl.w_max),
+        cu=torch.arange(0, T + 1, L, dtype=torch.int32),
+        alpha=torch.full((H,), 0.5, dtype=torch.float32),
+    )
+    if wl.backward:
+        out["dout"] = torch.randn(T, H, wl.head_dim, generator=g).to(wl.dtype)
+    return {kk: vv.to(device) for kk, vv in out.items()}

@@ -1,0 +1,181 @@
+/*
+ * dsalt_amd.h - C ABI of the MI355X (gfx950) DSALT sparse-attention library.
+ *
+ * Operator: query i of a packed sequence attends to A(i) = W(i) U L(i), where
+ *   W(i) = [i - w_i + 1, i]                     (causal adaptive window, w_i >= 1)
+ *   L(i) = { p in landmark set : 0 <= p < i - w_i + 1 }
+ * so a landmark inside the window is counted once (as a window key).  Landmark
+ * sets are chosen per (head, sequence) ("global") or per (head, sequence, query
+ * block of block_size rows) from earlier positions only ("block-causal").
+ *
+ * Conventions shared by every entry point:
+ *  - All pointers are device pointers unless stated otherwise.  The caller owns
+ *    and allocates every buffer, including the workspace whose size the
+ *    matching *_workspace_bytes() function returns.  The library never
+ *    allocates device memory and never synchronises the stream.
+ *  - Work is enqueued on `stream` (a hipStream_t passed as void*; NULL is the
+ *    default stream).  Calls are stateless and may be made from any host thread;
+ *    two calls that share a workspace must be ordered by the caller.
+ *  - Return value: 0 on success, otherwise a DSALT_ERR_* code; a readable
+ *    message for the last error of the calling thread is in dsalt_last_error().
+ *  - Token tensors are packed: row t of q/k/v/out/h is token t of the batch,
+ *    sequences delimited by cu_seqlens[0..num_seqs] (int32, cu_seqlens[0] = 0).
+ *    Strides are in elements; the innermost (head_dim / hidden) stride is 1.
+ *  - Landmark indices are int32, sequence-relative, ascending, padded with -1
+ *    at the end of each set.  Layout [n_heads, num_seqs, n_sets, k_lmk] with
+ *    n_sets = 1 (global) or ceil(max_seqlen / block_size) (block-causal).
+ */
+#ifndef DSALT_AMD_H
+#define DSALT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSALT_ABI_VERSION 1
+
+/* element types of token tensors */
+#define DSALT_DTYPE_F32  0
+#define DSALT_DTYPE_BF16 1
+#define DSALT_DTYPE_F16  2
+
+/* landmark selection variants */
+#define DSALT_SELECT_GLOBAL 0  /* one set per (head, sequence), whole-sequence scores   */
+#define DSALT_SELECT_BLOCK  1  /* one set per (head, sequence, query block), prefix scores */
+
+/* scope of the z-score statistics in the global variant */
+#define DSALT_STATS_PACKED   0 /* mean/std over all packed tokens (reference library) */
+#define DSALT_STATS_SEQUENCE 1 /* mean/std per sequence                                 */
+
+/* error codes */
+#define DSALT_OK              0
+#define DSALT_ERR_INVALID     1  /* bad argument (shape, dtype, null pointer)        */
+#define DSALT_ERR_UNSUPPORTED 2  /* valid but not implemented on this build          */
+#define DSALT_ERR_WORKSPACE   3  /* workspace missing or smaller than required       */
+#define DSALT_ERR_HIP         4  /* a HIP runtime call failed (message has details)  */
+
+typedef void* dsalt_stream_t; /* hipStream_t */
+
+/* Problem shape shared by selection, forward and backward. */
+typedef struct dsalt_problem {
+    int32_t total_len;   /* T, packed tokens                                         */
+    int32_t num_seqs;    /* S                                                        */
+    int32_t max_seqlen;  /* max over s of cu_seqlens[s+1]-cu_seqlens[s] (host value) */
+    int32_t n_heads;     /* H query heads                                            */
+    int32_t n_kv_heads;  /* key/value heads, divides H (GQA when < H)                */
+    int32_t head_dim;    /* D: 64 or 128                                             */
+    int32_t k_lmk;       /* landmark slots per set, 0..512                           */
+    int32_t select_mode; /* DSALT_SELECT_*                                           */
+    int32_t block_size;  /* query block of the block-causal variant (multiple of 64) */
+    int32_t dtype;       /* DSALT_DTYPE_* of the token tensors                       */
+} dsalt_problem;
+
+/*
+ * Landmark selection.  Replaces, as one stream-ordered call:
+ *   hybrid_scores_per_head        dsalt/kernels/landmark_tokens_ker.py:19-61
+ *   _compute_landmark_indices     dsalt/kernels/selectors.py:75-134
+ *   block-causal _select          results/causal_landmark_check.py:82-113
+ * Score of token j for head h (kv head g = h / (H / n_kv_heads)):
+ *   s = alpha_h * z(|v_{j,g}|) + (1 - alpha_h) * z(|h_j|)
+ * with norms rounded to `dtype`, z-statistics in fp64 (unbiased std clamped at
+ * 1e-6), candidates j_rel >= w_j (the token's own window), top-k with ties
+ * broken by the lower index.  `v` holds x W_V^T without bias (the value
+ * vectors); `h` the hidden states x.
+ */
+typedef struct dsalt_select_args {
+    dsalt_problem p;
+    int32_t hidden;            /* columns of h, multiple of 16 bytes / element size */
+    int32_t stats_scope;       /* DSALT_STATS_* (global variant only)               */
+    const void* h;   int64_t h_stride_t;                      /* [T, hidden]        */
+    const void* v;   int64_t v_stride_t;  int64_t v_stride_h; /* [T, n_kv, D]       */
+    const float* alpha;        /* [H], the mixing weight in (0, 1)                  */
+    const int32_t* w;          /* [T] window sizes as integers                      */
+    const int32_t* cu_seqlens; /* [S+1]                                             */
+    int32_t* lmk_idx;          /* out [H, S, n_sets, k_lmk]                         */
+    float* z_x;                /* optional out [T]      (global variant)            */
+    float* z_v;                /* optional out [T, n_kv] (global variant)           */
+    float* scores;             /* optional out [T, H]    (global variant)           */
+    void* workspace; size_t workspace_bytes;
+} dsalt_select_args;
+
+/* Attention forward.  Replaces _dsalt_fwd_kernel and its launcher
+ * dsalt/kernels/dsalt_triton_attn.py:27-169,184-209,259-311 (O and LSE).
+ * out: [T, H, D] in dtype; lse: [T, H] fp32 natural-log sum of exponentials of
+ * the scaled logits over A(i).  k/v may have n_kv_heads < n_heads (GQA). */
+typedef struct dsalt_fwd_args {
+    dsalt_problem p;
+    const void* q;  int64_t q_stride_t; int64_t q_stride_h;
+    const void* k;  int64_t k_stride_t; int64_t k_stride_h;
+    const void* v;  int64_t v_stride_t; int64_t v_stride_h;
+    const int32_t* w;          /* [T] window sizes (values < 1 act as 1)            */
+    const int32_t* cu_seqlens; /* [S+1]                                             */
+    const int32_t* lmk_idx;    /* [H, S, n_sets, k_lmk]                             */
+    const float* lmk_bias;     /* [H, S, n_sets, k_lmk] added to landmark logits, or NULL */
+    void* out;  int64_t o_stride_t; int64_t o_stride_h;
+    float* lse;                /* [T, H] contiguous                                 */
+    float scale;               /* logit scale, 1/sqrt(D) in the reference           */
+    void* workspace; size_t workspace_bytes;
+} dsalt_fwd_args;
+
+/* Attention backward.  Replaces _dsalt_bwd_preprocess + _dsalt_bwd_kernel and
+ * dsalt_triton_backward, dsalt/kernels/dsalt_triton_bwd.py:17-324.
+ * Deterministic: no floating-point atomics.  dq/dk/dv are [T, H, D] contiguous
+ * in dtype (n_kv_heads must equal n_heads); d_bias (optional) is fp32
+ * [H, S, n_sets, k_lmk].  Global selection variant only. */
+typedef struct dsalt_bwd_args {
+    dsalt_problem p;
+    const void* q;    int64_t q_stride_t;  int64_t q_stride_h;
+    const void* k;    int64_t k_stride_t;  int64_t k_stride_h;
+    const void* v;    int64_t v_stride_t;  int64_t v_stride_h;
+    const void* out;  int64_t o_stride_t;  int64_t o_stride_h;
+    const void* dout; int64_t do_stride_t; int64_t do_stride_h;
+    const float* lse;          /* [T, H] from the forward                           */
+    const int32_t* w;
+    const int32_t* cu_seqlens;
+    const int32_t* lmk_idx;
+    const float* lmk_bias;     /* or NULL                                           */
+    void* dq; void* dk; void* dv;
+    float* d_bias;             /* or NULL                                           */
+    float scale;
+    void* workspace; size_t workspace_bytes;
+} dsalt_bwd_args;
+
+/* Landmark K/V gather.  Replaces _build_landmark_kv, dsalt/kernels/selectors.py:137-159:
+ * lmk_k/lmk_v [H, S, n_sets, k_lmk, D] (dtype), rows of invalid (-1) slots zero. */
+typedef struct dsalt_gather_args {
+    dsalt_problem p;
+    const void* k;  int64_t k_stride_t; int64_t k_stride_h;
+    const void* v;  int64_t v_stride_t; int64_t v_stride_h;
+    const int32_t* cu_seqlens;
+    const int32_t* lmk_idx;
+    void* lmk_k; void* lmk_v;
+} dsalt_gather_args;
+
+int    dsalt_abi_version(void);
+const char* dsalt_last_error(void);
+
+size_t dsalt_select_workspace_bytes(const dsalt_select_args* a);
+int    dsalt_select(const dsalt_select_args* a, dsalt_stream_t stream);
+
+size_t dsalt_fwd_workspace_bytes(const dsalt_fwd_args* a);
+int    dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream);
+
+size_t dsalt_bwd_workspace_bytes(const dsalt_bwd_args* a);
+int    dsalt_bwd(const dsalt_bwd_args* a, dsalt_stream_t stream);
+
+int    dsalt_gather_landmarks(const dsalt_gather_args* a, dsalt_stream_t stream);
+
+/* Testing hook with no counterpart in the reference: dsalt_select with the LDS
+ * capacity of the top-k boundary bin limited to `border_cap` keys, so tests can
+ * drive the extra radix passes that large tie groups take.  dsalt_select is
+ * this call with the full capacity. */
+int    dsalt_select_with_border_cap(const dsalt_select_args* a, dsalt_stream_t stream, int border_cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSALT_AMD_H */

@@ -1,0 +1,136 @@
+"""Attention forward/backward on the GPU against the float64 oracle.
+
+Tolerances (relative, max|a-b| / max|b|): 1e-5 for fp32, 2e-2 for bf16 and fp16.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from dsalt_amd import ops
+from oracle import attention as OA
+from tests.helpers import f64, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+def _inputs(lens, H, G, D, K, wmax, dt, seed, mode=ops.SELECT_GLOBAL, block=128, bias=False):
+    g = torch.Generator().manual_seed(seed)
+    T = sum(lens)
+    q = torch.randn(T, H, D, generator=g).to(dt)
+    k = torch.randn(T, G, D, generator=g).to(dt)
+    v = torch.randn(T, G, D, generator=g).to(dt)
+    w = torch.randint(1, wmax + 1, (T,), generator=g, dtype=torch.int32)
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    maxlen = max(lens)
+    ns = ops.n_sets(mode, maxlen, block)
+    idx = torch.full((H, len(lens), ns, K), -1, dtype=torch.int32)
+    for hh in range(H):
+        for s, L in enumerate(lens):
+            for b in range(ns):
+                hi = L if mode == ops.SELECT_GLOBAL else min(L, b * block)
+                if hi <= 0:
+                    continue
+                n = min(K - (hh % 2), hi)  # leave some -1 padding
+                c = torch.randperm(hi, generator=g)[:n].sort().values
+                idx[hh, s, b, :n] = c.to(torch.int32)
+    lb = torch.randn(idx.shape, generator=g) * 0.5 if bias else None
+    return q, k, v, w, cu, idx, lb, maxlen
+
+
+def _fwd_check(q, k, v, w, cu, idx, lb, maxlen, mode=ops.SELECT_GLOBAL, block=128):
+    dt = q.dtype
+    D = q.shape[-1]
+    scale = 1.0 / math.sqrt(D)
+    out, lse = ops.attention_forward(*(t.to(DEV) for t in (q, k, v, w, cu, idx)),
+                                     lb.to(DEV) if lb is not None else None, scale=scale, max_seqlen=maxlen,
+                                     select_mode=mode, block_size=block)
+    torch.cuda.synchronize()
+    ro, rl = OA.attention_fwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale,
+                              lmk_bias=None if lb is None else lb.double().numpy(),
+                              block_size=None if mode == ops.SELECT_GLOBAL else block)
+    e_o = rel_err(f64(out), ro)
+    e_l = rel_err(f64(lse), rl)
+    assert e_o < TOL[dt], e_o
+    assert e_l < (1e-6 if dt == torch.float32 else 2e-3), e_l
+    return out, lse
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+def test_fwd_global(dt, D):
+    args = _inputs([300, 181, 64], 4, 4, D, 24, 90, dt, seed=D)
+    _fwd_check(*args)
+
+
+def test_fwd_bias_gqa_ragged():
+    args = _inputs([257, 130], 8, 2, 64, 40, 70, torch.bfloat16, seed=5, bias=True)
+    _fwd_check(*args)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_fwd_block_causal(dt):
+    q, k, v, w, cu, idx, lb, maxlen = _inputs([700, 512], 4, 4, 128, 32, 150, dt, seed=6,
+                                              mode=ops.SELECT_BLOCK, block=128)
+    _fwd_check(q, k, v, w, cu, idx, lb, maxlen, mode=ops.SELECT_BLOCK, block=128)
+
+
+def test_fwd_special_cases():
+    T, H, D = 200, 2, 64
+    g = torch.Generator().manual_seed(7)
+    q, k, v = (torch.randn(T, H, D, generator=g).to(torch.float32) for _ in range(3))
+    cu = torch.tensor([0, T], dtype=torch.int32)
+    idx = torch.full((H, 1, 1, 8), -1, dtype=torch.int32)
+    out, _ = ops.attention_forward(q.to(DEV), k.to(DEV), v.to(DEV), torch.ones(T, dtype=torch.int32, device=DEV),
+                                   cu.to(DEV), idx.to(DEV), max_seqlen=T)
+    assert rel_err(f64(out), f64(v)) < 1e-6  # w = 1, no landmarks: O = V
+    out, _ = ops.attention_forward(q.to(DEV), k.to(DEV), v.to(DEV), torch.full((T,), T, dtype=torch.int32,
+                                   device=DEV), cu.to(DEV), idx.to(DEV), max_seqlen=T)
+    ref = torch.nn.functional.scaled_dot_product_attention(q.transpose(0, 1), k.transpose(0, 1),
+                                                           v.transpose(0, 1), is_causal=True).transpose(0, 1)
+    assert rel_err(f64(out), f64(ref)) < 1e-5  # full windows, no landmarks: causal attention
+
+
+def _bwd_check(dt, lens, H, D, K, wmax, seed, bias=False):
+    q, k, v, w, cu, idx, lb, maxlen = _inputs(lens, H, H, D, K, wmax, dt, seed, bias=bias)
+    scale = 1.0 / math.sqrt(D)
+    g = torch.Generator().manual_seed(seed + 100)
+    do = torch.randn(q.shape, generator=g).to(dt)
+    dev = [t.to(DEV) for t in (q, k, v, w, cu, idx)]
+    lbd = lb.to(DEV) if lb is not None else None
+    out, lse = ops.attention_forward(*dev, lbd, scale=scale, max_seqlen=maxlen)
+    dq, dk, dv, db = ops.attention_backward(do.to(DEV), dev[0], dev[1], dev[2], out, lse, dev[3], dev[4], dev[5],
+                                            lbd, scale=scale, max_seqlen=maxlen)
+    torch.cuda.synchronize()
+    rdq, rdk, rdv, rdb = OA.attention_bwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale,
+                                          f64(do), lmk_bias=None if lb is None else lb.double().numpy())
+    for name, a, b in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv), ("dbias", db, rdb)):
+        e = rel_err(f64(a), b)
+        assert e < TOL[dt], (name, e)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32, torch.float16])
+def test_bwd_global(dt):
+    _bwd_check(dt, [300, 181, 64], 4, 64, 24, 90, seed=11)
+
+
+def test_bwd_bias_d128():
+    _bwd_check(torch.bfloat16, [333, 200], 2, 128, 40, 120, seed=12, bias=True)
+
+
+def test_bwd_deterministic():
+    q, k, v, w, cu, idx, lb, maxlen = _inputs([1024], 4, 4, 64, 64, 200, torch.bfloat16, seed=13)
+    do = torch.randn(q.shape).to(torch.bfloat16)
+    dev = [t.to(DEV) for t in (q, k, v, w, cu, idx)]
+    out, lse = ops.attention_forward(*dev, None, max_seqlen=maxlen)
+    r1 = ops.attention_backward(do.to(DEV), dev[0], dev[1], dev[2], out, lse, dev[3], dev[4], dev[5],
+                                max_seqlen=maxlen)
+    r2 = ops.attention_backward(do.to(DEV), dev[0], dev[1], dev[2], out, lse, dev[3], dev[4], dev[5],
+                                max_seqlen=maxlen)
+    for a, b in zip(r1, r2):
+        assert torch.equal(a, b)

@@ -1,0 +1,114 @@
+"""Landmark selection on the GPU against the oracle: indices bit-exact, z and scores
+bit-exact (same canonical arithmetic)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from dsalt_amd import ops
+from dsalt_amd.workloads import WORKLOADS, generate
+from oracle import select as OS
+from tests.helpers import bits, oracle_dtype
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _case(T_lens, hidden, G, D, H, dt, wmax, seed, scale_tails=False):
+    g = torch.Generator().manual_seed(seed)
+    T = sum(T_lens)
+    h = torch.randn(T, hidden, generator=g)
+    v = torch.randn(T, G, D, generator=g)
+    if scale_tails:
+        v = v * torch.exp(torch.randn(T, G, 1, generator=g))
+        h = h * torch.exp(0.5 * torch.randn(T, 1, generator=g))
+    alpha = torch.rand(H, generator=g) * 0.8 + 0.1
+    w = torch.randint(1, wmax + 1, (T,), generator=g, dtype=torch.int32)
+    cu = torch.tensor([0] + list(np.cumsum(T_lens)), dtype=torch.int32)
+    return h.to(dt), v.to(dt), alpha, w, cu
+
+
+def _run(h, v, alpha, w, cu, k, mode, block, scope, want=True, border_cap=None):
+    dev = [t.to(DEV) for t in (h, v, alpha, w, cu)]
+    maxlen = int((cu[1:] - cu[:-1]).max())
+    res = ops.select_landmarks(*dev, k, max_seqlen=maxlen, select_mode=mode, block_size=block,
+                               stats_scope=scope, want_scores=want and mode == ops.SELECT_GLOBAL,
+                               border_cap=border_cap)
+    torch.cuda.synchronize()
+    ref = OS.select(bits(h), bits(v), alpha.numpy(), w.numpy(), cu.numpy(), k, oracle_dtype(h.dtype), mode=mode,
+                    block_size=block, stats_scope=scope, want_scores=want and mode == ops.SELECT_GLOBAL)
+    return res, ref
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("scope", [ops.STATS_PACKED, ops.STATS_SEQUENCE])
+def test_global_select_bit_exact(dt, scope):
+    h, v, alpha, w, cu = _case([300, 517, 64], 256, 4, 64, 8, dt, 40, seed=1)
+    (idx, zx, zv, sc), (ridx, rzx, rzv, rsc) = _run(h, v, alpha, w, cu, 24, ops.SELECT_GLOBAL, 512, scope)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_array_equal(zx.cpu().numpy(), rzx)
+    np.testing.assert_array_equal(zv.cpu().numpy(), rzv)
+    np.testing.assert_array_equal(sc.cpu().numpy(), rsc)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+def test_block_select_bit_exact(dt, D):
+    h, v, alpha, w, cu = _case([1000, 700], 128, 2, D, 4, dt, 100, seed=2)
+    idx, ridx = _run(h, v, alpha, w, cu, 32, ops.SELECT_BLOCK, 128, ops.STATS_PACKED, want=False)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
+def test_padding_when_few_candidates():
+    h, v, alpha, w, cu = _case([90], 64, 1, 64, 2, torch.bfloat16, 200, seed=3)
+    w[:] = 80  # only positions >= 80 are candidates: 10 of them
+    idx, ridx = _run(h, v, alpha, w, cu, 16, ops.SELECT_GLOBAL, 512, ops.STATS_PACKED, want=False)
+    got = idx.cpu().numpy()
+    np.testing.assert_array_equal(got, ridx)
+    assert (got[:, 0, 0, 10:] == -1).all() and (got[:, 0, 0, :10] >= 80).all()
+
+
+@pytest.mark.parametrize("cap", [1, 7, 64])
+def test_ties_and_small_boundary_capacity(cap):
+    # integer-valued inputs: many exactly equal norms, so the boundary bin is a large tie group
+    g = torch.Generator().manual_seed(4)
+    T = 2000
+    h = torch.randint(-1, 2, (T, 64), generator=g).float().to(torch.bfloat16)
+    v = torch.randint(-1, 2, (T, 2, 64), generator=g).float().to(torch.bfloat16)
+    alpha = torch.tensor([0.5, 0.5, 1.0, 0.0])
+    w = torch.randint(1, 50, (T,), generator=g, dtype=torch.int32)
+    cu = torch.tensor([0, 1200, T], dtype=torch.int32)
+    idx, ridx = _run(h, v, alpha, w, cu, 50, ops.SELECT_GLOBAL, 512, ops.STATS_PACKED, want=False,
+                     border_cap=cap)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
+def test_constant_scores_pick_lowest_indices():
+    T = 500
+    h = torch.ones(T, 64, dtype=torch.bfloat16)
+    v = torch.ones(T, 1, 64, dtype=torch.bfloat16)
+    alpha = torch.tensor([0.3])
+    w = torch.full((T,), 5, dtype=torch.int32)
+    cu = torch.tensor([0, T], dtype=torch.int32)
+    idx, ridx = _run(h, v, alpha, w, cu, 20, ops.SELECT_GLOBAL, 512, ops.STATS_PACKED, want=False)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_array_equal(idx.cpu().numpy()[0, 0, 0], np.arange(5, 25))
+
+
+@pytest.mark.parametrize("name", ["fwd_f32_h4_l2048", "fwdbwd_bf16_b4_h8_l8192", "fwdbwd_bf16_h16_l32768"])
+def test_workload_selection_bit_exact(name):
+    wl = WORKLOADS[name]
+    x = generate(wl)
+    v = x["v"]
+    scope = ops.STATS_SEQUENCE
+    idx, ridx = _run(x["h"], v, x["alpha"], x["w"], x["cu"], wl.k_lmk, ops.SELECT_GLOBAL, 512, scope, want=False)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
+def test_block_workload_selection_bit_exact_shortened():
+    wl = WORKLOADS["fwd_bf16_h16_l131072_block"]
+    x = generate(wl, seqlen=8192, heads=4)
+    idx, ridx = _run(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, ops.SELECT_BLOCK, 512,
+                     ops.STATS_SEQUENCE, want=False)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
