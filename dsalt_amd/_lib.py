@@ -86,6 +86,8 @@ SIGNATURES = {
     "dsalt_bwd_workspace_bytes": ([ctypes.POINTER(BwdArgs)], _sz),
     "dsalt_bwd": ([ctypes.POINTER(BwdArgs), _vp], ctypes.c_int),
     "dsalt_gather_landmarks": ([ctypes.POINTER(GatherArgs), _vp], ctypes.c_int),
+    "dsalt_timing_enable": ([ctypes.c_int], ctypes.c_int),
+    "dsalt_timing_report": ([ctypes.c_char_p, _sz], ctypes.c_int),
 }
 
 _LIB = None

@@ -24,6 +24,7 @@ SOURCES = {
     "attn_fwd.hip": [],
     "attn_bwd.hip": [],
     "capi.hip": [],
+    "timing.hip": [],
 }
 
 

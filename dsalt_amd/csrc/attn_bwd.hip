@@ -18,6 +18,7 @@
 // LSE; dS = P (dP - delta), dP = dO V^T.
 #include "attn.h"
 #include "tiles.h"
+#include "timing.h"
 
 namespace dsalt {
 
@@ -32,8 +33,15 @@ template <> struct BwdShape<f16, 128> { static constexpr int BN = 32, BQ = 32, N
 template <> struct BwdShape<float, 64> { static constexpr int BN = 32, BQ = 16, NBUF = 2; };
 template <> struct BwdShape<float, 128> { static constexpr int BN = 16, BQ = 16, NBUF = 1; };
 
+__device__ __forceinline__ int seq_start_of(const AttnParams& p, int s) {
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
+    return st;
+}
 __device__ __forceinline__ int seq_len_of(const AttnParams& p, int s) {
-    return max(0, min(min(p.cu[s + 1], p.total_len) - p.cu[s], p.max_seqlen));
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
+    return len;
 }
 
 __device__ __forceinline__ int lower_bound_i(const int* a, int n, int x) {
@@ -50,7 +58,7 @@ __device__ __forceinline__ int lower_bound_i(const int* a, int n, int x) {
 __global__ __launch_bounds__(256) void bwd_rowinfo_kernel(AttnParams p) {
     __shared__ int wm[256];
     const int s = blockIdx.x, tid = threadIdx.x;
-    const int st = p.cu[s], len = seq_len_of(p, s);
+    const int st = seq_start_of(p, s), len = seq_len_of(p, s);
     const int nt16 = ceil_div(p.max_seqlen, 16);
     int wmax = 1;
     for (int t16 = tid; t16 < nt16; t16 += 256) {
@@ -122,7 +130,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
     const int t = L % p.n_tiles;
     const int s = (L / p.n_tiles) % p.num_seqs;
     const int h = L / (p.n_tiles * p.num_seqs);
-    const int st = p.cu[s];
+    const int st = seq_start_of(p, s);
     const int len = seq_len_of(p, s);
     const int r0 = t * 64;
     if (r0 >= len) return;
@@ -303,7 +311,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
     const int t = L % p.n_tiles;
     const int s = (L / p.n_tiles) % p.num_seqs;
     const int h = L / (p.n_tiles * p.num_seqs);
-    const int st = p.cu[s];
+    const int st = seq_start_of(p, s);
     const int len = seq_len_of(p, s);
     const int j0 = t * 64;
     if (j0 >= len) return;
@@ -488,7 +496,7 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     b /= p.n_chunks;
     const int s = b % p.num_seqs;
     const int h = b / p.num_seqs;
-    const int st = p.cu[s];
+    const int st = seq_start_of(p, s);
     const int len = seq_len_of(p, s);
     const int kvh = h / (p.n_heads / p.n_kv_heads);
     const int64_t set_off = (((int64_t)h * p.num_seqs + s) * p.n_sets) * K;
@@ -660,7 +668,7 @@ __global__ __launch_bounds__(256) void bwd_lmk_sum_kernel(AttnParams p) {
     }
     if (d == 0 && p.d_bias) p.d_bias[(((int64_t)h * p.num_seqs + s) * p.n_sets) * K + sl] = sb;
     if (pos < 0 || pos >= len) return;
-    const int64_t o = (int64_t)(p.cu[s] + pos) * p.n_heads * D + (int64_t)h * D + d;
+    const int64_t o = (int64_t)(seq_start_of(p, s) + pos) * p.n_heads * D + (int64_t)h * D + d;
     T* dk = (T*)p.dk;
     T* dv = (T*)p.dv;
     dk[o] = from_float<T>(to_float(dk[o]) + sk);
@@ -684,19 +692,19 @@ size_t bwd_workspace(const AttnParams& p) {
 template <typename T, int D>
 static void bwd_run(const AttnParams& p, hipStream_t stream) {
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
-    hipLaunchKernelGGL(bwd_rowinfo_kernel, dim3(p.num_seqs), dim3(256), 0, stream, p);
+    DSALT_LAUNCH("bwd_rowinfo", bwd_rowinfo_kernel, dim3(p.num_seqs), dim3(256), 0, stream, p);
     constexpr int LPR = D / (16 / (int)sizeof(T));
     const int64_t nrows = (int64_t)p.total_len * p.n_heads;
-    hipLaunchKernelGGL((bwd_delta_kernel<T, D>), dim3((unsigned)((nrows * LPR + 255) / 256)), dim3(256), 0, stream,
+    DSALT_LAUNCH("bwd_delta", (bwd_delta_kernel<T, D>), dim3((unsigned)((nrows * LPR + 255) / 256)), dim3(256), 0, stream,
                        p);
-    hipLaunchKernelGGL((bwd_dq_kernel<T, D>), dim3(total), dim3(256), 0, stream, p);
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D>), dim3(total), dim3(256), 0, stream, p);
+    DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D>), dim3(total), dim3(256), 0, stream, p);
+    DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D>), dim3(total), dim3(256), 0, stream, p);
     if (p.k_lmk > 0) {
         const int ngrp = ceil_div(p.k_lmk, 128);
-        hipLaunchKernelGGL((bwd_lmk_kernel<T, D>), dim3(p.n_heads * p.num_seqs * p.n_chunks * ngrp), dim3(256), 0,
+        DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D>), dim3(p.n_heads * p.num_seqs * p.n_chunks * ngrp), dim3(256), 0,
                            stream, p);
         const int64_t n = (int64_t)p.n_heads * p.num_seqs * p.k_lmk * D;
-        hipLaunchKernelGGL((bwd_lmk_sum_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p);
+        DSALT_LAUNCH("bwd_lmk_sum", (bwd_lmk_sum_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p);
     }
 }
 

@@ -15,6 +15,7 @@
 // 2^8), P rounded to the input dtype before P V as in the reference (:115,:147).
 #include "attn.h"
 #include "tiles.h"
+#include "timing.h"
 
 namespace dsalt {
 
@@ -65,8 +66,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     const int t = L % p.n_tiles;
     const int s = (L / p.n_tiles) % p.num_seqs;
     const int h = L / (p.n_tiles * p.num_seqs);
-    const int st = p.cu[s];
-    const int len = max(0, min(min(p.cu[s + 1], p.total_len) - st, p.max_seqlen));
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     const int r0 = t * kBM;
     if (r0 >= len) return;
     const int kvh = h / (p.n_heads / p.n_kv_heads);
@@ -262,9 +263,9 @@ static hipError_t fwd_dispatch(const AttnParams& p, hipStream_t stream) {
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
     if (total == 0) return hipSuccess;
     if (p.head_dim == 64)
-        hipLaunchKernelGGL((fwd_kernel<T, 64>), dim3(total), dim3(256), 0, stream, p);
+        DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, 64>), dim3(total), dim3(256), 0, stream, p);
     else
-        hipLaunchKernelGGL((fwd_kernel<T, 128>), dim3(total), dim3(256), 0, stream, p);
+        DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, 128>), dim3(total), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 

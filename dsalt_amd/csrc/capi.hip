@@ -44,8 +44,13 @@ int check_problem(const dsalt_problem& p, bool attention) {
     if (p.n_heads < 1 || p.n_kv_heads < 1 || p.n_heads % p.n_kv_heads)
         return fail(DSALT_ERR_INVALID, "n_heads (%d) must be a positive multiple of n_kv_heads (%d)", p.n_heads,
                     p.n_kv_heads);
-    if (p.head_dim != 64 && p.head_dim != 128)
-        return fail(DSALT_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", p.head_dim);
+    if (attention) {
+        if (p.head_dim != 64 && p.head_dim != 128)
+            return fail(DSALT_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", p.head_dim);
+    } else if (p.head_dim < 1 || (p.head_dim * esize(p.dtype)) % 16 || p.head_dim * esize(p.dtype) > 1024) {
+        return fail(DSALT_ERR_INVALID, "head_dim %d must be a multiple of 16 bytes, at most 1024 bytes",
+                    p.head_dim);
+    }
     if (p.k_lmk < 0 || p.k_lmk > dsalt::kMaxLandmarks)
         return fail(DSALT_ERR_INVALID, "k_lmk %d outside [0, %d]", p.k_lmk, dsalt::kMaxLandmarks);
     if (p.select_mode != DSALT_SELECT_GLOBAL && p.select_mode != DSALT_SELECT_BLOCK)
@@ -54,7 +59,6 @@ int check_problem(const dsalt_problem& p, bool attention) {
         return fail(DSALT_ERR_INVALID, "block_size %d must be a positive multiple of 64", p.block_size);
     if (p.dtype != DSALT_DTYPE_F32 && p.dtype != DSALT_DTYPE_BF16 && p.dtype != DSALT_DTYPE_F16)
         return fail(DSALT_ERR_INVALID, "unknown dtype %d", p.dtype);
-    (void)attention;
     return DSALT_OK;
 }
 
@@ -276,6 +280,7 @@ int dsalt_gather_landmarks(const dsalt_gather_args* a, dsalt_stream_t stream) {
     dsalt::GatherParams p;
     p.total_len = a->p.total_len;
     p.num_seqs = a->p.num_seqs;
+    p.max_seqlen = a->p.max_seqlen;
     p.n_heads = a->p.n_heads;
     p.n_kv_heads = a->p.n_kv_heads;
     p.head_dim = a->p.head_dim;

@@ -112,6 +112,14 @@ template <> __device__ __forceinline__ float round_norm<f16>(float f) { return (
 
 __host__ __device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// Start and length of sequence s, clamped to the packed buffer [0, total) and to
+// max_len, so malformed offsets can never address rows outside the tensors.
+__device__ __forceinline__ void seq_bounds(const int32_t* cu, int s, int total, int max_len, int& st, int& len) {
+    st = min(max(cu[s], 0), total);
+    int en = min(max(cu[s + 1], st), total);
+    len = min(en - st, max_len);
+}
+
 // XCD-aware block index: the hardware deals blocks round-robin to 8 XCDs;
 // remap so each XCD walks a contiguous range of logical tiles (L2 reuse of
 // the shared key band between neighbouring query tiles).

@@ -25,7 +25,7 @@ struct SelectParams {
 };
 
 struct GatherParams {
-    int total_len, num_seqs, n_heads, n_kv_heads, head_dim, k_lmk, n_sets, dtype;
+    int total_len, num_seqs, max_seqlen, n_heads, n_kv_heads, head_dim, k_lmk, n_sets, dtype;
     const void* k;
     int64_t k_stride_t, k_stride_h;
     const void* v;

@@ -21,6 +21,7 @@
 // restates; this file is compiled with -ffp-contract=off.
 #include "common.h"
 #include "select.h"
+#include "timing.h"
 
 namespace dsalt {
 
@@ -91,14 +92,16 @@ __device__ __forceinline__ void range_of(const SelectParams& p, int r, int& r0, 
             r0 = 0;
             r1 = p.total_len;
         } else {
-            r0 = p.cu[r];
-            r1 = min(p.cu[r + 1], p.total_len);
+            int len;
+            seq_bounds(p.cu, r, p.total_len, p.max_seqlen, r0, len);
+            r1 = r0 + len;
         }
     } else {
         int s = r / p.n_sets, b = r % p.n_sets;
-        int st = p.cu[s], en = min(p.cu[s + 1], p.total_len);
-        r0 = min(st + b * p.block_size, en);
-        r1 = min(r0 + p.block_size, en);
+        int st, len;
+        seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
+        r0 = min(st + b * p.block_size, st + len);
+        r1 = min(r0 + p.block_size, st + len);
     }
 }
 
@@ -160,7 +163,8 @@ __global__ void sel_stats_kernel(SelectParams p, const double* sums, double* sta
     } else {
         if (id >= p.num_seqs * nsig) return;
         int s = id / nsig, sig = id % nsig;
-        int len = min(p.cu[s + 1], p.total_len) - p.cu[s];
+        int st, len;
+        seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
         double p1 = 0.0, p2 = 0.0;
         for (int b = 0; b < p.n_sets; ++b) {
             int64_t o = ((int64_t)(s * p.n_sets + b) * nsig + sig) * 2;
@@ -199,9 +203,10 @@ __global__ __launch_bounds__(256) void sel_z_kernel(SelectParams p, const float*
                                                     const double* stats, float* zx, float* zv) {
     const int s = blockIdx.y;
     const int nsig = 1 + p.n_kv_heads;
-    int st = p.cu[s], en = min(p.cu[s + 1], p.total_len);
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     int t = st + blockIdx.x * 256 + threadIdx.x;
-    if (t >= en) return;
+    if (t >= st + len) return;
     int r = p.stats_scope == DSALT_STATS_PACKED ? 0 : s;
     const double* sr = stats + (int64_t)r * nsig * 2;
     float zxt = zscore(nx[t], sr[0], sr[1]);
@@ -297,8 +302,8 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
     const int h = blockIdx.x / (p.n_sets * p.num_seqs);
     const int K = p.k_lmk;
     int32_t* out = p.lmk_idx + (((int64_t)h * p.num_seqs + s) * p.n_sets + set) * K;
-    const int st = p.cu[s];
-    const int len = max(0, min(p.cu[s + 1], p.total_len) - st);
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     const bool block = p.select_mode == DSALT_SELECT_BLOCK;
     int n = len;
     KeyFn key;
@@ -438,7 +443,8 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherParams p) {
     const int h = (int)(row / ((int64_t)p.num_seqs * p.n_sets * p.k_lmk));
     const int g = h / (p.n_heads / p.n_kv_heads);
     const int pos = p.lmk_idx[row];
-    const int st = p.cu[s], len = max(0, min(p.cu[s + 1], p.total_len) - st);
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     u4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
     if (pos >= 0 && pos < len) {
         kv = *(const u4*)((const T*)p.k + (int64_t)(st + pos) * p.k_stride_t + (int64_t)g * p.k_stride_h + c * VW);
@@ -487,22 +493,22 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
     if (p.total_len > 0) {
         int blocks = min(ceil_div(p.total_len, 4), 65536);
         if (p.dtype == DSALT_DTYPE_BF16)
-            hipLaunchKernelGGL(sel_norms_kernel<bf16>, dim3(blocks), dim3(256), 0, stream, p, nx, nv);
+            DSALT_LAUNCH("sel_norms", sel_norms_kernel<bf16>, dim3(blocks), dim3(256), 0, stream, p, nx, nv);
         else if (p.dtype == DSALT_DTYPE_F16)
-            hipLaunchKernelGGL(sel_norms_kernel<f16>, dim3(blocks), dim3(256), 0, stream, p, nx, nv);
+            DSALT_LAUNCH("sel_norms", sel_norms_kernel<f16>, dim3(blocks), dim3(256), 0, stream, p, nx, nv);
         else
-            hipLaunchKernelGGL(sel_norms_kernel<float>, dim3(blocks), dim3(256), 0, stream, p, nx, nv);
-        hipLaunchKernelGGL(sel_sums_kernel, dim3(nranges, nsig), dim3(256), 0, stream, p, nx, nv, sums);
+            DSALT_LAUNCH("sel_norms", sel_norms_kernel<float>, dim3(blocks), dim3(256), 0, stream, p, nx, nv);
+        DSALT_LAUNCH("sel_sums", sel_sums_kernel, dim3(nranges, nsig), dim3(256), 0, stream, p, nx, nv, sums);
         int nst = p.select_mode == DSALT_SELECT_GLOBAL ? nranges * nsig : p.num_seqs * nsig;
-        hipLaunchKernelGGL(sel_stats_kernel, dim3(ceil_div(nst, 64)), dim3(64), 0, stream, p, sums, stats,
+        DSALT_LAUNCH("sel_stats", sel_stats_kernel, dim3(ceil_div(nst, 64)), dim3(64), 0, stream, p, sums, stats,
                            nranges);
         if (p.select_mode == DSALT_SELECT_GLOBAL)
-            hipLaunchKernelGGL(sel_z_kernel, dim3(ceil_div(p.max_seqlen, 256), p.num_seqs), dim3(256), 0,
+            DSALT_LAUNCH("sel_z", sel_z_kernel, dim3(ceil_div(p.max_seqlen, 256), p.num_seqs), dim3(256), 0,
                                stream, p, nx, nv, stats, zx, zv);
     }
     int nsets_total = p.n_heads * p.num_seqs * p.n_sets;
     if (nsets_total > 0 && p.k_lmk > 0)
-        hipLaunchKernelGGL(sel_topk_kernel, dim3(nsets_total), dim3(kSelThreads), 0, stream, p, zx, zv, nx,
+        DSALT_LAUNCH("sel_topk", sel_topk_kernel, dim3(nsets_total), dim3(kSelThreads), 0, stream, p, zx, zv, nx,
                            nv, stats, border_cap);
     return hipGetLastError();
 }
@@ -513,11 +519,11 @@ hipError_t gather_launch(const GatherParams& p, hipStream_t stream) {
     if (n == 0) return hipSuccess;
     dim3 grid((unsigned)((n + 255) / 256));
     if (p.dtype == DSALT_DTYPE_BF16)
-        hipLaunchKernelGGL(gather_kernel<bf16>, grid, dim3(256), 0, stream, p);
+        DSALT_LAUNCH("gather", gather_kernel<bf16>, grid, dim3(256), 0, stream, p);
     else if (p.dtype == DSALT_DTYPE_F16)
-        hipLaunchKernelGGL(gather_kernel<f16>, grid, dim3(256), 0, stream, p);
+        DSALT_LAUNCH("gather", gather_kernel<f16>, grid, dim3(256), 0, stream, p);
     else
-        hipLaunchKernelGGL(gather_kernel<float>, grid, dim3(256), 0, stream, p);
+        DSALT_LAUNCH("gather", gather_kernel<float>, grid, dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 

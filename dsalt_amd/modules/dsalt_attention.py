@@ -1,0 +1,132 @@
+"""DSALT attention layer on MI355X.
+
+Mirrors ``DSALTAttention`` of ``dsalt/modules/dsalt_attention.py:147-704`` (constructor,
+parameters and ``forward(x, cu_seqlens, max_seqlen, rope_cs, cu_list) -> (out, aux)``) with
+the inference branch of ``_packed`` (:610-634):
+  * q/k/v projections (library GEMMs), RoPE on q and k;
+  * windows ``w = floor(n_min + sigmoid(win_gate(x)) (n_max - n_min))``, at least 1
+    (:277-284), and ``alpha = sigmoid(alpha_w)`` (:228, :243-244);
+  * landmark selection (``_compute_landmark_indices``) and the sparse operator with zero
+    landmark bias (:622), k/v read per kv head (no materialised GQA repeat).
+``select_mode="block"`` switches to block-causal landmarks (``block_size`` query rows per
+set, statistics of the prefix), the variant of ``results/causal_landmark_check.py:150-189``.
+Batched ``[B, T, d]`` input is run as ``B`` packed sequences of length ``T``.
+
+Not provided here: the differentiable selectors of the training branch (soft window edge,
+landmark log-weight; ``:440-563``) -- in training mode the layer runs the hard-selection
+operator, whose gradients reach the projections but not ``win_gate`` / ``alpha_w`` -- and
+the dense ``_last_P`` rebuild for the metrics (``:636-702``), which stays ``None``.
+"""
+from __future__ import annotations
+
+import math
+import warnings
+
+import torch
+import torch.nn as nn
+
+from ..kernels.dsalt_attn import dsalt_attention
+from ..kernels.selectors import _compute_landmark_indices
+from ..kernels.window_utils import apply_rotary_emb, build_rope_cache
+
+
+class DSALTAttention(nn.Module):
+    def __init__(self, d_model: int, n_heads: int, n_min: int, n_max: int, k_lmk: int, max_seq_len: int,
+                 dropout: float = 0.0, yarn_scale: float = 1.0, layer_idx: int = 0, n_kv_heads: int | None = None,
+                 qkv_bias: bool = False, rope_base: float = 10000.0, select_mode: str = "global",
+                 block_size: int = 512, stats_scope: str = "packed"):
+        super().__init__()
+        assert d_model % n_heads == 0
+        self.d_model = d_model
+        self.n_heads = n_heads
+        self.head_dim = d_model // n_heads
+        self.n_kv_heads = n_kv_heads if n_kv_heads is not None else n_heads
+        assert n_heads % self.n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads"
+        self.n_rep = n_heads // self.n_kv_heads
+        self.kv_dim = self.n_kv_heads * self.head_dim
+        self.n_min, self.n_max, self.k_lmk = n_min, n_max, k_lmk
+        self.max_seq_len = max_seq_len
+        self.dropout = dropout
+        self.yarn_scale = yarn_scale
+        self.rope_base = rope_base
+        self.layer_idx = layer_idx
+        self.select_mode = select_mode
+        self.block_size = block_size
+        self.stats_scope = stats_scope
+        self.q_proj = nn.Linear(d_model, d_model, bias=qkv_bias)
+        self.k_proj = nn.Linear(d_model, self.kv_dim, bias=qkv_bias)
+        self.v_proj = nn.Linear(d_model, self.kv_dim, bias=qkv_bias)
+        self.out_proj = nn.Linear(d_model, d_model, bias=False)
+        self.win_gate = nn.Linear(d_model, 1, bias=True)
+        self.alpha_w = nn.Parameter(torch.full((n_heads,), math.log(0.6 / 0.4)))
+        self.tau_win, self.tau_lmk, self.win_edge = 1.0, 2.0, 4
+        self._last_P = None
+        self._collect_last_P = False
+        self._warned_training = False
+        cos, sin = build_rope_cache(max_seq_len, self.head_dim, torch.device("cpu"), base=rope_base, scale=yarn_scale)
+        self.register_buffer("rope_cos", cos, persistent=False)
+        self.register_buffer("rope_sin", sin, persistent=False)
+
+    def _alpha(self) -> torch.Tensor:
+        return torch.sigmoid(self.alpha_w)
+
+    def _window_continuous(self, x: torch.Tensor) -> torch.Tensor:
+        return self.n_min + torch.sigmoid(self.win_gate(x).squeeze(-1)) * (self.n_max - self.n_min)
+
+    @torch.no_grad()
+    def _window_sizes(self, x: torch.Tensor, floor: bool) -> torch.Tensor:
+        w = self._window_continuous(x)
+        return (w.floor() if floor else w.round()).clamp(min=1)
+
+    def _aux_zero(self, device, dtype):
+        return torch.zeros((), device=device, dtype=dtype)
+
+    def _apply_out_proj(self, out: torch.Tensor) -> torch.Tensor:
+        return self.out_proj(out.to(self.out_proj.weight.dtype))
+
+    @torch.no_grad()
+    def warmup(self, device) -> None:
+        was = self.training
+        self.eval()
+        n = max(self.n_min * 2, 64)
+        x = torch.randn(n, self.d_model, device=device, dtype=self.q_proj.weight.dtype)
+        self._packed(x, torch.tensor([0, n], dtype=torch.int32, device=device), n, device, cu_list=[0, n])
+        torch.cuda.synchronize(device)
+        self.train(was)
+
+    def forward(self, x, cu_seqlens=None, max_seqlen=None, rope_cs=None, cu_list=None):
+        if cu_seqlens is not None:
+            return self._packed(x, cu_seqlens, x.shape[0], x.device, rope_cs, cu_list)
+        B, T, _ = x.shape
+        cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=x.device)
+        out, aux = self._packed(x.reshape(B * T, -1), cu, B * T, x.device, None, list(range(0, (B + 1) * T, T)))
+        return out.view(B, T, -1), aux
+
+    def _packed(self, x, cu_seqlens, total_len, device, rope_cs=None, cu_list=None):
+        if self.training and not self._warned_training:
+            warnings.warn("DSALTAttention (dsalt_amd) trains through the hard-selection operator: win_gate and "
+                          "alpha_w receive no gradient")
+            self._warned_training = True
+        q = self.q_proj(x).view(total_len, self.n_heads, self.head_dim)
+        k = self.k_proj(x).view(total_len, self.n_kv_heads, self.head_dim)
+        v = self.v_proj(x).view(total_len, self.n_kv_heads, self.head_dim)
+        if rope_cs is None:
+            cu = cu_seqlens.long()
+            lens = cu[1:] - cu[:-1]
+            seq_ids = torch.repeat_interleave(torch.arange(lens.numel(), device=device), lens)
+            pos = torch.arange(total_len, device=device) - cu[:-1][seq_ids]
+            cos, sin = self.rope_cos[pos], self.rope_sin[pos]
+        else:
+            cos, sin = rope_cs
+        cos, sin = cos.to(q.dtype), sin.to(q.dtype)
+        q, k = apply_rotary_emb(q, k, cos.unsqueeze(1), sin.unsqueeze(1))
+        w = self._window_sizes(x, floor=True)
+        alpha = self._alpha()
+        lmk, _, _ = _compute_landmark_indices(x.detach(), self.v_proj.weight.detach(), alpha.detach().float(), w,
+                                              cu_seqlens, self.k_lmk, self.n_min, total_len, cu_list,
+                                              head_dim=self.head_dim, select_mode=self.select_mode,
+                                              block_size=self.block_size, stats_scope=self.stats_scope)
+        out = dsalt_attention(q.contiguous(), k.contiguous(), v.contiguous(), lmk, None, w, cu_seqlens,
+                              cu_list=cu_list, block_size=self.block_size)
+        self._last_P = None
+        return self._apply_out_proj(out.view(total_len, self.d_model)), self._aux_zero(x.device, x.dtype)

@@ -56,6 +56,19 @@ def _rows3(t: torch.Tensor, name: str) -> torch.Tensor:
     return t
 
 
+def _check_tokens(q, k, v, w, cu_seqlens):
+    T, H, D = q.shape
+    if k.shape[0] != T or v.shape != k.shape or k.shape[2] != D:
+        raise ValueError(f"k and v must be [T, n_kv, D] matching q {tuple(q.shape)}, got {tuple(k.shape)}, "
+                         f"{tuple(v.shape)}")
+    if H % k.shape[1]:
+        raise ValueError("n_heads must be a multiple of n_kv_heads")
+    if w.dim() != 1 or w.shape[0] != T:
+        raise ValueError("w must be [T]")
+    if cu_seqlens.dim() != 1 or cu_seqlens.shape[0] < 2:
+        raise ValueError("cu_seqlens must be [S+1] with S >= 1")
+
+
 def _max_seqlen(cu_seqlens: torch.Tensor, cu_list=None) -> int:
     if cu_list is not None:
         return max(1, max(int(cu_list[i + 1]) - int(cu_list[i]) for i in range(len(cu_list) - 1)))
@@ -152,8 +165,11 @@ def attention_forward(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias=None, *, scale=N
     T, H, D = q.shape
     G = k.shape[1]
     S = cu_seqlens.shape[0] - 1
+    _check_tokens(q, k, v, w, cu_seqlens)
     maxlen = max_seqlen if max_seqlen is not None else _max_seqlen(cu_seqlens)
     K = lmk_idx.shape[-1]
+    if lmk_bias is not None and tuple(lmk_bias.shape) != tuple(lmk_idx.shape):
+        raise ValueError("lmk_bias must have the shape of lmk_idx")
     if lmk_idx.shape[:2] != (H, S) or lmk_idx.dim() != 4:
         raise ValueError(f"lmk_idx must be [H, S, n_sets, K], got {tuple(lmk_idx.shape)}")
     if lmk_idx.shape[2] != n_sets(select_mode, maxlen, block_size):
@@ -195,8 +211,17 @@ def attention_backward(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias
         dout = dout.to(q.dtype)
     T, H, D = q.shape
     S = cu_seqlens.shape[0] - 1
+    _check_tokens(q, k, v, w, cu_seqlens)
+    if tuple(out.shape) != (T, H, D) or tuple(dout.shape) != (T, H, D) or tuple(lse.shape) != (T, H):
+        raise ValueError("out / dout must be [T, H, D] and lse [T, H]")
+    if k.shape[1] != H:
+        raise ValueError("the backward needs n_kv_heads == n_heads (expand grouped heads first)")
     maxlen = max_seqlen if max_seqlen is not None else _max_seqlen(cu_seqlens)
     K = lmk_idx.shape[-1]
+    if lmk_idx.dim() != 4 or lmk_idx.shape[:3] != (H, S, 1):
+        raise ValueError(f"lmk_idx must be [H, S, 1, K] (global variant), got {tuple(lmk_idx.shape)}")
+    if lmk_bias is not None and tuple(lmk_bias.shape) != tuple(lmk_idx.shape):
+        raise ValueError("lmk_bias must have the shape of lmk_idx")
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
     w_c = w.detach().to(torch.int32).contiguous()
     cu_c = cu_seqlens.detach().to(torch.int32).contiguous()
@@ -244,6 +269,9 @@ def gather_landmarks(k, v, cu_seqlens, lmk_idx, *, max_seqlen=None, select_mode=
     S = cu_seqlens.shape[0] - 1
     K = lmk_idx.shape[-1]
     maxlen = max_seqlen if max_seqlen is not None else _max_seqlen(cu_seqlens)
+    if lmk_idx.dim() != 4 or lmk_idx.shape[1] != S or lmk_idx.shape[2] != n_sets(select_mode, maxlen, block_size):
+        raise ValueError(f"lmk_idx must be [H, S, n_sets, K] matching select_mode/block_size, got "
+                         f"{tuple(lmk_idx.shape)}")
     li = lmk_idx.to(torch.int32).contiguous()
     cu_c = cu_seqlens.detach().to(torch.int32).contiguous()
     shape = tuple(lmk_idx.shape) + (D,)

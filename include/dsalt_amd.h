@@ -174,6 +174,16 @@ int    dsalt_gather_landmarks(const dsalt_gather_args* a, dsalt_stream_t stream)
  * this call with the full capacity. */
 int    dsalt_select_with_border_cap(const dsalt_select_args* a, dsalt_stream_t stream, int border_cap);
 
+/* Per-kernel timing, an instrumentation facility with no counterpart in the
+ * reference (its only timing is the CUDA-event fwd+bwd step of
+ * dsalt/kernels/autotune.py:176-189).  While enabled, every kernel the library
+ * enqueues is bracketed by two HIP events on its stream (events are created
+ * once and reused).  dsalt_timing_report waits for the recorded events, writes
+ * one line "kernel launches total_ms" per kernel name into buf (NUL-terminated,
+ * truncated to len), resets the totals and returns the full report length. */
+int    dsalt_timing_enable(int enable);
+int    dsalt_timing_report(char* buf, size_t len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,103 @@
+"""The reference library's CPU attention path, timed as the CPU baseline - TEST INFRASTRUCTURE ONLY.
+
+Restates the masked-SDPA fallback that ``DSALTAttention._packed`` takes without Triton
+(``dsalt/modules/dsalt_attention.py:626-634``): landmark scores and top-k
+(``oracle/select_oracle.c``), the boolean ``[T, T]`` mask of ``_build_mask_packed``
+(``dsalt_attention.py:95-144``: window band OR the per-sequence union of landmarks), the
+additive ``-inf`` mask in the input dtype and ``F.scaled_dot_product_attention``
+(``dsalt/kernels/sparse_attn.py:29-57``), with autograd for the backward.
+
+A dense masked SDPA costs O(T) per query row whatever the sparsity, so the timing runs the
+full-length selection and a bounded sample of query rows (all heads, all keys); the
+per-token time is ``t_select / T + t_attention / rows``; rows run in chunks of 256 query rows.  Only bench.py's ``cpu_baseline``
+leg calls this.
+"""
+from __future__ import annotations
+
+import os
+import time
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import select as OS
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.float32:
+        return t.numpy()
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+def _odt(dt: torch.dtype) -> int:
+    return {torch.float32: OS.DTYPE_F32, torch.bfloat16: OS.DTYPE_BF16, torch.float16: OS.DTYPE_F16}[dt]
+
+
+def literal_mask_rows(w: torch.Tensor, cu: torch.Tensor, idx: np.ndarray, rows: torch.Tensor) -> torch.Tensor:
+    """Rows ``rows`` of the reference fallback's [T, T] mask (one mask for all heads)."""
+    T = int(cu[-1])
+    seq = torch.searchsorted(cu[1:].long(), rows.long(), right=True)
+    st = cu[seq].long()
+    rel = rows.long() - st
+    lo = (rel - w[rows].long().clamp(min=1) + 1).clamp(min=0) + st
+    col = torch.arange(T).unsqueeze(0)
+    m = (col >= lo.unsqueeze(1)) & (col <= rows.long().unsqueeze(1))
+    for s in torch.unique(seq).tolist():
+        pos = idx[:, s].reshape(-1)
+        L = int(cu[s + 1] - cu[s])
+        pos = np.unique(pos[(pos >= 0) & (pos < L)])
+        if len(pos):
+            r = (seq == s).nonzero()[:, 0]
+            m[r.unsqueeze(1), torch.as_tensor(pos + int(cu[s])).unsqueeze(0)] = True
+    return m
+
+
+def _attention_rows(q, k, v, dout, mask):
+    qs = q.detach().clone().requires_grad_(True)
+    kk = k.detach().clone().requires_grad_(True)
+    vv = v.detach().clone().requires_grad_(True)
+    additive = torch.zeros(mask.shape, dtype=q.dtype).masked_fill(~mask, float("-inf"))[None, None]
+    out = F.scaled_dot_product_attention(qs.transpose(0, 1)[None], kk.transpose(0, 1)[None],
+                                         vv.transpose(0, 1)[None], attn_mask=additive)
+    out = out[0].transpose(0, 1)
+    out.backward(dout)
+    return out
+
+
+def time_baseline(x: dict, k_lmk: int, stats_scope: int, target_s: float = 12.0, backward: bool = True):
+    """Times the CPU path on the inputs ``x`` (CPU tensors from dsalt_amd.workloads).
+
+    Returns a dict with tokens_per_s, threads, rows and the timing split.
+    """
+    threads = torch.get_num_threads()
+    T = x["q"].shape[0]
+    t0 = time.perf_counter()
+    idx = OS.select(_bits(x["h"]), _bits(x["v"]), x["alpha"].numpy(), x["w"].numpy(), x["cu"].numpy(), k_lmk,
+                    _odt(x["h"].dtype), stats_scope=stats_scope)
+    t_sel = time.perf_counter() - t0
+
+    def attn(nrows, chunk=256):
+        t1 = time.perf_counter()
+        for r0 in range(T - nrows, T, chunk):
+            rows = torch.arange(r0, min(T, r0 + chunk))
+            m = literal_mask_rows(x["w"], x["cu"], idx, rows)
+            if backward:
+                _attention_rows(x["q"][rows], x["k"], x["v"], x["dout"][rows], m)
+            else:
+                with torch.no_grad():
+                    additive = torch.zeros(m.shape, dtype=x["q"].dtype).masked_fill(~m, float("-inf"))[None, None]
+                    F.scaled_dot_product_attention(x["q"][rows].transpose(0, 1)[None], x["k"].transpose(0, 1)[None],
+                                                   x["v"].transpose(0, 1)[None], attn_mask=additive)
+        return time.perf_counter() - t1
+
+    probe = min(T, 256)
+    attn(probe)  # first call pays one-time setup
+    t_probe = attn(probe)
+    rows = int(min(T, max(probe, (target_s / max(t_probe, 1e-3)) * probe)))
+    rows = max(probe, (rows // 256) * 256)
+    t_att = attn(rows)
+    per_token = t_sel / T + t_att / rows
+    return dict(tokens_per_s=1.0 / per_token, threads=threads, rows=rows, t_select=t_sel, t_attention=t_att,
+                cpu_count=os.cpu_count())

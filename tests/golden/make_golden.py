@@ -140,9 +140,9 @@ def gather_case(SEL):
                 lv=lv.numpy())
 
 
-def block_causal_case(CLC, gqa: bool, seed: int):
+def block_causal_case(CLC, gqa: bool, seed: int, T: int = 160, B: int = 32, dh: int = 8):
     g = torch.Generator().manual_seed(seed)
-    T, d, H, dh, k, B = 160, 16, 4, 8, 6, 32
+    d, H, k = 16, 4, 6
     G = 2 if gqa else H
     x = torch.randn(T, d, generator=g)
     W_V = torch.randn(G * dh, d, generator=g) / 4.0
@@ -179,6 +179,8 @@ def main():
     np.savez_compressed(os.path.join(OUT, "landmark_gather.npz"), **gather_case(SEL))
     np.savez_compressed(os.path.join(OUT, "block_causal_mha.npz"), **block_causal_case(CLC, False, 500))
     np.savez_compressed(os.path.join(OUT, "block_causal_gqa.npz"), **block_causal_case(CLC, True, 501))
+    np.savez_compressed(os.path.join(OUT, "block_causal_b64.npz"),
+                        **block_causal_case(CLC, True, 502, T=400, B=64, dh=64))
     print("golden vectors written to", OUT)
 
 

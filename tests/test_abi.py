@@ -1,0 +1,128 @@
+"""The C-ABI library (CPU only: no kernel launches).
+
+* every function declared in include/*.h is exported by libdsalt_amd.so;
+* the ctypes mirrors of the argument structs have the C compiler's sizes and offsets;
+* argument validation rejects bad problems with the documented error codes.
+"""
+from __future__ import annotations
+
+import ctypes
+import glob
+import os
+import re
+import subprocess
+
+import pytest
+
+from dsalt_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
+
+
+def declared_functions():
+    names = set()
+    for h in HEADERS:
+        src = open(h).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        for m in re.finditer(r"^\s*[A-Za-z_][\w\s\*]*?\b(dsalt_\w+)\s*\(", src, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_function():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(_lib.SIGNATURES) == names
+    assert lib.dsalt_abi_version() == 1
+
+
+STRUCTS = {
+    "dsalt_problem": _lib.Problem,
+    "dsalt_select_args": _lib.SelectArgs,
+    "dsalt_fwd_args": _lib.FwdArgs,
+    "dsalt_bwd_args": _lib.BwdArgs,
+    "dsalt_gather_args": _lib.GatherArgs,
+}
+
+
+def test_struct_layouts_match_c(tmp_path):
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADERS[0]}"', "int main(void){"]
+    for cname, cls in STRUCTS.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'printf("{cname}.{f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-o", str(exe), str(src)], check=True)
+    got = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                          check=True).stdout.splitlines())
+    for cname, cls in STRUCTS.items():
+        assert int(got[f"{cname} size"]) == ctypes.sizeof(cls), cname
+        for f, _ in cls._fields_:
+            assert int(got[f"{cname}.{f}"]) == getattr(cls, f).offset, (cname, f)
+
+
+def _valid_fwd():
+    a = _lib.FwdArgs()
+    a.p = _lib.Problem(128, 1, 128, 2, 2, 64, 8, 0, 0, _lib.DTYPE_BF16)
+    fake = 1 << 20  # never dereferenced: validation fails before any launch
+    a.q = a.k = a.v = a.out = fake
+    a.q_stride_t = a.k_stride_t = a.v_stride_t = a.o_stride_t = 128
+    a.q_stride_h = a.k_stride_h = a.v_stride_h = a.o_stride_h = 64
+    a.w = a.cu_seqlens = a.lmk_idx = a.lse = fake
+    a.scale = 0.125
+    return a
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("head_dim", 96, 2), ("k_lmk", 513, 1), ("n_kv_heads", 3, 1), ("dtype", 7, 1),
+    ("select_mode", 1, 1), ("max_seqlen", 0, 1)])
+def test_fwd_validation(field, value, code):
+    lib = _lib.load()
+    a = _valid_fwd()
+    setattr(a.p, field, value)
+    assert lib.dsalt_fwd(ctypes.byref(a), None) == code
+    assert lib.dsalt_last_error()
+
+
+def test_misaligned_and_null_pointers_rejected():
+    lib = _lib.load()
+    a = _valid_fwd()
+    a.q = (1 << 20) + 2
+    assert lib.dsalt_fwd(ctypes.byref(a), None) == 1
+    a = _valid_fwd()
+    a.q_stride_t = 100  # 200 bytes: not a multiple of 16
+    assert lib.dsalt_fwd(ctypes.byref(a), None) == 1
+    assert lib.dsalt_fwd(None, None) == 1
+
+
+def test_backward_rejects_unsupported_variants():
+    lib = _lib.load()
+    a = _lib.BwdArgs()
+    a.p = _lib.Problem(256, 1, 256, 4, 2, 64, 8, 0, 0, _lib.DTYPE_BF16)
+    assert lib.dsalt_bwd(ctypes.byref(a), None) == 2  # GQA backward
+    a.p = _lib.Problem(256, 1, 256, 4, 4, 64, 8, 1, 128, _lib.DTYPE_BF16)
+    assert lib.dsalt_bwd(ctypes.byref(a), None) == 2  # block-causal backward
+    assert b"block" in lib.dsalt_last_error()
+
+
+def test_workspace_sizes_and_small_workspace():
+    lib = _lib.load()
+    s = _lib.SelectArgs()
+    s.p = _lib.Problem(1024, 2, 512, 4, 4, 64, 16, 0, 0, _lib.DTYPE_BF16)
+    s.hidden, s.stats_scope = 256, _lib.STATS_SEQUENCE
+    fake = 1 << 20
+    s.h = s.v = s.alpha = s.w = s.cu_seqlens = s.lmk_idx = fake
+    s.h_stride_t, s.v_stride_t, s.v_stride_h = 256, 256, 64
+    need = lib.dsalt_select_workspace_bytes(ctypes.byref(s))
+    assert need >= 1024 * 5 * 4
+    s.workspace, s.workspace_bytes = fake, need - 1
+    assert lib.dsalt_select(ctypes.byref(s), None) == 3
+    s.p.select_mode, s.p.block_size = 1, 128
+    assert lib.dsalt_select_workspace_bytes(ctypes.byref(s)) > 0

@@ -1,0 +1,54 @@
+"""Host-side parts of the reference-named API (CPU): packed metadata and mask builders
+against the reference's golden outputs."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from dsalt_amd.kernels import selectors as SEL
+from dsalt_amd.kernels import window_utils as WU
+from tests.helpers import load_golden
+
+
+def test_seq_block_map_matches_reference():
+    z = load_golden("seq_block_map")
+    for n in range(3):
+        m, tot = SEL._build_seq_block_map(torch.tensor(z[f"cu{n}"]), int(z[f"bm{n}"]), torch.device("cpu"))
+        np.testing.assert_array_equal(m.numpy(), z[f"map{n}"])
+        assert tot == int(z[f"tot{n}"])
+
+
+def test_seq_block_map_cache_distinguishes_raggings():
+    # the reference keys its cache on (total_len, num_seqs, block_m): these two collide there
+    a, _ = SEL._build_seq_block_map(torch.tensor([0, 10, 100]), 16, torch.device("cpu"))
+    b, _ = SEL._build_seq_block_map(torch.tensor([0, 90, 100]), 16, torch.device("cpu"))
+    assert a.shape != b.shape or not torch.equal(a, b)
+
+
+def test_seq_meta():
+    cu = torch.tensor([0, 3, 8, 8, 12])
+    n, lens, starts, seq_ids, seq_off, max_len = SEL._seq_meta(cu, 12, torch.device("cpu"))
+    assert n == 4 and max_len == 5
+    assert seq_ids.tolist() == [0, 0, 0, 1, 1, 1, 1, 1, 3, 3, 3, 3]
+    assert seq_off.tolist() == [0, 1, 2, 0, 1, 2, 3, 4, 0, 1, 2, 3]
+
+
+def test_window_masks_match_reference():
+    z = load_golden("window_masks")
+    m1 = WU.build_local_window_mask(z["m1"].shape[0], torch.tensor(z["w1"]), torch.device("cpu"))
+    np.testing.assert_array_equal(m1.numpy(), z["m1"])
+    T = int(z["cu"][-1])
+    m2 = WU.build_local_window_mask_packed(torch.tensor(z["cu"]), torch.tensor(z["w2"]), T, torch.device("cpu"))
+    np.testing.assert_array_equal(m2.numpy(), z["m2"])
+
+
+def test_rope_cache_matches_closed_form():
+    cos, sin = WU.build_rope_cache(16, 8, torch.device("cpu"), dtype=torch.float64, base=100.0)
+    theta = 100.0 ** (-np.arange(0, 8, 2) / 8)
+    ang = np.arange(16)[:, None] * np.concatenate([theta, theta])[None, :]
+    np.testing.assert_allclose(cos.numpy(), np.cos(ang), atol=1e-12)
+    q = torch.randn(16, 2, 8, dtype=torch.float64)
+    qr, _ = WU.apply_rotary_emb(q, q, cos.unsqueeze(1), sin.unsqueeze(1))
+    # a rotation keeps every 2-d pair's norm
+    np.testing.assert_allclose((qr[..., :4] ** 2 + qr[..., 4:] ** 2).numpy(),
+                               (q[..., :4] ** 2 + q[..., 4:] ** 2).numpy(), atol=1e-12)

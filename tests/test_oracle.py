@@ -40,7 +40,7 @@ def test_select_matches_reference_golden(name):
     np.testing.assert_allclose(sc, z["scores"], atol=3e-6)
 
 
-@pytest.mark.parametrize("name", ["mha", "gqa"])
+@pytest.mark.parametrize("name", ["mha", "gqa", "b64"])
 def test_block_causal_matches_reference_golden(name):
     z = load_golden(f"block_causal_{name}")
     T, B, k = z["x"].shape[0], int(z["block"]), int(z["k"])
