@@ -38,8 +38,7 @@ def kernel_model(wl, T, H, D, hidden, pairs, e):
     return {
         "sel_norms": dict(bytes=T * hidden * e + thd, flops=0),
         "attn_fwd": dict(bytes=4 * thd + th4, flops=4 * D * pairs),
-        "bwd_delta": dict(bytes=2 * thd + th4, flops=0),
-        "bwd_dq": dict(bytes=5 * thd + 2 * th4, flops=4 * D * pairs),
+        "bwd_dq": dict(bytes=6 * thd + 2 * th4, flops=4 * D * pairs),
         "bwd_dkdv": dict(bytes=6 * thd + 2 * th4, flops=4 * D * pairs),
     }
 

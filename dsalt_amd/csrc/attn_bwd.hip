@@ -3,19 +3,22 @@
 // Replaces _dsalt_bwd_preprocess and _dsalt_bwd_kernel
 // (dsalt/kernels/dsalt_triton_bwd.py:17-216), which accumulate dK/dV with
 // atomic_add.  Here every output element has exactly one writer:
-//   bwd_rowinfo  per sequence: min/max window start of each 16-row tile and
-//                the largest window (bounds of the key-parallel sweep).
-//   bwd_delta    delta = rowsum(O * dO) from the stored O (:44).
-//   bwd_dq       query-parallel, like the forward: dQ = scale * dS K over the
-//                band and the landmark slots (:148,:196).
-//   bwd_dkdv     key-parallel over the band: 16 keys per wave, query rows
-//                staged in LDS; dV = P^T dO, dK = scale * dS^T Q (:198-199).
-//   bwd_lmk      landmark slots x row chunks: partial dK/dV/d_bias of each
-//                (head, sequence, slot) over 1024 rows (:150-155).
+//   bwd_init     clears the per-sequence largest window.
+//   bwd_dq       query-parallel, like the forward (64 rows per block, one row
+//                per lane): delta = rowsum(O dO) from the stored O (:44),
+//                dQ = scale * dS K over the band and the landmark slots
+//                (:148,:196); also records each 16-row tile's window-start
+//                range and the sequence's largest window for the sweep below.
+//   bwd_dkdv     key-parallel over the band: 16 keys per wave, the query rows
+//                that can see them staged row-major in LDS (double-buffered);
+//                dV = P^T dO, dK = scale * dS^T Q (:198-199).
+//   bwd_lmk      landmark slots x 1024-row chunks: partial dK/dV/d_bias of each
+//                (head, sequence, slot) (:150-155).
 //   bwd_lmk_sum  sums the partials in chunk order and adds them into the dK/dV
 //                rows at the landmark positions.
 // P = exp(q.k * scale + bias - LSE) is recomputed in base 2 from the forward's
-// LSE; dS = P (dP - delta), dP = dO V^T.
+// LSE; dS = P (dP - delta), dP = dO V^T.  Products over tokens read their
+// transposed operand from the row-major tiles with ds_read_b64_tr_b16.
 #include "attn.h"
 #include "tiles.h"
 #include "timing.h"
@@ -26,23 +29,12 @@ constexpr float kLog2eB = 1.4426950408889634f;
 constexpr int kRowChunk = 1024;
 
 template <typename T, int D> struct BwdShape;
-template <> struct BwdShape<bf16, 64> { static constexpr int BN = 64, BQ = 32, NBUF = 2; };
-template <> struct BwdShape<bf16, 128> { static constexpr int BN = 32, BQ = 32, NBUF = 1; };
-template <> struct BwdShape<f16, 64> { static constexpr int BN = 64, BQ = 32, NBUF = 2; };
-template <> struct BwdShape<f16, 128> { static constexpr int BN = 32, BQ = 32, NBUF = 1; };
-template <> struct BwdShape<float, 64> { static constexpr int BN = 32, BQ = 16, NBUF = 2; };
-template <> struct BwdShape<float, 128> { static constexpr int BN = 16, BQ = 16, NBUF = 1; };
-
-__device__ __forceinline__ int seq_start_of(const AttnParams& p, int s) {
-    int st, len;
-    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
-    return st;
-}
-__device__ __forceinline__ int seq_len_of(const AttnParams& p, int s) {
-    int st, len;
-    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
-    return len;
-}
+template <> struct BwdShape<bf16, 64> { static constexpr int BN = 64, BQ = 64; };
+template <> struct BwdShape<bf16, 128> { static constexpr int BN = 32, BQ = 32; };
+template <> struct BwdShape<f16, 64> { static constexpr int BN = 64, BQ = 64; };
+template <> struct BwdShape<f16, 128> { static constexpr int BN = 32, BQ = 32; };
+template <> struct BwdShape<float, 64> { static constexpr int BN = 32, BQ = 32; };
+template <> struct BwdShape<float, 128> { static constexpr int BN = 16, BQ = 16; };
 
 __device__ __forceinline__ int lower_bound_i(const int* a, int n, int x) {
     int lo = 0, hi = n;
@@ -54,60 +46,22 @@ __device__ __forceinline__ int lower_bound_i(const int* a, int n, int x) {
     return lo;
 }
 
-// ------------------------------------------------------------------ prep
-__global__ __launch_bounds__(256) void bwd_rowinfo_kernel(AttnParams p) {
-    __shared__ int wm[256];
-    const int s = blockIdx.x, tid = threadIdx.x;
-    const int st = seq_start_of(p, s), len = seq_len_of(p, s);
-    const int nt16 = ceil_div(p.max_seqlen, 16);
-    int wmax = 1;
-    for (int t16 = tid; t16 < nt16; t16 += 256) {
-        int mn = 0x7fffffff, mx = -1;
-        for (int r = 0; r < 16; ++r) {
-            int i = t16 * 16 + r;
-            if (i >= len) {
-                mx = 0x7fffffff;  // padding rows: never "fully valid"
-                continue;
-            }
-            int wi = max(p.w[st + i], 1);
-            wmax = max(wmax, min(wi, len));
-            int lo = max(i - wi + 1, 0);
-            mn = min(mn, lo);
-            mx = max(mx, lo);
-        }
-        p.tile_minlo[((int64_t)s * nt16 + t16) * 2] = mn;
-        p.tile_minlo[((int64_t)s * nt16 + t16) * 2 + 1] = mx;
-    }
-    wm[tid] = wmax;
+// loads a landmark set into LDS; returns the number of valid (non -1) slots
+__device__ __forceinline__ int load_set(const AttnParams& p, int64_t set_off, int* lpos, int* nvalid_s, int tid) {
+    if (tid == 0) *nvalid_s = 0;
     __syncthreads();
-    for (int off = 128; off >= 1; off >>= 1) {
-        if (tid < off) wm[tid] = max(wm[tid], wm[tid + off]);
-        __syncthreads();
+    for (int i = tid; i < p.k_lmk; i += 256) {
+        int v = p.lmk[set_off + i];
+        lpos[i] = v;
+        if (v >= 0 && (i + 1 == p.k_lmk || p.lmk[set_off + i + 1] < 0)) *nvalid_s = i + 1;
     }
-    if (tid == 0) p.seq_wmax[s] = wm[0];
+    __syncthreads();
+    return *nvalid_s;
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void bwd_delta_kernel(AttnParams p) {
-    constexpr int VW = 16 / (int)sizeof(T);
-    constexpr int LPR = D / VW;  // lanes per row
-    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-    const int64_t nrows = (int64_t)p.total_len * p.n_heads;
-    const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR;
-    const int sub = threadIdx.x % LPR;
-    float acc = 0.f;
-    if (row < nrows) {
-        const int64_t t = row / p.n_heads;
-        const int h = (int)(row % p.n_heads);
-        u4 a = *(const u4*)((const T*)p.o + t * p.o_st + (int64_t)h * p.o_sh + sub * VW);
-        u4 b = *(const u4*)((const T*)p.dout + t * p.do_st + (int64_t)h * p.do_sh + sub * VW);
-        const T* ea = (const T*)&a;
-        const T* eb = (const T*)&b;
-#pragma unroll
-        for (int i = 0; i < VW; ++i) acc += to_float(ea[i]) * to_float(eb[i]);
-    }
-    for (int off = LPR >> 1; off >= 1; off >>= 1) acc += wave_xor(acc, off);
-    if (row < nrows && sub == 0) p.delta[row] = acc;
+__global__ void bwd_init_kernel(AttnParams p) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s < p.num_seqs) p.seq_wmax[s] = 1;
 }
 
 // -------------------------------------------------------------------- dQ
@@ -115,12 +69,11 @@ template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
     constexpr int BN = BwdShape<T, D>::BN;
     constexpr int NST = BN / 16;
+    constexpr bool kHalf = sizeof(T) == 2;
     typedef Tile<T, D, BN> KT;
-    __shared__ __attribute__((aligned(16))) T Ks[BN * KT::RS];
-    __shared__ __attribute__((aligned(16))) T Kt[D * KT::TS];
-    __shared__ __attribute__((aligned(16))) T Vs[BN * KT::RS];
+    __shared__ __attribute__((aligned(16))) T Ks[2][KT::ELEMS];
+    __shared__ __attribute__((aligned(16))) T Vs[2][KT::ELEMS];
     __shared__ int lpos[kMaxLandmarks];
-    __shared__ float lb[kMaxLandmarks + 64];
     __shared__ int red[4][3];
     __shared__ int nvalid_s;
 
@@ -130,8 +83,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
     const int t = L % p.n_tiles;
     const int s = (L / p.n_tiles) % p.num_seqs;
     const int h = L / (p.n_tiles * p.num_seqs);
-    const int st = seq_start_of(p, s);
-    const int len = seq_len_of(p, s);
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     const int r0 = t * 64;
     if (r0 >= len) return;
     const int kvh = h / (p.n_heads / p.n_kv_heads);
@@ -139,36 +92,35 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
     const int64_t set_off = (((int64_t)h * p.num_seqs + s) * p.n_sets) * K;
     const float c2 = p.scale * kLog2eB;
     const float inv_scale = 1.0f / p.scale;
-
-    if (tid == 0) nvalid_s = 0;
-    __syncthreads();
-    for (int i = tid; i < K; i += 256) {
-        int v = p.lmk[set_off + i];
-        lpos[i] = v;
-        if (v >= 0 && (i + 1 == K || p.lmk[set_off + i + 1] < 0)) nvalid_s = i + 1;
-    }
-    for (int i = tid; i < K + 64; i += 256) lb[i] = (i < K && p.lbias) ? p.lbias[set_off + i] * inv_scale : 0.f;
-    __syncthreads();
-    const int nvalid = nvalid_s;
+    const bool has_bias = p.lbias != nullptr;
+    const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid);
 
     const int i = r0 + wave * 16 + (lane & 15);
     const bool valid = i < len;
-    int lo = 0x7fffffff, hi = -1, cnt = 0;
-    float lse2 = 0.f, dlt = 0.f;
+    int lo = 0x7fffffff, hi = -1, cnt = 0, wcl = 1;
     if (valid) {
-        int wi = max(p.w[st + i], 1);
+        const int wi = max(p.w[st + i], 1);
+        wcl = min(wi, len);
         lo = max(i - wi + 1, 0);
         hi = i;
         cnt = lower_bound_i(lpos, nvalid, lo);
-        lse2 = p.lse[(int64_t)(st + i) * p.n_heads + h] * kLog2eB;
-        dlt = p.delta[(int64_t)(st + i) * p.n_heads + h];
     }
-    const int wlo = min16(lo), whi = max16(hi), wLmax = max16(lo), wHmin = min16(hi);
-    const int wcmax = max16(cnt), wcmin = min16(valid ? cnt : 0);
+    const int wlo = uniform(min16(lo)), whi = uniform(max16(hi));
+    const int wLmax = uniform(max16(lo)), wHmin = uniform(min16(hi));
+    const int wcmax = uniform(max16(cnt)), wcmin = uniform(min16(valid ? cnt : 0));
+    const int wwmax = uniform(max16(wcl));
     if (lane == 0) {
         red[wave][0] = wlo;
         red[wave][1] = whi;
         red[wave][2] = wcmax;
+        // per 16-row tile: range of window starts, for the key-parallel sweep
+        if (h == 0 && r0 + wave * 16 < len) {
+            const int nt16 = ceil_div(p.max_seqlen, 16);
+            const int64_t ti = (int64_t)s * nt16 + (r0 >> 4) + wave;
+            p.tile_minlo[ti * 2] = wlo;
+            p.tile_minlo[ti * 2 + 1] = wLmax;
+            atomicMax(p.seq_wmax + s, wwmax);
+        }
     }
     __syncthreads();
     int blo = red[0][0], bhi = red[0][1], bcm = red[0][2];
@@ -177,94 +129,131 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
         bhi = max(bhi, red[w2][1]);
         bcm = max(bcm, red[w2][2]);
     }
+    blo = uniform(blo);
+    bhi = uniform(bhi);
+    bcm = uniform(bcm);
     const int cs = (blo / BN) * BN;
     const int nband = (bhi - cs) / BN + 1;
     const int nchunks = nband + ceil_div(bcm, BN);
 
-    RowReg<T, D> qr, dor;
-    qr.load(valid ? (const T*)p.q + (int64_t)(st + i) * p.q_st + (int64_t)h * p.q_sh : nullptr, g);
-    dor.load(valid ? (const T*)p.dout + (int64_t)(st + i) * p.do_st + (int64_t)h * p.do_sh : nullptr, g);
+    const T* qhead = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
+    const T* dohead = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
+    const T* ohead = (const T*)p.o + (int64_t)st * p.o_st + (int64_t)h * p.o_sh;
+    RowReg<T, D> qr, dor, orr;
+    qr.load(valid ? qhead + (int64_t)i * p.q_st : nullptr, qhead, g);
+    dor.load(valid ? dohead + (int64_t)i * p.do_st : nullptr, dohead, g);
+    orr.load(valid ? ohead + (int64_t)i * p.o_st : nullptr, ohead, g);
+    // delta = rowsum(O * dO) over the stored (rounded) O
+    float dpart = 0.f;
+    if constexpr (kHalf) {
+#pragma unroll
+        for (int dc = 0; dc < D / 32; ++dc)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dpart += to_float(orr.x[dc][e]) * to_float(dor.x[dc][e]);
+    } else {
+#pragma unroll
+        for (int m = 0; m < D / 4; ++m) dpart += orr.x[m] * dor.x[m];
+    }
+    const float dlt = sum_g4(dpart);
+    float lse2 = 0.f;
+    if (valid) {
+        lse2 = p.lse[(int64_t)(st + i) * p.n_heads + h] * kLog2eB;
+        if (g == 0) p.delta[(int64_t)(st + i) * p.n_heads + h] = dlt;
+    }
 
     const T* kbase = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)kvh * p.k_sh;
     const T* vbase = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)kvh * p.v_sh;
     auto rowpos = [&](int c, int rr) -> int {
         if (c < nband) {
-            int j = cs + c * BN + rr;
+            const int j = cs + c * BN + rr;
             return j <= bhi ? j : -1;
         }
-        int sl = (c - nband) * BN + rr;
-        int pos = sl < bcm ? lpos[sl] : -1;
+        const int sl = (c - nband) * BN + rr;
+        const int pos = sl < bcm ? lpos[sl] : -1;
         return pos < len ? pos : -1;
     };
+    KT kt, vt;
+    auto load_chunk = [&](int c) {
+        kt.load(tid, [&](int rr) { int j = rowpos(c, rr); return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr; },
+                kbase);
+        vt.load(tid, [&](int rr) { int j = rowpos(c, rr); return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr; },
+                vbase);
+    };
+    load_chunk(0);
+    kt.store(Ks[0], tid);
+    vt.store(Vs[0], tid);
+    __syncthreads();
 
     floatx4 acc[D / 16];
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     const float NEG = -INFINITY;
-    KT kt, vt;
+    const int lane_off = 4 * g;
     for (int c = 0; c < nchunks; ++c) {
-        kt.load(tid, [&](int rr) {
-            int j = rowpos(c, rr);
-            return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr;
-        });
-        vt.load(tid, [&](int rr) {
-            int j = rowpos(c, rr);
-            return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr;
-        });
-        __syncthreads();
-        kt.store_rows(Ks, tid);
-        kt.store_cols(Kt, tid);
-        vt.store_rows(Vs, tid);
-        __syncthreads();
+        const int buf = c & 1;
+        if (c + 1 < nchunks) load_chunk(c + 1);
         const bool band = c < nband;
         const int base = band ? cs + c * BN : (c - nband) * BN;
-        floatx4 P[NST];
+        floatx4 dS[NST];
         bool act[NST];
 #pragma unroll
         for (int stt = 0; stt < NST; ++stt) {
             const int a = base + stt * 16;
             act[stt] = band ? (a <= whi && a + 15 >= wlo) : (a < wcmax);
             if (!act[stt]) {
-                P[stt] = floatx4{0.f, 0.f, 0.f, 0.f};
+                dS[stt] = floatx4{0.f, 0.f, 0.f, 0.f};
                 continue;
             }
             floatx4 ci;
             if (band) {
                 if (a >= wLmax && a + 15 <= wHmin) {
                     ci = floatx4{0.f, 0.f, 0.f, 0.f};
-                } else {
+                } else if (a + 15 <= wHmin) {
+                    const int tl = lo - a - lane_off;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        int j = a + 4 * g + r;
-                        ci[r] = (j >= lo && j <= hi) ? 0.f : NEG;
-                    }
+                    for (int r = 0; r < 4; ++r) ci[r] = r < tl ? NEG : 0.f;
+                } else {
+                    const int tl = lo - a - lane_off, th = hi - a - lane_off;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ci[r] = (r < tl || r > th) ? NEG : 0.f;
                 }
             } else {
-                const bool full = a + 15 < wcmin;
+                floatx4 bv = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (has_bias) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    int sl = a + 4 * g + r;
-                    ci[r] = (full || sl < cnt) ? lb[sl] : NEG;
+                    for (int r = 0; r < 4; ++r) {
+                        const int sl = a + lane_off + r;
+                        bv[r] = sl < K ? p.lbias[set_off + sl] * inv_scale : 0.f;
+                    }
+                }
+                if (a + 15 < wcmin) {
+                    ci = bv;
+                } else {
+                    const int tc = cnt - a - lane_off;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ci[r] = r < tc ? bv[r] : NEG;
                 }
             }
-            floatx4 sc = dot_rows<T, D>(Ks, KT::RS, stt * 16, lane, qr, ci);
-            floatx4 dp = dot_rows<T, D>(Vs, KT::RS, stt * 16, lane, dor, floatx4{0.f, 0.f, 0.f, 0.f});
+            const floatx4 sc = dot_rows<T, D>(Ks[buf], KT::RS, stt * 16, lane, qr, ci);
+            const floatx4 dp = dot_rows<T, D>(Vs[buf], KT::RS, stt * 16, lane, dor, floatx4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float pr = __builtin_amdgcn_exp2f(sc[r] * c2 - lse2);
-                P[stt][r] = pr * (dp[r] - dlt);  // dS (without scale)
-            }
+            for (int r = 0; r < 4; ++r) dS[stt][r] = __builtin_amdgcn_exp2f(sc[r] * c2 - lse2) * (dp[r] - dlt);
         }
-        if constexpr (sizeof(T) == 2) {
+        if constexpr (kHalf) {
 #pragma unroll
             for (int hp = 0; hp < NST / 2; ++hp)
                 if (act[2 * hp] || act[2 * hp + 1])
-                    acc_cols<T, D>(Kt, KT::TS, hp * 32, lane, P[2 * hp], P[2 * hp + 1], acc);
+                    acc_tr<T, D>(Ks[buf], KT::RS, hp * 32, lane, dS[2 * hp], dS[2 * hp + 1], acc);
         } else {
 #pragma unroll
             for (int stt = 0; stt < NST; ++stt)
-                if (act[stt]) acc_cols32<D>((const float*)Kt, KT::TS, stt * 16, lane, P[stt], acc);
+                if (act[stt]) acc_rm32<D>((const float*)Ks[buf], KT::RS, stt * 16, lane, dS[stt], acc);
         }
+        if (c + 1 < nchunks) {
+            kt.store(Ks[buf ^ 1], tid);
+            vt.store(Vs[buf ^ 1], tid);
+        }
+        __syncthreads();
     }
     if (valid) {
         T* drow = (T*)p.dq + (int64_t)(st + i) * p.n_heads * D + (int64_t)h * D;
@@ -273,37 +262,52 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
             T ov[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) ov[r] = from_float<T>(acc[dt][r] * p.scale);
-            if constexpr (sizeof(T) == 2) *(uint2*)(drow + dt * 16 + 4 * g) = *(const uint2*)ov;
-            else *(floatx4*)(drow + dt * 16 + 4 * g) = *(const floatx4*)ov;
+            if constexpr (kHalf) *(uint2*)(drow + dt * 16 + lane_off) = *(const uint2*)ov;
+            else *(floatx4*)(drow + dt * 16 + lane_off) = *(const floatx4*)ov;
         }
     }
 }
 
 // ----------------------------------------------------- query-row staging
-// Query rows i0..i0+BQ-1 of one (head, sequence): Q and dO row-major and
-// transposed, plus per-row LSE (base 2), delta, window start and landmark count.
+// Query rows i0..i0+BQ-1 of one (head, sequence): Q and dO row-major, plus
+// per-row LSE (base 2), delta, and a per-row key: the window start in the
+// dK/dV sweep (INT_MAX past the end), the visible landmark count in the
+// landmark sweep (0 past the end).
 template <typename T, int D, int BQ>
 struct QStage {
     typedef Tile<T, D, BQ> QT;
-    T qs[BQ * QT::RS];
-    T qt[D * QT::TS];
-    T ds[BQ * QT::RS];
-    T dt[D * QT::TS];
+    T q[QT::ELEMS];
+    T d[QT::ELEMS];
     float lse2[BQ];
     float dlt[BQ];
-    int lo[BQ];   // window start, INT_MAX for rows past the end
-    int cnt[BQ];  // visible landmark slots
+    int key[BQ];
+};
+
+template <typename T, int D, int BQ>
+struct QLoader {
+    typedef Tile<T, D, BQ> QT;
+    QT tq, tdo;
+    __device__ __forceinline__ void load(const AttnParams& p, const T* qb, const T* db, int i0, int iend, int tid) {
+        tq.load(tid, [&](int rr) { return i0 + rr < iend ? qb + (int64_t)(i0 + rr) * p.q_st : (const T*)nullptr; },
+                qb);
+        tdo.load(tid, [&](int rr) { return i0 + rr < iend ? db + (int64_t)(i0 + rr) * p.do_st : (const T*)nullptr; },
+                 db);
+    }
+    __device__ __forceinline__ void store(QStage<T, D, BQ>& q, int tid) const {
+        tq.store(q.q, tid);
+        tdo.store(q.d, tid);
+    }
 };
 
 // -------------------------------------------------------------- band dK/dV
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
     constexpr int BQ = BwdShape<T, D>::BQ;
-    constexpr int NB = BwdShape<T, D>::NBUF;
     constexpr int NQS = BQ / 16;
+    constexpr bool kHalf = sizeof(T) == 2;
     typedef QStage<T, D, BQ> QS;
     typedef typename QS::QT QT;
-    __shared__ __attribute__((aligned(16))) QS sq[NB];
+    __shared__ __attribute__((aligned(16))) QS sq[2];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
@@ -311,55 +315,50 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
     const int t = L % p.n_tiles;
     const int s = (L / p.n_tiles) % p.num_seqs;
     const int h = L / (p.n_tiles * p.num_seqs);
-    const int st = seq_start_of(p, s);
-    const int len = seq_len_of(p, s);
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     const int j0 = t * 64;
     if (j0 >= len) return;
     const int nt16 = ceil_div(p.max_seqlen, 16);
     const int* tinfo = p.tile_minlo + (int64_t)s * nt16 * 2;
     const float c2 = p.scale * kLog2eB;
 
-    const int wj0 = j0 + wave * 16;
+    const int wj0 = uniform(j0 + wave * 16);
     const int j = wj0 + (lane & 15);
     const bool jvalid = j < len;
+    const int jj = jvalid ? j : -1;  // never >= a window start when past the end
+    const T* khead = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)h * p.k_sh;
+    const T* vhead = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)h * p.v_sh;
     RowReg<T, D> kr, vr;
-    kr.load(jvalid ? (const T*)p.k + (int64_t)(st + j) * p.k_st + (int64_t)h * p.k_sh : nullptr, g);
-    vr.load(jvalid ? (const T*)p.v + (int64_t)(st + j) * p.v_st + (int64_t)h * p.v_sh : nullptr, g);
+    kr.load(jvalid ? khead + (int64_t)j * p.k_st : nullptr, khead, g);
+    vr.load(jvalid ? vhead + (int64_t)j * p.v_st : nullptr, vhead, g);
 
-    // rows that can see keys j0..j0+63: i in [j0, min(len, j0 + 63 + wmax))
-    const int iend = min(len, j0 + 63 + p.seq_wmax[s]);
+    // rows that can see keys j0..j0+63: i in [j0, min(len, j0 + 63 + largest window))
+    const int iend = uniform(min(len, j0 + 63 + p.seq_wmax[s]));
     const int nq = ceil_div(iend - j0, BQ);
     const T* qb = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
     const T* db = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
     auto chunk_needed = [&](int c) {
-        int i0 = j0 + c * BQ;
-        for (int q16 = 0; q16 < NQS; ++q16) {
-            int ti = i0 / 16 + q16;
-            if (i0 + q16 * 16 < iend && tinfo[ti * 2] <= j0 + 63) return true;
-        }
-        return false;
+        const int i0 = j0 + c * BQ;
+        bool need = false;
+#pragma unroll
+        for (int q16 = 0; q16 < NQS; ++q16)
+            need |= (i0 + q16 * 16 < iend) && tinfo[(i0 / 16 + q16) * 2] <= j0 + 63;
+        return need;
     };
-    QT tq, tdo;
-    auto load_chunk = [&](int c) {
-        int i0 = j0 + c * BQ;
-        tq.load(tid, [&](int rr) { return i0 + rr < iend ? qb + (int64_t)(i0 + rr) * p.q_st : (const T*)nullptr; });
-        tdo.load(tid, [&](int rr) { return i0 + rr < iend ? db + (int64_t)(i0 + rr) * p.do_st : (const T*)nullptr; });
-    };
+    QLoader<T, D, BQ> ld;
     auto store_chunk = [&](int c, QS& q) {
-        int i0 = j0 + c * BQ;
-        tq.store_rows(q.qs, tid);
-        tq.store_cols(q.qt, tid);
-        tdo.store_rows(q.ds, tid);
-        tdo.store_cols(q.dt, tid);
+        const int i0 = j0 + c * BQ;
+        ld.store(q, tid);
         if (tid < BQ) {
-            int i = i0 + tid;
+            const int i = i0 + tid;
             if (i < iend) {
-                int wi = max(p.w[st + i], 1);
-                q.lo[tid] = max(i - wi + 1, 0);
+                const int wi = max(p.w[st + i], 1);
+                q.key[tid] = max(i - wi + 1, 0);
                 q.lse2[tid] = p.lse[(int64_t)(st + i) * p.n_heads + h] * kLog2eB;
                 q.dlt[tid] = p.delta[(int64_t)(st + i) * p.n_heads + h];
             } else {
-                q.lo[tid] = 0x7fffffff;
+                q.key[tid] = 0x7fffffff;
                 q.lse2[tid] = 0.f;
                 q.dlt[tid] = 0.f;
             }
@@ -373,10 +372,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
         adv[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
     const float NEG = -INFINITY;
+    const int lane_off = 4 * g;
     int c = 0;
     while (c < nq && !chunk_needed(c)) ++c;
     if (c < nq) {
-        load_chunk(c);
+        ld.load(p, qb, db, j0 + c * BQ, iend, tid);
         store_chunk(c, sq[0]);
     }
     __syncthreads();
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
     while (c < nq) {
         int cn = c + 1;
         while (cn < nq && !chunk_needed(cn)) ++cn;
-        if (cn < nq) load_chunk(cn);
+        if (cn < nq) ld.load(p, qb, db, j0 + cn * BQ, iend, tid);
         QS& q = sq[buf];
         const int i0 = j0 + c * BQ;
         floatx4 P[NQS], dS[NQS];
@@ -392,61 +392,62 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
 #pragma unroll
         for (int qs = 0; qs < NQS; ++qs) {
             const int qa = i0 + qs * 16;
-            const int ti = qa / 16;
-            const int tmin = qa < iend ? tinfo[ti * 2] : 0x7fffffff;
-            const int tmax = qa < iend ? tinfo[ti * 2 + 1] : 0x7fffffff;
-            act[qs] = qa < iend && tmin <= wj0 + 15 && qa + 15 >= wj0 && wj0 < len;
+            const bool inr = qa < iend;
+            const int tmin = inr ? tinfo[(qa >> 4) * 2] : 0x7fffffff;
+            const int tmax = inr ? tinfo[(qa >> 4) * 2 + 1] : 0x7fffffff;
+            act[qs] = inr && tmin <= wj0 + 15 && qa + 15 >= wj0 && wj0 < len;
             if (!act[qs]) {
                 P[qs] = floatx4{0.f, 0.f, 0.f, 0.f};
                 dS[qs] = P[qs];
                 continue;
             }
             floatx4 ci;
-            const bool full = tmax <= wj0 && qa >= wj0 + 15 && qa + 15 < iend && wj0 + 15 < len;
-            if (full) {
+            if (tmax <= wj0 && qa >= wj0 + 15 && qa + 15 < iend && wj0 + 15 < len) {
                 ci = floatx4{0.f, 0.f, 0.f, 0.f};
             } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    int rr = qs * 16 + 4 * g + r;
-                    int i = i0 + rr;
-                    ci[r] = (jvalid && j >= q.lo[rr] && j <= i) ? 0.f : NEG;
+                const int4 lo4 = *(const int4*)(q.key + qs * 16 + lane_off);
+                if (qa >= wj0 + 15) {  // every row at or after every key of the wave
+                    ci[0] = jj >= lo4.x ? 0.f : NEG;
+                    ci[1] = jj >= lo4.y ? 0.f : NEG;
+                    ci[2] = jj >= lo4.z ? 0.f : NEG;
+                    ci[3] = jj >= lo4.w ? 0.f : NEG;
+                } else {
+                    const int qd = qa + lane_off - jj;  // row index minus key index, r = 0
+                    ci[0] = (jj >= lo4.x && qd >= 0) ? 0.f : NEG;
+                    ci[1] = (jj >= lo4.y && qd + 1 >= 0) ? 0.f : NEG;
+                    ci[2] = (jj >= lo4.z && qd + 2 >= 0) ? 0.f : NEG;
+                    ci[3] = (jj >= lo4.w && qd + 3 >= 0) ? 0.f : NEG;
                 }
             }
-            floatx4 sc = dot_rows<T, D>(q.qs, QT::RS, qs * 16, lane, kr, ci);
-            floatx4 dp = dot_rows<T, D>(q.ds, QT::RS, qs * 16, lane, vr, floatx4{0.f, 0.f, 0.f, 0.f});
+            const floatx4 sc = dot_rows<T, D>(q.q, QT::RS, qs * 16, lane, kr, ci);
+            const floatx4 dp = dot_rows<T, D>(q.d, QT::RS, qs * 16, lane, vr, floatx4{0.f, 0.f, 0.f, 0.f});
+            const floatx4 l4 = *(const floatx4*)(q.lse2 + qs * 16 + lane_off);
+            const floatx4 d4 = *(const floatx4*)(q.dlt + qs * 16 + lane_off);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                int rr = qs * 16 + 4 * g + r;
-                float pr = __builtin_amdgcn_exp2f(sc[r] * c2 - q.lse2[rr]);
+                const float pr = __builtin_amdgcn_exp2f(sc[r] * c2 - l4[r]);
                 P[qs][r] = pr;
-                dS[qs][r] = pr * (dp[r] - q.dlt[rr]);
+                dS[qs][r] = pr * (dp[r] - d4[r]);
             }
         }
-        if constexpr (sizeof(T) == 2) {
+        if constexpr (kHalf) {
 #pragma unroll
             for (int hp = 0; hp < NQS / 2; ++hp)
                 if (act[2 * hp] || act[2 * hp + 1]) {
-                    acc_cols<T, D>(q.dt, QT::TS, hp * 32, lane, P[2 * hp], P[2 * hp + 1], adv);
-                    acc_cols<T, D>(q.qt, QT::TS, hp * 32, lane, dS[2 * hp], dS[2 * hp + 1], adk);
+                    acc_tr<T, D>(q.d, QT::RS, hp * 32, lane, P[2 * hp], P[2 * hp + 1], adv);
+                    acc_tr<T, D>(q.q, QT::RS, hp * 32, lane, dS[2 * hp], dS[2 * hp + 1], adk);
                 }
         } else {
 #pragma unroll
             for (int qs = 0; qs < NQS; ++qs)
                 if (act[qs]) {
-                    acc_cols32<D>((const float*)q.dt, QT::TS, qs * 16, lane, P[qs], adv);
-                    acc_cols32<D>((const float*)q.qt, QT::TS, qs * 16, lane, dS[qs], adk);
+                    acc_rm32<D>((const float*)q.d, QT::RS, qs * 16, lane, P[qs], adv);
+                    acc_rm32<D>((const float*)q.q, QT::RS, qs * 16, lane, dS[qs], adk);
                 }
         }
-        if constexpr (NB == 2) {
-            if (cn < nq) store_chunk(cn, sq[buf ^ 1]);
-            __syncthreads();
-            buf ^= 1;
-        } else {
-            __syncthreads();
-            if (cn < nq) store_chunk(cn, sq[0]);
-            __syncthreads();
-        }
+        if (cn < nq) store_chunk(cn, sq[buf ^ 1]);
+        __syncthreads();
+        buf ^= 1;
         c = cn;
     }
     if (jvalid) {
@@ -460,12 +461,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
                 ok[r] = from_float<T>(adk[dt][r] * p.scale);
                 ov[r] = from_float<T>(adv[dt][r]);
             }
-            if constexpr (sizeof(T) == 2) {
-                *(uint2*)(kd + dt * 16 + 4 * g) = *(const uint2*)ok;
-                *(uint2*)(vd + dt * 16 + 4 * g) = *(const uint2*)ov;
+            if constexpr (kHalf) {
+                *(uint2*)(kd + dt * 16 + lane_off) = *(const uint2*)ok;
+                *(uint2*)(vd + dt * 16 + lane_off) = *(const uint2*)ov;
             } else {
-                *(floatx4*)(kd + dt * 16 + 4 * g) = *(const floatx4*)ok;
-                *(floatx4*)(vd + dt * 16 + 4 * g) = *(const floatx4*)ov;
+                *(floatx4*)(kd + dt * 16 + lane_off) = *(const floatx4*)ok;
+                *(floatx4*)(vd + dt * 16 + lane_off) = *(const floatx4*)ov;
             }
         }
     }
@@ -478,12 +479,12 @@ template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     constexpr int BQ = BwdShape<T, D>::BQ;
     constexpr int NQS = BQ / 16;
+    constexpr bool kHalf = sizeof(T) == 2;
     typedef QStage<T, D, BQ> QS;
     typedef typename QS::QT QT;
     __shared__ __attribute__((aligned(16))) QS q;
     __shared__ int lpos[kMaxLandmarks];
-    __shared__ float lb[kMaxLandmarks + 64];
-    __shared__ int cmin_s[BQ / 16], cmax_s[BQ / 16];
+    __shared__ int cmin_s[NQS], cmax_s[NQS];
     __shared__ int nvalid_s;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
@@ -496,38 +497,29 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     b /= p.n_chunks;
     const int s = b % p.num_seqs;
     const int h = b / p.num_seqs;
-    const int st = seq_start_of(p, s);
-    const int len = seq_len_of(p, s);
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     const int kvh = h / (p.n_heads / p.n_kv_heads);
     const int64_t set_off = (((int64_t)h * p.num_seqs + s) * p.n_sets) * K;
     const float c2 = p.scale * kLog2eB;
     const float inv_scale = 1.0f / p.scale;
     const int rbeg = chunk * kRowChunk, rend = min(len, rbeg + kRowChunk);
-
-    if (tid == 0) nvalid_s = 0;
-    __syncthreads();
-    for (int i = tid; i < K; i += 256) {
-        int v = p.lmk[set_off + i];
-        lpos[i] = v;
-        if (v >= 0 && (i + 1 == K || p.lmk[set_off + i + 1] < 0)) nvalid_s = i + 1;
-    }
-    for (int i = tid; i < K + 64; i += 256) lb[i] = (i < K && p.lbias) ? p.lbias[set_off + i] * inv_scale : 0.f;
-    __syncthreads();
-    const int nvalid = nvalid_s;
+    const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid);
 
     // slots of this lane (two subtiles)
-    const int sl0 = grp * 128 + wave * 32;
+    const int sl0 = uniform(grp * 128 + wave * 32);
     RowReg<T, D> kr[2], vr[2];
     int slot[2];
-    bool sval[2];
+    float bsl[2];
     const T* kbase = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)kvh * p.k_sh;
     const T* vbase = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)kvh * p.v_sh;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         slot[u] = sl0 + u * 16 + (lane & 15);
-        sval[u] = slot[u] < nvalid && lpos[slot[u]] < len;
-        kr[u].load(sval[u] ? kbase + (int64_t)lpos[slot[u]] * p.k_st : nullptr, g);
-        vr[u].load(sval[u] ? vbase + (int64_t)lpos[slot[u]] * p.v_st : nullptr, g);
+        const bool sval = slot[u] < nvalid && lpos[slot[u]] < len;
+        kr[u].load(sval ? kbase + (int64_t)lpos[slot[u]] * p.k_st : nullptr, kbase, g);
+        vr[u].load(sval ? vbase + (int64_t)lpos[slot[u]] * p.v_st : nullptr, vbase, g);
+        bsl[u] = (p.lbias && slot[u] < K) ? p.lbias[set_off + slot[u]] * inv_scale : 0.f;
     }
     floatx4 adk[2][D / 16], adv[2][D / 16];
     float dbias[2] = {0.f, 0.f};
@@ -541,30 +533,27 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     const T* qb = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
     const T* db = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
     const float NEG = -INFINITY;
+    const int lane_off = 4 * g;
     // first row with any visible landmark: lo_i > lpos[0]  =>  i > lpos[0]
     const int first_row = nvalid > 0 ? lpos[0] + 1 : 0x7fffffff;
     const int istart = max(rbeg, (first_row / BQ) * BQ);
-    QT tq, tdo;
     // the loop bound is uniform over the block (every wave reaches each barrier);
     // waves whose slots are all empty skip their products through act[] below
     const bool any_slot = grp * 128 < nvalid;
+    QLoader<T, D, BQ> ld;
     for (int i0 = istart; any_slot && i0 < rend; i0 += BQ) {
-        tq.load(tid, [&](int rr) { return i0 + rr < rend ? qb + (int64_t)(i0 + rr) * p.q_st : (const T*)nullptr; });
-        tdo.load(tid, [&](int rr) { return i0 + rr < rend ? db + (int64_t)(i0 + rr) * p.do_st : (const T*)nullptr; });
+        ld.load(p, qb, db, i0, rend, tid);
         __syncthreads();
-        tq.store_rows(q.qs, tid);
-        tq.store_cols(q.qt, tid);
-        tdo.store_rows(q.ds, tid);
-        tdo.store_cols(q.dt, tid);
+        ld.store(q, tid);
         if (tid < BQ) {
-            int i = i0 + tid;
+            const int i = i0 + tid;
             if (i < rend) {
-                int wi = max(p.w[st + i], 1);
-                q.cnt[tid] = lower_bound_i(lpos, nvalid, max(i - wi + 1, 0));
+                const int wi = max(p.w[st + i], 1);
+                q.key[tid] = lower_bound_i(lpos, nvalid, max(i - wi + 1, 0));
                 q.lse2[tid] = p.lse[(int64_t)(st + i) * p.n_heads + h] * kLog2eB;
                 q.dlt[tid] = p.delta[(int64_t)(st + i) * p.n_heads + h];
             } else {
-                q.cnt[tid] = 0;
+                q.key[tid] = 0;
                 q.lse2[tid] = 0.f;
                 q.dlt[tid] = 0.f;
             }
@@ -573,8 +562,8 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
         if (tid < NQS) {
             int mn = 0x7fffffff, mx = 0;
             for (int r = 0; r < 16; ++r) {
-                mn = min(mn, q.cnt[tid * 16 + r]);
-                mx = max(mx, q.cnt[tid * 16 + r]);
+                mn = min(mn, q.key[tid * 16 + r]);
+                mx = max(mx, q.key[tid * 16 + r]);
             }
             cmin_s[tid] = mn;
             cmax_s[tid] = mx;
@@ -587,44 +576,48 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
             bool act[NQS];
 #pragma unroll
             for (int qs = 0; qs < NQS; ++qs) {
-                act[qs] = cmax_s[qs] > a;
+                act[qs] = uniform(cmax_s[qs]) > a;
                 if (!act[qs]) {
                     P[qs] = floatx4{0.f, 0.f, 0.f, 0.f};
                     dS[qs] = P[qs];
                     continue;
                 }
                 floatx4 ci;
-                const bool full = cmin_s[qs] > a + 15;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    int rr = qs * 16 + 4 * g + r;
-                    ci[r] = (full || slot[u] < q.cnt[rr]) ? lb[slot[u]] : NEG;
+                if (uniform(cmin_s[qs]) > a + 15) {
+                    ci = floatx4{bsl[u], bsl[u], bsl[u], bsl[u]};
+                } else {
+                    const int4 c4 = *(const int4*)(q.key + qs * 16 + lane_off);
+                    ci[0] = slot[u] < c4.x ? bsl[u] : NEG;
+                    ci[1] = slot[u] < c4.y ? bsl[u] : NEG;
+                    ci[2] = slot[u] < c4.z ? bsl[u] : NEG;
+                    ci[3] = slot[u] < c4.w ? bsl[u] : NEG;
                 }
-                floatx4 sc = dot_rows<T, D>(q.qs, QT::RS, qs * 16, lane, kr[u], ci);
-                floatx4 dp = dot_rows<T, D>(q.ds, QT::RS, qs * 16, lane, vr[u], floatx4{0.f, 0.f, 0.f, 0.f});
+                const floatx4 sc = dot_rows<T, D>(q.q, QT::RS, qs * 16, lane, kr[u], ci);
+                const floatx4 dp = dot_rows<T, D>(q.d, QT::RS, qs * 16, lane, vr[u], floatx4{0.f, 0.f, 0.f, 0.f});
+                const floatx4 l4 = *(const floatx4*)(q.lse2 + qs * 16 + lane_off);
+                const floatx4 d4 = *(const floatx4*)(q.dlt + qs * 16 + lane_off);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    int rr = qs * 16 + 4 * g + r;
-                    float pr = __builtin_amdgcn_exp2f(sc[r] * c2 - q.lse2[rr]);
-                    float d = pr * (dp[r] - q.dlt[rr]);
+                    const float pr = __builtin_amdgcn_exp2f(sc[r] * c2 - l4[r]);
+                    const float dd = pr * (dp[r] - d4[r]);
                     P[qs][r] = pr;
-                    dS[qs][r] = d;
-                    dbias[u] += d;
+                    dS[qs][r] = dd;
+                    dbias[u] += dd;
                 }
             }
-            if constexpr (sizeof(T) == 2) {
+            if constexpr (kHalf) {
 #pragma unroll
                 for (int hp = 0; hp < NQS / 2; ++hp)
                     if (act[2 * hp] || act[2 * hp + 1]) {
-                        acc_cols<T, D>(q.dt, QT::TS, hp * 32, lane, P[2 * hp], P[2 * hp + 1], adv[u]);
-                        acc_cols<T, D>(q.qt, QT::TS, hp * 32, lane, dS[2 * hp], dS[2 * hp + 1], adk[u]);
+                        acc_tr<T, D>(q.d, QT::RS, hp * 32, lane, P[2 * hp], P[2 * hp + 1], adv[u]);
+                        acc_tr<T, D>(q.q, QT::RS, hp * 32, lane, dS[2 * hp], dS[2 * hp + 1], adk[u]);
                     }
             } else {
 #pragma unroll
                 for (int qs = 0; qs < NQS; ++qs)
                     if (act[qs]) {
-                        acc_cols32<D>((const float*)q.dt, QT::TS, qs * 16, lane, P[qs], adv[u]);
-                        acc_cols32<D>((const float*)q.qt, QT::TS, qs * 16, lane, dS[qs], adk[u]);
+                        acc_rm32<D>((const float*)q.d, QT::RS, qs * 16, lane, P[qs], adv[u]);
+                        acc_rm32<D>((const float*)q.q, QT::RS, qs * 16, lane, dS[qs], adk[u]);
                     }
             }
         }
@@ -632,15 +625,15 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     // partials: [chunk][h][s][slot][D]
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-        float db2 = sum_g4(dbias[u]);
+        const float db2 = sum_g4(dbias[u]);
         if (slot[u] >= K) continue;
         const int64_t row = (((int64_t)chunk * p.n_heads + h) * p.num_seqs + s) * K + slot[u];
         float* pk = p.part_k + row * D;
         float* pv = p.part_v + row * D;
 #pragma unroll
         for (int dt = 0; dt < D / 16; ++dt) {
-            *(floatx4*)(pk + dt * 16 + 4 * g) = adk[u][dt] * p.scale;
-            *(floatx4*)(pv + dt * 16 + 4 * g) = adv[u][dt];
+            *(floatx4*)(pk + dt * 16 + lane_off) = adk[u][dt] * p.scale;
+            *(floatx4*)(pv + dt * 16 + lane_off) = adv[u][dt];
         }
         if (g == 0) p.part_b[row] = db2;
     }
@@ -658,7 +651,8 @@ __global__ __launch_bounds__(256) void bwd_lmk_sum_kernel(AttnParams p) {
     const int s = (int)((row / K) % p.num_seqs);
     const int h = (int)(row / ((int64_t)K * p.num_seqs));
     const int pos = p.lmk[(((int64_t)h * p.num_seqs + s) * p.n_sets) * K + sl];
-    const int len = seq_len_of(p, s);
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     float sk = 0.f, sv = 0.f, sb = 0.f;
     for (int ch = 0; ch < p.n_chunks; ++ch) {
         const int64_t pr = ((int64_t)ch * p.n_heads + h) * p.num_seqs * K + (int64_t)s * K + sl;
@@ -668,7 +662,7 @@ __global__ __launch_bounds__(256) void bwd_lmk_sum_kernel(AttnParams p) {
     }
     if (d == 0 && p.d_bias) p.d_bias[(((int64_t)h * p.num_seqs + s) * p.n_sets) * K + sl] = sb;
     if (pos < 0 || pos >= len) return;
-    const int64_t o = (int64_t)(seq_start_of(p, s) + pos) * p.n_heads * D + (int64_t)h * D + d;
+    const int64_t o = (int64_t)(st + pos) * p.n_heads * D + (int64_t)h * D + d;
     T* dk = (T*)p.dk;
     T* dv = (T*)p.dv;
     dk[o] = from_float<T>(to_float(dk[o]) + sk);
@@ -692,19 +686,16 @@ size_t bwd_workspace(const AttnParams& p) {
 template <typename T, int D>
 static void bwd_run(const AttnParams& p, hipStream_t stream) {
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
-    DSALT_LAUNCH("bwd_rowinfo", bwd_rowinfo_kernel, dim3(p.num_seqs), dim3(256), 0, stream, p);
-    constexpr int LPR = D / (16 / (int)sizeof(T));
-    const int64_t nrows = (int64_t)p.total_len * p.n_heads;
-    DSALT_LAUNCH("bwd_delta", (bwd_delta_kernel<T, D>), dim3((unsigned)((nrows * LPR + 255) / 256)), dim3(256), 0, stream,
-                       p);
+    DSALT_LAUNCH("bwd_init", bwd_init_kernel, dim3(ceil_div(p.num_seqs, 256)), dim3(256), 0, stream, p);
     DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D>), dim3(total), dim3(256), 0, stream, p);
     DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D>), dim3(total), dim3(256), 0, stream, p);
     if (p.k_lmk > 0) {
         const int ngrp = ceil_div(p.k_lmk, 128);
-        DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D>), dim3(p.n_heads * p.num_seqs * p.n_chunks * ngrp), dim3(256), 0,
-                           stream, p);
+        DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D>), dim3(p.n_heads * p.num_seqs * p.n_chunks * ngrp), dim3(256),
+                     0, stream, p);
         const int64_t n = (int64_t)p.n_heads * p.num_seqs * p.k_lmk * D;
-        DSALT_LAUNCH("bwd_lmk_sum", (bwd_lmk_sum_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p);
+        DSALT_LAUNCH("bwd_lmk_sum", (bwd_lmk_sum_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     stream, p);
     }
 }
 

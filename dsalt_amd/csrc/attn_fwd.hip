@@ -4,15 +4,17 @@
 // One 256-thread block (4 waves) owns 64 query rows of one (head, sequence);
 // wave w owns rows 16w..16w+15 and each lane one query row (column of the
 // transposed score tile S^T = K Q^T).  The block walks the union of its rows'
-// windows [min_i lo_i, max_i i] in BN-key chunks staged in LDS (K row-major,
-// V transposed, double-buffered), then the landmark slots of its set in the
-// same buffers.  Masks are folded into the MFMA accumulator initialisation
-// (0 or -inf, or bias/scale for landmarks); 16-key subtiles outside a wave's
-// own range are skipped.  Landmarks arrive sorted, so the landmarks visible to
-// row i are exactly the first cnt_i = #{p < i - w_i + 1} slots -- a landmark
-// inside the window is never counted twice.  Online softmax in base 2 with a
-// lazy rescale (the running max only moves when a row max grows by more than
-// 2^8), P rounded to the input dtype before P V as in the reference (:115,:147).
+// windows [min_i lo_i, max_i i] in BN-key chunks staged row-major in LDS
+// (double-buffered), then the landmark slots of its set through the same
+// buffers.  Masks are folded into the MFMA accumulator initialisation (0 or
+// -inf, bias/scale for landmarks); 16-key subtiles outside a wave's own range
+// are skipped with scalar branches.  Landmarks arrive sorted, so the landmarks
+// visible to row i are exactly the first cnt_i = #{p < i - w_i + 1} slots -- a
+// landmark inside the window is never counted twice.  Online softmax in base 2
+// with a lazy rescale (the running max moves only when a row max grows by more
+// than 2^8); P is rounded to the input dtype before P V as in the reference
+// (:115,:147), V^T comes from the row-major tile through the transpose read,
+// and the row sums come from the same packed P through a ones operand.
 #include "attn.h"
 #include "tiles.h"
 #include "timing.h"
@@ -30,14 +32,6 @@ template <> struct FwdShape<f16, 128> { static constexpr int BN = 32; };
 template <> struct FwdShape<float, 64> { static constexpr int BN = 32; };
 template <> struct FwdShape<float, 128> { static constexpr int BN = 16; };
 
-// Per-lane row bounds shared by the forward and dq kernels.
-struct RowInfo {
-    int i;       // sequence-relative row
-    bool valid;  // i < len
-    int lo, hi;  // window [lo, hi], or lo = INT_MAX, hi = -1 for padding rows
-    int cnt;     // visible landmark slots
-};
-
 __device__ __forceinline__ int lower_bound_lds(const int* a, int n, int x) {
     int lo = 0, hi = n;
     while (lo < hi) {
@@ -52,11 +46,11 @@ template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     constexpr int BN = FwdShape<T, D>::BN;
     constexpr int NST = BN / 16;
+    constexpr bool kHalf = sizeof(T) == 2;
     typedef Tile<T, D, BN> KT;
-    __shared__ __attribute__((aligned(16))) T Ks[2][BN * KT::RS];
-    __shared__ __attribute__((aligned(16))) T Vt[2][D * KT::TS];
+    __shared__ __attribute__((aligned(16))) T Ks[2][KT::ELEMS];
+    __shared__ __attribute__((aligned(16))) T Vs[2][KT::ELEMS];
     __shared__ int lpos[kMaxLandmarks];
-    __shared__ float lb[kMaxLandmarks + 64];
     __shared__ int red[4][3];
     __shared__ int nvalid_s;
 
@@ -76,6 +70,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     const int64_t set_off = (((int64_t)h * p.num_seqs + s) * p.n_sets + set) * K;
     const float c2 = p.scale * kLog2e;
     const float inv_scale = 1.0f / p.scale;
+    const bool has_bias = p.lbias != nullptr;
 
     if (tid == 0) nvalid_s = 0;
     __syncthreads();
@@ -84,27 +79,23 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
         lpos[i] = v;
         if (v >= 0 && (i + 1 == K || p.lmk[set_off + i + 1] < 0)) nvalid_s = i + 1;
     }
-    for (int i = tid; i < K + 64; i += 256) lb[i] = (i < K && p.lbias) ? p.lbias[set_off + i] * inv_scale : 0.f;
     __syncthreads();
     const int nvalid = nvalid_s;
 
-    // rows of this lane
-    RowInfo ri;
-    ri.i = r0 + wave * 16 + (lane & 15);
-    ri.valid = ri.i < len;
-    if (ri.valid) {
-        int wi = max(p.w[st + ri.i], 1);
-        ri.lo = max(ri.i - wi + 1, 0);
-        ri.hi = ri.i;
-        ri.cnt = lower_bound_lds(lpos, nvalid, ri.lo);
-    } else {
-        ri.lo = 0x7fffffff;
-        ri.hi = -1;
-        ri.cnt = 0;
+    // the row of this lane: window [lo, hi] and visible landmark count
+    const int i = r0 + wave * 16 + (lane & 15);
+    const bool valid = i < len;
+    int lo = 0x7fffffff, hi = -1, cnt = 0;
+    if (valid) {
+        const int wi = max(p.w[st + i], 1);
+        lo = max(i - wi + 1, 0);
+        hi = i;
+        cnt = lower_bound_lds(lpos, nvalid, lo);
     }
-    const int wlo = min16(ri.lo), whi = max16(ri.hi);
-    const int wLmax = max16(ri.lo), wHmin = min16(ri.hi);
-    const int wcmax = max16(ri.cnt), wcmin = min16(ri.valid ? ri.cnt : 0);
+    // wave-uniform bounds (scalar registers: the subtile branches below are scalar)
+    const int wlo = uniform(min16(lo)), whi = uniform(max16(hi));
+    const int wLmax = uniform(max16(lo)), wHmin = uniform(min16(hi));
+    const int wcmax = uniform(max16(cnt)), wcmin = uniform(min16(valid ? cnt : 0));
     if (lane == 0) {
         red[wave][0] = wlo;
         red[wave][1] = whi;
@@ -117,54 +108,53 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
         bhi = max(bhi, red[w2][1]);
         bcm = max(bcm, red[w2][2]);
     }
+    blo = uniform(blo);
+    bhi = uniform(bhi);
+    bcm = uniform(bcm);
     const int cs = (blo / BN) * BN;
     const int nband = (bhi - cs) / BN + 1;
     const int nchunks = nband + ceil_div(bcm, BN);
 
+    const T* qhead = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
     RowReg<T, D> qr;
-    qr.load(ri.valid ? (const T*)p.q + (int64_t)(st + ri.i) * p.q_st + (int64_t)h * p.q_sh : nullptr, g);
+    qr.load(valid ? qhead + (int64_t)i * p.q_st : nullptr, qhead, g);
 
     const T* kbase = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)kvh * p.k_sh;
     const T* vbase = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)kvh * p.v_sh;
-    auto krow = [&](int c, int rr) -> const T* {
+    auto rowpos = [&](int c, int rr) -> int {
         if (c < nband) {
-            int j = cs + c * BN + rr;
-            return j <= bhi ? kbase + (int64_t)j * p.k_st : nullptr;
+            const int j = cs + c * BN + rr;
+            return j <= bhi ? j : -1;
         }
-        int sl = (c - nband) * BN + rr;
-        int pos = sl < bcm ? lpos[sl] : -1;
-        return (pos >= 0 && pos < len) ? kbase + (int64_t)pos * p.k_st : nullptr;
+        const int sl = (c - nband) * BN + rr;
+        const int pos = sl < bcm ? lpos[sl] : -1;
+        return pos < len ? pos : -1;
     };
-    auto vrow = [&](int c, int rr) -> const T* {
-        if (c < nband) {
-            int j = cs + c * BN + rr;
-            return j <= bhi ? vbase + (int64_t)j * p.v_st : nullptr;
-        }
-        int sl = (c - nband) * BN + rr;
-        int pos = sl < bcm ? lpos[sl] : -1;
-        return (pos >= 0 && pos < len) ? vbase + (int64_t)pos * p.v_st : nullptr;
-    };
-
     KT kt, vt;
-    kt.load(tid, [&](int rr) { return krow(0, rr); });
-    vt.load(tid, [&](int rr) { return vrow(0, rr); });
-    kt.store_rows(Ks[0], tid);
-    vt.store_cols(Vt[0], tid);
+    auto load_chunk = [&](int c) {
+        kt.load(tid, [&](int rr) { int j = rowpos(c, rr); return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr; },
+                kbase);
+        vt.load(tid, [&](int rr) { int j = rowpos(c, rr); return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr; },
+                vbase);
+    };
+    load_chunk(0);
+    kt.store(Ks[0], tid);
+    vt.store(Vs[0], tid);
     __syncthreads();
 
     floatx4 acc[D / 16];
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.f;
+    floatx4 lacc = floatx4{0.f, 0.f, 0.f, 0.f};  // row sums (16-bit path: ones x P)
+    float l_run = 0.f;                             // row sums (fp32 path)
+    float m_run = -INFINITY;
     const float thr = 8.0f / c2;
     const float NEG = -INFINITY;
+    const int lane_off = 4 * g;
 
     for (int c = 0; c < nchunks; ++c) {
         const int buf = c & 1;
-        if (c + 1 < nchunks) {
-            kt.load(tid, [&](int rr) { return krow(c + 1, rr); });
-            vt.load(tid, [&](int rr) { return vrow(c + 1, rr); });
-        }
+        if (c + 1 < nchunks) load_chunk(c + 1);
         const bool band = c < nband;
         const int base = band ? cs + c * BN : (c - nband) * BN;
         floatx4 S[NST];
@@ -181,19 +171,30 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
             if (band) {
                 if (a >= wLmax && a + 15 <= wHmin) {
                     ci = floatx4{0.f, 0.f, 0.f, 0.f};
-                } else {
+                } else if (a + 15 <= wHmin) {  // below every row's diagonal: lower bound only
+                    const int tl = lo - a - lane_off;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        int j = a + 4 * g + r;
-                        ci[r] = (j >= ri.lo && j <= ri.hi) ? 0.f : NEG;
-                    }
+                    for (int r = 0; r < 4; ++r) ci[r] = r < tl ? NEG : 0.f;
+                } else {
+                    const int tl = lo - a - lane_off, th = hi - a - lane_off;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ci[r] = (r < tl || r > th) ? NEG : 0.f;
                 }
             } else {
-                const bool full = a + 15 < wcmin;
+                floatx4 bv = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (has_bias) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    int sl = a + 4 * g + r;
-                    ci[r] = (full || sl < ri.cnt) ? lb[sl] : NEG;
+                    for (int r = 0; r < 4; ++r) {
+                        const int sl = a + lane_off + r;
+                        bv[r] = sl < K ? p.lbias[set_off + sl] * inv_scale : 0.f;
+                    }
+                }
+                if (a + 15 < wcmin) {
+                    ci = bv;
+                } else {
+                    const int tc = cnt - a - lane_off;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ci[r] = r < tc ? bv[r] : NEG;
                 }
             }
             S[stt] = dot_rows<T, D>(Ks[buf], KT::RS, stt * 16, lane, qr, ci);
@@ -210,6 +211,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
             const float alpha = m_run == NEG ? 0.f : __builtin_amdgcn_exp2f((m_run - mnew) * c2);
 #pragma unroll
             for (int dt = 0; dt < D / 16; ++dt) acc[dt] *= alpha;
+            lacc *= alpha;
             l_run *= alpha;
             m_run = mnew;
         }
@@ -217,44 +219,43 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
 #pragma unroll
         for (int stt = 0; stt < NST; ++stt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float e = __builtin_amdgcn_exp2f(S[stt][r] * c2 - msc);
-                S[stt][r] = e;
-                l_run += e;
-            }
-        if constexpr (sizeof(T) == 2) {
+            for (int r = 0; r < 4; ++r) S[stt][r] = __builtin_amdgcn_exp2f(S[stt][r] * c2 - msc);
+        if constexpr (kHalf) {
+            const typename Vec8<T>::type ones = ones8<T>();
 #pragma unroll
             for (int hp = 0; hp < NST / 2; ++hp)
-                if (act[2 * hp] || act[2 * hp + 1])
-                    acc_cols<T, D>(Vt[buf], KT::TS, hp * 32, lane, S[2 * hp], S[2 * hp + 1], acc);
+                if (act[2 * hp] || act[2 * hp + 1]) {
+                    auto b = acc_tr<T, D>(Vs[buf], KT::RS, hp * 32, lane, S[2 * hp], S[2 * hp + 1], acc);
+                    lacc = mma(ones, b, lacc);
+                }
         } else {
 #pragma unroll
             for (int stt = 0; stt < NST; ++stt)
-                if (act[stt]) acc_cols32<D>((const float*)Vt[buf], KT::TS, stt * 16, lane, S[stt], acc);
+                if (act[stt]) {
+                    l_run += S[stt][0] + S[stt][1] + S[stt][2] + S[stt][3];
+                    acc_rm32<D>((const float*)Vs[buf], KT::RS, stt * 16, lane, S[stt], acc);
+                }
         }
         if (c + 1 < nchunks) {
-            kt.store_rows(Ks[buf ^ 1], tid);
-            vt.store_cols(Vt[buf ^ 1], tid);
+            kt.store(Ks[buf ^ 1], tid);
+            vt.store(Vs[buf ^ 1], tid);
         }
         __syncthreads();
     }
 
-    const float l_tot = sum_g4(l_run);
-    if (ri.valid) {
+    const float l_tot = kHalf ? lacc[0] : sum_g4(l_run);
+    if (valid) {
         const float inv = 1.0f / l_tot;
-        T* orow = (T*)p.o + (int64_t)(st + ri.i) * p.o_st + (int64_t)h * p.o_sh;
+        T* orow = (T*)p.o + (int64_t)(st + i) * p.o_st + (int64_t)h * p.o_sh;
 #pragma unroll
         for (int dt = 0; dt < D / 16; ++dt) {
             T ov[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) ov[r] = from_float<T>(acc[dt][r] * inv);
-            if constexpr (sizeof(T) == 2) {
-                *(uint2*)(orow + dt * 16 + 4 * g) = *(const uint2*)ov;
-            } else {
-                *(floatx4*)(orow + dt * 16 + 4 * g) = *(const floatx4*)ov;
-            }
+            if constexpr (kHalf) *(uint2*)(orow + dt * 16 + lane_off) = *(const uint2*)ov;
+            else *(floatx4*)(orow + dt * 16 + lane_off) = *(const floatx4*)ov;
         }
-        if (g == 0) p.lse_out[(int64_t)(st + ri.i) * p.n_heads + h] = m_run * p.scale + __logf(l_tot);
+        if (g == 0) p.lse_out[(int64_t)(st + i) * p.n_heads + h] = m_run * p.scale + __logf(l_tot);
     }
 }
 

@@ -1,20 +1,23 @@
 // LDS tile staging and MFMA operand fetch shared by the attention kernels.
 //
-// A tile holds ROWS token rows of D elements.  It is staged through registers
-// (16-byte global loads, coalesced along D) and written to LDS either
-// row-major [ROWS][D + RPAD] or transposed [D][ROWS + TPAD].
-//
-// Operand conventions for the 16x16 MFMA (see common.h): with rows of the
-// output as "keys" and columns as "queries", lane l = 16*g + c works on
-// column c and on rows 4g..4g+3.
-//  * row_op16(): 8 consecutive D elements of one row (A or B operand over D),
-//    D-chunk dc covers elements 32*dc + 8g .. +7.
-//  * col_op16(): elements of one D index at token offsets kb + 4g + 0..3 and
-//    kb + 16 + 4g + 0..3 of a transposed tile -- the permuted K order that
-//    matches two stacked 16x16 accumulator tiles used as the other operand.
-//  * fp32: K = 4 per instruction; row_op32 gives D/4 consecutive elements
-//    (lane g covers D indices g*D/4 .. +D/4-1, one per instruction) and
-//    col_op32 the 4 token offsets kb + 4g + 0..3 of one D index.
+// A tile holds ROWS token rows of D elements, staged through registers
+// (16-byte global loads along D, branch-free zero fill for missing rows) and
+// stored row-major in LDS as [ROWS][D + pad].  Both operand orientations come
+// from that one copy:
+//  * row_op16(): 8 consecutive D elements of one row -- the A or B operand of
+//    a product that reduces over D (lane l: row l & 15, D chunk 32*dc + 8*(l>>4)).
+//  * tr_op16(): the operand that reduces over tokens: lane l = 16g + i gets
+//    elements (token kb + 4g + r, column c0 + i) for r = 0..3, then the same
+//    for tokens kb + 16 + 4g + r.  gfx950's ds_read_b64_tr_b16 transposes
+//    within each 16-lane group: lane i receives element (i & 3) of the 8-byte
+//    rows addressed by lanes 4r + (i >> 2), so lane j of group g addresses
+//    row kb + 4g + (j >> 2), columns c0 + 4 (j & 3) .. +3.
+//    That token order (4g..4g+3, 16+4g..16+4g+3) is the one in which two
+//    stacked 16x16 accumulator tiles sit in a lane, so accumulators feed the
+//    other MFMA operand directly (pack8).
+//  * fp32 (K = 4 per instruction): row_op32() gives D/4 consecutive elements
+//    (lane group g covers D indices g*D/4 ..), col_f32() the element
+//    (token kb + 4g + r, column c) for instruction r.
 #pragma once
 
 #include "common.h"
@@ -22,9 +25,11 @@
 namespace dsalt {
 
 template <typename T> struct Pad;
-template <> struct Pad<bf16> { static constexpr int R = 8, C = 4; };
-template <> struct Pad<f16> { static constexpr int R = 8, C = 4; };
-template <> struct Pad<float> { static constexpr int R = 4, C = 4; };
+template <> struct Pad<bf16> { static constexpr int R = 8; };
+template <> struct Pad<f16> { static constexpr int R = 8; };
+template <> struct Pad<float> { static constexpr int R = 4; };
+
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
 template <typename T, int D, int ROWS>
 struct Tile {
@@ -32,35 +37,27 @@ struct Tile {
     static constexpr int CPR = D / VW;               // vectors per row
     static constexpr int NV = ROWS * CPR / 256;      // vectors per thread (256 threads)
     static_assert(ROWS * CPR % 256 == 0, "tile must split evenly over 256 threads");
-    static constexpr int RS = D + Pad<T>::R;         // row-major row stride (elements)
-    static constexpr int TS = ROWS + Pad<T>::C;      // transposed row stride (elements)
-    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-    u4 r[NV];
+    static constexpr int RS = D + Pad<T>::R;         // LDS row stride (elements)
+    static constexpr int ELEMS = ROWS * RS;
+    u4v r[NV];
 
-    // row(rr) returns the global pointer of tile row rr or nullptr (zero row)
+    // row(rr) returns the global pointer of tile row rr, or nullptr for a zero row
     template <typename RowFn>
-    __device__ __forceinline__ void load(int tid, RowFn row) {
+    __device__ __forceinline__ void load(int tid, RowFn row, const T* any_valid) {
 #pragma unroll
         for (int n = 0; n < NV; ++n) {
-            int vi = tid + 256 * n, rr = vi / CPR, c = vi % CPR;
+            const int vi = tid + 256 * n, rr = vi / CPR, c = vi % CPR;
             const T* src = row(rr);
-            r[n] = src ? *(const u4*)(src + c * VW) : u4{0u, 0u, 0u, 0u};
+            const bool ok = src != nullptr;
+            u4v v = *(const u4v*)((ok ? src : any_valid) + c * VW);
+            r[n] = ok ? v : u4v{0u, 0u, 0u, 0u};
         }
     }
-    __device__ __forceinline__ void store_rows(T* lds, int tid) const {
+    __device__ __forceinline__ void store(T* lds, int tid) const {
 #pragma unroll
         for (int n = 0; n < NV; ++n) {
-            int vi = tid + 256 * n, rr = vi / CPR, c = vi % CPR;
-            *(u4*)(lds + rr * RS + c * VW) = r[n];
-        }
-    }
-    __device__ __forceinline__ void store_cols(T* lds, int tid) const {
-#pragma unroll
-        for (int n = 0; n < NV; ++n) {
-            int vi = tid + 256 * n, rr = vi / CPR, c = vi % CPR;
-            const T* e = (const T*)&r[n];
-#pragma unroll
-            for (int i = 0; i < VW; ++i) lds[(c * VW + i) * TS + rr] = e[i];
+            const int vi = tid + 256 * n, rr = vi / CPR, c = vi % CPR;
+            *(u4v*)(lds + rr * RS + c * VW) = r[n];
         }
     }
 };
@@ -70,19 +67,25 @@ __device__ __forceinline__ typename Vec8<T>::type row_op16(const T* lds, int rs,
     return *(const typename Vec8<T>::type*)(lds + row * rs + dc * 32 + 8 * g);
 }
 
+__device__ __forceinline__ bf16x4 tr_read(const bf16* p) {
+    typedef __attribute__((address_space(3))) bf16x4* lp;
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lp)p);
+}
+__device__ __forceinline__ f16x4 tr_read(const f16* p) {
+    typedef __fp16 h4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) h4* lp;
+    return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lp)p));
+}
+
 template <typename T>
-__device__ __forceinline__ typename Vec8<T>::type col_op16(const T* lds, int ts, int drow, int kb, int g) {
-    typedef typename Vec8<T>::half H4;
-    H4 lo = *(const H4*)(lds + drow * ts + kb + 4 * g);
-    H4 hi = *(const H4*)(lds + drow * ts + kb + 16 + 4 * g);
+__device__ __forceinline__ typename Vec8<T>::type tr_op16(const T* lds, int rs, int c0, int kb, int lane) {
+    const int g = lane >> 4, j = lane & 15;
+    const T* p = lds + (kb + 4 * g + (j >> 2)) * rs + c0 + 4 * (j & 3);
+    typename Vec8<T>::half lo = tr_read(p), hi = tr_read(p + 16 * rs);
     typename Vec8<T>::type v;
     v[0] = lo[0]; v[1] = lo[1]; v[2] = lo[2]; v[3] = lo[3];
     v[4] = hi[0]; v[5] = hi[1]; v[6] = hi[2]; v[7] = hi[3];
     return v;
-}
-
-__device__ __forceinline__ floatx4 col_op32(const float* lds, int ts, int drow, int kb, int g) {
-    return *(const floatx4*)(lds + drow * ts + kb + 4 * g);
 }
 
 // D/4 consecutive fp32 of a row starting at g*D/4
@@ -96,32 +99,38 @@ __device__ __forceinline__ void row_op32(const float* lds, int rs, int row, int 
 }
 
 // Register copy of one token row in operand layout (queries in the forward
-// and dq kernels, keys/values in the dk/dv kernels).
+// and dq kernels, keys/values in the key-parallel kernels).
 template <typename T, int D>
 struct RowReg {
     typename Vec8<T>::type x[D / 32];
-    __device__ __forceinline__ void load(const T* src, int g) {
+    __device__ __forceinline__ void load(const T* src, const T* any_valid, int g) {
+        const bool ok = src != nullptr;
+        const T* p = ok ? src : any_valid;
 #pragma unroll
         for (int dc = 0; dc < D / 32; ++dc) {
-            if (src) x[dc] = *(const typename Vec8<T>::type*)(src + dc * 32 + 8 * g);
-            else for (int e = 0; e < 8; ++e) x[dc][e] = from_float<T>(0.f);
+            typename Vec8<T>::type v = *(const typename Vec8<T>::type*)(p + dc * 32 + 8 * g);
+            if (!ok) v = typename Vec8<T>::type{};
+            x[dc] = v;
         }
     }
 };
 template <int D>
 struct RowReg<float, D> {
     float x[D / 4];
-    __device__ __forceinline__ void load(const float* src, int g) {
+    __device__ __forceinline__ void load(const float* src, const float* any_valid, int g) {
+        const bool ok = src != nullptr;
+        const float* p = ok ? src : any_valid;
 #pragma unroll
         for (int m = 0; m < D / 16; ++m) {
-            floatx4 v = src ? *(const floatx4*)(src + g * (D / 4) + 4 * m) : floatx4{0.f, 0.f, 0.f, 0.f};
+            floatx4 v = *(const floatx4*)(p + g * (D / 4) + 4 * m);
+            if (!ok) v = floatx4{0.f, 0.f, 0.f, 0.f};
             x[4 * m] = v[0]; x[4 * m + 1] = v[1]; x[4 * m + 2] = v[2]; x[4 * m + 3] = v[3];
         }
     }
 };
 
-// acc = sum over D of A-rows (from LDS, row-major) times the register row:
-// output tile (16 LDS rows) x (16 register rows).
+// acc + (16 LDS rows from row0) x (16 register rows), reduced over D:
+// output row = LDS row (4g + r), output column = register row (lane & 15).
 template <typename T, int D>
 __device__ __forceinline__ floatx4 dot_rows(const T* lds, int rs, int row0, int lane, const RowReg<T, D>& reg,
                                             floatx4 acc) {
@@ -149,58 +158,40 @@ __device__ __forceinline__ floatx4 dot_rows<float, 128>(const float* lds, int rs
     return acc;
 }
 
-// Same product with the operands swapped: the register row is the A operand
-// (output rows = 16 register rows), LDS rows are B (output cols = LDS rows).
+// acc[dt] += (row-major LDS tile, tokens kb..kb+31, columns 16dt..16dt+15)^T
+//            x P, with P two stacked 16-token accumulator tiles (p0: tokens
+// kb..kb+15, p1: kb+16..kb+31).  Returns the packed P operand so callers can
+// reuse it (row sums through a ones operand).
 template <typename T, int D>
-__device__ __forceinline__ floatx4 dot_rows_t(const T* lds, int rs, int row0, int lane, const RowReg<T, D>& reg,
-                                              floatx4 acc) {
-    const int g = lane >> 4, rr = row0 + (lane & 15);
+__device__ __forceinline__ typename Vec8<T>::type acc_tr(const T* lds, int rs, int kb, int lane, floatx4 p0,
+                                                         floatx4 p1, floatx4 (&acc)[D / 16]) {
+    typename Vec8<T>::type b = pack8<T>(p0, p1);
+    typename Vec8<T>::type a[D / 16];
 #pragma unroll
-    for (int dc = 0; dc < D / 32; ++dc) acc = mma(reg.x[dc], row_op16<T>(lds, rs, rr, dc, g), acc);
-    return acc;
-}
-template <>
-__device__ __forceinline__ floatx4 dot_rows_t<float, 64>(const float* lds, int rs, int row0, int lane,
-                                                         const RowReg<float, 64>& reg, floatx4 acc) {
-    float a[16];
-    row_op32<64>(lds, rs, row0 + (lane & 15), lane >> 4, a);
+    for (int dt = 0; dt < D / 16; ++dt) a[dt] = tr_op16<T>(lds, rs, dt * 16, kb, lane);
 #pragma unroll
-    for (int m = 0; m < 16; ++m) acc = mma(reg.x[m], a[m], acc);
-    return acc;
-}
-template <>
-__device__ __forceinline__ floatx4 dot_rows_t<float, 128>(const float* lds, int rs, int row0, int lane,
-                                                          const RowReg<float, 128>& reg, floatx4 acc) {
-    float a[32];
-    row_op32<128>(lds, rs, row0 + (lane & 15), lane >> 4, a);
-#pragma unroll
-    for (int m = 0; m < 32; ++m) acc = mma(reg.x[m], a[m], acc);
-    return acc;
+    for (int dt = 0; dt < D / 16; ++dt) acc[dt] = mma(a[dt], b, acc[dt]);
+    return b;
 }
 
-// acc[dt] += (transposed LDS tile rows dt*16.., token cols kb..kb+31) x P,
-// where P is two stacked 16-token accumulator tiles (p0: tokens kb..kb+15,
-// p1: kb+16..kb+31) used as the K x 16 operand.
-template <typename T, int D>
-__device__ __forceinline__ void acc_cols(const T* ldsT, int ts, int kb, int lane, floatx4 p0, floatx4 p1,
+// fp32: acc[dt] += (tokens kb..kb+15 of the row-major tile)^T x p (one 16-token tile)
+template <int D>
+__device__ __forceinline__ void acc_rm32(const float* lds, int rs, int kb, int lane, floatx4 p,
                                          floatx4 (&acc)[D / 16]) {
     const int g = lane >> 4, c = lane & 15;
-    typename Vec8<T>::type b = pack8<T>(p0, p1);
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) acc[dt] = mma(col_op16<T>(ldsT, ts, dt * 16 + c, kb, g), b, acc[dt]);
+    for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[dt] = mma(lds[(kb + 4 * g + r) * rs + dt * 16 + c], p[r], acc[dt]);
 }
 
-// fp32 variant: one 16-token accumulator tile p (tokens kb..kb+15)
-template <int D>
-__device__ __forceinline__ void acc_cols32(const float* ldsT, int ts, int kb, int lane, floatx4 p,
-                                           floatx4 (&acc)[D / 16]) {
-    const int g = lane >> 4, c = lane & 15;
+template <typename T> __device__ __forceinline__ typename Vec8<T>::type ones8() {
+    typename Vec8<T>::type v;
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-        floatx4 a = col_op32(ldsT, ts, dt * 16 + c, kb, g);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[dt] = mma(a[r], p[r], acc[dt]);
-    }
+    for (int e = 0; e < 8; ++e) v[e] = from_float<T>(1.0f);
+    return v;
 }
+
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 }  // namespace dsalt
