@@ -6,6 +6,15 @@ Prints one JSON line (see --help for the options).  Default workload: B=1, H=16,
 head_dim 64, bf16, w_max 512, k=128 global landmarks, forward + backward.
 
   python bench.py [--gpus 1] [--steps 30] [--warmup 5] [--workload NAME] [--no-cpu-baseline]
+
+HBM traffic per launch comes from rocprofv3 counter runs, each in a process of its own:
+  rocprofv3 --pmc FETCH_SIZE -d P/fetch -o run --output-format csv -- python bench.py --steps 2 --warmup 1 --no-cpu-baseline
+  rocprofv3 --pmc WRITE_SIZE -d P/write ...     (same program)
+  rocprofv3 --pmc FETCH_SIZE -d P/copy_fetch -o run --output-format csv -- python bench.py --copy-calibration 1024
+  rocprofv3 --pmc WRITE_SIZE -d P/copy_write ...  (same program)
+  python bench.py --traffic-from P     # writes profiles/traffic_<workload>.json
+The copy runs give the factor between each counter's reading and the bytes a plain copy of
+known size must move; the kernels' readings are scaled by it.
 """
 from __future__ import annotations
 
@@ -28,7 +37,77 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="fwdbwd_bf16_h16_l32768")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only copy (negate) a MIB-MiB device buffer five times (HBM counter calibration) and exit")
+    ap.add_argument("--traffic-from", metavar="DIR",
+                    help="summarise rocprofv3 --pmc output under DIR/{fetch,write,copy_fetch,copy_write} into "
+                         "profiles/traffic_<workload>.json and exit (no GPU needed)")
+    ap.add_argument("--pmc-summary", metavar="DIR",
+                    help="print per-kernel means of every counter found under DIR and exit (no GPU needed)")
     return ap.parse_args()
+
+
+LABELS = ("sel_norms", "sel_sums", "sel_stats", "sel_z", "sel_topk", "gather", "attn_fwd", "bwd_init", "bwd_dq",
+          "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum")
+
+
+def short_kernel_name(name: str) -> str:
+    """Label of a library kernel (the one dsalt_timing_report uses) from a profiler kernel name."""
+    import re
+    m = re.search(r"(sel_norms|sel_sums|sel_stats|sel_z|sel_topk|gather|fwd|bwd_init|bwd_dq|bwd_dkdv|bwd_lmk_sum|"
+                  r"bwd_lmk)_kernel", name)
+    if not m:
+        return name
+    return "attn_fwd" if m.group(1) == "fwd" else m.group(1)
+
+
+def read_pmc(root: str) -> dict:
+    """{kernel label: {counter: mean value per dispatch}} over every counter_collection.csv under root."""
+    import csv
+    acc = {}
+    for dirpath, _, files in os.walk(root):
+        for fn in files:
+            if not fn.endswith("counter_collection.csv"):
+                continue
+            with open(os.path.join(dirpath, fn), newline="") as f:
+                for row in csv.DictReader(f):
+                    k = short_kernel_name(row["Kernel_Name"])
+                    key = (row["Counter_Name"], row.get("Dispatch_Id", ""))
+                    d = acc.setdefault(k, {})
+                    d[key] = d.get(key, 0.0) + float(row["Counter_Value"])
+    out = {}
+    for k, d in acc.items():
+        per = {}
+        for (cname, _), v in d.items():
+            per.setdefault(cname, []).append(v)
+        out[k] = {c: sum(v) / len(v) for c, v in per.items()}
+        out[k]["dispatches"] = max(len(v) for v in per.values())
+    return out
+
+
+def traffic_from(root: str, wl_name: str, copy_mib: int = 1024) -> dict:
+    """HBM bytes per launch of each kernel: FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled by
+    the ratio of a plain copy's known bytes to that counter's reading for the copy."""
+    known = copy_mib * 2**20
+
+    def copy_reading(sub, counter):
+        d = read_pmc(os.path.join(root, sub))
+        best = max(d.values(), key=lambda c: c.get(counter, 0.0))
+        return best[counter] * 1024.0
+
+    f_fac = known / copy_reading("copy_fetch", "FETCH_SIZE")
+    w_fac = known / copy_reading("copy_write", "WRITE_SIZE")
+    fetch = read_pmc(os.path.join(root, "fetch"))
+    write = read_pmc(os.path.join(root, "write"))
+    res = {"_calibration": {"copy_bytes": known, "fetch_factor": f_fac, "write_factor": w_fac}}
+    for k in sorted(set(fetch) & set(write) & set(LABELS)):
+        fb = fetch[k]["FETCH_SIZE"] * 1024.0 * f_fac
+        wb = write[k]["WRITE_SIZE"] * 1024.0 * w_fac
+        res[k] = {"fetch_bytes": round(fb), "write_bytes": round(wb), "bytes": round(fb + wb)}
+    path = os.path.join(HERE, "profiles", f"traffic_{wl_name}.json")
+    with open(path, "w") as f:
+        json.dump(res, f, indent=1)
+    return res
 
 
 def kernel_model(wl, T, H, D, hidden, pairs, e):
@@ -45,6 +124,13 @@ def kernel_model(wl, T, H, D, hidden, pairs, e):
 
 def main():
     args = parse()
+    if args.traffic_from:
+        print(json.dumps(traffic_from(args.traffic_from, args.workload, args.copy_calibration or 1024), indent=1))
+        return
+    if args.pmc_summary:
+        for k, d in sorted(read_pmc(args.pmc_summary).items()):
+            print(k, json.dumps({c: round(v, 1) for c, v in sorted(d.items())}))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the operator shards over "
               "(batch, head) with no communication, so run one process per GPU.", file=sys.stderr)
@@ -59,6 +145,16 @@ def main():
     lib = _lib.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        n = args.copy_calibration * 2**20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            torch.neg(src, out=dst)  # an elementwise kernel: reads n bytes, writes n bytes
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n, "launches": 5}), flush=True)
+        return
     x_cpu = generate(wl)
     x = {k: v.to(dev) for k, v in x_cpu.items()}
     T, H, D = x["q"].shape
@@ -135,7 +231,7 @@ def main():
         tpath = os.path.join(HERE, "profiles", f"traffic_{wl.name}.json")
         if os.path.exists(tpath):
             with open(tpath) as f:
-                traffic = json.load(f).get(dom)
+                traffic = (json.load(f).get(dom) or {}).get("bytes")
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "algorithmic_bytes": model[dom]["bytes"],

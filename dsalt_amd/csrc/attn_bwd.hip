@@ -163,21 +163,32 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
 
     const T* kbase = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)kvh * p.k_sh;
     const T* vbase = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)kvh * p.v_sh;
-    auto rowpos = [&](int c, int rr) -> int {
-        if (c < nband) {
-            const int j = cs + c * BN + rr;
-            return j <= bhi ? j : -1;
-        }
-        const int sl = (c - nband) * BN + rr;
-        const int pos = sl < bcm ? lpos[sl] : -1;
-        return pos < len ? pos : -1;
-    };
+    // band chunks through buffer resources bounded at bhi, landmark chunks gathered
+    const uint32_t krb = (uint32_t)(p.k_st * (int64_t)sizeof(T)), vrb = (uint32_t)(p.v_st * (int64_t)sizeof(T));
+    uint32_t koff[KT::NV], voff[KT::NV];
+#pragma unroll
+    for (int n = 0; n < KT::NV; ++n) {
+        koff[n] = KT::row_offset(tid, n, krb);
+        voff[n] = KT::row_offset(tid, n, vrb);
+    }
     KT kt, vt;
     auto load_chunk = [&](int c) {
-        kt.load(tid, [&](int rr) { int j = rowpos(c, rr); return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr; },
-                kbase);
-        vt.load(tid, [&](int rr) { int j = rowpos(c, rr); return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr; },
-                vbase);
+        if (c < nband) {
+            const int j0 = cs + c * BN;
+            const int rows = min(BN, bhi + 1 - j0);
+            kt.load_rows(rows_rsrc(kbase + (int64_t)j0 * p.k_st, rows, krb, D * sizeof(T)), koff);
+            vt.load_rows(rows_rsrc(vbase + (int64_t)j0 * p.v_st, rows, vrb, D * sizeof(T)), voff);
+        } else {
+            auto pos = [&](int rr) -> int {
+                const int sl = (c - nband) * BN + rr;
+                const int q = sl < bcm ? lpos[sl] : -1;
+                return q < len ? q : -1;
+            };
+            kt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr; },
+                    kbase);
+            vt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr; },
+                    vbase);
+        }
     };
     load_chunk(0);
     kt.store(Ks[0], tid);
@@ -287,11 +298,22 @@ template <typename T, int D, int BQ>
 struct QLoader {
     typedef Tile<T, D, BQ> QT;
     QT tq, tdo;
-    __device__ __forceinline__ void load(const AttnParams& p, const T* qb, const T* db, int i0, int iend, int tid) {
-        tq.load(tid, [&](int rr) { return i0 + rr < iend ? qb + (int64_t)(i0 + rr) * p.q_st : (const T*)nullptr; },
-                qb);
-        tdo.load(tid, [&](int rr) { return i0 + rr < iend ? db + (int64_t)(i0 + rr) * p.do_st : (const T*)nullptr; },
-                 db);
+    uint32_t qoff[QT::NV], doff[QT::NV];
+    uint32_t qrb, drb;
+    __device__ __forceinline__ QLoader(const AttnParams& p, int tid) {
+        qrb = (uint32_t)(p.q_st * (int64_t)sizeof(T));
+        drb = (uint32_t)(p.do_st * (int64_t)sizeof(T));
+#pragma unroll
+        for (int n = 0; n < QT::NV; ++n) {
+            qoff[n] = QT::row_offset(tid, n, qrb);
+            doff[n] = QT::row_offset(tid, n, drb);
+        }
+    }
+    // rows i0 .. min(i0 + BQ, iend) - 1; later rows read as zero
+    __device__ __forceinline__ void load(const AttnParams& p, const T* qb, const T* db, int i0, int iend, int) {
+        const int rows = min(BQ, iend - i0);
+        tq.load_rows(rows_rsrc(qb + (int64_t)i0 * p.q_st, rows, qrb, D * sizeof(T)), qoff);
+        tdo.load_rows(rows_rsrc(db + (int64_t)i0 * p.do_st, rows, drb, D * sizeof(T)), doff);
     }
     __device__ __forceinline__ void store(QStage<T, D, BQ>& q, int tid) const {
         tq.store(q.q, tid);
@@ -346,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
             need |= (i0 + q16 * 16 < iend) && tinfo[(i0 / 16 + q16) * 2] <= j0 + 63;
         return need;
     };
-    QLoader<T, D, BQ> ld;
+    QLoader<T, D, BQ> ld(p, tid);
     auto store_chunk = [&](int c, QS& q) {
         const int i0 = j0 + c * BQ;
         ld.store(q, tid);
@@ -540,7 +562,7 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     // the loop bound is uniform over the block (every wave reaches each barrier);
     // waves whose slots are all empty skip their products through act[] below
     const bool any_slot = grp * 128 < nvalid;
-    QLoader<T, D, BQ> ld;
+    QLoader<T, D, BQ> ld(p, tid);
     for (int i0 = istart; any_slot && i0 < rend; i0 += BQ) {
         ld.load(p, qb, db, i0, rend, tid);
         __syncthreads();

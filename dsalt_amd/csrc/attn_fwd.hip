@@ -121,21 +121,33 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
 
     const T* kbase = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)kvh * p.k_sh;
     const T* vbase = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)kvh * p.v_sh;
-    auto rowpos = [&](int c, int rr) -> int {
-        if (c < nband) {
-            const int j = cs + c * BN + rr;
-            return j <= bhi ? j : -1;
-        }
-        const int sl = (c - nband) * BN + rr;
-        const int pos = sl < bcm ? lpos[sl] : -1;
-        return pos < len ? pos : -1;
-    };
+    // band chunks: consecutive rows through buffer resources bounded at bhi
+    // (loop-invariant per-thread offsets); landmark chunks: gathered rows
+    const uint32_t krb = (uint32_t)(p.k_st * (int64_t)sizeof(T)), vrb = (uint32_t)(p.v_st * (int64_t)sizeof(T));
+    uint32_t koff[KT::NV], voff[KT::NV];
+#pragma unroll
+    for (int n = 0; n < KT::NV; ++n) {
+        koff[n] = KT::row_offset(tid, n, krb);
+        voff[n] = KT::row_offset(tid, n, vrb);
+    }
     KT kt, vt;
     auto load_chunk = [&](int c) {
-        kt.load(tid, [&](int rr) { int j = rowpos(c, rr); return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr; },
-                kbase);
-        vt.load(tid, [&](int rr) { int j = rowpos(c, rr); return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr; },
-                vbase);
+        if (c < nband) {
+            const int j0 = cs + c * BN;
+            const int rows = min(BN, bhi + 1 - j0);
+            kt.load_rows(rows_rsrc(kbase + (int64_t)j0 * p.k_st, rows, krb, D * sizeof(T)), koff);
+            vt.load_rows(rows_rsrc(vbase + (int64_t)j0 * p.v_st, rows, vrb, D * sizeof(T)), voff);
+        } else {
+            auto pos = [&](int rr) -> int {
+                const int sl = (c - nband) * BN + rr;
+                const int q = sl < bcm ? lpos[sl] : -1;
+                return q < len ? q : -1;
+            };
+            kt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr; },
+                    kbase);
+            vt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr; },
+                    vbase);
+        }
     };
     load_chunk(0);
     kt.store(Ks[0], tid);
@@ -183,11 +195,11 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
             } else {
                 floatx4 bv = floatx4{0.f, 0.f, 0.f, 0.f};
                 if (has_bias) {
+                    float braw[4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int sl = a + lane_off + r;
-                        bv[r] = sl < K ? p.lbias[set_off + sl] * inv_scale : 0.f;
-                    }
+                    for (int r = 0; r < 4; ++r) braw[r] = p.lbias[set_off + min(a + lane_off + r, K - 1)];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) bv[r] = a + lane_off + r < K ? braw[r] * inv_scale : 0.f;
                 }
                 if (a + 15 < wcmin) {
                     ci = bv;

@@ -45,14 +45,25 @@ __device__ __forceinline__ int max16(int v) {
     for (int o = 1; o < 16; o <<= 1) v = max(v, wave_xor(v, o));
     return v;
 }
-// reductions over the 4 lanes l, l^16, l^32, l^48
+// reductions over the 4 lanes l, l^16, l^32, l^48, with gfx950's lane-swap
+// instructions (VALU, no LDS round trip): permlane32_swap(x, x) yields the lower
+// and the upper 32 lanes each broadcast to both halves; permlane16_swap(y, y)
+// the even and the odd 16-lane rows each broadcast over their pair.
 __device__ __forceinline__ float max_g4(float v) {
-    v = fmaxf(v, wave_xor(v, 16));
-    return fmaxf(v, wave_xor(v, 32));
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const float m = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
+    const uint32_t um = __builtin_bit_cast(uint32_t, m);
+    auto b = __builtin_amdgcn_permlane16_swap(um, um, false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
 }
 __device__ __forceinline__ float sum_g4(float v) {
-    v += wave_xor(v, 16);
-    return v + wave_xor(v, 32);
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const float m = __builtin_bit_cast(float, (uint32_t)a[0]) + __builtin_bit_cast(float, (uint32_t)a[1]);
+    const uint32_t um = __builtin_bit_cast(uint32_t, m);
+    auto b = __builtin_amdgcn_permlane16_swap(um, um, false, false);
+    return __builtin_bit_cast(float, (uint32_t)b[0]) + __builtin_bit_cast(float, (uint32_t)b[1]);
 }
 
 // ------------------------------------------------------------------- MFMA

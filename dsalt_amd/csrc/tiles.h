@@ -31,6 +31,19 @@ template <> struct Pad<float> { static constexpr int R = 4; };
 
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
+// Raw buffer resource (stride 0, gfx9 word 3): loads at byte offsets >= bytes
+// return zero without touching memory, so rows past a bound need no select.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// rsrc over `rows` consecutive token rows from `base` (row stride `row_bytes`,
+// `row_len` meaningful bytes per row); rows >= rows read as zero.
+__device__ __forceinline__ rsrc_t rows_rsrc(const void* base, int rows, uint32_t row_bytes, uint32_t row_len) {
+    const uint32_t n = rows > 0 ? (uint32_t)(rows - 1) * row_bytes + row_len : 0u;
+    return make_rsrc(base, n);
+}
+
 template <typename T, int D, int ROWS>
 struct Tile {
     static constexpr int VW = 16 / (int)sizeof(T);  // elements per 16-byte vector
@@ -52,6 +65,16 @@ struct Tile {
             u4v v = *(const u4v*)((ok ? src : any_valid) + c * VW);
             r[n] = ok ? v : u4v{0u, 0u, 0u, 0u};
         }
+    }
+    // byte offsets of this thread's vectors in a tile of consecutive rows
+    __device__ __forceinline__ static uint32_t row_offset(int tid, int n, uint32_t row_bytes) {
+        const int vi = tid + 256 * n;
+        return (uint32_t)(vi / CPR) * row_bytes + (uint32_t)(vi % CPR) * 16u;
+    }
+    // consecutive rows through a buffer resource (zero past its bound)
+    __device__ __forceinline__ void load_rows(rsrc_t rs, const uint32_t (&off)[NV]) {
+#pragma unroll
+        for (int n = 0; n < NV; ++n) r[n] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[n], 0, 0);
     }
     __device__ __forceinline__ void store(T* lds, int tid) const {
 #pragma unroll
