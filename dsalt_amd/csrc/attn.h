@@ -36,7 +36,6 @@ struct AttnParams {
     float* d_bias;
     // backward workspace
     float* delta;            // [T, H]
-    int* tile_minlo;         // [S, ceil(max_seqlen/16)] min window start of 16-row tiles
     int* seq_wmax;           // [S] max clamped window per sequence
     float* part_k;           // [n_chunks, H, S, K, D] landmark dK partials
     float* part_v;           // [n_chunks, H, S, K, D]

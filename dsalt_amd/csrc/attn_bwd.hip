@@ -27,6 +27,7 @@ namespace dsalt {
 
 constexpr float kLog2eB = 1.4426950408889634f;
 constexpr int kRowChunk = 1024;
+constexpr int kSeg = 1024;  // rows compacted at a time in the dK/dV sweep
 
 template <typename T, int D> struct BwdShape;
 template <> struct BwdShape<bf16, 64> { static constexpr int BN = 64, BQ = 64; };
@@ -113,14 +114,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
         red[wave][0] = wlo;
         red[wave][1] = whi;
         red[wave][2] = wcmax;
-        // per 16-row tile: range of window starts, for the key-parallel sweep
-        if (h == 0 && r0 + wave * 16 < len) {
-            const int nt16 = ceil_div(p.max_seqlen, 16);
-            const int64_t ti = (int64_t)s * nt16 + (r0 >> 4) + wave;
-            p.tile_minlo[ti * 2] = wlo;
-            p.tile_minlo[ti * 2 + 1] = wLmax;
-            atomicMax(p.seq_wmax + s, wwmax);
-        }
+        // largest window of the sequence bounds the key-parallel sweep
+        if (h == 0 && r0 + wave * 16 < len) atomicMax(p.seq_wmax + s, wwmax);
     }
     __syncthreads();
     int blo = red[0][0], bhi = red[0][1], bcm = red[0][2];
@@ -280,10 +275,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
 }
 
 // ----------------------------------------------------- query-row staging
-// Query rows i0..i0+BQ-1 of one (head, sequence): Q and dO row-major, plus
-// per-row LSE (base 2), delta, and a per-row key: the window start in the
-// dK/dV sweep (INT_MAX past the end), the visible landmark count in the
-// landmark sweep (0 past the end).
+// BQ query rows of one (head, sequence): Q and dO row-major, plus per-row LSE
+// (base 2), delta, and a per-row key: the window start in the dK/dV sweep, the
+// visible landmark count in the landmark sweep (0 past the end).  Rows past
+// the end are zero with LSE 0 and delta 0, so they contribute exactly zero.
 template <typename T, int D, int BQ>
 struct QStage {
     typedef Tile<T, D, BQ> QT;
@@ -315,6 +310,21 @@ struct QLoader {
         tq.load_rows(rows_rsrc(qb + (int64_t)i0 * p.q_st, rows, qrb, D * sizeof(T)), qoff);
         tdo.load_rows(rows_rsrc(db + (int64_t)i0 * p.do_st, rows, drb, D * sizeof(T)), doff);
     }
+    // rows base + list[idx0 + rr] for idx0 + rr < n (list in LDS, offsets < nrows); later rows zero
+    __device__ __forceinline__ void gather(const AttnParams& p, const T* qb, const T* db, int base, int nrows,
+                                           const short* list, int idx0, int n, int tid) {
+        const rsrc_t rq = rows_rsrc(qb + (int64_t)base * p.q_st, nrows, qrb, D * sizeof(T));
+        const rsrc_t rd = rows_rsrc(db + (int64_t)base * p.do_st, nrows, drb, D * sizeof(T));
+#pragma unroll
+        for (int v = 0; v < QT::NV; ++v) {
+            const int vi = tid + 256 * v, idx = idx0 + vi / QT::CPR;
+            const uint32_t cb = (uint32_t)(vi % QT::CPR) * 16u;
+            const bool ok = idx < n;
+            const uint32_t row = (uint32_t)list[min(idx, kSeg - 1)];
+            tq.r[v] = __builtin_amdgcn_raw_buffer_load_b128(rq, ok ? row * qrb + cb : 0x80000000u, 0, 0);
+            tdo.r[v] = __builtin_amdgcn_raw_buffer_load_b128(rd, ok ? row * drb + cb : 0x80000000u, 0, 0);
+        }
+    }
     __device__ __forceinline__ void store(QStage<T, D, BQ>& q, int tid) const {
         tq.store(q.q, tid);
         tdo.store(q.d, tid);
@@ -322,14 +332,28 @@ struct QLoader {
 };
 
 // -------------------------------------------------------------- band dK/dV
+// Block = 64 keys j0..j0+63 of one (head, sequence); wave w owns keys
+// j0+16w..+15, one key per lane (column of the transposed tiles).  Query rows
+// that see any of these keys are i in [j0, j0 + 63 + largest window).  They are
+// taken in three kinds:
+//   diagonal rows j0..j0+63 (contiguous; window start and causal masks),
+//   then, per segment of kSeg rows after the diagonal, the rows compacted
+//   by their window start lo_i into
+//     full rows    lo_i <= j0           (see all 64 keys: no mask), and
+//     partial rows j0 < lo_i <= j0+63   (see keys >= lo_i: one-sided mask);
+// rows with lo_i > j0 + 63 are skipped.  List order is row order, so the sum
+// order is fixed and results are deterministic.
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
     constexpr int BQ = BwdShape<T, D>::BQ;
     constexpr int NQS = BQ / 16;
+    constexpr int NDIAG = 64 / BQ;
     constexpr bool kHalf = sizeof(T) == 2;
     typedef QStage<T, D, BQ> QS;
     typedef typename QS::QT QT;
     __shared__ __attribute__((aligned(16))) QS sq[2];
+    __shared__ short lst[2][kSeg];
+    __shared__ int wcnt[4][8];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
@@ -341,49 +365,36 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     const int j0 = t * 64;
     if (j0 >= len) return;
-    const int nt16 = ceil_div(p.max_seqlen, 16);
-    const int* tinfo = p.tile_minlo + (int64_t)s * nt16 * 2;
     const float c2 = p.scale * kLog2eB;
 
     const int wj0 = uniform(j0 + wave * 16);
     const int j = wj0 + (lane & 15);
     const bool jvalid = j < len;
-    const int jj = jvalid ? j : -1;  // never >= a window start when past the end
+    const int jj = jvalid ? j : -1;  // below every window start when past the end
     const T* khead = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)h * p.k_sh;
     const T* vhead = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)h * p.v_sh;
     RowReg<T, D> kr, vr;
     kr.load(jvalid ? khead + (int64_t)j * p.k_st : nullptr, khead, g);
     vr.load(jvalid ? vhead + (int64_t)j * p.v_st : nullptr, vhead, g);
 
-    // rows that can see keys j0..j0+63: i in [j0, min(len, j0 + 63 + largest window))
     const int iend = uniform(min(len, j0 + 63 + p.seq_wmax[s]));
-    const int nq = ceil_div(iend - j0, BQ);
     const T* qb = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
     const T* db = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
-    auto chunk_needed = [&](int c) {
-        const int i0 = j0 + c * BQ;
-        bool need = false;
-#pragma unroll
-        for (int q16 = 0; q16 < NQS; ++q16)
-            need |= (i0 + q16 * 16 < iend) && tinfo[(i0 / 16 + q16) * 2] <= j0 + 63;
-        return need;
-    };
+    const int* wrow = p.w + st;
+    const float* lrow = p.lse + (int64_t)st * p.n_heads + h;
+    const float* drow = p.delta + (int64_t)st * p.n_heads + h;
     QLoader<T, D, BQ> ld(p, tid);
-    auto store_chunk = [&](int c, QS& q) {
-        const int i0 = j0 + c * BQ;
-        ld.store(q, tid);
-        if (tid < BQ) {
-            const int i = i0 + tid;
-            if (i < iend) {
-                const int wi = max(p.w[st + i], 1);
-                q.key[tid] = max(i - wi + 1, 0);
-                q.lse2[tid] = p.lse[(int64_t)(st + i) * p.n_heads + h] * kLog2eB;
-                q.dlt[tid] = p.delta[(int64_t)(st + i) * p.n_heads + h];
-            } else {
-                q.key[tid] = 0x7fffffff;
-                q.lse2[tid] = 0.f;
-                q.dlt[tid] = 0.f;
-            }
+    // per-row data of staged row i (or of no row when !ok)
+    auto stage_row = [&](QS& q, int r, int i, bool ok) {
+        if (ok) {
+            const int wi = max(wrow[i], 1);
+            q.key[r] = max(i - wi + 1, 0);
+            q.lse2[r] = lrow[(int64_t)i * p.n_heads] * kLog2eB;
+            q.dlt[r] = drow[(int64_t)i * p.n_heads];
+        } else {
+            q.key[r] = 0x7fffffff;
+            q.lse2[r] = 0.f;
+            q.dlt[r] = 0.f;
         }
     };
 
@@ -395,40 +406,24 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
     }
     const float NEG = -INFINITY;
     const int lane_off = 4 * g;
-    int c = 0;
-    while (c < nq && !chunk_needed(c)) ++c;
-    if (c < nq) {
-        ld.load(p, qb, db, j0 + c * BQ, iend, tid);
-        store_chunk(c, sq[0]);
-    }
-    __syncthreads();
-    int buf = 0;
-    while (c < nq) {
-        int cn = c + 1;
-        while (cn < nq && !chunk_needed(cn)) ++cn;
-        if (cn < nq) ld.load(p, qb, db, j0 + cn * BQ, iend, tid);
-        QS& q = sq[buf];
-        const int i0 = j0 + c * BQ;
+
+    // one staged chunk; kind 0: diagonal rows from i0, 1: full rows, 2: partial rows
+    auto compute = [&](const QS& q, int kind, int i0) {
         floatx4 P[NQS], dS[NQS];
         bool act[NQS];
 #pragma unroll
         for (int qs = 0; qs < NQS; ++qs) {
             const int qa = i0 + qs * 16;
-            const bool inr = qa < iend;
-            const int tmin = inr ? tinfo[(qa >> 4) * 2] : 0x7fffffff;
-            const int tmax = inr ? tinfo[(qa >> 4) * 2 + 1] : 0x7fffffff;
-            act[qs] = inr && tmin <= wj0 + 15 && qa + 15 >= wj0 && wj0 < len;
+            act[qs] = kind != 0 || qa + 15 >= wj0;
             if (!act[qs]) {
                 P[qs] = floatx4{0.f, 0.f, 0.f, 0.f};
                 dS[qs] = P[qs];
                 continue;
             }
-            floatx4 ci;
-            if (tmax <= wj0 && qa >= wj0 + 15 && qa + 15 < iend && wj0 + 15 < len) {
-                ci = floatx4{0.f, 0.f, 0.f, 0.f};
-            } else {
+            floatx4 ci = floatx4{0.f, 0.f, 0.f, 0.f};
+            if (kind != 1) {
                 const int4 lo4 = *(const int4*)(q.key + qs * 16 + lane_off);
-                if (qa >= wj0 + 15) {  // every row at or after every key of the wave
+                if (kind == 2 || qa >= wj0 + 15) {
                     ci[0] = jj >= lo4.x ? 0.f : NEG;
                     ci[1] = jj >= lo4.y ? 0.f : NEG;
                     ci[2] = jj >= lo4.z ? 0.f : NEG;
@@ -467,11 +462,109 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
                     acc_rm32<D>((const float*)q.q, QT::RS, qs * 16, lane, dS[qs], adk);
                 }
         }
-        if (cn < nq) store_chunk(cn, sq[buf ^ 1]);
+    };
+
+    // ---- diagonal rows j0 .. j0+63 (contiguous), double-buffered
+    const int ndiag = uniform(min(NDIAG, ceil_div(iend - j0, BQ)));
+    ld.load(p, qb, db, j0, iend, tid);
+    ld.store(sq[0], tid);
+    if (tid < BQ) stage_row(sq[0], tid, j0 + tid, j0 + tid < iend);
+    __syncthreads();
+    for (int c = 0; c < ndiag; ++c) {
+        const int buf = c & 1;
+        if (c + 1 < ndiag) ld.load(p, qb, db, j0 + (c + 1) * BQ, iend, tid);
+        compute(sq[buf], 0, j0 + c * BQ);
+        if (c + 1 < ndiag) {
+            ld.store(sq[buf ^ 1], tid);
+            const int i = j0 + (c + 1) * BQ + tid;
+            if (tid < BQ) stage_row(sq[buf ^ 1], tid, i, i < iend);
+        }
         __syncthreads();
-        buf ^= 1;
-        c = cn;
     }
+
+    // ---- rows after the diagonal, segment by segment
+    for (int seg = j0 + 64; seg < iend; seg += kSeg) {
+        const int nrows = uniform(min(kSeg, iend - seg));
+        uint64_t bf[kSeg / 256], bp[kSeg / 256];
+#pragma unroll
+        for (int u = 0; u < kSeg / 256; ++u) {
+            const int r = u * 256 + tid;
+            bool f = false, pp = false;
+            if (r < nrows) {
+                const int i = seg + r;
+                const int lo = max(i - max(wrow[i], 1) + 1, 0);
+                f = lo <= j0;
+                pp = !f && lo <= j0 + 63;
+            }
+            bf[u] = __ballot(f);
+            bp[u] = __ballot(pp);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int u = 0; u < kSeg / 256; ++u) {
+                wcnt[wave][u] = __popcll(bf[u]);
+                wcnt[wave][4 + u] = __popcll(bp[u]);
+            }
+        }
+        __syncthreads();
+        // list order: (u, wave, lane) = row order
+        int nf = 0, np = 0, basef[kSeg / 256], basep[kSeg / 256];
+#pragma unroll
+        for (int u = 0; u < kSeg / 256; ++u) {
+            basef[u] = nf;
+            basep[u] = np;
+            for (int w2 = 0; w2 < 4; ++w2) {
+                const int cf = wcnt[w2][u], cp = wcnt[w2][4 + u];
+                if (w2 < wave) {
+                    basef[u] += cf;
+                    basep[u] += cp;
+                }
+                nf += cf;
+                np += cp;
+            }
+        }
+        nf = uniform(nf);
+        np = uniform(np);
+#pragma unroll
+        for (int u = 0; u < kSeg / 256; ++u) {
+            const uint32_t flo = (uint32_t)bf[u], fhi = (uint32_t)(bf[u] >> 32);
+            const uint32_t plo = (uint32_t)bp[u], phi = (uint32_t)(bp[u] >> 32);
+            const int rf = __builtin_amdgcn_mbcnt_hi(fhi, __builtin_amdgcn_mbcnt_lo(flo, 0));
+            const int rp = __builtin_amdgcn_mbcnt_hi(phi, __builtin_amdgcn_mbcnt_lo(plo, 0));
+            const uint64_t me = 1ull << lane;
+            if (bf[u] & me) lst[0][basef[u] + rf] = (short)(u * 256 + tid);
+            if (bp[u] & me) lst[1][basep[u] + rp] = (short)(u * 256 + tid);
+        }
+        __syncthreads();
+        const int nfc = ceil_div(nf, BQ), nc = nfc + ceil_div(np, BQ);
+        auto gather_chunk = [&](int c) {
+            if (c < nfc) ld.gather(p, qb, db, seg, nrows, lst[0], c * BQ, nf, tid);
+            else ld.gather(p, qb, db, seg, nrows, lst[1], (c - nfc) * BQ, np, tid);
+        };
+        auto stage_chunk = [&](int c, QS& q) {
+            ld.store(q, tid);
+            if (tid < BQ) {
+                const bool full = c < nfc;
+                const int idx = (full ? c : c - nfc) * BQ + tid;
+                const int n = full ? nf : np;
+                const bool ok = idx < n;
+                stage_row(q, tid, seg + (ok ? (int)lst[full ? 0 : 1][idx] : 0), ok);
+            }
+        };
+        if (nc > 0) {
+            gather_chunk(0);
+            stage_chunk(0, sq[0]);
+        }
+        __syncthreads();
+        for (int c = 0; c < nc; ++c) {
+            const int buf = c & 1;
+            if (c + 1 < nc) gather_chunk(c + 1);
+            compute(sq[buf], c < nfc ? 1 : 2, 0);
+            if (c + 1 < nc) stage_chunk(c + 1, sq[buf ^ 1]);
+            __syncthreads();
+        }
+    }
+
     if (jvalid) {
         T* kd = (T*)p.dk + (int64_t)(st + j) * p.n_heads * D + (int64_t)h * D;
         T* vd = (T*)p.dv + (int64_t)(st + j) * p.n_heads * D + (int64_t)h * D;
@@ -694,11 +787,9 @@ __global__ __launch_bounds__(256) void bwd_lmk_sum_kernel(AttnParams p) {
 // ---------------------------------------------------------------- launch
 size_t bwd_workspace(const AttnParams& p) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    const int nt16 = ceil_div(p.max_seqlen, 16);
     const int nch = ceil_div(p.max_seqlen, kRowChunk);
     size_t b = 0;
     b += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
-    b += al(sizeof(int) * 2 * (size_t)p.num_seqs * nt16);
     b += al(sizeof(int) * (size_t)p.num_seqs);
     b += 2 * al(sizeof(float) * (size_t)nch * p.n_heads * p.num_seqs * p.k_lmk * p.head_dim);
     b += al(sizeof(float) * (size_t)nch * p.n_heads * p.num_seqs * p.k_lmk);
@@ -723,13 +814,10 @@ static void bwd_run(const AttnParams& p, hipStream_t stream) {
 
 hipError_t bwd_launch(AttnParams p, void* ws, hipStream_t stream) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    const int nt16 = ceil_div(p.max_seqlen, 16);
     p.n_chunks = ceil_div(p.max_seqlen, kRowChunk);
     char* w = (char*)ws;
     p.delta = (float*)w;
     w += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
-    p.tile_minlo = (int*)w;
-    w += al(sizeof(int) * 2 * (size_t)p.num_seqs * nt16);
     p.seq_wmax = (int*)w;
     w += al(sizeof(int) * (size_t)p.num_seqs);
     const size_t npart = (size_t)p.n_chunks * p.n_heads * p.num_seqs * p.k_lmk;

@@ -69,9 +69,9 @@ int check_rows(const void* ptr, int64_t st, int64_t sh, int dtype, const char* n
     if ((st * (int64_t)es) % 16 || (sh * (int64_t)es) % 16 || st <= 0 || sh < 0)
         return fail(DSALT_ERR_INVALID, "%s strides (%lld, %lld) must be positive multiples of 16 bytes", name,
                     (long long)st, (long long)sh);
-    // tiles of 64 rows are addressed with 32-bit byte offsets from the tile's first row
-    if (st * (int64_t)es > (int64_t)(1u << 25))
-        return fail(DSALT_ERR_UNSUPPORTED, "%s token stride of %lld bytes exceeds 32 MiB", name,
+    // runs of up to 1024 rows are addressed with 32-bit byte offsets from their first row
+    if (st * (int64_t)es > (int64_t)(1u << 20))
+        return fail(DSALT_ERR_UNSUPPORTED, "%s token stride of %lld bytes exceeds 1 MiB", name,
                     (long long)(st * (int64_t)es));
     return DSALT_OK;
 }

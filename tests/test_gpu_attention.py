@@ -134,3 +134,14 @@ def test_bwd_deterministic():
                                 max_seqlen=maxlen)
     for a, b in zip(r1, r2):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_bwd_long_windows(dt):
+    # windows up to the whole sequence: the key-parallel sweep takes the rows after
+    # each key block in several compacted segments
+    _bwd_check(dt, [2300, 700], 2, 64, 16, 2300, seed=14)
+
+
+def test_bwd_long_windows_d128():
+    _bwd_check(torch.bfloat16, [1500, 90], 2, 128, 8, 1500, seed=15, bias=True)
