@@ -47,14 +47,14 @@ def parse():
     return ap.parse_args()
 
 
-LABELS = ("sel_norms", "sel_sums", "sel_stats", "sel_z", "sel_topk", "gather", "attn_fwd", "bwd_init", "bwd_dq",
-          "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum")
+LABELS = ("sel_norms", "sel_sums", "sel_stats", "sel_z", "sel_topk", "gather", "row_plan", "attn_fwd", "bwd_init",
+          "bwd_dq", "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum")
 
 
 def short_kernel_name(name: str) -> str:
     """Label of a library kernel (the one dsalt_timing_report uses) from a profiler kernel name."""
     import re
-    m = re.search(r"(sel_norms|sel_sums|sel_stats|sel_z|sel_topk|gather|fwd|bwd_init|bwd_dq|bwd_dkdv|bwd_lmk_sum|"
+    m = re.search(r"(sel_norms|sel_sums|sel_stats|sel_z|sel_topk|gather|row_plan|fwd|bwd_init|bwd_dq|bwd_dkdv|bwd_lmk_sum|"
                   r"bwd_lmk)_kernel", name)
     if not m:
         return name

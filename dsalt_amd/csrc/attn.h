@@ -14,6 +14,9 @@ struct AttnParams {
     int dtype;
     int n_tiles;             // 64-row tiles per sequence, ceil(max_seqlen / 64)
     float scale;
+    float c2;                // scale * log2(e)
+    float inv_scale;         // 1 / scale
+    float thr;               // lazy-rescale threshold in raw logits, 8 / c2
     const void* q;
     int64_t q_st, q_sh;
     const void* k;
@@ -34,6 +37,10 @@ struct AttnParams {
     void* dk;
     void* dv;
     float* d_bias;
+    // row plan (forward and backward workspace), per 64-row tile of each sequence:
+    // rows ordered by window start, and per 16-row group {min lo, max lo, max i, min i}
+    uint8_t* plan_perm;      // [S * n_tiles * 64] row offset within the tile
+    int* plan_bounds;        // [S * n_tiles * 4 * 4]
     // backward workspace
     float* delta;            // [T, H]
     int* seq_wmax;           // [S] max clamped window per sequence
@@ -43,7 +50,10 @@ struct AttnParams {
     int n_chunks;            // row chunks of the landmark backward
 };
 
-hipError_t fwd_launch(const AttnParams& p, hipStream_t stream);
+size_t plan_bytes(const AttnParams& p);
+void plan_carve(AttnParams& p, char*& ws);  // assigns plan_perm / plan_bounds from a workspace
+hipError_t plan_launch(const AttnParams& p, hipStream_t stream);
+hipError_t fwd_launch(AttnParams p, void* ws, hipStream_t stream);
 size_t bwd_workspace(const AttnParams& p);
 hipError_t bwd_launch(AttnParams p, void* ws, hipStream_t stream);
 

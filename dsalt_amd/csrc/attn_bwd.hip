@@ -75,7 +75,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) T Ks[2][KT::ELEMS];
     __shared__ __attribute__((aligned(16))) T Vs[2][KT::ELEMS];
     __shared__ int lpos[kMaxLandmarks];
-    __shared__ int red[4][3];
+    __shared__ int red[4];
     __shared__ int nvalid_s;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
@@ -91,42 +91,31 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
     const int kvh = h / (p.n_heads / p.n_kv_heads);
     const int K = p.k_lmk;
     const int64_t set_off = (((int64_t)h * p.num_seqs + s) * p.n_sets) * K;
-    const float c2 = p.scale * kLog2eB;
-    const float inv_scale = 1.0f / p.scale;
+    const float c2 = p.c2;
+    const float inv_scale = p.inv_scale;
     const bool has_bias = p.lbias != nullptr;
     const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid);
 
-    const int i = r0 + wave * 16 + (lane & 15);
+    // this wave's rows (ordered by window start) and their bounds, from the row plan
+    const int uw = uniform(wave);
+    const int64_t tile = (int64_t)s * p.n_tiles + t;
+    const int* bnd = p.plan_bounds + tile * 16;
+    const int wlo = bnd[uw * 4], wLmax = bnd[uw * 4 + 1], whi = bnd[uw * 4 + 2], wHmin = bnd[uw * 4 + 3];
+    const int blo = min(min(bnd[0], bnd[4]), min(bnd[8], bnd[12]));
+    const int bhi = max(max(bnd[2], bnd[6]), max(bnd[10], bnd[14]));
+    const int i = r0 + p.plan_perm[tile * 64 + uw * 16 + (lane & 15)];
     const bool valid = i < len;
-    int lo = 0x7fffffff, hi = -1, cnt = 0, wcl = 1;
+    int lo = 0x7fffffff, hi = -1, cnt = 0;
     if (valid) {
         const int wi = max(p.w[st + i], 1);
-        wcl = min(wi, len);
         lo = max(i - wi + 1, 0);
         hi = i;
         cnt = lower_bound_i(lpos, nvalid, lo);
     }
-    const int wlo = uniform(min16(lo)), whi = uniform(max16(hi));
-    const int wLmax = uniform(max16(lo)), wHmin = uniform(min16(hi));
-    const int wcmax = uniform(max16(cnt)), wcmin = uniform(min16(valid ? cnt : 0));
-    const int wwmax = uniform(max16(wcl));
-    if (lane == 0) {
-        red[wave][0] = wlo;
-        red[wave][1] = whi;
-        red[wave][2] = wcmax;
-        // largest window of the sequence bounds the key-parallel sweep
-        if (h == 0 && r0 + wave * 16 < len) atomicMax(p.seq_wmax + s, wwmax);
-    }
+    const int wcmax = uniform(row_max16(cnt)), wcmin = uniform(row_min16(valid ? cnt : 0));
+    if (lane == 0) red[uw] = wcmax;
     __syncthreads();
-    int blo = red[0][0], bhi = red[0][1], bcm = red[0][2];
-    for (int w2 = 1; w2 < 4; ++w2) {
-        blo = min(blo, red[w2][0]);
-        bhi = max(bhi, red[w2][1]);
-        bcm = max(bcm, red[w2][2]);
-    }
-    blo = uniform(blo);
-    bhi = uniform(bhi);
-    bcm = uniform(bcm);
+    const int bcm = uniform(max(max(red[0], red[1]), max(red[2], red[3])));
     const int cs = (blo / BN) * BN;
     const int nband = (bhi - cs) / BN + 1;
     const int nchunks = nband + ceil_div(bcm, BN);
@@ -616,8 +605,8 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     const int kvh = h / (p.n_heads / p.n_kv_heads);
     const int64_t set_off = (((int64_t)h * p.num_seqs + s) * p.n_sets) * K;
-    const float c2 = p.scale * kLog2eB;
-    const float inv_scale = 1.0f / p.scale;
+    const float c2 = p.c2;
+    const float inv_scale = p.inv_scale;
     const int rbeg = chunk * kRowChunk, rend = min(len, rbeg + kRowChunk);
     const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid);
 
@@ -788,7 +777,7 @@ __global__ __launch_bounds__(256) void bwd_lmk_sum_kernel(AttnParams p) {
 size_t bwd_workspace(const AttnParams& p) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const int nch = ceil_div(p.max_seqlen, kRowChunk);
-    size_t b = 0;
+    size_t b = plan_bytes(p);
     b += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
     b += al(sizeof(int) * (size_t)p.num_seqs);
     b += 2 * al(sizeof(float) * (size_t)nch * p.n_heads * p.num_seqs * p.k_lmk * p.head_dim);
@@ -800,6 +789,7 @@ template <typename T, int D>
 static void bwd_run(const AttnParams& p, hipStream_t stream) {
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
     DSALT_LAUNCH("bwd_init", bwd_init_kernel, dim3(ceil_div(p.num_seqs, 256)), dim3(256), 0, stream, p);
+    plan_launch(p, stream);
     DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D>), dim3(total), dim3(256), 0, stream, p);
     DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D>), dim3(total), dim3(256), 0, stream, p);
     if (p.k_lmk > 0) {
@@ -816,6 +806,7 @@ hipError_t bwd_launch(AttnParams p, void* ws, hipStream_t stream) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     p.n_chunks = ceil_div(p.max_seqlen, kRowChunk);
     char* w = (char*)ws;
+    plan_carve(p, w);
     p.delta = (float*)w;
     w += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
     p.seq_wmax = (int*)w;

@@ -21,8 +21,7 @@
 
 namespace dsalt {
 
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kBM = 64;
+
 
 template <typename T, int D> struct FwdShape;
 template <> struct FwdShape<bf16, 64> { static constexpr int BN = 64; };
@@ -42,7 +41,142 @@ __device__ __forceinline__ int lower_bound_lds(const int* a, int n, int x) {
     return lo;
 }
 
-template <typename T, int D>
+// ------------------------------------------------------------- row plan
+// Head-independent preparation shared by the forward and dQ kernels.  Within
+// each 64-row tile the rows are ordered by window start lo_i (ties by row;
+// rows past the end last), so the 16 rows a wave takes have close window
+// starts: the wave's key range [min lo, max i] and its count of masked
+// subtiles shrink.  Each 16-row group's {min lo, max lo, max i, min i} is
+// recorded, and, when seq_wmax is set, the largest clamped window of each
+// sequence (bounding the key-parallel backward sweep).
+__global__ __launch_bounds__(64) void row_plan_kernel(AttnParams p) {
+    __shared__ int sp[64];
+    const int l = threadIdx.x;
+    const int tile = blockIdx.x;  // s * n_tiles + t
+    const int s = tile / p.n_tiles, t = tile % p.n_tiles;
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
+    const int r0 = t * 64;
+    const int i = r0 + l;
+    const bool valid = i < len;
+    int lo = 0x7fffffff, wcl = 0;
+    if (valid) {
+        const int wi = max(p.w[st + i], 1);
+        lo = max(i - wi + 1, 0);
+        wcl = min(wi, len);
+    }
+    const uint32_t khi = (uint32_t)lo >> 26, klo = ((uint32_t)lo << 6) | (uint32_t)l;  // key lo * 64 + l
+    int rank = 0;
+    for (int j = 0; j < 64; ++j) {
+        const uint32_t jhi = (uint32_t)__builtin_amdgcn_readlane((int)khi, j);
+        const uint32_t jlo = (uint32_t)__builtin_amdgcn_readlane((int)klo, j);
+        rank += (jhi < khi || (jhi == khi && jlo < klo)) ? 1 : 0;
+    }
+    sp[rank] = l;
+    __syncthreads();
+    const int pl = sp[l];  // row offset at sorted position l
+    p.plan_perm[(int64_t)tile * 64 + l] = (uint8_t)pl;
+    const int ri = r0 + pl;
+    const bool rv = ri < len;
+    int rlo = 0x7fffffff, rlmax = (int)0x80000000, rhi = -1, rhmin = 0x7fffffff;
+    if (rv) {
+        rlo = max(ri - max(p.w[st + ri], 1) + 1, 0);
+        rlmax = rlo;
+        rhi = ri;
+        rhmin = ri;
+    }
+    rlo = row_min16(rlo);
+    rlmax = row_max16(rlmax);
+    rhi = row_max16(rhi);
+    rhmin = row_min16(rhmin);
+    if ((l & 15) == 0) {
+        int* b = p.plan_bounds + ((int64_t)tile * 4 + (l >> 4)) * 4;
+        b[0] = rlo;
+        b[1] = rlmax;
+        b[2] = rhi;
+        b[3] = rhmin;
+    }
+    if (p.seq_wmax) {
+        const int m = row_max16(wcl);
+        if ((l & 15) == 0 && m > 0) atomicMax(p.seq_wmax + s, m);
+    }
+}
+
+size_t plan_bytes(const AttnParams& p) {
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t tiles = (size_t)p.num_seqs * p.n_tiles;
+    return al(tiles * 64) + al(tiles * 16 * sizeof(int));
+}
+
+void plan_carve(AttnParams& p, char*& ws) {
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t tiles = (size_t)p.num_seqs * p.n_tiles;
+    p.plan_perm = (uint8_t*)ws;
+    ws += al(tiles * 64);
+    p.plan_bounds = (int*)ws;
+    ws += al(tiles * 16 * sizeof(int));
+}
+
+hipError_t plan_launch(const AttnParams& p, hipStream_t stream) {
+    const int tiles = p.num_seqs * p.n_tiles;
+    if (tiles == 0) return hipSuccess;
+    DSALT_LAUNCH("row_plan", row_plan_kernel, dim3(tiles), dim3(64), 0, stream, p);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- forward
+// Rows of one 16-row group: per lane the row, its window [lo, hi] and visible
+// landmark count; per group (wave-uniform) the bounds that classify subtiles.
+struct RowGroup {
+    int i, lo, hi, cnt;
+    bool valid;
+    int wlo, wLmax, whi, wHmin, wcmax, wcmin;
+};
+
+// Block group (plan tile u, group within it) taken by wave w: groups are ordered
+// by window start inside a plan tile, so wave w pairs the w-th group of tile 0
+// with the (3-w)-th of tile 1 and the waves of a block get even work.
+template <int RG>
+__device__ __forceinline__ int group_of(int w, int u) {
+    return RG == 1 ? w : 4 * u + (u & 1 ? 3 - w : w);
+}
+
+// Fills the lane's row of block group G (0 .. 4*RG-1) from the row plan.
+__device__ __forceinline__ void plan_group(const AttnParams& p, int64_t tile0, int ntl, int G, int r0, int st,
+                                           int len, const int* lpos, int nvalid, int lane, RowGroup& rg) {
+    rg.i = -1;
+    rg.lo = 0x7fffffff;
+    rg.hi = -1;
+    rg.cnt = 0;
+    rg.valid = false;
+    rg.wlo = 0x7fffffff;
+    rg.wLmax = (int)0x80000000;
+    rg.whi = -1;
+    rg.wHmin = 0x7fffffff;
+    if (G < 4 * ntl) {
+        const int* bnd = p.plan_bounds + (tile0 + G / 4) * 16 + (G % 4) * 4;
+        rg.wlo = bnd[0];
+        rg.wLmax = bnd[1];
+        rg.whi = bnd[2];
+        rg.wHmin = bnd[3];
+        rg.i = r0 + (G / 4) * 64 + p.plan_perm[(tile0 + G / 4) * 64 + (G % 4) * 16 + (lane & 15)];
+        rg.valid = rg.i < len;
+        if (rg.valid) {
+            const int wi = max(p.w[st + rg.i], 1);
+            rg.lo = max(rg.i - wi + 1, 0);
+            rg.hi = rg.i;
+            rg.cnt = lower_bound_lds(lpos, nvalid, rg.lo);
+        }
+    }
+    rg.wcmax = uniform(row_max16(rg.cnt));
+    rg.wcmin = uniform(row_min16(rg.valid ? rg.cnt : 0));
+}
+
+// One 256-thread block (4 waves) owns 64*RG query rows of one (head, sequence),
+// taken in the row plan's order; wave w owns the 16-row groups RG*w .. RG*w+RG-1
+// (each lane one query row per group).  The K and V^T operands fetched from
+// LDS for a subtile serve all of a wave's groups.
+template <typename T, int D, int RG>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     constexpr int BN = FwdShape<T, D>::BN;
     constexpr int NST = BN / 16;
@@ -51,25 +185,26 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) T Ks[2][KT::ELEMS];
     __shared__ __attribute__((aligned(16))) T Vs[2][KT::ELEMS];
     __shared__ int lpos[kMaxLandmarks];
-    __shared__ int red[4][3];
+    __shared__ int red[4];
     __shared__ int nvalid_s;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
-    const int total = p.n_heads * p.num_seqs * p.n_tiles;
+    const int nblk = ceil_div(p.n_tiles, RG);
+    const int total = p.n_heads * p.num_seqs * nblk;
     const int L = xcd_swizzle(blockIdx.x, total);
-    const int t = L % p.n_tiles;
-    const int s = (L / p.n_tiles) % p.num_seqs;
-    const int h = L / (p.n_tiles * p.num_seqs);
+    const int b = L % nblk;
+    const int s = (L / nblk) % p.num_seqs;
+    const int h = L / (nblk * p.num_seqs);
     int st, len;
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
-    const int r0 = t * kBM;
+    const int r0 = b * 64 * RG;
     if (r0 >= len) return;
     const int kvh = h / (p.n_heads / p.n_kv_heads);
     const int set = p.block_size ? r0 / p.block_size : 0;
     const int K = p.k_lmk;
     const int64_t set_off = (((int64_t)h * p.num_seqs + s) * p.n_sets + set) * K;
-    const float c2 = p.scale * kLog2e;
-    const float inv_scale = 1.0f / p.scale;
+    const float c2 = p.c2;
+    const float inv_scale = p.inv_scale;
     const bool has_bias = p.lbias != nullptr;
 
     if (tid == 0) nvalid_s = 0;
@@ -82,42 +217,35 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     __syncthreads();
     const int nvalid = nvalid_s;
 
-    // the row of this lane: window [lo, hi] and visible landmark count
-    const int i = r0 + wave * 16 + (lane & 15);
-    const bool valid = i < len;
-    int lo = 0x7fffffff, hi = -1, cnt = 0;
-    if (valid) {
-        const int wi = max(p.w[st + i], 1);
-        lo = max(i - wi + 1, 0);
-        hi = i;
-        cnt = lower_bound_lds(lpos, nvalid, lo);
-    }
-    // wave-uniform bounds (scalar registers: the subtile branches below are scalar)
-    const int wlo = uniform(min16(lo)), whi = uniform(max16(hi));
-    const int wLmax = uniform(max16(lo)), wHmin = uniform(min16(hi));
-    const int wcmax = uniform(max16(cnt)), wcmin = uniform(min16(valid ? cnt : 0));
-    if (lane == 0) {
-        red[wave][0] = wlo;
-        red[wave][1] = whi;
-        red[wave][2] = wcmax;
-    }
-    __syncthreads();
-    int blo = red[0][0], bhi = red[0][1], bcm = red[0][2];
-    for (int w2 = 1; w2 < 4; ++w2) {
-        blo = min(blo, red[w2][0]);
-        bhi = max(bhi, red[w2][1]);
-        bcm = max(bcm, red[w2][2]);
+    // row groups of this wave and block-wide key range, from the row plan
+    const int uw = uniform(wave);
+    const int64_t tile0 = (int64_t)s * p.n_tiles + (int64_t)b * RG;
+    const int ntl = min(RG, p.n_tiles - b * RG);
+    int blo = 0x7fffffff, bhi = -1;
+    for (int G = 0; G < 4 * ntl; ++G) {
+        blo = min(blo, p.plan_bounds[tile0 * 16 + G * 4]);
+        bhi = max(bhi, p.plan_bounds[tile0 * 16 + G * 4 + 2]);
     }
     blo = uniform(blo);
     bhi = uniform(bhi);
-    bcm = uniform(bcm);
+    RowGroup rg[RG];
+    int wcm = 0;
+#pragma unroll
+    for (int u = 0; u < RG; ++u) {
+        plan_group(p, tile0, ntl, group_of<RG>(uw, u), r0, st, len, lpos, nvalid, lane, rg[u]);
+        wcm = max(wcm, rg[u].wcmax);
+    }
+    if (lane == 0) red[uw] = wcm;
+    __syncthreads();
+    const int bcm = uniform(max(max(red[0], red[1]), max(red[2], red[3])));
     const int cs = (blo / BN) * BN;
-    const int nband = (bhi - cs) / BN + 1;
+    const int nband = bhi >= blo ? (bhi - cs) / BN + 1 : 0;
     const int nchunks = nband + ceil_div(bcm, BN);
 
     const T* qhead = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
-    RowReg<T, D> qr;
-    qr.load(valid ? qhead + (int64_t)i * p.q_st : nullptr, qhead, g);
+    RowReg<T, D> qr[RG];
+#pragma unroll
+    for (int u = 0; u < RG; ++u) qr[u].load(rg[u].valid ? qhead + (int64_t)rg[u].i * p.q_st : nullptr, qhead, g);
 
     const T* kbase = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)kvh * p.k_sh;
     const T* vbase = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)kvh * p.v_sh;
@@ -149,18 +277,26 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
                     vbase);
         }
     };
-    load_chunk(0);
-    kt.store(Ks[0], tid);
-    vt.store(Vs[0], tid);
+    if (nchunks > 0) {
+        load_chunk(0);
+        kt.store(Ks[0], tid);
+        vt.store(Vs[0], tid);
+    }
     __syncthreads();
 
-    floatx4 acc[D / 16];
+    floatx4 acc[RG][D / 16];
+    floatx4 lacc[RG];  // row sums (16-bit path: ones x P)
+    float l_run[RG];   // row sums (fp32 path)
+    float m_run[RG];
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    floatx4 lacc = floatx4{0.f, 0.f, 0.f, 0.f};  // row sums (16-bit path: ones x P)
-    float l_run = 0.f;                             // row sums (fp32 path)
-    float m_run = -INFINITY;
-    const float thr = 8.0f / c2;
+    for (int u = 0; u < RG; ++u) {
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) acc[u][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        lacc[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+        l_run[u] = 0.f;
+        m_run[u] = -INFINITY;
+    }
+    const float thr = p.thr;
     const float NEG = -INFINITY;
     const int lane_off = 4 * g;
 
@@ -169,84 +305,157 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
         if (c + 1 < nchunks) load_chunk(c + 1);
         const bool band = c < nband;
         const int base = band ? cs + c * BN : (c - nband) * BN;
-        floatx4 S[NST];
-        bool act[NST];
+        const T* kl = Ks[buf];
+        floatx4 S[RG][NST];
+        bool act[RG][NST];
+        bool gact[RG];
 #pragma unroll
-        for (int stt = 0; stt < NST; ++stt) {
-            const int a = base + stt * 16;
-            act[stt] = band ? (a <= whi && a + 15 >= wlo) : (a < wcmax);
-            if (!act[stt]) {
-                S[stt] = floatx4{NEG, NEG, NEG, NEG};
-                continue;
-            }
-            floatx4 ci;
+        for (int u = 0; u < RG; ++u) {
+            const RowGroup& R = rg[u];
+            // chunk class for this group (wave-uniform): 0 no row sees it; 1 every
+            // row sees every key; 2 all subtiles in range, window starts only;
+            // 3 all in range, both window ends; 4 landmarks all visible, no bias;
+            // 5 anything else (subtile by subtile)
+            int kind;
             if (band) {
-                if (a >= wLmax && a + 15 <= wHmin) {
-                    ci = floatx4{0.f, 0.f, 0.f, 0.f};
-                } else if (a + 15 <= wHmin) {  // below every row's diagonal: lower bound only
-                    const int tl = lo - a - lane_off;
+                const int last = base + BN - 1;
+                if (base > R.whi || last < R.wlo) kind = 0;
+                else if (base + 15 < R.wlo || last - 15 > R.whi) kind = 5;
+                else if (base >= R.wLmax && last <= R.wHmin) kind = 1;
+                else if (last <= R.wHmin) kind = 2;
+                else kind = 3;
+            } else {
+                if (base >= R.wcmax) kind = 0;
+                else if (!has_bias && base + BN - 1 < R.wcmin) kind = 4;
+                else kind = 5;
+            }
+            gact[u] = kind != 0;
+#pragma unroll
+            for (int stt = 0; stt < NST; ++stt) act[u][stt] = kind != 0;
+            const floatx4 zero = floatx4{0.f, 0.f, 0.f, 0.f};
+            if (kind == 1 || kind == 4) {
+#pragma unroll
+                for (int stt = 0; stt < NST; ++stt) {
+                    KOp<T, D> ko;
+                    ko.load(kl, KT::RS, stt * 16, lane);
+                    S[u][stt] = ko.dot(qr[u], zero);
+                }
+            } else if (kind == 2) {
+#pragma unroll
+                for (int stt = 0; stt < NST; ++stt) {
+                    const int tl = R.lo - (base + stt * 16) - lane_off;
+                    floatx4 ci;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) ci[r] = r < tl ? NEG : 0.f;
-                } else {
-                    const int tl = lo - a - lane_off, th = hi - a - lane_off;
+                    KOp<T, D> ko;
+                    ko.load(kl, KT::RS, stt * 16, lane);
+                    S[u][stt] = ko.dot(qr[u], ci);
+                }
+            } else if (kind == 3) {
+#pragma unroll
+                for (int stt = 0; stt < NST; ++stt) {
+                    const int tl = R.lo - (base + stt * 16) - lane_off, th = R.hi - (base + stt * 16) - lane_off;
+                    floatx4 ci;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) ci[r] = (r < tl || r > th) ? NEG : 0.f;
+                    KOp<T, D> ko;
+                    ko.load(kl, KT::RS, stt * 16, lane);
+                    S[u][stt] = ko.dot(qr[u], ci);
                 }
-            } else {
-                floatx4 bv = floatx4{0.f, 0.f, 0.f, 0.f};
-                if (has_bias) {
-                    float braw[4];
+            } else if (kind == 5) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) braw[r] = p.lbias[set_off + min(a + lane_off + r, K - 1)];
+                for (int stt = 0; stt < NST; ++stt) {
+                    const int a = base + stt * 16;
+                    act[u][stt] = band ? (a <= R.whi && a + 15 >= R.wlo) : (a < R.wcmax);
+                    if (!act[u][stt]) {
+                        S[u][stt] = floatx4{NEG, NEG, NEG, NEG};
+                        continue;
+                    }
+                    floatx4 ci;
+                    if (band) {
+                        const int tl = R.lo - a - lane_off, th = R.hi - a - lane_off;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) bv[r] = a + lane_off + r < K ? braw[r] * inv_scale : 0.f;
-                }
-                if (a + 15 < wcmin) {
-                    ci = bv;
-                } else {
-                    const int tc = cnt - a - lane_off;
+                        for (int r = 0; r < 4; ++r) ci[r] = (r < tl || r > th) ? NEG : 0.f;
+                    } else {
+                        floatx4 bv = zero;
+                        if (has_bias) {
+                            float braw[4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ci[r] = r < tc ? bv[r] : NEG;
+                            for (int r = 0; r < 4; ++r) braw[r] = p.lbias[set_off + min(a + lane_off + r, K - 1)];
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) bv[r] = a + lane_off + r < K ? braw[r] * inv_scale : 0.f;
+                        }
+                        const int tc = R.cnt - a - lane_off;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) ci[r] = r < tc ? bv[r] : NEG;
+                    }
+                    KOp<T, D> ko;
+                    ko.load(kl, KT::RS, stt * 16, lane);
+                    S[u][stt] = ko.dot(qr[u], ci);
                 }
             }
-            S[stt] = dot_rows<T, D>(Ks[buf], KT::RS, stt * 16, lane, qr, ci);
         }
-        // online softmax over the chunk
-        float mx = NEG;
+        // online softmax per group (skipped by groups with no row in the chunk)
 #pragma unroll
-        for (int stt = 0; stt < NST; ++stt)
+        for (int u = 0; u < RG; ++u) {
+            if (!gact[u]) continue;
+            float mx = NEG;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, S[stt][r]);
-        mx = max_g4(mx);
-        const float mnew = fmaxf(m_run, mx);
-        if (__any(mnew > m_run + thr)) {
-            const float alpha = m_run == NEG ? 0.f : __builtin_amdgcn_exp2f((m_run - mnew) * c2);
+            for (int stt = 0; stt < NST; ++stt)
 #pragma unroll
-            for (int dt = 0; dt < D / 16; ++dt) acc[dt] *= alpha;
-            lacc *= alpha;
-            l_run *= alpha;
-            m_run = mnew;
+                for (int r = 0; r < 4; ++r) mx = fmaxf(mx, S[u][stt][r]);
+            mx = max_g4(mx);
+            const float mnew = fmaxf(m_run[u], mx);
+            if (__any(mnew > m_run[u] + thr)) {
+                const float alpha = m_run[u] == NEG ? 0.f : __builtin_amdgcn_exp2f((m_run[u] - mnew) * c2);
+#pragma unroll
+                for (int dt = 0; dt < D / 16; ++dt) acc[u][dt] *= alpha;
+                lacc[u] *= alpha;
+                l_run[u] *= alpha;
+                m_run[u] = mnew;
+            }
+            const float msc = m_run[u] == NEG ? 0.f : m_run[u] * c2;
+#pragma unroll
+            for (int stt = 0; stt < NST; ++stt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) S[u][stt][r] = __builtin_amdgcn_exp2f(S[u][stt][r] * c2 - msc);
         }
-        const float msc = m_run == NEG ? 0.f : m_run * c2;
-#pragma unroll
-        for (int stt = 0; stt < NST; ++stt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) S[stt][r] = __builtin_amdgcn_exp2f(S[stt][r] * c2 - msc);
         if constexpr (kHalf) {
             const typename Vec8<T>::type ones = ones8<T>();
 #pragma unroll
-            for (int hp = 0; hp < NST / 2; ++hp)
-                if (act[2 * hp] || act[2 * hp + 1]) {
-                    auto b = acc_tr<T, D>(Vs[buf], KT::RS, hp * 32, lane, S[2 * hp], S[2 * hp + 1], acc);
-                    lacc = mma(ones, b, lacc);
+            for (int hp = 0; hp < NST / 2; ++hp) {
+                bool pa[RG], any = false;
+#pragma unroll
+                for (int u = 0; u < RG; ++u) {
+                    pa[u] = act[u][2 * hp] || act[u][2 * hp + 1];
+                    any |= pa[u];
                 }
+                if (!any) continue;
+                VOp<T, D> vo;
+                vo.load(Vs[buf], KT::RS, hp * 32, lane);
+#pragma unroll
+                for (int u = 0; u < RG; ++u)
+                    if (pa[u]) {
+                        const auto bp = vo.acc(S[u][2 * hp], S[u][2 * hp + 1], acc[u]);
+                        lacc[u] = mma(ones, bp, lacc[u]);
+                    }
+            }
         } else {
 #pragma unroll
-            for (int stt = 0; stt < NST; ++stt)
-                if (act[stt]) {
-                    l_run += S[stt][0] + S[stt][1] + S[stt][2] + S[stt][3];
-                    acc_rm32<D>((const float*)Vs[buf], KT::RS, stt * 16, lane, S[stt], acc);
-                }
+            for (int stt = 0; stt < NST; ++stt) {
+                bool any = false;
+#pragma unroll
+                for (int u = 0; u < RG; ++u) any |= act[u][stt];
+                if (!any) continue;
+                VOp<T, D> vo;
+                vo.load(Vs[buf], KT::RS, stt * 16, lane);
+#pragma unroll
+                for (int u = 0; u < RG; ++u)
+                    if (act[u][stt]) {
+                        l_run[u] += S[u][stt][0] + S[u][stt][1] + S[u][stt][2] + S[u][stt][3];
+                        vo.acc(S[u][stt], acc[u]);
+                    }
+            }
         }
         if (c + 1 < nchunks) {
             kt.store(Ks[buf ^ 1], tid);
@@ -255,34 +464,59 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
         __syncthreads();
     }
 
-    const float l_tot = kHalf ? lacc[0] : sum_g4(l_run);
-    if (valid) {
+#pragma unroll
+    for (int u = 0; u < RG; ++u) {
+        const float l_tot = kHalf ? lacc[u][0] : sum_g4(l_run[u]);
+        if (!rg[u].valid) continue;
         const float inv = 1.0f / l_tot;
-        T* orow = (T*)p.o + (int64_t)(st + i) * p.o_st + (int64_t)h * p.o_sh;
+        T* orow = (T*)p.o + (int64_t)(st + rg[u].i) * p.o_st + (int64_t)h * p.o_sh;
 #pragma unroll
         for (int dt = 0; dt < D / 16; ++dt) {
             T ov[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) ov[r] = from_float<T>(acc[dt][r] * inv);
+            for (int r = 0; r < 4; ++r) ov[r] = from_float<T>(acc[u][dt][r] * inv);
             if constexpr (kHalf) *(uint2*)(orow + dt * 16 + lane_off) = *(const uint2*)ov;
             else *(floatx4*)(orow + dt * 16 + lane_off) = *(const floatx4*)ov;
         }
-        if (g == 0) p.lse_out[(int64_t)(st + i) * p.n_heads + h] = m_run * p.scale + __logf(l_tot);
+        if (g == 0) p.lse_out[(int64_t)(st + rg[u].i) * p.n_heads + h] = m_run[u] * p.scale + __logf(l_tot);
     }
+}
+
+// two row groups per wave where the registers allow (16-bit, head_dim 64) and a
+// block of 128 rows stays within one landmark set (block_size a multiple of 128)
+constexpr int kFwdGroups = 1;
+template <typename T, int D>
+static int fwd_groups(const AttnParams& p) {
+    return (kFwdGroups == 2 && sizeof(T) == 2 && D == 64 && (p.block_size == 0 || p.block_size % 128 == 0)) ? 2 : 1;
+}
+
+template <typename T, int D>
+static void fwd_run(const AttnParams& p, hipStream_t stream) {
+    const int rg = fwd_groups<T, D>(p);
+    const int total = p.n_heads * p.num_seqs * ceil_div(p.n_tiles, rg);
+    if constexpr (sizeof(T) == 2 && D == 64) {
+        if (rg == 2) {
+            DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 2>), dim3(total), dim3(256), 0, stream, p);
+            return;
+        }
+    }
+    DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 1>), dim3(total), dim3(256), 0, stream, p);
 }
 
 template <typename T>
 static hipError_t fwd_dispatch(const AttnParams& p, hipStream_t stream) {
-    const int total = p.n_heads * p.num_seqs * p.n_tiles;
-    if (total == 0) return hipSuccess;
-    if (p.head_dim == 64)
-        DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, 64>), dim3(total), dim3(256), 0, stream, p);
-    else
-        DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, 128>), dim3(total), dim3(256), 0, stream, p);
+    if (p.n_heads * p.num_seqs * p.n_tiles == 0) return hipSuccess;
+    const hipError_t e = plan_launch(p, stream);
+    if (e != hipSuccess) return e;
+    if (p.head_dim == 64) fwd_run<T, 64>(p, stream);
+    else fwd_run<T, 128>(p, stream);
     return hipGetLastError();
 }
 
-hipError_t fwd_launch(const AttnParams& p, hipStream_t stream) {
+hipError_t fwd_launch(AttnParams p, void* ws, hipStream_t stream) {
+    char* w = (char*)ws;
+    plan_carve(p, w);
+    p.seq_wmax = nullptr;
     if (p.dtype == DSALT_DTYPE_BF16) return fwd_dispatch<bf16>(p, stream);
     if (p.dtype == DSALT_DTYPE_F16) return fwd_dispatch<f16>(p, stream);
     return fwd_dispatch<float>(p, stream);

@@ -139,6 +139,9 @@ dsalt::AttnParams attn_common(const dsalt_problem& q, float scale) {
     p.dtype = q.dtype;
     p.n_tiles = (q.max_seqlen + 63) / 64;
     p.scale = scale;
+    p.c2 = scale * 1.4426950408889634f;
+    p.inv_scale = 1.0f / scale;
+    p.thr = 8.0f / p.c2;
     return p;
 }
 
@@ -171,8 +174,8 @@ int dsalt_select(const dsalt_select_args* a, dsalt_stream_t stream) {
 }
 
 size_t dsalt_fwd_workspace_bytes(const dsalt_fwd_args* a) {
-    (void)a;
-    return 0;
+    if (!a || check_problem(a->p, true)) return 0;
+    return dsalt::plan_bytes(attn_common(a->p, 1.0f));
 }
 
 int dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream) {
@@ -205,7 +208,10 @@ int dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream) {
     p.cu = a->cu_seqlens;
     p.lmk = a->lmk_idx;
     p.lbias = a->lmk_bias;
-    return hip_status(dsalt::fwd_launch(p, (hipStream_t)stream), "dsalt_fwd");
+    const size_t need = dsalt::plan_bytes(p);
+    if (!a->workspace || a->workspace_bytes < need)
+        return fail(DSALT_ERR_WORKSPACE, "forward needs %zu workspace bytes, got %zu", need, a->workspace_bytes);
+    return hip_status(dsalt::fwd_launch(p, a->workspace, (hipStream_t)stream), "dsalt_fwd");
 }
 
 static int bwd_params(const dsalt_bwd_args* a, dsalt::AttnParams* out) {

@@ -45,6 +45,28 @@ __device__ __forceinline__ int max16(int v) {
     for (int o = 1; o < 16; o <<= 1) v = max(v, wave_xor(v, o));
     return v;
 }
+// reductions within each 16-lane row through DPP row rotations (VALU only)
+__device__ __forceinline__ int dpp_ror(int v, int n) {
+    switch (n) {
+        case 1: return __builtin_amdgcn_update_dpp(0, v, 0x121, 0xf, 0xf, false);
+        case 2: return __builtin_amdgcn_update_dpp(0, v, 0x122, 0xf, 0xf, false);
+        case 4: return __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false);
+        default: return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false);
+    }
+}
+__device__ __forceinline__ int row_min16(int v) {
+    v = min(v, dpp_ror(v, 1));
+    v = min(v, dpp_ror(v, 2));
+    v = min(v, dpp_ror(v, 4));
+    return min(v, dpp_ror(v, 8));
+}
+__device__ __forceinline__ int row_max16(int v) {
+    v = max(v, dpp_ror(v, 1));
+    v = max(v, dpp_ror(v, 2));
+    v = max(v, dpp_ror(v, 4));
+    return max(v, dpp_ror(v, 8));
+}
+
 // reductions over the 4 lanes l, l^16, l^32, l^48, with gfx950's lane-swap
 // instructions (VALU, no LDS round trip): permlane32_swap(x, x) yields the lower
 // and the upper 32 lanes each broadcast to both halves; permlane16_swap(y, y)

@@ -208,6 +208,72 @@ __device__ __forceinline__ void acc_rm32(const float* lds, int rs, int kb, int l
         for (int r = 0; r < 4; ++r) acc[dt] = mma(lds[(kb + 4 * g + r) * rs + dt * 16 + c], p[r], acc[dt]);
 }
 
+// The LDS operand of one 16-row subtile for products reduced over D, fetched
+// once and applied to several register row sets (row groups of a wave).
+template <typename T, int D>
+struct KOp {
+    typename Vec8<T>::type a[D / 32];
+    __device__ __forceinline__ void load(const T* lds, int rs, int row0, int lane) {
+#pragma unroll
+        for (int dc = 0; dc < D / 32; ++dc) a[dc] = row_op16<T>(lds, rs, row0 + (lane & 15), dc, lane >> 4);
+    }
+    __device__ __forceinline__ floatx4 dot(const RowReg<T, D>& reg, floatx4 acc) const {
+#pragma unroll
+        for (int dc = 0; dc < D / 32; ++dc) acc = mma(a[dc], reg.x[dc], acc);
+        return acc;
+    }
+};
+template <int D>
+struct KOp<float, D> {
+    float a[D / 4];
+    __device__ __forceinline__ void load(const float* lds, int rs, int row0, int lane) {
+        row_op32<D>(lds, rs, row0 + (lane & 15), lane >> 4, a);
+    }
+    __device__ __forceinline__ floatx4 dot(const RowReg<float, D>& reg, floatx4 acc) const {
+#pragma unroll
+        for (int m = 0; m < D / 4; ++m) acc = mma(a[m], reg.x[m], acc);
+        return acc;
+    }
+};
+
+// The transposed LDS operand of a slab of tokens for products reduced over
+// tokens (P V, dS K, ...): 16-bit types take 32 tokens kb..kb+31 through the
+// transpose read, fp32 16 tokens kb..kb+15 element by element.
+template <typename T, int D>
+struct VOp {
+    static constexpr int TOK = 32;
+    typename Vec8<T>::type a[D / 16];
+    __device__ __forceinline__ void load(const T* lds, int rs, int kb, int lane) {
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) a[dt] = tr_op16<T>(lds, rs, dt * 16, kb, lane);
+    }
+    // acc += slab^T x (p0 | p1); returns the packed P operand
+    __device__ __forceinline__ typename Vec8<T>::type acc(floatx4 p0, floatx4 p1, floatx4 (&c)[D / 16]) const {
+        const typename Vec8<T>::type b = pack8<T>(p0, p1);
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) c[dt] = mma(a[dt], b, c[dt]);
+        return b;
+    }
+};
+template <int D>
+struct VOp<float, D> {
+    static constexpr int TOK = 16;
+    float a[D / 16][4];
+    __device__ __forceinline__ void load(const float* lds, int rs, int kb, int lane) {
+        const int g = lane >> 4, c = lane & 15;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) a[dt][r] = lds[(kb + 4 * g + r) * rs + dt * 16 + c];
+    }
+    __device__ __forceinline__ void acc(floatx4 p, floatx4 (&c)[D / 16]) const {
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) c[dt] = mma(a[dt][r], p[r], c[dt]);
+    }
+};
+
 template <typename T> __device__ __forceinline__ typename Vec8<T>::type ones8() {
     typename Vec8<T>::type v;
 #pragma unroll

@@ -194,6 +194,8 @@ def attention_forward(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias=None, *, scale=N
     if T == 0:
         return out, lse
     L = _lib.load()
+    ws = _workspace(L.dsalt_fwd_workspace_bytes(ctypes.byref(a)), dev)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     _lib.check("dsalt_fwd", L.dsalt_fwd(ctypes.byref(a), _stream(dev)))
     return out, lse
 
