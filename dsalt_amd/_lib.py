@@ -81,6 +81,7 @@ SIGNATURES = {
     "dsalt_select_workspace_bytes": ([ctypes.POINTER(SelectArgs)], _sz),
     "dsalt_select": ([ctypes.POINTER(SelectArgs), _vp], ctypes.c_int),
     "dsalt_select_with_border_cap": ([ctypes.POINTER(SelectArgs), _vp, ctypes.c_int], ctypes.c_int),
+    "dsalt_select_workspace_bytes_cap": ([ctypes.POINTER(SelectArgs), ctypes.c_int], _sz),
     "dsalt_fwd_workspace_bytes": ([ctypes.POINTER(FwdArgs)], _sz),
     "dsalt_fwd": ([ctypes.POINTER(FwdArgs), _vp], ctypes.c_int),
     "dsalt_bwd_workspace_bytes": ([ctypes.POINTER(BwdArgs)], _sz),

@@ -158,14 +158,19 @@ size_t dsalt_select_workspace_bytes(const dsalt_select_args* a) {
     return dsalt::select_workspace(select_params(a));
 }
 
+size_t dsalt_select_workspace_bytes_cap(const dsalt_select_args* a, int border_cap) {
+    if (check_select(a) || border_cap < 1) return 0;
+    return dsalt::select_workspace_cap(select_params(a), border_cap);
+}
+
 int dsalt_select_with_border_cap(const dsalt_select_args* a, dsalt_stream_t stream, int border_cap) {
     int rc = check_select(a);
     if (rc) return rc;
+    if (border_cap < 1) return fail(DSALT_ERR_INVALID, "border_cap must be >= 1");
     dsalt::SelectParams p = select_params(a);
-    size_t need = dsalt::select_workspace(p);
+    size_t need = dsalt::select_workspace_cap(p, border_cap);
     if (!a->workspace || a->workspace_bytes < need)
         return fail(DSALT_ERR_WORKSPACE, "selection needs %zu workspace bytes, got %zu", need, a->workspace_bytes);
-    if (border_cap < 1) return fail(DSALT_ERR_INVALID, "border_cap must be >= 1");
     return hip_status(dsalt::select_launch(p, a->workspace, (hipStream_t)stream, border_cap), "dsalt_select");
 }
 

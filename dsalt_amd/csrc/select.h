@@ -37,6 +37,7 @@ struct GatherParams {
 };
 
 size_t select_workspace(const SelectParams& p);
+size_t select_workspace_cap(const SelectParams& p, int border_cap);  // workspace of a border_cap call
 hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, int border_cap);
 hipError_t gather_launch(const GatherParams& p, hipStream_t stream);
 

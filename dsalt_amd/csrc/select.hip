@@ -5,18 +5,25 @@
 // block-causal _select (results/causal_landmark_check.py:82-113).
 //
 // Pipeline (all stream-ordered, no host sync):
-//   sel_norms   one wave per token: |h_t| and |v_{t,g}| (fp64 sums of squares,
-//               lane-strided 16-byte chunks + xor butterfly), rounded to fp32 and
-//               then to the input dtype.
+//   sel_norms   one wave per token: |h_t| and |v_{t,g}| as fp64 sums of squares
+//               (lane-strided 16-byte chunks + xor butterfly); the block then
+//               takes the square roots of its tokens' sums lane-parallel and
+//               rounds them to fp32 and then to the input dtype.
 //   sel_sums    one 256-thread block per (range, signal): fp64 S1, S2 by 256
-//               strided partials and a halving tree.
-//   sel_stats   mean / unbiased std per scope, or per block-causal prefix by
-//               adding whole-block sums in block order.
-//   sel_z       (global) z = fp32((a - mean)/std) in fp64, optional API outputs.
-//   sel_topk    one 1024-thread block per landmark set: radix select on the
-//               64-bit key (order(score) << 32 | ~index) -- so ties go to the
-//               lower index -- 8 bits per pass until the boundary bin fits in
-//               LDS, then a bitonic sort of that bin; output ascending indices.
+//               strided partials and a halving tree; in the global variant the
+//               same block turns them into mean / unbiased std.
+//   sel_stats   (block-causal) mean / std per prefix by adding whole-block sums
+//               in block order.
+//   sel_z       (global) z = fp32((a - mean)/std) in fp64, one thread per
+//               (token, signal); sel_scores the optional per-head scores.
+//   top-k on the 64-bit key (order(score) << 32 | ~index), so ties go to the
+//   lower index; output ascending indices:
+//     global:   sel_part sorts the keys of each part of a set's candidates in
+//               LDS and keeps its best k; sel_merge sorts the survivors of up
+//               to G parts per block, level by level, and writes the indices.
+//     block:    sel_topk, one 1024-thread block per landmark set: radix select
+//               8 bits per pass until the boundary bin fits in LDS, then a
+//               bitonic sort of that bin.
 // The arithmetic order above is the canonical one that the CPU oracle
 // restates; this file is compiled with -ffp-contract=off.
 #include "common.h"
@@ -36,16 +43,23 @@ __device__ __forceinline__ int pow2ceil64(int n) {
 }
 
 // ------------------------------------------------------------------ norms
+constexpr int kNormTPW = 2;              // tokens per wave
+constexpr int kNormTB = 4 * kNormTPW;    // tokens per 256-thread block
+
 template <typename T>
 __global__ __launch_bounds__(256) void sel_norms_kernel(SelectParams p, float* nx, float* nv) {
     constexpr int VW = 16 / (int)sizeof(T);
     typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-    const int lane = threadIdx.x & 63;
-    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    extern __shared__ double ss[];  // [kNormTB][1 + n_kv] sums of squares
+    const int nsig = 1 + p.n_kv_heads;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t0 = blockIdx.x * kNormTB;
     const int hch = p.hidden / VW, gh = pow2ceil64(hch);
     const int vch = p.head_dim / VW, gv = pow2ceil64(vch);
     const int hpp = 64 / gv;  // value heads per pass
-    for (int t = (blockIdx.x * blockDim.x + threadIdx.x) >> 6; t < p.total_len; t += nwaves) {
+    for (int i = 0; i < kNormTPW; ++i) {
+        const int tl = wave * kNormTPW + i, t = t0 + tl;
+        if (t >= p.total_len) break;
         // hidden-state norm
         const T* hr = (const T*)p.h + (int64_t)t * p.h_stride_t;
         double acc = 0.0;
@@ -54,14 +68,14 @@ __global__ __launch_bounds__(256) void sel_norms_kernel(SelectParams p, float* n
                 u4 raw = *(const u4*)(hr + ch * VW);
                 const T* e = (const T*)&raw;
 #pragma unroll
-                for (int i = 0; i < VW; ++i) {
-                    double x = (double)to_float(e[i]);
+                for (int q = 0; q < VW; ++q) {
+                    double x = (double)to_float(e[q]);
                     acc = __dadd_rn(acc, __dmul_rn(x, x));
                 }
             }
         }
         for (int off = gh >> 1; off >= 1; off >>= 1) acc = __dadd_rn(acc, wave_xor(acc, off));
-        if (lane == 0) nx[t] = round_norm<T>((float)canon_sqrt64(acc));
+        if (lane == 0) ss[tl * nsig] = acc;
         // value-vector norms, gv lanes per kv head
         for (int g0 = 0; g0 < p.n_kv_heads; g0 += hpp) {
             int g = g0 + lane / gv, sub = lane % gv;
@@ -71,15 +85,22 @@ __global__ __launch_bounds__(256) void sel_norms_kernel(SelectParams p, float* n
                 u4 raw = *(const u4*)(vr + sub * VW);
                 const T* e = (const T*)&raw;
 #pragma unroll
-                for (int i = 0; i < VW; ++i) {
-                    double x = (double)to_float(e[i]);
+                for (int q = 0; q < VW; ++q) {
+                    double x = (double)to_float(e[q]);
                     a2 = __dadd_rn(a2, __dmul_rn(x, x));
                 }
             }
             for (int off = gv >> 1; off >= 1; off >>= 1) a2 = __dadd_rn(a2, wave_xor(a2, off));
-            if (sub == 0 && g < p.n_kv_heads)
-                nv[(int64_t)g * p.total_len + t] = round_norm<T>((float)canon_sqrt64(a2));
+            if (sub == 0 && g < p.n_kv_heads) ss[tl * nsig + 1 + g] = a2;
         }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < kNormTB * nsig; idx += 256) {
+        const int tl = idx / nsig, sig = idx % nsig, t = t0 + tl;
+        if (t >= p.total_len) continue;
+        const float nr = round_norm<T>((float)canon_sqrt64(ss[idx]));
+        if (sig == 0) nx[t] = nr;
+        else nv[(int64_t)(sig - 1) * p.total_len + t] = nr;
     }
 }
 
@@ -105,18 +126,43 @@ __device__ __forceinline__ void range_of(const SelectParams& p, int r, int& r0, 
     }
 }
 
+__device__ __forceinline__ void mean_std(double s1, double s2, int n, double& mean, double& sd) {
+    double m = __ddiv_rn(s1, (double)n);
+    double den = (double)(n - 1 > 1 ? n - 1 : 1);
+    double var = __ddiv_rn(__dadd_rn(s2, -__dmul_rn(__dmul_rn((double)n, m), m)), den);
+    if (!(var > 0.0)) var = 0.0;
+    double s = canon_sqrt64(var);
+    if (s < 1e-6) s = 1e-6;
+    mean = m;
+    sd = s;
+}
+
 __global__ __launch_bounds__(256) void sel_sums_kernel(SelectParams p, const float* nx, const float* nv,
-                                                       double* sums) {
+                                                       double* sums, double* stats) {
+    // U loads in flight per thread (one memory round trip per 256*U values).  The
+    // summation order is the canonical one; reads past the range return zero, and
+    // adding +0 to these sums of non-negative norms changes no bit.
+    constexpr int U = 64;
     __shared__ double a1[256], a2[256];
     const int r = blockIdx.x, sig = blockIdx.y, t = threadIdx.x;
     const float* x = sig == 0 ? nx : nv + (int64_t)(sig - 1) * p.total_len;
     int r0, r1;
     range_of(p, r, r0, r1);
     double s1 = 0.0, s2 = 0.0;
-    for (int j = r0 + t; j < r1; j += 256) {
-        double v = (double)x[j];
-        s1 = __dadd_rn(s1, v);
-        s2 = __dadd_rn(s2, __dmul_rn(v, v));
+    for (int j0 = r0; j0 < r1; j0 += 256 * U) {
+        const int n = min(256 * U, r1 - j0);
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(x + j0), (short)0, (int)(n * sizeof(float)), 0x00020000);
+        float xv[U];
+#pragma unroll
+        for (int k = 0; k < U; ++k)
+            xv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)(t + 256 * k) * 4u, 0, 0));
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+            double v = (double)xv[k];
+            s1 = __dadd_rn(s1, v);
+            s2 = __dadd_rn(s2, __dmul_rn(v, v));
+        }
     }
     a1[t] = s1;
     a2[t] = s2;
@@ -129,38 +175,25 @@ __global__ __launch_bounds__(256) void sel_sums_kernel(SelectParams p, const flo
         __syncthreads();
     }
     if (t == 0) {
-        int nsig = 1 + p.n_kv_heads;
-        sums[((int64_t)r * nsig + sig) * 2 + 0] = a1[0];
-        sums[((int64_t)r * nsig + sig) * 2 + 1] = a2[0];
+        const int nsig = 1 + p.n_kv_heads;
+        const int64_t o = ((int64_t)r * nsig + sig) * 2;
+        sums[o] = a1[0];
+        sums[o + 1] = a2[0];
+        if (stats) {  // global variant: statistics of this range
+            double m = 0.0, sd = 1.0;
+            if (r1 > r0) mean_std(a1[0], a2[0], r1 - r0, m, sd);
+            stats[o] = m;
+            stats[o + 1] = sd;
+        }
     }
 }
 
-__device__ __forceinline__ void mean_std(double s1, double s2, int n, double& mean, double& sd) {
-    double m = __ddiv_rn(s1, (double)n);
-    double den = (double)(n - 1 > 1 ? n - 1 : 1);
-    double var = __ddiv_rn(__dadd_rn(s2, -__dmul_rn(__dmul_rn((double)n, m), m)), den);
-    if (!(var > 0.0)) var = 0.0;
-    double s = canon_sqrt64(var);
-    if (s < 1e-6) s = 1e-6;
-    mean = m;
-    sd = s;
-}
-
-// stats[(r * nsig + sig) * 2] = {mean, std}; r indexes ranges (global) or
-// (sequence, block) sets (block-causal, prefix over earlier blocks).
-__global__ void sel_stats_kernel(SelectParams p, const double* sums, double* stats, int nranges) {
+// stats[(r * nsig + sig) * 2] = {mean, std} of the block-causal prefixes: r
+// indexes (sequence, block) sets, statistics over the blocks before it.
+__global__ void sel_stats_kernel(SelectParams p, const double* sums, double* stats) {
     const int nsig = 1 + p.n_kv_heads;
     const int id = blockIdx.x * blockDim.x + threadIdx.x;
-    if (p.select_mode == DSALT_SELECT_GLOBAL) {
-        if (id >= nranges * nsig) return;
-        int r = id / nsig;
-        int r0, r1;
-        range_of(p, r, r0, r1);
-        double m = 0.0, sd = 1.0;
-        if (r1 > r0) mean_std(sums[id * 2], sums[id * 2 + 1], r1 - r0, m, sd);
-        stats[id * 2] = m;
-        stats[id * 2 + 1] = sd;
-    } else {
+    {
         if (id >= p.num_seqs * nsig) return;
         int s = id / nsig, sig = id % nsig;
         int st, len;
@@ -198,29 +231,46 @@ __device__ __forceinline__ uint32_t order_key(float s) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// global variant: z per token (head-major zv for the selection), API outputs
+// global variant: z per (token, signal), head-major zv for the selection, API outputs
 __global__ __launch_bounds__(256) void sel_z_kernel(SelectParams p, const float* nx, const float* nv,
                                                     const double* stats, float* zx, float* zv) {
+    const int s = blockIdx.y, sig = blockIdx.z;
+    const int nsig = 1 + p.n_kv_heads;
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
+    const int t = st + blockIdx.x * 256 + threadIdx.x;
+    if (t >= st + len) return;
+    const int r = p.stats_scope == DSALT_STATS_PACKED ? 0 : s;
+    const double* sr = stats + ((int64_t)r * nsig + sig) * 2;
+    if (sig == 0) {
+        const float z = zscore(nx[t], sr[0], sr[1]);
+        zx[t] = z;
+        if (p.z_x) p.z_x[t] = z;
+    } else {
+        const int g = sig - 1;
+        const float z = zscore(nv[(int64_t)g * p.total_len + t], sr[0], sr[1]);
+        zv[(int64_t)g * p.total_len + t] = z;
+        if (p.z_v) p.z_v[(int64_t)t * p.n_kv_heads + g] = z;
+    }
+}
+
+// global variant, optional output: per-head scores [T, H]
+__global__ __launch_bounds__(256) void sel_scores_kernel(SelectParams p, const float* nx, const float* nv,
+                                                         const double* stats) {
     const int s = blockIdx.y;
     const int nsig = 1 + p.n_kv_heads;
     int st, len;
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
-    int t = st + blockIdx.x * 256 + threadIdx.x;
+    const int t = st + blockIdx.x * 256 + threadIdx.x;
     if (t >= st + len) return;
-    int r = p.stats_scope == DSALT_STATS_PACKED ? 0 : s;
+    const int r = p.stats_scope == DSALT_STATS_PACKED ? 0 : s;
     const double* sr = stats + (int64_t)r * nsig * 2;
-    float zxt = zscore(nx[t], sr[0], sr[1]);
-    zx[t] = zxt;
-    if (p.z_x) p.z_x[t] = zxt;
-    for (int g = 0; g < p.n_kv_heads; ++g) {
-        float z = zscore(nv[(int64_t)g * p.total_len + t], sr[2 * (g + 1)], sr[2 * (g + 1) + 1]);
-        zv[(int64_t)g * p.total_len + t] = z;
-        if (p.z_v) p.z_v[(int64_t)t * p.n_kv_heads + g] = z;
-    }
-    if (p.scores) {
-        int rep = p.n_heads / p.n_kv_heads;
-        for (int h = 0; h < p.n_heads; ++h)
-            p.scores[(int64_t)t * p.n_heads + h] = mix_score(p.alpha[h], zv[(int64_t)(h / rep) * p.total_len + t], zxt);
+    const float zxt = zscore(nx[t], sr[0], sr[1]);
+    const int rep = p.n_heads / p.n_kv_heads;
+    for (int h = 0; h < p.n_heads; ++h) {
+        const int g = h / rep;
+        const float zvt = zscore(nv[(int64_t)g * p.total_len + t], sr[2 * (g + 1)], sr[2 * (g + 1) + 1]);
+        p.scores[(int64_t)t * p.n_heads + h] = mix_score(p.alpha[h], zvt, zxt);
     }
 }
 
@@ -260,10 +310,12 @@ struct KeyFn {
     }
 };
 
+// bitonic sorts of n (a power of two) LDS elements by NT threads
+template <int NT>
 __device__ void bitonic_desc_u64(unsigned long long* a, int n, int tid) {
     for (int size = 2; size <= n; size <<= 1)
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = tid; i < (n >> 1); i += kSelThreads) {
+            for (int i = tid; i < (n >> 1); i += NT) {
                 int lo = (i / stride) * 2 * stride + (i % stride), hi = lo + stride;
                 bool desc = (lo & size) == 0;
                 unsigned long long x = a[lo], y = a[hi];
@@ -276,10 +328,11 @@ __device__ void bitonic_desc_u64(unsigned long long* a, int n, int tid) {
         }
 }
 
+template <int NT>
 __device__ void bitonic_asc_i32(int* a, int n, int tid) {
     for (int size = 2; size <= n; size <<= 1)
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = tid; i < (n >> 1); i += kSelThreads) {
+            for (int i = tid; i < (n >> 1); i += NT) {
                 int lo = (i / stride) * 2 * stride + (i % stride), hi = lo + stride;
                 bool asc = (lo & size) == 0;
                 int x = a[lo], y = a[hi];
@@ -290,6 +343,163 @@ __device__ void bitonic_asc_i32(int* a, int n, int tid) {
             }
             __syncthreads();
         }
+}
+
+// Descending bitonic sort of N = NT*E 64-bit keys held E per thread (element
+// i = tid*E + e): partners within a thread swap in registers, partners in
+// another lane of the wave through lane shuffles, others through LDS (`lds`
+// holds N keys, stored key-slot-major so that a wave's accesses fall in
+// distinct banks).
+template <int NT, int E>
+__device__ void block_sort_desc(unsigned long long (&k)[E], unsigned long long* lds, int tid) {
+    constexpr int N = NT * E;
+#pragma unroll
+    for (int size = 2; size <= N; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride < E) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const int f = e ^ stride;
+                    if (f > e) {
+                        const bool desc = ((tid * E + e) & size) == 0;
+                        const unsigned long long x = k[e], y = k[f];
+                        const bool sw = desc ? (x < y) : (x > y);
+                        k[e] = sw ? y : x;
+                        k[f] = sw ? x : y;
+                    }
+                }
+            } else if (stride / E < 64) {  // partner lane in the same wave
+                const int m = stride / E;
+                const bool lower = (tid & m) == 0;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const int i = tid * E + e;
+                    const unsigned long long x = k[e];
+                    const uint32_t ylo = (uint32_t)__shfl_xor((int)(uint32_t)x, m, 64);
+                    const uint32_t yhi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), m, 64);
+                    const unsigned long long y = ((unsigned long long)yhi << 32) | ylo;
+                    const bool desc = (i & size) == 0;
+                    const unsigned long long hi = x > y ? x : y, lo = x > y ? y : x;
+                    k[e] = (lower == desc) ? hi : lo;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) lds[e * NT + tid] = k[e];
+                __syncthreads();
+                const int pt = tid ^ (stride / E);
+                const bool lower = (tid & (stride / E)) == 0;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const int i = tid * E + e;
+                    const unsigned long long x = k[e], y = lds[e * NT + pt];
+                    const bool desc = (i & size) == 0;
+                    const unsigned long long hi = x > y ? x : y, lo = x > y ? y : x;
+                    k[e] = (lower == desc) ? hi : lo;
+                }
+                __syncthreads();
+            }
+        }
+    }
+}
+
+// ------------------------------------------- global variant: parts + merges
+constexpr int kPartMax = 2048;   // candidates per part (keys sorted in LDS)
+constexpr int kMergeMax = 4096;  // keys sorted per merge block (1024 threads x 4)
+
+__device__ __forceinline__ KeyFn global_key(const SelectParams& p, const float* zx, const float* zv, int st, int h) {
+    KeyFn key;
+    key.w = p.w;
+    key.total_len = p.total_len;
+    key.st = st;
+    key.h = h;
+    key.rep_g = h / (p.n_heads / p.n_kv_heads);
+    key.alpha = p.alpha[h];
+    key.block = false;
+    key.zx = zx;
+    key.zv = zv;
+    key.nx = nullptr;
+    key.nv = nullptr;
+    key.mx = key.sx = key.mv = key.sv = 0.0;
+    return key;
+}
+
+// part q of set (h, s): candidates [q*psize, (q+1)*psize); writes its kpad best
+// keys, descending (zero keys where it has fewer)
+constexpr int kSortThreads = 1024;
+
+__global__ __launch_bounds__(kSortThreads) void sel_part_kernel(SelectParams p, const float* zx, const float* zv,
+                                                                int psize, int nparts, int kpad,
+                                                                unsigned long long* out) {
+    constexpr int E = kPartMax / kSortThreads;
+    __shared__ unsigned long long keys[kPartMax];
+    const int tid = threadIdx.x;
+    const int part = blockIdx.x % nparts, sidx = blockIdx.x / nparts;
+    const int s = sidx % p.num_seqs, h = sidx / p.num_seqs;
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
+    const KeyFn key = global_key(p, zx, zv, st, h);
+    const int j0 = part * psize;
+    unsigned long long kr[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = tid * E + e, j = j0 + i;
+        kr[e] = (i < psize && j < len) ? key(j) : 0ull;
+    }
+    block_sort_desc<kSortThreads, E>(kr, keys, tid);
+    unsigned long long* o = out + ((int64_t)sidx * nparts + part) * kpad;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = tid * E + e;
+        if (i < kpad) o[i] = kr[e];
+    }
+}
+
+// merge parts [op*G, op*G+G) of set sidx (E keys per thread, 1024*E >= G*kpad):
+// with `out`, keep the kpad best keys; without, write the set's landmark
+// indices (ascending, -1 padded)
+template <int E>
+__global__ __launch_bounds__(kSortThreads) void sel_merge_kernel(SelectParams p, const unsigned long long* in,
+                                                                 int nin, int G, int kpad, unsigned long long* out,
+                                                                 int nout) {
+    __shared__ unsigned long long keys[kSortThreads * E];
+    __shared__ int sel[kMaxLandmarks];
+    const int tid = threadIdx.x;
+    const int op = blockIdx.x % nout, sidx = blockIdx.x / nout;
+    const int q0 = op * G, q1 = min(nin, q0 + G);
+    const int m = (q1 - q0) * kpad;
+    const unsigned long long* src = in + ((int64_t)sidx * nin + q0) * kpad;
+    unsigned long long kr[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = tid * E + e;
+        kr[e] = i < m ? src[i] : 0ull;
+    }
+    block_sort_desc<kSortThreads, E>(kr, keys, tid);
+    if (out) {
+        unsigned long long* o = out + ((int64_t)sidx * nout + op) * kpad;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = tid * E + e;
+            if (i < kpad) o[i] = kr[e];
+        }
+        return;
+    }
+    const int K = p.k_lmk;
+    int ks = 1;
+    while (ks < K) ks <<= 1;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = tid * E + e;
+        if (i < ks) {
+            const unsigned long long kj = i < K ? kr[e] : 0ull;
+            sel[i] = kj ? (int)(0xffffffffu - (uint32_t)(kj & 0xffffffffull)) : 0x7fffffff;
+        }
+    }
+    __syncthreads();
+    bitonic_asc_i32<kSortThreads>(sel, ks, tid);
+    int32_t* o = p.lmk_idx + (int64_t)sidx * K;
+    for (int i = tid; i < K; i += kSortThreads) o[i] = sel[i] == 0x7fffffff ? -1 : sel[i];
 }
 
 __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, const float* zx, const float* zv,
@@ -414,7 +624,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
         while (nb2 < nb) nb2 <<= 1;
         for (int i = nb + tid; i < nb2; i += kSelThreads) sh.border[i] = 0ull;
         __syncthreads();
-        bitonic_desc_u64(sh.border, nb2, tid);
+        bitonic_desc_u64<kSelThreads>(sh.border, nb2, tid);
         for (int i = tid; i < (int)k_rem; i += kSelThreads)
             sh.sel[nsel + i] = (int)(0xffffffffu - (uint32_t)(sh.border[i] & 0xffffffffull));
         nsel += (int)k_rem;
@@ -424,7 +634,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
     while (ns2 < nsel) ns2 <<= 1;
     for (int i = nsel + tid; i < ns2; i += kSelThreads) sh.sel[i] = 0x7fffffff;
     __syncthreads();
-    bitonic_asc_i32(sh.sel, ns2, tid);
+    bitonic_asc_i32<kSelThreads>(sh.sel, ns2, tid);
     for (int i = tid; i < K; i += kSelThreads) out[i] = i < nsel ? sh.sel[i] : -1;
 }
 
@@ -455,61 +665,135 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherParams p) {
 }
 
 // ------------------------------------------------------------- launchers
+namespace {
+
+struct TopkPlan {
+    int psize, nparts, kpad, G;
+};
+
+// global variant: part size and merge fan-in (the testing hook's border_cap
+// shrinks both, to drive many parts and several merge levels)
+TopkPlan topk_plan(const SelectParams& p, int border_cap) {
+    TopkPlan t;
+    t.kpad = 1;
+    while (t.kpad < p.k_lmk) t.kpad <<= 1;
+    const int full = border_cap >= (1 << 20);
+    t.psize = kPartMax;
+    if (!full) {
+        t.psize = 16;
+        while (t.psize < border_cap && t.psize < kPartMax) t.psize <<= 1;
+    }
+    t.nparts = ceil_div(p.max_seqlen, t.psize);
+    t.G = kMergeMax / t.kpad;
+    if (!full) t.G = max(2, min(t.G, border_cap));
+    return t;
+}
+
+int n_ranges(const SelectParams& p) {
+    return p.select_mode == DSALT_SELECT_GLOBAL ? (p.stats_scope == DSALT_STATS_PACKED ? 1 : p.num_seqs)
+                                                : p.num_seqs * p.n_sets;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+
 size_t select_workspace(const SelectParams& p) {
+    return select_workspace_cap(p, 1 << 30);
+}
+
+size_t select_workspace_cap(const SelectParams& p, int border_cap) {
     const int nsig = 1 + p.n_kv_heads;
-    const int nranges = p.select_mode == DSALT_SELECT_GLOBAL
-                            ? (p.stats_scope == DSALT_STATS_PACKED ? 1 : p.num_seqs)
-                            : p.num_seqs * p.n_sets;
+    const int nranges = n_ranges(p);
     size_t b = 0;
-    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    b += al(sizeof(float) * (size_t)p.total_len * nsig);           // norms
-    b += al(sizeof(double) * 2 * (size_t)nranges * nsig);          // sums
-    b += al(sizeof(double) * 2 * (size_t)nranges * nsig);          // stats
-    if (p.select_mode == DSALT_SELECT_GLOBAL)
-        b += al(sizeof(float) * (size_t)p.total_len * nsig);       // z
+    b += align256(sizeof(float) * (size_t)p.total_len * nsig);           // norms
+    b += align256(sizeof(double) * 2 * (size_t)nranges * nsig);          // sums
+    b += align256(sizeof(double) * 2 * (size_t)nranges * nsig);          // stats
+    if (p.select_mode == DSALT_SELECT_GLOBAL) {
+        b += align256(sizeof(float) * (size_t)p.total_len * nsig);       // z
+        if (p.k_lmk > 0) {
+            const TopkPlan t = topk_plan(p, border_cap);
+            b += 2 * align256(sizeof(unsigned long long) * (size_t)p.n_heads * p.num_seqs * t.nparts * t.kpad);
+        }
+    }
     return b;
 }
 
 hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, int border_cap) {
     const int nsig = 1 + p.n_kv_heads;
-    const int nranges = p.select_mode == DSALT_SELECT_GLOBAL
-                            ? (p.stats_scope == DSALT_STATS_PACKED ? 1 : p.num_seqs)
-                            : p.num_seqs * p.n_sets;
-    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const int nranges = n_ranges(p);
+    const bool global = p.select_mode == DSALT_SELECT_GLOBAL;
     char* w = (char*)ws;
     float* nx = (float*)w;
     float* nv = nx + p.total_len;
-    w += al(sizeof(float) * (size_t)p.total_len * nsig);
+    w += align256(sizeof(float) * (size_t)p.total_len * nsig);
     double* sums = (double*)w;
-    w += al(sizeof(double) * 2 * (size_t)nranges * nsig);
+    w += align256(sizeof(double) * 2 * (size_t)nranges * nsig);
     double* stats = (double*)w;
-    w += al(sizeof(double) * 2 * (size_t)nranges * nsig);
+    w += align256(sizeof(double) * 2 * (size_t)nranges * nsig);
     float* zx = nullptr;
     float* zv = nullptr;
-    if (p.select_mode == DSALT_SELECT_GLOBAL) {
+    if (global) {
         zx = (float*)w;
         zv = zx + p.total_len;
+        w += align256(sizeof(float) * (size_t)p.total_len * nsig);
     }
     if (p.total_len > 0) {
-        int blocks = min(ceil_div(p.total_len, 4), 65536);
+        const int blocks = ceil_div(p.total_len, kNormTB);
+        const size_t shm = sizeof(double) * kNormTB * nsig;
         if (p.dtype == DSALT_DTYPE_BF16)
-            DSALT_LAUNCH("sel_norms", sel_norms_kernel<bf16>, dim3(blocks), dim3(256), 0, stream, p, nx, nv);
+            DSALT_LAUNCH("sel_norms", sel_norms_kernel<bf16>, dim3(blocks), dim3(256), shm, stream, p, nx, nv);
         else if (p.dtype == DSALT_DTYPE_F16)
-            DSALT_LAUNCH("sel_norms", sel_norms_kernel<f16>, dim3(blocks), dim3(256), 0, stream, p, nx, nv);
+            DSALT_LAUNCH("sel_norms", sel_norms_kernel<f16>, dim3(blocks), dim3(256), shm, stream, p, nx, nv);
         else
-            DSALT_LAUNCH("sel_norms", sel_norms_kernel<float>, dim3(blocks), dim3(256), 0, stream, p, nx, nv);
-        DSALT_LAUNCH("sel_sums", sel_sums_kernel, dim3(nranges, nsig), dim3(256), 0, stream, p, nx, nv, sums);
-        int nst = p.select_mode == DSALT_SELECT_GLOBAL ? nranges * nsig : p.num_seqs * nsig;
-        DSALT_LAUNCH("sel_stats", sel_stats_kernel, dim3(ceil_div(nst, 64)), dim3(64), 0, stream, p, sums, stats,
-                           nranges);
-        if (p.select_mode == DSALT_SELECT_GLOBAL)
-            DSALT_LAUNCH("sel_z", sel_z_kernel, dim3(ceil_div(p.max_seqlen, 256), p.num_seqs), dim3(256), 0,
-                               stream, p, nx, nv, stats, zx, zv);
+            DSALT_LAUNCH("sel_norms", sel_norms_kernel<float>, dim3(blocks), dim3(256), shm, stream, p, nx, nv);
+        DSALT_LAUNCH("sel_sums", sel_sums_kernel, dim3(nranges, nsig), dim3(256), 0, stream, p, nx, nv, sums,
+                     global ? stats : nullptr);
+        if (global) {
+            DSALT_LAUNCH("sel_z", sel_z_kernel, dim3(ceil_div(p.max_seqlen, 256), p.num_seqs, nsig), dim3(256), 0,
+                         stream, p, nx, nv, stats, zx, zv);
+            if (p.scores)
+                DSALT_LAUNCH("sel_scores", sel_scores_kernel, dim3(ceil_div(p.max_seqlen, 256), p.num_seqs),
+                             dim3(256), 0, stream, p, nx, nv, stats);
+        } else {
+            DSALT_LAUNCH("sel_stats", sel_stats_kernel, dim3(ceil_div(p.num_seqs * nsig, 64)), dim3(64), 0, stream,
+                         p, sums, stats);
+        }
     }
-    int nsets_total = p.n_heads * p.num_seqs * p.n_sets;
-    if (nsets_total > 0 && p.k_lmk > 0)
-        DSALT_LAUNCH("sel_topk", sel_topk_kernel, dim3(nsets_total), dim3(kSelThreads), 0, stream, p, zx, zv, nx,
-                           nv, stats, border_cap);
+    const int nsets_total = p.n_heads * p.num_seqs * p.n_sets;
+    if (nsets_total == 0 || p.k_lmk == 0) return hipGetLastError();
+    if (!global) {
+        DSALT_LAUNCH("sel_topk", sel_topk_kernel, dim3(nsets_total), dim3(kSelThreads), 0, stream, p, zx, zv, nx, nv,
+                     stats, border_cap);
+        return hipGetLastError();
+    }
+    const TopkPlan t = topk_plan(p, border_cap);
+    const size_t kb = align256(sizeof(unsigned long long) * (size_t)nsets_total * t.nparts * t.kpad);
+    unsigned long long* ka = (unsigned long long*)w;
+    unsigned long long* kb2 = (unsigned long long*)(w + kb);
+    DSALT_LAUNCH("sel_part", sel_part_kernel, dim3(nsets_total * t.nparts), dim3(kSortThreads), 0, stream, p, zx, zv,
+                 t.psize, t.nparts, t.kpad, ka);
+    // keys per merge block <= kMergeMax; sort width from the largest group
+    auto merge = [&](int nin, unsigned long long* out, int nout) {
+        const int keysn = min(nin, t.G) * t.kpad;
+        const dim3 grid(nsets_total * nout), blk(kSortThreads);
+        if (keysn <= kSortThreads)
+            DSALT_LAUNCH("sel_merge", sel_merge_kernel<1>, grid, blk, 0, stream, p, ka, nin, t.G, t.kpad, out, nout);
+        else if (keysn <= 2 * kSortThreads)
+            DSALT_LAUNCH("sel_merge", sel_merge_kernel<2>, grid, blk, 0, stream, p, ka, nin, t.G, t.kpad, out, nout);
+        else
+            DSALT_LAUNCH("sel_merge", sel_merge_kernel<4>, grid, blk, 0, stream, p, ka, nin, t.G, t.kpad, out, nout);
+    };
+    int nin = t.nparts;
+    while (nin > t.G) {
+        const int nout = ceil_div(nin, t.G);
+        merge(nin, kb2, nout);
+        unsigned long long* tmp = ka;
+        ka = kb2;
+        kb2 = tmp;
+        nin = nout;
+    }
+    merge(nin, nullptr, 1);
     return hipGetLastError();
 }
 

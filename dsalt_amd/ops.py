@@ -137,7 +137,10 @@ def select_landmarks(h: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, w: t
     a.z_v = zv.data_ptr() if zv is not None else None
     a.scores = sc.data_ptr() if sc is not None else None
     L = _lib.load()
-    need = L.dsalt_select_workspace_bytes(ctypes.byref(a))
+    if border_cap is None:
+        need = L.dsalt_select_workspace_bytes(ctypes.byref(a))
+    else:
+        need = L.dsalt_select_workspace_bytes_cap(ctypes.byref(a), int(border_cap))
     if need == 0:
         _lib.check("dsalt_select", L.dsalt_select(ctypes.byref(a), None))
     ws = _workspace(need, dev)

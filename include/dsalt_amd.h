@@ -168,11 +168,16 @@ int    dsalt_bwd(const dsalt_bwd_args* a, dsalt_stream_t stream);
 
 int    dsalt_gather_landmarks(const dsalt_gather_args* a, dsalt_stream_t stream);
 
-/* Testing hook with no counterpart in the reference: dsalt_select with the LDS
- * capacity of the top-k boundary bin limited to `border_cap` keys, so tests can
- * drive the extra radix passes that large tie groups take.  dsalt_select is
- * this call with the full capacity. */
+/* Testing hook with no counterpart in the reference: dsalt_select with its
+ * top-k working sets shrunk by `border_cap` so tests can drive the paths that
+ * large inputs and large tie groups take.  Block-causal sets: LDS capacity of
+ * the radix boundary bin limited to `border_cap` keys (extra radix passes).
+ * Global sets: candidates sorted per part and parts merged per merge block
+ * limited by `border_cap` (many parts, several merge levels).  dsalt_select is
+ * this call with the full capacity; the workspace it needs is
+ * dsalt_select_workspace_bytes_cap(a, border_cap). */
 int    dsalt_select_with_border_cap(const dsalt_select_args* a, dsalt_stream_t stream, int border_cap);
+size_t dsalt_select_workspace_bytes_cap(const dsalt_select_args* a, int border_cap);
 
 /* Per-kernel timing, an instrumentation facility with no counterpart in the
  * reference (its only timing is the CUDA-event fwd+bwd step of

@@ -69,9 +69,8 @@ def test_padding_when_few_candidates():
     assert (got[:, 0, 0, 10:] == -1).all() and (got[:, 0, 0, :10] >= 80).all()
 
 
-@pytest.mark.parametrize("cap", [1, 7, 64])
-def test_ties_and_small_boundary_capacity(cap):
-    # integer-valued inputs: many exactly equal norms, so the boundary bin is a large tie group
+def _tie_case():
+    # integer-valued inputs: many exactly equal norms, so selections cut through large tie groups
     g = torch.Generator().manual_seed(4)
     T = 2000
     h = torch.randint(-1, 2, (T, 64), generator=g).float().to(torch.bfloat16)
@@ -79,8 +78,21 @@ def test_ties_and_small_boundary_capacity(cap):
     alpha = torch.tensor([0.5, 0.5, 1.0, 0.0])
     w = torch.randint(1, 50, (T,), generator=g, dtype=torch.int32)
     cu = torch.tensor([0, 1200, T], dtype=torch.int32)
-    idx, ridx = _run(h, v, alpha, w, cu, 50, ops.SELECT_GLOBAL, 512, ops.STATS_PACKED, want=False,
-                     border_cap=cap)
+    return h, v, alpha, w, cu
+
+
+@pytest.mark.parametrize("cap", [1, 7, 64, None])
+def test_ties_global_many_parts_and_merge_levels(cap):
+    # global sets: small caps sort 16-candidate parts and merge 2 or 7 parts per block
+    # (several merge levels); None is the production plan
+    idx, ridx = _run(*_tie_case(), 50, ops.SELECT_GLOBAL, 512, ops.STATS_PACKED, want=False, border_cap=cap)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
+@pytest.mark.parametrize("cap", [1, 7, 64])
+def test_ties_block_small_boundary_capacity(cap):
+    # block-causal sets: the radix boundary bin limited to `cap` keys forces extra passes
+    idx, ridx = _run(*_tie_case(), 50, ops.SELECT_BLOCK, 256, ops.STATS_PACKED, want=False, border_cap=cap)
     np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
 
 
