@@ -43,6 +43,7 @@ struct AttnParams {
     int* plan_bounds;        // [S * n_tiles * 4 * 4]
     // backward workspace
     float* delta;            // [T, H]
+    int* cnt;                // [T, H] landmarks visible to each row (written by the dQ pass)
     int* seq_wmax;           // [S] max clamped window per sequence
     float* part_k;           // [n_chunks, H, S, K, D] landmark dK partials
     float* part_v;           // [n_chunks, H, S, K, D]

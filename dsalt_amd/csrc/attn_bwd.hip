@@ -112,6 +112,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
         hi = i;
         cnt = lower_bound_i(lpos, nvalid, lo);
     }
+    if (valid && g == 0 && p.cnt) p.cnt[(int64_t)(st + i) * p.n_heads + h] = cnt;
     const int wcmax = uniform(row_max16(cnt)), wcmin = uniform(row_min16(valid ? cnt : 0));
     if (lane == 0) red[uw] = wcmax;
     __syncthreads();
@@ -577,8 +578,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
 }
 
 // -------------------------------------------------------- landmark dK/dV
-// Block = (head, sequence, 1024-row chunk, group of 128 slots); wave w owns
-// slots grp*128 + 32w .. +31 as two 16-slot subtiles.
+// Block = (head, sequence, 1024-row chunk, group of 64*kLmkSub slots); wave w
+// owns slots grp*64*kLmkSub + 16*kLmkSub*w .. as kLmkSub 16-slot subtiles.
+constexpr int kLmkSub = 1;
+constexpr int kLmkGroup = 64 * kLmkSub;
+
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     constexpr int BQ = BwdShape<T, D>::BQ;
@@ -593,7 +597,7 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
     const int K = p.k_lmk;
-    const int ngrp = ceil_div(K, 128);
+    const int ngrp = ceil_div(K, kLmkGroup);
     int b = blockIdx.x;
     const int grp = b % ngrp;
     b /= ngrp;
@@ -610,25 +614,27 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     const int rbeg = chunk * kRowChunk, rend = min(len, rbeg + kRowChunk);
     const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid);
 
-    // slots of this lane (two subtiles)
-    const int sl0 = uniform(grp * 128 + wave * 32);
-    RowReg<T, D> kr[2], vr[2];
-    int slot[2];
-    float bsl[2];
+    // slots of this lane (kLmkSub subtiles)
+    const int sl0 = uniform(grp * kLmkGroup + wave * 16 * kLmkSub);
+    RowReg<T, D> kr[kLmkSub], vr[kLmkSub];
+    int slot[kLmkSub];
+    float bsl[kLmkSub];
     const T* kbase = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)kvh * p.k_sh;
     const T* vbase = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)kvh * p.v_sh;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < kLmkSub; ++u) {
         slot[u] = sl0 + u * 16 + (lane & 15);
         const bool sval = slot[u] < nvalid && lpos[slot[u]] < len;
         kr[u].load(sval ? kbase + (int64_t)lpos[slot[u]] * p.k_st : nullptr, kbase, g);
         vr[u].load(sval ? vbase + (int64_t)lpos[slot[u]] * p.v_st : nullptr, vbase, g);
         bsl[u] = (p.lbias && slot[u] < K) ? p.lbias[set_off + slot[u]] * inv_scale : 0.f;
     }
-    floatx4 adk[2][D / 16], adv[2][D / 16];
-    float dbias[2] = {0.f, 0.f};
+    floatx4 adk[kLmkSub][D / 16], adv[kLmkSub][D / 16];
+    float dbias[kLmkSub];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < kLmkSub; ++u) dbias[u] = 0.f;
+#pragma unroll
+    for (int u = 0; u < kLmkSub; ++u)
 #pragma unroll
         for (int dt = 0; dt < D / 16; ++dt) {
             adk[u][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -643,38 +649,34 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     const int istart = max(rbeg, (first_row / BQ) * BQ);
     // the loop bound is uniform over the block (every wave reaches each barrier);
     // waves whose slots are all empty skip their products through act[] below
-    const bool any_slot = grp * 128 < nvalid;
+    const bool any_slot = grp * kLmkGroup < nvalid;
     QLoader<T, D, BQ> ld(p, tid);
+    // rows staged in LDS; visible landmark counts come from the dQ pass
     for (int i0 = istart; any_slot && i0 < rend; i0 += BQ) {
         ld.load(p, qb, db, i0, rend, tid);
         __syncthreads();
         ld.store(q, tid);
         if (tid < BQ) {
             const int i = i0 + tid;
+            int c = 0;
             if (i < rend) {
-                const int wi = max(p.w[st + i], 1);
-                q.key[tid] = lower_bound_i(lpos, nvalid, max(i - wi + 1, 0));
+                c = p.cnt[(int64_t)(st + i) * p.n_heads + h];
                 q.lse2[tid] = p.lse[(int64_t)(st + i) * p.n_heads + h] * kLog2eB;
                 q.dlt[tid] = p.delta[(int64_t)(st + i) * p.n_heads + h];
             } else {
-                q.key[tid] = 0;
                 q.lse2[tid] = 0.f;
                 q.dlt[tid] = 0.f;
             }
-        }
-        __syncthreads();
-        if (tid < NQS) {
-            int mn = 0x7fffffff, mx = 0;
-            for (int r = 0; r < 16; ++r) {
-                mn = min(mn, q.key[tid * 16 + r]);
-                mx = max(mx, q.key[tid * 16 + r]);
+            q.key[tid] = c;
+            const int mn = row_min16(c), mx = row_max16(c);
+            if ((tid & 15) == 0) {
+                cmin_s[tid >> 4] = mn;
+                cmax_s[tid >> 4] = mx;
             }
-            cmin_s[tid] = mn;
-            cmax_s[tid] = mx;
         }
         __syncthreads();
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < kLmkSub; ++u) {
             const int a = sl0 + u * 16;
             floatx4 P[NQS], dS[NQS];
             bool act[NQS];
@@ -728,7 +730,7 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     }
     // partials: [chunk][h][s][slot][D]
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < kLmkSub; ++u) {
         const float db2 = sum_g4(dbias[u]);
         if (slot[u] >= K) continue;
         const int64_t row = (((int64_t)chunk * p.n_heads + h) * p.num_seqs + s) * K + slot[u];
@@ -779,6 +781,7 @@ size_t bwd_workspace(const AttnParams& p) {
     const int nch = ceil_div(p.max_seqlen, kRowChunk);
     size_t b = plan_bytes(p);
     b += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
+    b += al(sizeof(int) * (size_t)p.total_len * p.n_heads);
     b += al(sizeof(int) * (size_t)p.num_seqs);
     b += 2 * al(sizeof(float) * (size_t)nch * p.n_heads * p.num_seqs * p.k_lmk * p.head_dim);
     b += al(sizeof(float) * (size_t)nch * p.n_heads * p.num_seqs * p.k_lmk);
@@ -793,7 +796,7 @@ static void bwd_run(const AttnParams& p, hipStream_t stream) {
     DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D>), dim3(total), dim3(256), 0, stream, p);
     DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D>), dim3(total), dim3(256), 0, stream, p);
     if (p.k_lmk > 0) {
-        const int ngrp = ceil_div(p.k_lmk, 128);
+        const int ngrp = ceil_div(p.k_lmk, kLmkGroup);
         DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D>), dim3(p.n_heads * p.num_seqs * p.n_chunks * ngrp), dim3(256),
                      0, stream, p);
         const int64_t n = (int64_t)p.n_heads * p.num_seqs * p.k_lmk * D;
@@ -809,6 +812,8 @@ hipError_t bwd_launch(AttnParams p, void* ws, hipStream_t stream) {
     plan_carve(p, w);
     p.delta = (float*)w;
     w += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
+    p.cnt = (int*)w;
+    w += al(sizeof(int) * (size_t)p.total_len * p.n_heads);
     p.seq_wmax = (int*)w;
     w += al(sizeof(int) * (size_t)p.num_seqs);
     const size_t npart = (size_t)p.n_chunks * p.n_heads * p.num_seqs * p.k_lmk;
