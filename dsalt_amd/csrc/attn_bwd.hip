@@ -27,7 +27,7 @@ namespace dsalt {
 
 constexpr float kLog2eB = 1.4426950408889634f;
 constexpr int kRowChunk = 1024;
-constexpr int kSeg = 1024;  // rows compacted at a time in the dK/dV sweep
+constexpr int kSeg = 512;  // rows compacted at a time in the dK/dV sweep
 
 template <typename T, int D> struct BwdShape;
 template <> struct BwdShape<bf16, 64> { static constexpr int BN = 64, BQ = 64; };
@@ -333,8 +333,9 @@ struct QLoader {
 //     partial rows j0 < lo_i <= j0+63   (see keys >= lo_i: one-sided mask);
 // rows with lo_i > j0 + 63 are skipped.  List order is row order, so the sum
 // order is fixed and results are deterministic.
+// four waves per SIMD for 16-bit head_dim 64 (at a few spilled registers), two otherwise
 template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_dkdv_kernel(AttnParams p) {
     constexpr int BQ = BwdShape<T, D>::BQ;
     constexpr int NQS = BQ / 16;
     constexpr int NDIAG = 64 / BQ;
@@ -397,60 +398,62 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(AttnParams p) {
     const float NEG = -INFINITY;
     const int lane_off = 4 * g;
 
-    // one staged chunk; kind 0: diagonal rows from i0, 1: full rows, 2: partial rows
+    // one staged chunk; kind 0: diagonal rows from i0, 1: full rows, 2: partial rows.
+    // Query subtiles are taken in the groups one accumulation consumes (two 16-row
+    // subtiles for 16-bit types), so only one group's P and dS are live at a time.
+    constexpr int GQ = kHalf ? 2 : 1;
     auto compute = [&](const QS& q, int kind, int i0) {
-        floatx4 P[NQS], dS[NQS];
-        bool act[NQS];
 #pragma unroll
-        for (int qs = 0; qs < NQS; ++qs) {
-            const int qa = i0 + qs * 16;
-            act[qs] = kind != 0 || qa + 15 >= wj0;
-            if (!act[qs]) {
-                P[qs] = floatx4{0.f, 0.f, 0.f, 0.f};
-                dS[qs] = P[qs];
-                continue;
-            }
-            floatx4 ci = floatx4{0.f, 0.f, 0.f, 0.f};
-            if (kind != 1) {
-                const int4 lo4 = *(const int4*)(q.key + qs * 16 + lane_off);
-                if (kind == 2 || qa >= wj0 + 15) {
-                    ci[0] = jj >= lo4.x ? 0.f : NEG;
-                    ci[1] = jj >= lo4.y ? 0.f : NEG;
-                    ci[2] = jj >= lo4.z ? 0.f : NEG;
-                    ci[3] = jj >= lo4.w ? 0.f : NEG;
-                } else {
-                    const int qd = qa + lane_off - jj;  // row index minus key index, r = 0
-                    ci[0] = (jj >= lo4.x && qd >= 0) ? 0.f : NEG;
-                    ci[1] = (jj >= lo4.y && qd + 1 >= 0) ? 0.f : NEG;
-                    ci[2] = (jj >= lo4.z && qd + 2 >= 0) ? 0.f : NEG;
-                    ci[3] = (jj >= lo4.w && qd + 3 >= 0) ? 0.f : NEG;
+        for (int hp = 0; hp < NQS / GQ; ++hp) {
+            floatx4 P[GQ], dS[GQ];
+            bool act[GQ];
+            bool any = false;
+#pragma unroll
+            for (int u = 0; u < GQ; ++u) {
+                const int qs = hp * GQ + u;
+                const int qa = i0 + qs * 16;
+                act[u] = kind != 0 || qa + 15 >= wj0;
+                any |= act[u];
+                if (!act[u]) {
+                    P[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+                    dS[u] = P[u];
+                    continue;
+                }
+                floatx4 ci = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (kind != 1) {
+                    const int4 lo4 = *(const int4*)(q.key + qs * 16 + lane_off);
+                    if (kind == 2 || qa >= wj0 + 15) {
+                        ci[0] = jj >= lo4.x ? 0.f : NEG;
+                        ci[1] = jj >= lo4.y ? 0.f : NEG;
+                        ci[2] = jj >= lo4.z ? 0.f : NEG;
+                        ci[3] = jj >= lo4.w ? 0.f : NEG;
+                    } else {
+                        const int qd = qa + lane_off - jj;  // row index minus key index, r = 0
+                        ci[0] = (jj >= lo4.x && qd >= 0) ? 0.f : NEG;
+                        ci[1] = (jj >= lo4.y && qd + 1 >= 0) ? 0.f : NEG;
+                        ci[2] = (jj >= lo4.z && qd + 2 >= 0) ? 0.f : NEG;
+                        ci[3] = (jj >= lo4.w && qd + 3 >= 0) ? 0.f : NEG;
+                    }
+                }
+                const floatx4 sc = dot_rows<T, D>(q.q, QT::RS, qs * 16, lane, kr, ci);
+                const floatx4 dp = dot_rows<T, D>(q.d, QT::RS, qs * 16, lane, vr, floatx4{0.f, 0.f, 0.f, 0.f});
+                const floatx4 l4 = *(const floatx4*)(q.lse2 + qs * 16 + lane_off);
+                const floatx4 d4 = *(const floatx4*)(q.dlt + qs * 16 + lane_off);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float pr = __builtin_amdgcn_exp2f(sc[r] * c2 - l4[r]);
+                    P[u][r] = pr;
+                    dS[u][r] = pr * (dp[r] - d4[r]);
                 }
             }
-            const floatx4 sc = dot_rows<T, D>(q.q, QT::RS, qs * 16, lane, kr, ci);
-            const floatx4 dp = dot_rows<T, D>(q.d, QT::RS, qs * 16, lane, vr, floatx4{0.f, 0.f, 0.f, 0.f});
-            const floatx4 l4 = *(const floatx4*)(q.lse2 + qs * 16 + lane_off);
-            const floatx4 d4 = *(const floatx4*)(q.dlt + qs * 16 + lane_off);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float pr = __builtin_amdgcn_exp2f(sc[r] * c2 - l4[r]);
-                P[qs][r] = pr;
-                dS[qs][r] = pr * (dp[r] - d4[r]);
+            if (!any) continue;
+            if constexpr (kHalf) {
+                acc_tr<T, D>(q.d, QT::RS, hp * 32, lane, P[0], P[1], adv);
+                acc_tr<T, D>(q.q, QT::RS, hp * 32, lane, dS[0], dS[1], adk);
+            } else {
+                acc_rm32<D>((const float*)q.d, QT::RS, hp * 16, lane, P[0], adv);
+                acc_rm32<D>((const float*)q.q, QT::RS, hp * 16, lane, dS[0], adk);
             }
-        }
-        if constexpr (kHalf) {
-#pragma unroll
-            for (int hp = 0; hp < NQS / 2; ++hp)
-                if (act[2 * hp] || act[2 * hp + 1]) {
-                    acc_tr<T, D>(q.d, QT::RS, hp * 32, lane, P[2 * hp], P[2 * hp + 1], adv);
-                    acc_tr<T, D>(q.q, QT::RS, hp * 32, lane, dS[2 * hp], dS[2 * hp + 1], adk);
-                }
-        } else {
-#pragma unroll
-            for (int qs = 0; qs < NQS; ++qs)
-                if (act[qs]) {
-                    acc_rm32<D>((const float*)q.d, QT::RS, qs * 16, lane, P[qs], adv);
-                    acc_rm32<D>((const float*)q.q, QT::RS, qs * 16, lane, dS[qs], adk);
-                }
         }
     };
 
