@@ -43,7 +43,7 @@ __device__ __forceinline__ int pow2ceil64(int n) {
 }
 
 // ------------------------------------------------------------------ norms
-constexpr int kNormTPW = 2;              // tokens per wave
+constexpr int kNormTPW = 1;              // tokens per wave
 constexpr int kNormTB = 4 * kNormTPW;    // tokens per 256-thread block
 
 template <typename T>
