@@ -44,17 +44,20 @@ def parse():
                          "profiles/traffic_<workload>.json and exit (no GPU needed)")
     ap.add_argument("--pmc-summary", metavar="DIR",
                     help="print per-kernel means of every counter found under DIR and exit (no GPU needed)")
+    ap.add_argument("--kernel-stats", metavar="DIR",
+                    help="print the kernel table of a rocprofv3 --kernel-trace --stats run under DIR and exit")
     return ap.parse_args()
 
 
-LABELS = ("sel_norms", "sel_sums", "sel_stats", "sel_z", "sel_topk", "gather", "row_plan", "attn_fwd", "bwd_init",
-          "bwd_dq", "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum")
+LABELS = ("sel_norms", "sel_sums", "sel_stats", "sel_z", "sel_scores", "sel_part", "sel_merge", "sel_topk", "gather",
+          "row_plan", "attn_fwd", "bwd_init", "bwd_dq", "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum")
 
 
 def short_kernel_name(name: str) -> str:
     """Label of a library kernel (the one dsalt_timing_report uses) from a profiler kernel name."""
     import re
-    m = re.search(r"(sel_norms|sel_sums|sel_stats|sel_z|sel_topk|gather|row_plan|fwd|bwd_init|bwd_dq|bwd_dkdv|bwd_lmk_sum|"
+    m = re.search(r"(sel_norms|sel_sums|sel_stats|sel_z|sel_scores|sel_part|sel_merge|sel_topk|gather|row_plan|fwd|bwd_init|bwd_dq|"
+                  r"bwd_dkdv|bwd_lmk_sum|"
                   r"bwd_lmk)_kernel", name)
     if not m:
         return name
@@ -126,6 +129,18 @@ def main():
     args = parse()
     if args.traffic_from:
         print(json.dumps(traffic_from(args.traffic_from, args.workload, args.copy_calibration or 1024), indent=1))
+        return
+    if args.kernel_stats:
+        import csv
+        for dirpath, _, files in os.walk(args.kernel_stats):
+            for fn in sorted(files):
+                if fn.endswith("kernel_stats.csv"):
+                    rows = list(csv.DictReader(open(os.path.join(dirpath, fn), newline="")))
+                    print(f"{'kernel':<14} {'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'pct':>6}  name")
+                    for r in rows:
+                        print(f"{short_kernel_name(r['Name'])[:14]:<14} {r['Calls']:>6} {float(r['AverageNs']) / 1e3:9.2f} "
+                              f"{float(r['MinNs']) / 1e3:9.2f} {float(r['MaxNs']) / 1e3:9.2f} "
+                              f"{float(r['Percentage']):6.2f}  {r['Name'][:70]}")
         return
     if args.pmc_summary:
         for k, d in sorted(read_pmc(args.pmc_summary).items()):
