@@ -67,6 +67,14 @@ class BwdArgs(ctypes.Structure):
                 ("workspace", _vp), ("workspace_bytes", _sz)]
 
 
+class TrainFwdArgs(ctypes.Structure):
+    _fields_ = [("base", FwdArgs), ("w_cont", _vp), ("tau_win", _f32), ("win_edge", _f32)]
+
+
+class TrainBwdArgs(ctypes.Structure):
+    _fields_ = [("base", BwdArgs), ("w_cont", _vp), ("tau_win", _f32), ("win_edge", _f32), ("d_w", _vp)]
+
+
 class GatherArgs(ctypes.Structure):
     _fields_ = [("p", Problem),
                 ("k", _vp), ("k_stride_t", _i64), ("k_stride_h", _i64),
@@ -87,6 +95,10 @@ SIGNATURES = {
     "dsalt_bwd_workspace_bytes": ([ctypes.POINTER(BwdArgs)], _sz),
     "dsalt_bwd": ([ctypes.POINTER(BwdArgs), _vp], ctypes.c_int),
     "dsalt_gather_landmarks": ([ctypes.POINTER(GatherArgs), _vp], ctypes.c_int),
+    "dsalt_train_fwd_workspace_bytes": ([ctypes.POINTER(TrainFwdArgs)], _sz),
+    "dsalt_train_fwd": ([ctypes.POINTER(TrainFwdArgs), _vp], ctypes.c_int),
+    "dsalt_train_bwd_workspace_bytes": ([ctypes.POINTER(TrainBwdArgs)], _sz),
+    "dsalt_train_bwd": ([ctypes.POINTER(TrainBwdArgs), _vp], ctypes.c_int),
     "dsalt_timing_enable": ([ctypes.c_int], ctypes.c_int),
     "dsalt_timing_report": ([ctypes.c_char_p, _sz], ctypes.c_int),
 }

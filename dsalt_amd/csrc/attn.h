@@ -37,6 +37,13 @@ struct AttnParams {
     void* dk;
     void* dv;
     float* d_bias;
+    // training variant: soft window edge (w_cont null for the inference operator)
+    const float* w_cont;     // [T] continuous windows w~ (values below 0 act as 0)
+    float tau_inv;           // 1 / tau_win
+    float edge;              // win_edge: band keys with d > w~ - edge carry log sigmoid((w~ - d) / tau)
+    int edge_keys;           // ceil(win_edge): bound on the band keys of a row that carry the edge bias
+    float* dw_h;             // [T, H] d loss / d w~ per head (training backward workspace)
+    float* d_w;              // [T] d loss / d w~ summed over heads (training backward output)
     // row plan (forward and backward workspace), per 64-row tile of each sequence:
     // rows ordered by window start, and per 16-row group {min lo, max lo, max i, min i}
     uint8_t* plan_perm;      // [S * n_tiles * 64] row offset within the tile
@@ -51,11 +58,31 @@ struct AttnParams {
     int n_chunks;            // row chunks of the landmark backward
 };
 
+// Training variant, band key at distance d = i - j of a row with continuous window wt:
+// logit bias log sigmoid((wt - d) / tau) outside the core d <= wt - edge, 0 inside,
+// returned in raw-score units (divided by the logit scale).
+__device__ __forceinline__ float edge_bias(const AttnParams& p, float wt, int d) {
+    const float fd = wt - (float)d;
+    return fd >= p.edge ? 0.f : -__logf(1.f + __expf(-fd * p.tau_inv)) * p.inv_scale;
+}
+// d bias / d wt of the same key: (1 - sigmoid((wt - d) / tau)) / tau outside the core
+// (keys outside the band get a finite value; callers mask them)
+__device__ __forceinline__ float edge_grad(const AttnParams& p, float wt, int d) {
+    const float fd = fmaxf(wt - (float)d, 0.f);
+    if (fd >= p.edge) return 0.f;
+    const float e = __expf(-fd * p.tau_inv);
+    return e / (1.f + e) * p.tau_inv;
+}
+
 size_t plan_bytes(const AttnParams& p);
 void plan_carve(AttnParams& p, char*& ws);  // assigns plan_perm / plan_bounds from a workspace
 hipError_t plan_launch(const AttnParams& p, hipStream_t stream);
 hipError_t fwd_launch(AttnParams p, void* ws, hipStream_t stream);
+// training variant: integer windows floor(w~) + 1 written into `w_int` ([T] int32)
+hipError_t train_windows_launch(const AttnParams& p, int* w_int, hipStream_t stream);
 size_t bwd_workspace(const AttnParams& p);
 hipError_t bwd_launch(AttnParams p, void* ws, hipStream_t stream);
+// training variant: d_w[t] = sum over heads of dw_h[t, h], in head order
+hipError_t train_dw_launch(const AttnParams& p, hipStream_t stream);
 
 }  // namespace dsalt

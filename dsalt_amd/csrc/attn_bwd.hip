@@ -66,7 +66,9 @@ __global__ void bwd_init_kernel(AttnParams p) {
 }
 
 // -------------------------------------------------------------------- dQ
-template <typename T, int D>
+// TR: training variant -- band keys near the window start carry the soft edge bias,
+// and the lane also sums dS * d(bias)/d(w~) of its row into dw_h.
+template <typename T, int D, bool TR>
 __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
     constexpr int BN = BwdShape<T, D>::BN;
     constexpr int NST = BN / 16;
@@ -106,12 +108,16 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
     const int i = r0 + p.plan_perm[tile * 64 + uw * 16 + (lane & 15)];
     const bool valid = i < len;
     int lo = 0x7fffffff, hi = -1, cnt = 0;
+    float wt = 0.f;
     if (valid) {
         const int wi = max(p.w[st + i], 1);
         lo = max(i - wi + 1, 0);
         hi = i;
         cnt = lower_bound_i(lpos, nvalid, lo);
+        if (TR) wt = p.w_cont[st + i];
     }
+    const int lo_edge = TR ? wLmax + p.edge_keys : wLmax;  // keys from here on carry no edge bias
+    float dwacc = 0.f;
     if (valid && g == 0 && p.cnt) p.cnt[(int64_t)(st + i) * p.n_heads + h] = cnt;
     const int wcmax = uniform(row_max16(cnt)), wcmin = uniform(row_min16(valid ? cnt : 0));
     if (lane == 0) red[uw] = wcmax;
@@ -201,17 +207,24 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
                 continue;
             }
             floatx4 ci;
+            floatx4 eg = floatx4{0.f, 0.f, 0.f, 0.f};  // d(bias)/d(w~) per key (training variant)
             if (band) {
-                if (a >= wLmax && a + 15 <= wHmin) {
+                const int tl = lo - a - lane_off, th = hi - a - lane_off;
+                if (a >= lo_edge && a + 15 <= wHmin) {
                     ci = floatx4{0.f, 0.f, 0.f, 0.f};
-                } else if (a + 15 <= wHmin) {
-                    const int tl = lo - a - lane_off;
+                } else if (a + 15 <= wHmin) {  // below every row's diagonal: window start only
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ci[r] = r < tl ? NEG : 0.f;
+                    for (int r = 0; r < 4; ++r) {
+                        ci[r] = r < tl ? NEG : (TR ? edge_bias(p, wt, th - r) : 0.f);
+                        if (TR) eg[r] = r < tl ? 0.f : edge_grad(p, wt, th - r);
+                    }
                 } else {
-                    const int tl = lo - a - lane_off, th = hi - a - lane_off;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ci[r] = (r < tl || r > th) ? NEG : 0.f;
+                    for (int r = 0; r < 4; ++r) {
+                        const bool out = r < tl || r > th;
+                        ci[r] = out ? NEG : (TR ? edge_bias(p, wt, th - r) : 0.f);
+                        if (TR) eg[r] = out ? 0.f : edge_grad(p, wt, th - r);
+                    }
                 }
             } else {
                 floatx4 bv = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -234,6 +247,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
             const floatx4 dp = dot_rows<T, D>(Vs[buf], KT::RS, stt * 16, lane, dor, floatx4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
             for (int r = 0; r < 4; ++r) dS[stt][r] = __builtin_amdgcn_exp2f(sc[r] * c2 - lse2) * (dp[r] - dlt);
+            if (TR && band)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dwacc += dS[stt][r] * eg[r];
         }
         if constexpr (kHalf) {
 #pragma unroll
@@ -250,6 +266,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
             vt.store(Vs[buf ^ 1], tid);
         }
         __syncthreads();
+    }
+    if (TR) {
+        const float dw = sum_g4(dwacc);
+        if (valid && g == 0) p.dw_h[(int64_t)(st + i) * p.n_heads + h] = dw;
     }
     if (valid) {
         T* drow = (T*)p.dq + (int64_t)(st + i) * p.n_heads * D + (int64_t)h * D;
@@ -269,7 +289,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
 // (base 2), delta, and a per-row key: the window start in the dK/dV sweep, the
 // visible landmark count in the landmark sweep (0 past the end).  Rows past
 // the end are zero with LSE 0 and delta 0, so they contribute exactly zero.
-template <typename T, int D, int BQ>
+template <typename T, int D, int BQ, bool TR = false>
 struct QStage {
     typedef Tile<T, D, BQ> QT;
     T q[QT::ELEMS];
@@ -277,6 +297,8 @@ struct QStage {
     float lse2[BQ];
     float dlt[BQ];
     int key[BQ];
+    float wt[TR ? BQ : 4];  // training variant: continuous window of the row
+    int ri[TR ? BQ : 4];    // training variant: row index
 };
 
 template <typename T, int D, int BQ>
@@ -315,7 +337,8 @@ struct QLoader {
             tdo.r[v] = __builtin_amdgcn_raw_buffer_load_b128(rd, ok ? row * drb + cb : 0x80000000u, 0, 0);
         }
     }
-    __device__ __forceinline__ void store(QStage<T, D, BQ>& q, int tid) const {
+    template <class QS>
+    __device__ __forceinline__ void store(QS& q, int tid) const {
         tq.store(q.q, tid);
         tdo.store(q.d, tid);
     }
@@ -333,14 +356,16 @@ struct QLoader {
 //     partial rows j0 < lo_i <= j0+63   (see keys >= lo_i: one-sided mask);
 // rows with lo_i > j0 + 63 are skipped.  List order is row order, so the sum
 // order is fixed and results are deterministic.
-// four waves per SIMD for 16-bit head_dim 64 (at a few spilled registers), two otherwise
-template <typename T, int D>
+// four waves per SIMD for 16-bit head_dim 64 (at a few spilled registers), two otherwise.
+// TR: training variant -- fully visible rows must also see every key of the block
+// past their edge_keys edge-bias keys; other rows add the soft edge bias.
+template <typename T, int D, bool TR>
 __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_dkdv_kernel(AttnParams p) {
     constexpr int BQ = BwdShape<T, D>::BQ;
     constexpr int NQS = BQ / 16;
     constexpr int NDIAG = 64 / BQ;
     constexpr bool kHalf = sizeof(T) == 2;
-    typedef QStage<T, D, BQ> QS;
+    typedef QStage<T, D, BQ, TR> QS;
     typedef typename QS::QT QT;
     __shared__ __attribute__((aligned(16))) QS sq[2];
     __shared__ short lst[2][kSeg];
@@ -382,10 +407,18 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_
             q.key[r] = max(i - wi + 1, 0);
             q.lse2[r] = lrow[(int64_t)i * p.n_heads] * kLog2eB;
             q.dlt[r] = drow[(int64_t)i * p.n_heads];
+            if (TR) {
+                q.wt[r] = p.w_cont[st + i];
+                q.ri[r] = i;
+            }
         } else {
             q.key[r] = 0x7fffffff;
             q.lse2[r] = 0.f;
             q.dlt[r] = 0.f;
+            if (TR) {
+                q.wt[r] = 0.f;
+                q.ri[r] = 0;
+            }
         }
     };
 
@@ -422,17 +455,26 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_
                 floatx4 ci = floatx4{0.f, 0.f, 0.f, 0.f};
                 if (kind != 1) {
                     const int4 lo4 = *(const int4*)(q.key + qs * 16 + lane_off);
+                    floatx4 eb = floatx4{0.f, 0.f, 0.f, 0.f};
+                    if (TR) {
+                        const floatx4 w4 = *(const floatx4*)(q.wt + qs * 16 + lane_off);
+                        const int4 i4 = *(const int4*)(q.ri + qs * 16 + lane_off);
+                        eb[0] = edge_bias(p, w4[0], i4.x - jj);
+                        eb[1] = edge_bias(p, w4[1], i4.y - jj);
+                        eb[2] = edge_bias(p, w4[2], i4.z - jj);
+                        eb[3] = edge_bias(p, w4[3], i4.w - jj);
+                    }
                     if (kind == 2 || qa >= wj0 + 15) {
-                        ci[0] = jj >= lo4.x ? 0.f : NEG;
-                        ci[1] = jj >= lo4.y ? 0.f : NEG;
-                        ci[2] = jj >= lo4.z ? 0.f : NEG;
-                        ci[3] = jj >= lo4.w ? 0.f : NEG;
+                        ci[0] = jj >= lo4.x ? eb[0] : NEG;
+                        ci[1] = jj >= lo4.y ? eb[1] : NEG;
+                        ci[2] = jj >= lo4.z ? eb[2] : NEG;
+                        ci[3] = jj >= lo4.w ? eb[3] : NEG;
                     } else {
                         const int qd = qa + lane_off - jj;  // row index minus key index, r = 0
-                        ci[0] = (jj >= lo4.x && qd >= 0) ? 0.f : NEG;
-                        ci[1] = (jj >= lo4.y && qd + 1 >= 0) ? 0.f : NEG;
-                        ci[2] = (jj >= lo4.z && qd + 2 >= 0) ? 0.f : NEG;
-                        ci[3] = (jj >= lo4.w && qd + 3 >= 0) ? 0.f : NEG;
+                        ci[0] = (jj >= lo4.x && qd >= 0) ? eb[0] : NEG;
+                        ci[1] = (jj >= lo4.y && qd + 1 >= 0) ? eb[1] : NEG;
+                        ci[2] = (jj >= lo4.z && qd + 2 >= 0) ? eb[2] : NEG;
+                        ci[3] = (jj >= lo4.w && qd + 3 >= 0) ? eb[3] : NEG;
                     }
                 }
                 const floatx4 sc = dot_rows<T, D>(q.q, QT::RS, qs * 16, lane, kr, ci);
@@ -486,7 +528,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_
             if (r < nrows) {
                 const int i = seg + r;
                 const int lo = max(i - max(wrow[i], 1) + 1, 0);
-                f = lo <= j0;
+                f = lo <= j0 - (TR ? p.edge_keys : 0);
                 pp = !f && lo <= j0 + 63;
             }
             bf[u] = __ballot(f);
@@ -778,6 +820,21 @@ __global__ __launch_bounds__(256) void bwd_lmk_sum_kernel(AttnParams p) {
     dv[o] = from_float<T>(to_float(dv[o]) + sv);
 }
 
+// training variant: d w~ per token, the per-head sums added in head order
+__global__ __launch_bounds__(256) void train_dw_kernel(AttnParams p) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= p.total_len) return;
+    float s = 0.f;
+    for (int h = 0; h < p.n_heads; ++h) s += p.dw_h[(int64_t)t * p.n_heads + h];
+    p.d_w[t] = s;
+}
+
+hipError_t train_dw_launch(const AttnParams& p, hipStream_t stream) {
+    if (p.total_len == 0) return hipSuccess;
+    DSALT_LAUNCH("train_dw", train_dw_kernel, dim3(ceil_div(p.total_len, 256)), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- launch
 size_t bwd_workspace(const AttnParams& p) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -796,8 +853,13 @@ static void bwd_run(const AttnParams& p, hipStream_t stream) {
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
     DSALT_LAUNCH("bwd_init", bwd_init_kernel, dim3(ceil_div(p.num_seqs, 256)), dim3(256), 0, stream, p);
     plan_launch(p, stream);
-    DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D>), dim3(total), dim3(256), 0, stream, p);
-    DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D>), dim3(total), dim3(256), 0, stream, p);
+    if (p.w_cont) {
+        DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, true>), dim3(total), dim3(256), 0, stream, p);
+        DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D, true>), dim3(total), dim3(256), 0, stream, p);
+    } else {
+        DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, false>), dim3(total), dim3(256), 0, stream, p);
+        DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D, false>), dim3(total), dim3(256), 0, stream, p);
+    }
     if (p.k_lmk > 0) {
         const int ngrp = ceil_div(p.k_lmk, kLmkGroup);
         DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D>), dim3(p.n_heads * p.num_seqs * p.n_chunks * ngrp), dim3(256),

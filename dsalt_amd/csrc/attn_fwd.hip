@@ -130,6 +130,7 @@ hipError_t plan_launch(const AttnParams& p, hipStream_t stream) {
 struct RowGroup {
     int i, lo, hi, cnt;
     bool valid;
+    float wt;  // continuous window of the row (training variant)
     int wlo, wLmax, whi, wHmin, wcmax, wcmin;
 };
 
@@ -149,6 +150,7 @@ __device__ __forceinline__ void plan_group(const AttnParams& p, int64_t tile0, i
     rg.hi = -1;
     rg.cnt = 0;
     rg.valid = false;
+    rg.wt = 0.f;
     rg.wlo = 0x7fffffff;
     rg.wLmax = (int)0x80000000;
     rg.whi = -1;
@@ -166,6 +168,7 @@ __device__ __forceinline__ void plan_group(const AttnParams& p, int64_t tile0, i
             rg.lo = max(rg.i - wi + 1, 0);
             rg.hi = rg.i;
             rg.cnt = lower_bound_lds(lpos, nvalid, rg.lo);
+            if (p.w_cont) rg.wt = p.w_cont[st + rg.i];
         }
     }
     rg.wcmax = uniform(row_max16(rg.cnt));
@@ -176,7 +179,11 @@ __device__ __forceinline__ void plan_group(const AttnParams& p, int64_t tile0, i
 // taken in the row plan's order; wave w owns the 16-row groups RG*w .. RG*w+RG-1
 // (each lane one query row per group).  The K and V^T operands fetched from
 // LDS for a subtile serve all of a wave's groups.
-template <typename T, int D, int RG>
+//
+// TR: the training variant -- band keys near a row's window start carry the soft
+// edge bias (edge_bias), so chunks classed "every row sees every key" must also
+// lie past every row's first edge_keys band keys.
+template <typename T, int D, int RG, bool TR>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     constexpr int BN = FwdShape<T, D>::BN;
     constexpr int NST = BN / 16;
@@ -321,7 +328,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
                 const int last = base + BN - 1;
                 if (base > R.whi || last < R.wlo) kind = 0;
                 else if (base + 15 < R.wlo || last - 15 > R.whi) kind = 5;
-                else if (base >= R.wLmax && last <= R.wHmin) kind = 1;
+                else if (base >= R.wLmax + (TR ? p.edge_keys : 0) && last <= R.wHmin) kind = 1;
                 else if (last <= R.wHmin) kind = 2;
                 else kind = 3;
             } else {
@@ -346,7 +353,10 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
                     const int tl = R.lo - (base + stt * 16) - lane_off;
                     floatx4 ci;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ci[r] = r < tl ? NEG : 0.f;
+                    for (int r = 0; r < 4; ++r) {
+                        const float eb = TR ? edge_bias(p, R.wt, tl - r + R.i - R.lo) : 0.f;
+                        ci[r] = r < tl ? NEG : eb;
+                    }
                     KOp<T, D> ko;
                     ko.load(kl, KT::RS, stt * 16, lane);
                     S[u][stt] = ko.dot(qr[u], ci);
@@ -357,7 +367,10 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
                     const int tl = R.lo - (base + stt * 16) - lane_off, th = R.hi - (base + stt * 16) - lane_off;
                     floatx4 ci;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ci[r] = (r < tl || r > th) ? NEG : 0.f;
+                    for (int r = 0; r < 4; ++r) {
+                        const float eb = TR ? edge_bias(p, R.wt, th - r) : 0.f;
+                        ci[r] = (r < tl || r > th) ? NEG : eb;
+                    }
                     KOp<T, D> ko;
                     ko.load(kl, KT::RS, stt * 16, lane);
                     S[u][stt] = ko.dot(qr[u], ci);
@@ -375,7 +388,10 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
                     if (band) {
                         const int tl = R.lo - a - lane_off, th = R.hi - a - lane_off;
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) ci[r] = (r < tl || r > th) ? NEG : 0.f;
+                        for (int r = 0; r < 4; ++r) {
+                            const float eb = TR ? edge_bias(p, R.wt, th - r) : 0.f;
+                            ci[r] = (r < tl || r > th) ? NEG : eb;
+                        }
                     } else {
                         floatx4 bv = zero;
                         if (has_bias) {
@@ -490,17 +506,17 @@ static int fwd_groups(const AttnParams& p) {
     return (kFwdGroups == 2 && sizeof(T) == 2 && D == 64 && (p.block_size == 0 || p.block_size % 128 == 0)) ? 2 : 1;
 }
 
-template <typename T, int D>
+template <typename T, int D, bool TR>
 static void fwd_run(const AttnParams& p, hipStream_t stream) {
     const int rg = fwd_groups<T, D>(p);
     const int total = p.n_heads * p.num_seqs * ceil_div(p.n_tiles, rg);
-    if constexpr (sizeof(T) == 2 && D == 64) {
+    if constexpr (sizeof(T) == 2 && D == 64 && kFwdGroups == 2) {
         if (rg == 2) {
-            DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 2>), dim3(total), dim3(256), 0, stream, p);
+            DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 2, TR>), dim3(total), dim3(256), 0, stream, p);
             return;
         }
     }
-    DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 1>), dim3(total), dim3(256), 0, stream, p);
+    DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 1, TR>), dim3(total), dim3(256), 0, stream, p);
 }
 
 template <typename T>
@@ -508,8 +524,32 @@ static hipError_t fwd_dispatch(const AttnParams& p, hipStream_t stream) {
     if (p.n_heads * p.num_seqs * p.n_tiles == 0) return hipSuccess;
     const hipError_t e = plan_launch(p, stream);
     if (e != hipSuccess) return e;
-    if (p.head_dim == 64) fwd_run<T, 64>(p, stream);
-    else fwd_run<T, 128>(p, stream);
+    const bool tr = p.w_cont != nullptr;
+    if (p.head_dim == 64) {
+        if (tr) fwd_run<T, 64, true>(p, stream);
+        else fwd_run<T, 64, false>(p, stream);
+    } else {
+        if (tr) fwd_run<T, 128, true>(p, stream);
+        else fwd_run<T, 128, false>(p, stream);
+    }
+    return hipGetLastError();
+}
+
+// training variant: integer windows floor(w~) + 1 (w~ below 0 as 0, at most max_seqlen);
+// in the backward also clears the per-head window gradients
+__global__ __launch_bounds__(256) void train_windows_kernel(AttnParams p, int* w_int) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= p.total_len) return;
+    const float wt = fminf(fmaxf(p.w_cont[t], 0.f), (float)p.max_seqlen);
+    w_int[t] = (int)floorf(wt) + 1;
+    if (p.dw_h)  // backward: rows outside every sequence keep a zero gradient
+        for (int h = 0; h < p.n_heads; ++h) p.dw_h[(int64_t)t * p.n_heads + h] = 0.f;
+}
+
+hipError_t train_windows_launch(const AttnParams& p, int* w_int, hipStream_t stream) {
+    if (p.total_len == 0) return hipSuccess;
+    DSALT_LAUNCH("train_windows", train_windows_kernel, dim3(ceil_div(p.total_len, 256)), dim3(256), 0, stream, p,
+                 w_int);
     return hipGetLastError();
 }
 

@@ -178,12 +178,8 @@ int dsalt_select(const dsalt_select_args* a, dsalt_stream_t stream) {
     return dsalt_select_with_border_cap(a, stream, 1 << 30);
 }
 
-size_t dsalt_fwd_workspace_bytes(const dsalt_fwd_args* a) {
-    if (!a || check_problem(a->p, true)) return 0;
-    return dsalt::plan_bytes(attn_common(a->p, 1.0f));
-}
-
-int dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream) {
+// forward parameters; `need_w` is false for the training variant (windows from w_cont)
+static int fwd_params(const dsalt_fwd_args* a, bool need_w, dsalt::AttnParams* out) {
     if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
     int rc = check_problem(a->p, true);
     if (rc) return rc;
@@ -192,7 +188,7 @@ int dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream) {
     if ((rc = check_rows(a->k, a->k_stride_t, a->k_stride_h, dt, "k"))) return rc;
     if ((rc = check_rows(a->v, a->v_stride_t, a->v_stride_h, dt, "v"))) return rc;
     if ((rc = check_rows(a->out, a->o_stride_t, a->o_stride_h, dt, "out"))) return rc;
-    if (!a->w || !a->cu_seqlens || !a->lse || (a->p.k_lmk > 0 && !a->lmk_idx))
+    if ((need_w && !a->w) || !a->cu_seqlens || !a->lse || (a->p.k_lmk > 0 && !a->lmk_idx))
         return fail(DSALT_ERR_INVALID, "w, cu_seqlens, lse and lmk_idx are required");
     if (!(a->scale > 0.f)) return fail(DSALT_ERR_INVALID, "scale must be positive");
     dsalt::AttnParams p = attn_common(a->p, a->scale);
@@ -213,13 +209,64 @@ int dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream) {
     p.cu = a->cu_seqlens;
     p.lmk = a->lmk_idx;
     p.lbias = a->lmk_bias;
+    *out = p;
+    return DSALT_OK;
+}
+
+// training variant: soft-edge parameters on top of the operator's
+static int train_params(const float* w_cont, float tau_win, float win_edge, dsalt::AttnParams* p) {
+    if (!w_cont) return fail(DSALT_ERR_INVALID, "w_cont is required");
+    if (!(tau_win > 0.f)) return fail(DSALT_ERR_INVALID, "tau_win must be positive");
+    if (!(win_edge >= 0.f) || win_edge > 65536.f) return fail(DSALT_ERR_INVALID, "win_edge must be in [0, 65536]");
+    if (p->block_size != 0) return fail(DSALT_ERR_UNSUPPORTED, "the training variant takes global landmark sets");
+    p->w_cont = w_cont;
+    p->tau_inv = 1.0f / tau_win;
+    p->edge = win_edge;
+    p->edge_keys = (int)ceilf(win_edge);
+    return DSALT_OK;
+}
+
+static size_t wint_bytes(const dsalt::AttnParams& p) { return ((size_t)p.total_len * sizeof(int) + 255) & ~(size_t)255; }
+
+size_t dsalt_fwd_workspace_bytes(const dsalt_fwd_args* a) {
+    if (!a || check_problem(a->p, true)) return 0;
+    return dsalt::plan_bytes(attn_common(a->p, 1.0f));
+}
+
+int dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream) {
+    dsalt::AttnParams p;
+    int rc = fwd_params(a, true, &p);
+    if (rc) return rc;
     const size_t need = dsalt::plan_bytes(p);
     if (!a->workspace || a->workspace_bytes < need)
         return fail(DSALT_ERR_WORKSPACE, "forward needs %zu workspace bytes, got %zu", need, a->workspace_bytes);
     return hip_status(dsalt::fwd_launch(p, a->workspace, (hipStream_t)stream), "dsalt_fwd");
 }
 
-static int bwd_params(const dsalt_bwd_args* a, dsalt::AttnParams* out) {
+size_t dsalt_train_fwd_workspace_bytes(const dsalt_train_fwd_args* a) {
+    if (!a || check_problem(a->base.p, true)) return 0;
+    const dsalt::AttnParams p = attn_common(a->base.p, 1.0f);
+    return wint_bytes(p) + dsalt::plan_bytes(p);
+}
+
+int dsalt_train_fwd(const dsalt_train_fwd_args* a, dsalt_stream_t stream) {
+    if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
+    dsalt::AttnParams p;
+    int rc = fwd_params(&a->base, false, &p);
+    if (rc) return rc;
+    if ((rc = train_params(a->w_cont, a->tau_win, a->win_edge, &p))) return rc;
+    const size_t need = wint_bytes(p) + dsalt::plan_bytes(p);
+    if (!a->base.workspace || a->base.workspace_bytes < need)
+        return fail(DSALT_ERR_WORKSPACE, "training forward needs %zu workspace bytes, got %zu", need,
+                    a->base.workspace_bytes);
+    int* w_int = (int*)a->base.workspace;
+    p.w = w_int;
+    hipError_t e = dsalt::train_windows_launch(p, w_int, (hipStream_t)stream);
+    if (e == hipSuccess) e = dsalt::fwd_launch(p, (char*)a->base.workspace + wint_bytes(p), (hipStream_t)stream);
+    return hip_status(e, "dsalt_train_fwd");
+}
+
+static int bwd_params(const dsalt_bwd_args* a, dsalt::AttnParams* out, bool need_w = true) {
     if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
     int rc = check_problem(a->p, true);
     if (rc) return rc;
@@ -235,7 +282,7 @@ static int bwd_params(const dsalt_bwd_args* a, dsalt::AttnParams* out) {
     if ((rc = check_rows(a->dout, a->do_stride_t, a->do_stride_h, dt, "dout"))) return rc;
     if (!a->dq || !a->dk || !a->dv || !aligned16(a->dq) || !aligned16(a->dk) || !aligned16(a->dv))
         return fail(DSALT_ERR_INVALID, "dq, dk, dv must be non-null and 16-byte aligned");
-    if (!a->w || !a->cu_seqlens || !a->lse || (a->p.k_lmk > 0 && !a->lmk_idx))
+    if ((need_w && !a->w) || !a->cu_seqlens || !a->lse || (a->p.k_lmk > 0 && !a->lmk_idx))
         return fail(DSALT_ERR_INVALID, "w, cu_seqlens, lse and lmk_idx are required");
     if (!(a->scale > 0.f)) return fail(DSALT_ERR_INVALID, "scale must be positive");
     dsalt::AttnParams p = attn_common(a->p, a->scale);
@@ -281,6 +328,39 @@ int dsalt_bwd(const dsalt_bwd_args* a, dsalt_stream_t stream) {
     if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
         return fail(DSALT_ERR_WORKSPACE, "backward needs %zu workspace bytes, got %zu", need, a->workspace_bytes);
     return hip_status(dsalt::bwd_launch(p, a->workspace, (hipStream_t)stream), "dsalt_bwd");
+}
+
+// training backward workspace: integer windows, per-head d w~, then the operator's
+static size_t train_bwd_extra(const dsalt::AttnParams& p) {
+    return wint_bytes(p) + (((size_t)p.total_len * p.n_heads * sizeof(float) + 255) & ~(size_t)255);
+}
+
+size_t dsalt_train_bwd_workspace_bytes(const dsalt_train_bwd_args* a) {
+    dsalt::AttnParams p;
+    if (!a || bwd_params(&a->base, &p, false)) return 0;
+    return train_bwd_extra(p) + dsalt::bwd_workspace(p);
+}
+
+int dsalt_train_bwd(const dsalt_train_bwd_args* a, dsalt_stream_t stream) {
+    if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
+    dsalt::AttnParams p;
+    int rc = bwd_params(&a->base, &p, false);
+    if (rc) return rc;
+    if ((rc = train_params(a->w_cont, a->tau_win, a->win_edge, &p))) return rc;
+    if (!a->d_w) return fail(DSALT_ERR_INVALID, "d_w is required");
+    const size_t need = train_bwd_extra(p) + dsalt::bwd_workspace(p);
+    if (!a->base.workspace || a->base.workspace_bytes < need || !aligned16(a->base.workspace))
+        return fail(DSALT_ERR_WORKSPACE, "training backward needs %zu workspace bytes, got %zu", need,
+                    a->base.workspace_bytes);
+    char* w = (char*)a->base.workspace;
+    int* w_int = (int*)w;
+    p.w = w_int;
+    p.dw_h = (float*)(w + wint_bytes(p));
+    p.d_w = a->d_w;
+    hipError_t e = dsalt::train_windows_launch(p, w_int, (hipStream_t)stream);
+    if (e == hipSuccess) e = dsalt::bwd_launch(p, w + train_bwd_extra(p), (hipStream_t)stream);
+    if (e == hipSuccess) e = dsalt::train_dw_launch(p, (hipStream_t)stream);
+    return hip_status(e, "dsalt_train_bwd");
 }
 
 int dsalt_gather_landmarks(const dsalt_gather_args* a, dsalt_stream_t stream) {

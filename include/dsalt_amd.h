@@ -157,6 +157,32 @@ typedef struct dsalt_gather_args {
 int    dsalt_abi_version(void);
 const char* dsalt_last_error(void);
 
+/* Training variant with differentiable selectors.  Replaces _train_fwd_kernel,
+ * _train_bwd_kernel and _train_bwd_dkdv_kernel with their wrapper
+ * DSALTTrainFunction (dsalt/kernels/dsalt_triton_train.py:74-216,241-490,586-762),
+ * whose semantics are the dense log-bias of dsalt/modules/dsalt_attention.py:520-563:
+ * band keys j with 0 <= i - j <= w~(i) (continuous window w_cont, values below 0 act
+ * as 0) carry the logit bias log sigmoid((w~ - d) / tau_win) where d = i - j >
+ * w~ - win_edge (0 in the core); landmarks p with p < i - w~ get lmk_bias (the
+ * log-weight log sigmoid(s / tau_lmk), -inf for empty slots).  base.w is not read.
+ * Global landmark sets only. */
+typedef struct dsalt_train_fwd_args {
+    dsalt_fwd_args base;       /* lmk_bias = landmark log-weights                    */
+    const float* w_cont;       /* [T] continuous windows                             */
+    float tau_win;             /* > 0                                                */
+    float win_edge;            /* >= 0                                               */
+} dsalt_train_fwd_args;
+
+/* Backward of the training variant: dq, dk, dv, d_bias (= d lmk_logw) as
+ * dsalt_bwd, plus d_w [T]: d loss / d w~ summed over heads (:708-757). */
+typedef struct dsalt_train_bwd_args {
+    dsalt_bwd_args base;
+    const float* w_cont;
+    float tau_win;
+    float win_edge;
+    float* d_w;                /* out [T]                                            */
+} dsalt_train_bwd_args;
+
 size_t dsalt_select_workspace_bytes(const dsalt_select_args* a);
 int    dsalt_select(const dsalt_select_args* a, dsalt_stream_t stream);
 
@@ -167,6 +193,11 @@ size_t dsalt_bwd_workspace_bytes(const dsalt_bwd_args* a);
 int    dsalt_bwd(const dsalt_bwd_args* a, dsalt_stream_t stream);
 
 int    dsalt_gather_landmarks(const dsalt_gather_args* a, dsalt_stream_t stream);
+
+size_t dsalt_train_fwd_workspace_bytes(const dsalt_train_fwd_args* a);
+int    dsalt_train_fwd(const dsalt_train_fwd_args* a, dsalt_stream_t stream);
+size_t dsalt_train_bwd_workspace_bytes(const dsalt_train_bwd_args* a);
+int    dsalt_train_bwd(const dsalt_train_bwd_args* a, dsalt_stream_t stream);
 
 /* Testing hook with no counterpart in the reference: dsalt_select with its
  * top-k working sets shrunk by `border_cap` so tests can drive the paths that

@@ -12,7 +12,9 @@ fallback mask ``_build_mask_packed`` (dsalt/modules/dsalt_attention.py:95-144) w
 builders (dsalt/kernels/window_utils.py:19-70), the packed block map
 (dsalt/kernels/selectors.py:37-67), the landmark gather (selectors.py:137-159), and the
 block-causal selection and exact kernel-semantics attention of
-results/causal_landmark_check.py:68-147.  Inputs are small, seeded and float32.
+results/causal_landmark_check.py:68-147, and the training log-bias of
+dsalt/modules/dsalt_attention.py:520-563 with its SDPA gradients.  Inputs are small and
+seeded (float32; the training case float64).
 """
 from __future__ import annotations
 
@@ -169,8 +171,53 @@ def block_causal_case(CLC, gqa: bool, seed: int, T: int = 160, B: int = 32, dh: 
                 out=np.concatenate(outs, 0))
 
 
+def train_case(DA, seed: int = 600):
+    """Training semantics: the dense log-bias of ``DSALTAttention._dense_logbias_from_kernel``
+    (dsalt/modules/dsalt_attention.py:520-563: hard band ``0 <= d <= w~`` with the soft edge
+    ``log sigmoid((w~ - d)/tau_win)`` outside the core ``d <= w~ - win_edge``, landmarks at
+    ``lmk_pos`` weighted by ``lmk_logw`` where ``pos <= i`` and ``pos < i - w~``) fed to SDPA
+    as in ``_packed_train`` (:488-518); float64 autograd gives the reference gradients of
+    q, k, v, w~ and lmk_logw for a random cotangent."""
+    g = torch.Generator().manual_seed(seed)
+    N, L, H, D, K = 2, 48, 2, 8, 6
+    tau_win, win_edge = 1.5, 4.0
+    T = N * L
+    q = torch.randn(T, H, D, generator=g, dtype=torch.float64)
+    kk = torch.randn(T, H, D, generator=g, dtype=torch.float64)
+    vv = torch.randn(T, H, D, generator=g, dtype=torch.float64)
+    w_cont = 1.0 + torch.rand(T, generator=g, dtype=torch.float64) * 18.0
+    pos = torch.full((H, N, K), -1, dtype=torch.int64)
+    for h in range(H):
+        for s in range(N):
+            n = K - (h + s) % 2
+            pos[h, s, :n] = torch.randperm(L, generator=g)[:n]
+    logw = torch.log(torch.sigmoid(torch.randn(H, N, K, generator=g, dtype=torch.float64)))
+    logw = torch.where(pos >= 0, logw, torch.full_like(logw, float("-inf")))
+    cot = torch.randn(T, H, D, generator=g, dtype=torch.float64)
+    ns = types.SimpleNamespace(n_heads=H, tau_win=tau_win, win_edge=win_edge)
+    qr, kr, vr, wr, lr = (t.clone().requires_grad_(True) for t in (q, kk, vv, w_cont, logw))
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)  # the reference builds its -inf fills in the default dtype
+    try:
+        bias = DA.DSALTAttention._dense_logbias_from_kernel(ns, wr, pos, lr, N, L, torch.device("cpu"))
+    finally:
+        torch.set_default_dtype(prev)
+    qb = qr.view(N, L, H, D).transpose(1, 2)
+    kb = kr.view(N, L, H, D).transpose(1, 2)
+    vb = vr.view(N, L, H, D).transpose(1, 2)
+    ob = torch.nn.functional.scaled_dot_product_attention(qb, kb, vb, attn_mask=bias)
+    out = ob.transpose(1, 2).reshape(T, H, D)
+    (out * cot).sum().backward()
+    return dict(q=q.numpy(), k=kk.numpy(), v=vv.numpy(), w_cont=w_cont.numpy(), lmk_pos=pos.numpy(),
+                lmk_logw=logw.numpy(), tau_win=np.float64(tau_win), win_edge=np.float64(win_edge),
+                cu=np.arange(0, T + 1, L, dtype=np.int32), cot=cot.numpy(), bias=bias.detach().numpy(),
+                out=out.detach().numpy(), dq=qr.grad.numpy(), dk=kr.grad.numpy(), dv=vr.grad.numpy(),
+                dw=wr.grad.numpy(), dlogw=lr.grad.numpy())
+
+
 def main():
     LT, SEL, SA, WU, DA, CLC = _import_reference()
+    np.savez_compressed(os.path.join(OUT, "train_dense.npz"), **train_case(DA))
     for name, c in selection_cases(LT, SEL).items():
         np.savez_compressed(os.path.join(OUT, f"select_{name}.npz"), **c)
     np.savez_compressed(os.path.join(OUT, "literal_fallback.npz"), **literal_case(LT, SEL, SA, DA))

@@ -46,6 +46,8 @@ STRUCTS = {
     "dsalt_fwd_args": _lib.FwdArgs,
     "dsalt_bwd_args": _lib.BwdArgs,
     "dsalt_gather_args": _lib.GatherArgs,
+    "dsalt_train_fwd_args": _lib.TrainFwdArgs,
+    "dsalt_train_bwd_args": _lib.TrainBwdArgs,
 }
 
 

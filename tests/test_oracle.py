@@ -13,6 +13,10 @@ Parity status of each oracle function (how it is pinned):
                                  causal-SDPA and O=V special cases + no-double-count
   attention.attention_bwd        central finite differences + torch autograd of the dense form
   attention.literal_mask         golden (reference _build_mask_packed + masked SDPA)
+  train.train_bias / train_fwd   golden (reference _dense_logbias_from_kernel + SDPA, float64)
+                                 + win_edge 0 reduces to attention_fwd with window floor(w~)+1
+  train.train_bwd                golden (float64 autograd of the reference dense form)
+                                 + central finite differences in w~ and lmk_logw
 """
 from __future__ import annotations
 
@@ -24,6 +28,7 @@ import torch
 
 from oracle import attention as OA
 from oracle import select as OS
+from oracle import train as OT
 from tests.helpers import load_golden, rel_err
 
 
@@ -294,3 +299,93 @@ def test_bwd_gqa_sums_groups_and_matches_autograd():
     assert rel_err(dq, qt.grad.numpy()) < 1e-12
     assert rel_err(dk, kt.grad.numpy()) < 1e-12
     assert rel_err(dv, vt.grad.numpy()) < 1e-12
+
+
+# ------------------------------------------------------------- training variant
+def _train_args(g):
+    return (g["q"], g["k"], g["v"], g["w_cont"], g["cu"], g["lmk_pos"], g["lmk_logw"],
+            1.0 / math.sqrt(g["q"].shape[-1]), float(g["tau_win"]), float(g["win_edge"]))
+
+
+def test_train_bias_matches_reference_golden():
+    g = load_golden("train_dense")
+    L = int(g["cu"][1])
+    for h in range(g["q"].shape[1]):
+        for s in range(len(g["cu"]) - 1):
+            b, _ = OT.train_bias(g["w_cont"][s * L:(s + 1) * L], g["lmk_pos"][h, s], g["lmk_logw"][h, s],
+                                 float(g["tau_win"]), float(g["win_edge"]))
+            ref = g["bias"][s, h]
+            np.testing.assert_array_equal(np.isinf(b), np.isinf(ref))
+            fin = np.isfinite(ref)
+            assert np.abs(b[fin] - ref[fin]).max() < 1e-12
+
+
+def test_train_fwd_bwd_match_reference_golden():
+    g = load_golden("train_dense")
+    a = _train_args(g)
+    o, _ = OT.train_fwd(*a)
+    assert rel_err(o, g["out"]) < 1e-12
+    dq, dk, dv, dw, dlogw = OT.train_bwd(*a, g["cot"])
+    for got, key in ((dq, "dq"), (dk, "dk"), (dv, "dv"), (dw, "dw")):
+        assert rel_err(got, g[key]) < 1e-10, key
+    fin = np.isfinite(g["lmk_logw"])
+    assert np.abs(dlogw[fin] - g["dlogw"][fin]).max() < 1e-10
+    assert np.all(dlogw[~fin] == 0)
+    assert np.abs(dw).max() > 1e-3  # the soft edge carries gradient in this case
+
+
+def test_train_without_soft_edge_is_the_inference_operator():
+    """win_edge 0 puts the whole band in the core: attention over [i - floor(w~), i] plus the
+    landmarks left of it, each with its log weight as an additive logit."""
+    rng = np.random.default_rng(21)
+    lens, H, D, K = (37, 29), 2, 8, 5
+    T = sum(lens)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    q, k, v = (rng.standard_normal((T, H, D)) for _ in range(3))
+    w_cont = rng.uniform(0.0, 14.0, T)
+    w_cont[::7] = np.floor(w_cont[::7])          # integer windows hit the strict landmark cut
+    pos = np.full((H, 2, K), -1)
+    for h in range(H):
+        for s, L in enumerate(lens):
+            pos[h, s, :K - 1] = np.sort(rng.choice(L, K - 1, replace=False))
+    logw = np.where(pos >= 0, np.log(rng.uniform(0.05, 1.0, pos.shape)), -np.inf)
+    o, lse = OT.train_fwd(q, k, v, w_cont, cu, pos, logw, 0.4, 1.3, 0.0)
+    bias = np.where(pos >= 0, logw, 0.0)[:, :, None, :]
+    o2, lse2 = OA.attention_fwd(q, k, v, np.floor(w_cont).astype(int) + 1, cu, pos[:, :, None, :], 0.4,
+                                lmk_bias=bias)
+    assert np.abs(o - o2).max() < 1e-12
+    assert np.abs(lse - lse2).max() < 1e-12
+
+
+def test_train_bwd_matches_finite_differences_in_selectors():
+    rng = np.random.default_rng(31)
+    lens, H, D, K = (26, 19), 2, 4, 4
+    T = sum(lens)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    q, k, v, do = (rng.standard_normal((T, H, D)) for _ in range(4))
+    w_cont = rng.uniform(1.0, 12.0, T)
+    pos = np.full((H, 2, K), -1)
+    for h in range(H):
+        for s, L in enumerate(lens):
+            pos[h, s, :K - 1] = rng.choice(L, K - 1, replace=False)
+    logw = np.where(pos >= 0, np.log(rng.uniform(0.05, 1.0, pos.shape)), -np.inf)
+    scale, tau, edge = 0.5, 0.8, 3.0
+    _, _, _, dw, dlogw = OT.train_bwd(q, k, v, w_cont, cu, pos, logw, scale, tau, edge, do)
+
+    def loss(w_, lw_):
+        o, _ = OT.train_fwd(q, k, v, w_, cu, pos, lw_, scale, tau, edge)
+        return float((o * do).sum())
+
+    eps = 1e-6
+    for t in range(T):
+        wp, wm = w_cont.copy(), w_cont.copy()
+        wp[t] += eps
+        wm[t] -= eps
+        fd = (loss(wp, logw) - loss(wm, logw)) / (2 * eps)
+        assert abs(fd - dw[t]) < 1e-6 + 1e-5 * abs(fd), t
+    for ix in zip(*np.nonzero(pos >= 0)):
+        lp, lm = logw.copy(), logw.copy()
+        lp[ix] += eps
+        lm[ix] -= eps
+        fd = (loss(w_cont, lp) - loss(w_cont, lm)) / (2 * eps)
+        assert abs(fd - dlogw[ix]) < 1e-6 + 1e-5 * abs(fd), ix
