@@ -13,7 +13,8 @@ import torch
 
 from . import _lib
 from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, SELECT_BLOCK, SELECT_GLOBAL, STATS_PACKED,
-                   STATS_SEQUENCE, BwdArgs, FwdArgs, GatherArgs, Problem, SelectArgs)
+                   STATS_SEQUENCE, BwdArgs, FwdArgs, GatherArgs, Problem, SelectArgs, TrainBwdArgs,
+                   TrainFwdArgs)
 
 _DT = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
 MAX_LANDMARKS = 512
@@ -156,10 +157,9 @@ def select_landmarks(h: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, w: t
 
 
 # ------------------------------------------------------------------------ forward
-def attention_forward(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias=None, *, scale=None,
-                      max_seqlen=None, select_mode=SELECT_GLOBAL, block_size=512):
-    """(out [T,H,D] in q.dtype, lse [T,H] fp32).  lmk_idx [H,S,n_sets,K] int32 ascending with
-    -1 padding at the end of each set (as select_landmarks returns)."""
+def _fwd_args(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias, scale, max_seqlen, select_mode, block_size,
+              need_w=True):
+    """Checked FwdArgs with fresh outputs; returns (args, out, lse, tensors to keep alive)."""
     dev = _gpu(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias)
     q, k, v = _rows3(q, "q"), _rows3(k, "k"), _rows3(v, "v")
     dt = dtype_code(q.dtype)
@@ -178,7 +178,7 @@ def attention_forward(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias=None, *, scale=N
     if lmk_idx.shape[2] != n_sets(select_mode, maxlen, block_size):
         raise ValueError("lmk_idx n_sets does not match select_mode / block_size / max_seqlen")
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    w_c = w.detach().to(torch.int32).contiguous()
+    w_c = w.detach().to(torch.int32).contiguous() if need_w else None
     cu_c = cu_seqlens.detach().to(torch.int32).contiguous()
     li = lmk_idx.to(torch.int32).contiguous()
     lb = lmk_bias.detach().to(torch.float32).contiguous() if lmk_bias is not None else None
@@ -189,13 +189,24 @@ def attention_forward(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias=None, *, scale=N
     a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
     a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
     a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
-    a.w, a.cu_seqlens = w_c.data_ptr(), cu_c.data_ptr()
+    a.w = w_c.data_ptr() if w_c is not None else None
+    a.cu_seqlens = cu_c.data_ptr()
     a.lmk_idx = li.data_ptr() if li.numel() else None
     a.lmk_bias = lb.data_ptr() if lb is not None and lb.numel() else None
     a.out, a.o_stride_t, a.o_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
     a.lse, a.scale = lse.data_ptr(), scale
-    if T == 0:
+    return a, out, lse, (q, k, v, w_c, cu_c, li, lb)
+
+
+def attention_forward(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias=None, *, scale=None,
+                      max_seqlen=None, select_mode=SELECT_GLOBAL, block_size=512):
+    """(out [T,H,D] in q.dtype, lse [T,H] fp32).  lmk_idx [H,S,n_sets,K] int32 ascending with
+    -1 padding at the end of each set (as select_landmarks returns)."""
+    a, out, lse, keep = _fwd_args(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias, scale, max_seqlen, select_mode,
+                                  block_size)
+    if q.shape[0] == 0:
         return out, lse
+    dev = out.device
     L = _lib.load()
     ws = _workspace(L.dsalt_fwd_workspace_bytes(ctypes.byref(a)), dev)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
@@ -203,11 +214,36 @@ def attention_forward(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias=None, *, scale=N
     return out, lse
 
 
+def _w_cont(w_cont: torch.Tensor, T: int) -> torch.Tensor:
+    if w_cont.dim() != 1 or w_cont.shape[0] != T:
+        raise ValueError("w_cont must be [T]")
+    return w_cont.detach().to(torch.float32).contiguous()
+
+
+def train_forward(q, k, v, w_cont, cu_seqlens, lmk_idx, lmk_logw, *, tau_win=1.0, win_edge=4.0, scale=None,
+                  max_seqlen=None):
+    """Training variant: (out [T,H,D] in q.dtype, lse [T,H] fp32).  w_cont [T] continuous
+    windows; lmk_idx [H,S,1,K] ascending with -1 last; lmk_logw [H,S,1,K] landmark log-weights
+    (-inf or any value in -1 slots)."""
+    a, out, lse, keep = _fwd_args(q, k, v, w_cont, cu_seqlens, lmk_idx, lmk_logw, scale, max_seqlen,
+                                  SELECT_GLOBAL, 0, need_w=False)
+    if q.shape[0] == 0:
+        return out, lse
+    dev = out.device
+    wc = _w_cont(w_cont, q.shape[0])
+    t = TrainFwdArgs()
+    t.base, t.w_cont, t.tau_win, t.win_edge = a, wc.data_ptr(), float(tau_win), float(win_edge)
+    L = _lib.load()
+    ws = _workspace(L.dsalt_train_fwd_workspace_bytes(ctypes.byref(t)), dev)
+    t.base.workspace, t.base.workspace_bytes = ws.data_ptr(), ws.numel()
+    _lib.check("dsalt_train_fwd", L.dsalt_train_fwd(ctypes.byref(t), _stream(dev)))
+    return out, lse
+
+
 # ----------------------------------------------------------------------- backward
-def attention_backward(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias=None, *,
-                       scale=None, max_seqlen=None, want_dbias=True):
-    """(dq, dk, dv) in q.dtype, [T,H,D], and d_bias [H,S,1,K] fp32 (or None).
-    Global selection variant, n_kv_heads == n_heads."""
+def _bwd_args(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias, scale, max_seqlen, want_dbias,
+              need_w=True):
+    """Checked BwdArgs with fresh gradients; returns (args, dq, dk, dv, d_bias, keep-alive)."""
     dev = _gpu(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias)
     q, k, v, out, dout = (_rows3(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out"),
                                                    (dout, "dout")))
@@ -228,7 +264,7 @@ def attention_backward(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias
     if lmk_bias is not None and tuple(lmk_bias.shape) != tuple(lmk_idx.shape):
         raise ValueError("lmk_bias must have the shape of lmk_idx")
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    w_c = w.detach().to(torch.int32).contiguous()
+    w_c = w.detach().to(torch.int32).contiguous() if need_w else None
     cu_c = cu_seqlens.detach().to(torch.int32).contiguous()
     li = lmk_idx.to(torch.int32).contiguous()
     lb = lmk_bias.detach().to(torch.float32).contiguous() if lmk_bias is not None else None
@@ -244,14 +280,25 @@ def attention_backward(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias
     a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
     a.out, a.o_stride_t, a.o_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
     a.dout, a.do_stride_t, a.do_stride_h = dout.data_ptr(), dout.stride(0), dout.stride(1)
-    a.lse, a.w, a.cu_seqlens = lse.data_ptr(), w_c.data_ptr(), cu_c.data_ptr()
+    a.lse, a.cu_seqlens = lse.data_ptr(), cu_c.data_ptr()
+    a.w = w_c.data_ptr() if w_c is not None else None
     a.lmk_idx = li.data_ptr() if li.numel() else None
     a.lmk_bias = lb.data_ptr() if lb is not None and lb.numel() else None
     a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
     a.d_bias = db.data_ptr() if db is not None and db.numel() else None
     a.scale = scale
-    if T == 0:
+    return a, dq, dk, dv, db, (q, k, v, out, dout, w_c, cu_c, li, lb, lse)
+
+
+def attention_backward(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias=None, *,
+                       scale=None, max_seqlen=None, want_dbias=True):
+    """(dq, dk, dv) in q.dtype, [T,H,D], and d_bias [H,S,1,K] fp32 (or None).
+    Global selection variant, n_kv_heads == n_heads."""
+    a, dq, dk, dv, db, keep = _bwd_args(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias, scale,
+                                        max_seqlen, want_dbias)
+    if q.shape[0] == 0:
         return dq.zero_(), dk.zero_(), dv.zero_(), db
+    dev = dq.device
     L = _lib.load()
     need = L.dsalt_bwd_workspace_bytes(ctypes.byref(a))
     if need == 0:
@@ -260,6 +307,31 @@ def attention_backward(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     _lib.check("dsalt_bwd", L.dsalt_bwd(ctypes.byref(a), _stream(dev)))
     return dq, dk, dv, db
+
+
+def train_backward(dout, q, k, v, out, lse, w_cont, cu_seqlens, lmk_idx, lmk_logw, *, tau_win=1.0,
+                   win_edge=4.0, scale=None, max_seqlen=None, want_dlogw=True):
+    """Training variant: (dq, dk, dv) in q.dtype, d_logw [H,S,1,K] fp32 (or None) and
+    d_w [T] fp32, the window gradient summed over heads.  n_kv_heads == n_heads."""
+    a, dq, dk, dv, db, keep = _bwd_args(dout, q, k, v, out, lse, w_cont, cu_seqlens, lmk_idx, lmk_logw, scale,
+                                        max_seqlen, want_dlogw, need_w=False)
+    T = q.shape[0]
+    d_w = torch.zeros(T, dtype=torch.float32, device=dq.device)
+    if T == 0:
+        return dq.zero_(), dk.zero_(), dv.zero_(), db, d_w
+    dev = dq.device
+    wc = _w_cont(w_cont, T)
+    t = TrainBwdArgs()
+    t.base, t.w_cont, t.tau_win, t.win_edge, t.d_w = a, wc.data_ptr(), float(tau_win), float(win_edge), \
+        d_w.data_ptr()
+    L = _lib.load()
+    need = L.dsalt_train_bwd_workspace_bytes(ctypes.byref(t))
+    if need == 0:
+        _lib.check("dsalt_train_bwd", L.dsalt_train_bwd(ctypes.byref(t), None))
+    ws = _workspace(need, dev)
+    t.base.workspace, t.base.workspace_bytes = ws.data_ptr(), ws.numel()
+    _lib.check("dsalt_train_bwd", L.dsalt_train_bwd(ctypes.byref(t), _stream(dev)))
+    return dq, dk, dv, db, d_w
 
 
 # ------------------------------------------------------------------------- gather

@@ -128,3 +128,50 @@ def test_workspace_sizes_and_small_workspace():
     assert lib.dsalt_select(ctypes.byref(s), None) == 3
     s.p.select_mode, s.p.block_size = 1, 128
     assert lib.dsalt_select_workspace_bytes(ctypes.byref(s)) > 0
+
+
+def _valid_train_fwd():
+    t = _lib.TrainFwdArgs()
+    t.base = _valid_fwd()
+    t.base.w = None  # the training variant reads w_cont, not w
+    t.w_cont, t.tau_win, t.win_edge = 1 << 20, 1.0, 4.0
+    return t
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("tau_win", 0.0, 1), ("tau_win", -1.0, 1), ("win_edge", -0.5, 1), ("win_edge", float("nan"), 1),
+    ("w_cont", None, 1)])
+def test_train_validation(field, value, code):
+    lib = _lib.load()
+    t = _valid_train_fwd()
+    setattr(t, field, value)
+    assert lib.dsalt_train_fwd(ctypes.byref(t), None) == code
+    assert lib.dsalt_last_error()
+
+
+def test_train_rejects_block_sets_and_small_workspace():
+    lib = _lib.load()
+    t = _valid_train_fwd()
+    need = lib.dsalt_train_fwd_workspace_bytes(ctypes.byref(t))
+    assert need >= 128 * 4
+    t.base.workspace, t.base.workspace_bytes = 1 << 20, need - 1
+    assert lib.dsalt_train_fwd(ctypes.byref(t), None) == 3
+    t.base.p.select_mode, t.base.p.block_size = 1, 64
+    assert lib.dsalt_train_fwd(ctypes.byref(t), None) == 2
+    b = _lib.TrainBwdArgs()
+    b.base.p = _lib.Problem(128, 1, 128, 2, 2, 64, 8, 0, 0, _lib.DTYPE_BF16)
+    fake = 1 << 20
+    b.base.q = b.base.k = b.base.v = b.base.out = b.base.dout = fake
+    b.base.dq = b.base.dk = b.base.dv = fake
+    for f in ("q", "k", "v", "o", "do"):
+        setattr(b.base, f + "_stride_t", 128)
+        setattr(b.base, f + "_stride_h", 64)
+    b.base.cu_seqlens = b.base.lmk_idx = b.base.lse = fake
+    b.base.scale = 0.125
+    b.w_cont, b.tau_win, b.win_edge = fake, 1.0, 4.0
+    assert lib.dsalt_train_bwd(ctypes.byref(b), None) == 1  # d_w missing
+    b.d_w = fake
+    need = lib.dsalt_train_bwd_workspace_bytes(ctypes.byref(b))
+    assert need >= 128 * 4 + 128 * 2 * 4
+    b.base.workspace, b.base.workspace_bytes = fake, need - 16
+    assert lib.dsalt_train_bwd(ctypes.byref(b), None) == 3
