@@ -1,8 +1,8 @@
 """DSALT attention layer on MI355X.
 
 Mirrors ``DSALTAttention`` of ``dsalt/modules/dsalt_attention.py:147-704`` (constructor,
-parameters and ``forward(x, cu_seqlens, max_seqlen, rope_cs, cu_list) -> (out, aux)``) with
-the inference branch of ``_packed`` (:610-634):
+parameters and ``forward(x, cu_seqlens, max_seqlen, rope_cs, cu_list) -> (out, aux)``).
+Inference branch of ``_packed`` (:610-634):
   * q/k/v projections (library GEMMs), RoPE on q and k;
   * windows ``w = floor(n_min + sigmoid(win_gate(x)) (n_max - n_min))``, at least 1
     (:277-284), and ``alpha = sigmoid(alpha_w)`` (:228, :243-244);
@@ -12,20 +12,26 @@ the inference branch of ``_packed`` (:610-634):
 set, statistics of the prefix), the variant of ``results/causal_landmark_check.py:150-189``.
 Batched ``[B, T, d]`` input is run as ``B`` packed sequences of length ``T``.
 
-Not provided here: the differentiable selectors of the training branch (soft window edge,
-landmark log-weight; ``:440-563``) -- in training mode the layer runs the hard-selection
-operator, whose gradients reach the projections but not ``win_gate`` / ``alpha_w`` -- and
-the dense ``_last_P`` rebuild for the metrics (``:636-702``), which stays ``None``.
+Training branch (``self.training``, :597-603, :440-487): the differentiable selectors --
+continuous windows ``w~ = n_min + sigmoid(win_gate(x)) (n_max - n_min)`` (gradient to
+``win_gate`` through the soft window edge) and landmark log-weights
+``log sigmoid(s / tau_lmk)`` of the hybrid score at the hard-selected positions (gradient to
+``alpha_w``, ``x`` and ``v_proj``) -- feed the training attention kernels.  Global landmark
+sets only, as in the reference.
+
+Not provided here: the dense ``_last_P`` rebuild for the metrics (``:636-702``), which stays
+``None``.
 """
 from __future__ import annotations
 
 import math
-import warnings
 
 import torch
 import torch.nn as nn
 
 from ..kernels.dsalt_attn import dsalt_attention
+from ..kernels.dsalt_train import dsalt_train_attention
+from ..kernels.landmark_tokens_ker import hybrid_scores_per_head
 from ..kernels.selectors import _compute_landmark_indices
 from ..kernels.window_utils import apply_rotary_emb, build_rope_cache
 
@@ -62,7 +68,6 @@ class DSALTAttention(nn.Module):
         self.tau_win, self.tau_lmk, self.win_edge = 1.0, 2.0, 4
         self._last_P = None
         self._collect_last_P = False
-        self._warned_training = False
         cos, sin = build_rope_cache(max_seq_len, self.head_dim, torch.device("cpu"), base=rope_base, scale=yarn_scale)
         self.register_buffer("rope_cos", cos, persistent=False)
         self.register_buffer("rope_sin", sin, persistent=False)
@@ -102,11 +107,37 @@ class DSALTAttention(nn.Module):
         out, aux = self._packed(x.reshape(B * T, -1), cu, B * T, x.device, None, list(range(0, (B + 1) * T, T)))
         return out.view(B, T, -1), aux
 
+    def _train_selectors(self, x, cu_seqlens, total_len, device, cu_list=None):
+        """``(w_cont [T], lmk_pos [H, S, k] int64, lmk_logw [H, S, k])`` of the training branch
+        (``dsalt_attention.py:457-487``): hard landmark positions from the floored windows,
+        log-weights differentiable in ``alpha_w`` (and in ``x`` / ``v_proj`` through the
+        hybrid score), windows differentiable in ``win_gate``."""
+        w_cont = self._window_continuous(x)
+        alpha = self._alpha()
+        with torch.no_grad():
+            w_disc = w_cont.floor().clamp(min=1)
+            lmk_pos, _, _ = _compute_landmark_indices(x.detach(), self.v_proj.weight.detach(),
+                                                      alpha.detach().float(), w_disc, cu_seqlens, self.k_lmk,
+                                                      self.n_min, total_len, cu_list, head_dim=self.head_dim,
+                                                      stats_scope=self.stats_scope)
+        scores, _, _ = hybrid_scores_per_head(x, self.v_proj.weight, alpha, self.n_heads, self.head_dim)
+        starts = cu_seqlens[:-1].to(device).long()
+        abs_pos = starts[None, :, None] + lmk_pos.clamp(min=0)
+        head_ix = torch.arange(self.n_heads, device=device)[:, None, None]
+        s_sel = scores[abs_pos, head_ix]
+        lmk_logw = torch.log(torch.sigmoid(s_sel / self.tau_lmk).clamp(min=1e-20))
+        lmk_logw = torch.where(lmk_pos >= 0, lmk_logw, torch.full_like(lmk_logw, float("-inf")))
+        return w_cont, lmk_pos, lmk_logw
+
+    def _packed_train_triton(self, q, k, v, x, cu_seqlens, total_len, device, cu_list=None):
+        """Differentiable sparse training attention (``dsalt_attention.py:440-455``)."""
+        if self.select_mode != "global":
+            raise NotImplementedError("the training branch takes global landmark sets (select_mode='global')")
+        w_cont, lmk_pos, lmk_logw = self._train_selectors(x, cu_seqlens, total_len, device, cu_list)
+        return dsalt_train_attention(q, k, v, lmk_pos, lmk_logw, w_cont, cu_seqlens, tau_win=self.tau_win,
+                                     win_edge=float(self.win_edge), n_max=self.n_max, cu_list=cu_list)
+
     def _packed(self, x, cu_seqlens, total_len, device, rope_cs=None, cu_list=None):
-        if self.training and not self._warned_training:
-            warnings.warn("DSALTAttention (dsalt_amd) trains through the hard-selection operator: win_gate and "
-                          "alpha_w receive no gradient")
-            self._warned_training = True
         q = self.q_proj(x).view(total_len, self.n_heads, self.head_dim)
         k = self.k_proj(x).view(total_len, self.n_kv_heads, self.head_dim)
         v = self.v_proj(x).view(total_len, self.n_kv_heads, self.head_dim)
@@ -120,6 +151,11 @@ class DSALTAttention(nn.Module):
             cos, sin = rope_cs
         cos, sin = cos.to(q.dtype), sin.to(q.dtype)
         q, k = apply_rotary_emb(q, k, cos.unsqueeze(1), sin.unsqueeze(1))
+        self._last_P = None
+        if self.training:
+            out = self._packed_train_triton(q.contiguous(), k.contiguous(), v.contiguous(), x, cu_seqlens,
+                                            total_len, device, cu_list)
+            return self._apply_out_proj(out.view(total_len, self.d_model)), self._aux_zero(x.device, x.dtype)
         w = self._window_sizes(x, floor=True)
         alpha = self._alpha()
         lmk, _, _ = _compute_landmark_indices(x.detach(), self.v_proj.weight.detach(), alpha.detach().float(), w,

@@ -26,7 +26,7 @@ __all__ = ["train_bias", "train_fwd", "train_bwd"]
 
 
 def _sigmoid(x):
-    return 1.0 / (1.0 + np.exp(-x))
+    return np.exp(-np.logaddexp(0.0, -x))
 
 
 def train_bias(w_seq, lmk_pos_hs, lmk_logw_hs, tau_win, win_edge):

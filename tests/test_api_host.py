@@ -52,3 +52,28 @@ def test_rope_cache_matches_closed_form():
     # a rotation keeps every 2-d pair's norm
     np.testing.assert_allclose((qr[..., :4] ** 2 + qr[..., 4:] ** 2).numpy(),
                                (q[..., :4] ** 2 + q[..., 4:] ** 2).numpy(), atol=1e-12)
+
+
+def _zscore(n):
+    return (n - n.mean(0, keepdim=True)) / n.std(0, keepdim=True).clamp(min=1e-6)
+
+
+def test_zscore_gradient_closed_form_matches_autograd():
+    from dsalt_amd.kernels.landmark_tokens_ker import _norm_grad, _zscore_grad
+    g = torch.Generator().manual_seed(3)
+    for shape, const in (((97, 3), False), ((40, 1), True), ((2, 2), False)):
+        n = (torch.rand(shape, generator=g, dtype=torch.float64) * 3 + 1).requires_grad_(True)
+        if const:  # std 0: clamped, the std term carries no gradient
+            n = torch.full(shape, 2.5, dtype=torch.float64, requires_grad=True)
+        up = torch.randn(shape, generator=g, dtype=torch.float64)
+        z = _zscore(n)
+        (z * up).sum().backward()
+        got = _zscore_grad(up, z.detach(), n.detach())
+        assert torch.allclose(got, n.grad, rtol=1e-10, atol=1e-12)
+    vec = torch.randn(30, 4, 8, generator=g, dtype=torch.float64)
+    vec[3, 1] = 0.0
+    vr = vec.clone().requires_grad_(True)
+    dn = torch.randn(30, 4, generator=g, dtype=torch.float64)
+    (vr.norm(dim=-1) * dn).sum().backward()
+    got = _norm_grad(dn, vec, vec.norm(dim=-1))
+    assert torch.allclose(got, vr.grad, atol=1e-12)

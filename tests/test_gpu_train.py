@@ -170,3 +170,125 @@ def test_autograd_function_gqa_unsorted_slots():
         assert e < 2e-2, (name, e)
     assert lwd.grad.dtype == torch.float32 and wd.grad.dtype == torch.float32
     assert torch.all(lwd.grad.cpu()[pos < 0] == 0)
+
+
+# ------------------------------------------------------------- the layer's training branch
+def _hybrid_ref(x, W, alpha, H, dh):
+    """float64 torch restatement of the hybrid score (dsalt/kernels/landmark_tokens_ker.py:19-61)."""
+    T = x.shape[0]
+    n = x.norm(dim=-1)
+    zx = (n - n.mean()) / n.std().clamp(min=1e-6)
+    G = W.shape[0] // dh
+    nv = (x @ W.T).view(T, G, dh).norm(dim=-1)
+    zv = (nv - nv.mean(0, keepdim=True)) / nv.std(0, keepdim=True).clamp(min=1e-6)
+    zv = zv.repeat_interleave(H // G, dim=1)
+    return alpha * zv + (1.0 - alpha) * zx[:, None]
+
+
+def _dense_bias_ref(w_seq, pos, logw, tau, edge):
+    """Differentiable [H, L, L] training log-bias of one sequence, out of place (the dense form
+    of dsalt/modules/dsalt_attention.py:520-563); checked against the oracle's train_bias."""
+    L = w_seq.shape[0]
+    i = torch.arange(L, dtype=torch.float64)
+    d = i[:, None] - i[None, :]
+    wi = w_seq[:, None]
+    lb = torch.log(torch.sigmoid((wi - d) / tau).clamp(min=1e-20))
+    lb = torch.where(d <= wi - edge, torch.zeros_like(lb), lb)
+    lb = lb.masked_fill(~((d >= 0) & (d <= wi)), float("-inf"))
+    out = []
+    for h in range(pos.shape[0]):
+        b = lb
+        for s in range(pos.shape[1]):
+            p = int(pos[h, s])
+            if p < 0:
+                continue
+            rows = (p <= i) & (p < i - w_seq)
+            hit = rows[:, None] & (torch.arange(L)[None, :] == p)
+            b = torch.maximum(b, torch.where(hit, logw[h, s], torch.full_like(b, float("-inf"))))
+        out.append(b)
+    return torch.stack(out)
+
+
+def test_hybrid_score_gradients_match_torch_float64():
+    from dsalt_amd.kernels import hybrid_scores_per_head
+    g = torch.Generator().manual_seed(50)
+    T, d, H, G, dh = 333, 128, 4, 2, 32
+    x = torch.randn(T, d, generator=g)
+    W = torch.randn(G * dh, d, generator=g) / math.sqrt(d)
+    alpha = torch.sigmoid(torch.randn(H, generator=g))
+    up = torch.randn(T, H, generator=g)
+    xd, Wd, ad = (t.to(DEV).requires_grad_(True) for t in (x, W, alpha))
+    s, _, _ = hybrid_scores_per_head(xd, Wd, ad, H, dh)
+    (s * up.to(DEV)).sum().backward()
+    xr, Wr, ar = (t.double().requires_grad_(True) for t in (x, W, alpha))
+    sr = _hybrid_ref(xr, Wr, ar, H, dh)
+    (sr * up.double()).sum().backward()
+    assert rel_err(f64(s), f64(sr)) < 1e-6
+    for name, a, b in (("x", xd.grad, xr.grad), ("W_V", Wd.grad, Wr.grad), ("alpha", ad.grad, ar.grad)):
+        e = rel_err(f64(a), f64(b))
+        assert e < 1e-5, (name, e)
+
+
+def test_layer_training_branch_against_float64_dense():
+    """DSALTAttention in training mode (fp32): output and the gradients of every parameter
+    (win_gate through the soft window edge, alpha_w through the landmark log-weights) and of
+    x, against the dense float64 composition of the same selectors."""
+    import copy
+
+    from dsalt_amd.kernels import window_utils as WU
+    from dsalt_amd.modules import DSALTAttention
+    torch.manual_seed(51)
+    d, H, G, L, S = 256, 4, 2, 192, 2
+    T, dh = L * S, 64
+    m = DSALTAttention(d, H, 4, 48, 16, 1024, n_kv_heads=G, qkv_bias=True).to(DEV).train()
+    with torch.no_grad():
+        m.win_gate.weight.mul_(8.0)  # spread the windows over [n_min, n_max]
+    mr = copy.deepcopy(m).cpu().double()
+    x = torch.randn(T, d)
+    cot = torch.randn(T, d)
+    cu_list = [0, L, T]
+    cu = torch.tensor(cu_list, dtype=torch.int32)
+    xd = x.to(DEV).requires_grad_(True)
+    out, _ = m(xd, cu.to(DEV), cu_list=cu_list)
+    (out * cot.to(DEV)).sum().backward()
+    with torch.no_grad():
+        w_gpu, pos, _ = m._train_selectors(xd.detach(), cu.to(DEV), T, torch.device(DEV), cu_list)
+    pos = pos.cpu()
+
+    xr = x.double().requires_grad_(True)
+    q = mr.q_proj(xr).view(T, H, dh)
+    k = mr.k_proj(xr).view(T, G, dh)
+    v = mr.v_proj(xr).view(T, G, dh)
+    p_ids = torch.cat([torch.arange(L)] * S)
+    q, k = WU.apply_rotary_emb(q, k, mr.rope_cos[p_ids].unsqueeze(1), mr.rope_sin[p_ids].unsqueeze(1))
+    k, v = k.repeat_interleave(H // G, 1), v.repeat_interleave(H // G, 1)
+    w_ref = mr._window_continuous(xr)
+    w_c = w_ref + (w_gpu.cpu().double() - w_ref).detach()  # the GPU's fp32 windows, gradient of w_ref
+    sc = _hybrid_ref(xr, mr.v_proj.weight, mr._alpha(), H, dh)
+    outs = []
+    for s in range(S):
+        st = s * L
+        ps = pos[:, s]
+        s_sel = sc[st + ps.clamp(min=0), torch.arange(H)[:, None]]
+        lw = torch.log(torch.sigmoid(s_sel / mr.tau_lmk).clamp(min=1e-20))
+        lw = torch.where(ps >= 0, lw, torch.full_like(lw, float("-inf")))
+        bias = _dense_bias_ref(w_c[st:st + L], ps, lw, mr.tau_win, float(mr.win_edge))
+        for h in range(H):
+            ob, _ = OT.train_bias(w_c[st:st + L].detach().numpy(), ps[h].numpy(), lw[h].detach().numpy(),
+                                  mr.tau_win, float(mr.win_edge))
+            fin = np.isfinite(ob)
+            assert np.array_equal(fin, torch.isfinite(bias[h]).numpy())
+            assert np.abs(ob[fin] - bias[h].detach().numpy()[fin]).max() < 1e-12
+        qs, ks, vs = (t[st:st + L].transpose(0, 1) for t in (q, k, v))
+        a = torch.softmax(qs @ ks.transpose(1, 2) / math.sqrt(dh) + bias, -1)
+        outs.append((a @ vs).transpose(0, 1).reshape(L, d))
+    ref = mr.out_proj(torch.cat(outs))
+    (ref * cot.double()).sum().backward()
+    assert rel_err(f64(out), f64(ref)) < 2e-5
+    named = dict(m.named_parameters())
+    for n, pr in mr.named_parameters():
+        e = rel_err(f64(named[n].grad), f64(pr.grad))
+        assert e < 1e-4, (n, e)
+    assert float(named["win_gate.weight"].grad.abs().max()) > 0
+    assert float(named["alpha_w"].grad.abs().max()) > 0
+    assert rel_err(f64(xd.grad), f64(xr.grad)) < 1e-4
