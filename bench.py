@@ -178,22 +178,43 @@ def main():
     maxlen = wl.seqlen
     e = x["q"].element_size()
 
-    def step():
-        idx = ops.select_landmarks(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, max_seqlen=maxlen,
-                                   select_mode=mode, block_size=wl.block_size, stats_scope=scope)
-        out, lse = ops.attention_forward(x["q"], x["k"], x["v"], x["w"], x["cu"], idx, None, max_seqlen=maxlen,
-                                         select_mode=mode, block_size=wl.block_size)
-        if wl.backward:
-            ops.attention_backward(x["dout"], x["q"], x["k"], x["v"], out, lse, x["w"], x["cu"], idx, None,
-                                   max_seqlen=maxlen, want_dbias=False)
-        return idx
+    if wl.train:
+        tau_win, win_edge = wl.tau_win, wl.win_edge
+        starts = x["cu"][:-1].long()
+
+        def step():
+            # the training forward of the layer: hard selection from floor(w~), landmark
+            # log-weights log sigmoid(s / tau_lmk) at the selected positions, then the
+            # training kernels forward and backward
+            idx, _, _, sc = ops.select_landmarks(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk,
+                                                 max_seqlen=maxlen, stats_scope=scope, want_scores=True)
+            pos = idx[:, :, 0].long()
+            s_sel = sc[starts[None, :, None] + pos.clamp(min=0), torch.arange(H, device=dev)[:, None, None]]
+            logw = torch.log(torch.sigmoid(s_sel / wl.tau_lmk).clamp(min=1e-20))
+            logw = torch.where(pos >= 0, logw, torch.full_like(logw, float("-inf"))).unsqueeze(2)
+            out, lse = ops.train_forward(x["q"], x["k"], x["v"], x["w_cont"], x["cu"], idx, logw, tau_win=tau_win,
+                                         win_edge=win_edge, max_seqlen=maxlen)
+            ops.train_backward(x["dout"], x["q"], x["k"], x["v"], out, lse, x["w_cont"], x["cu"], idx, logw,
+                               tau_win=tau_win, win_edge=win_edge, max_seqlen=maxlen)
+            return idx
+    else:
+        def step():
+            idx = ops.select_landmarks(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, max_seqlen=maxlen,
+                                       select_mode=mode, block_size=wl.block_size, stats_scope=scope)
+            out, lse = ops.attention_forward(x["q"], x["k"], x["v"], x["w"], x["cu"], idx, None, max_seqlen=maxlen,
+                                             select_mode=mode, block_size=wl.block_size)
+            if wl.backward:
+                ops.attention_backward(x["dout"], x["q"], x["k"], x["v"], out, lse, x["w"], x["cu"], idx, None,
+                                       max_seqlen=maxlen, want_dbias=False)
+            return idx
 
     for _ in range(args.warmup):
         idx = step()
     torch.cuda.synchronize()
 
     # exact number of attended (query, key) pairs: window + visible landmarks
-    wv = x["w"].long().clamp(min=1)
+    # (training variant: the band of w~ is the integer window floor(w~) + 1)
+    wv = (x["w"].long() + 1) if wl.train else x["w"].long().clamp(min=1)
     pos = torch.arange(T, device=dev) - x["cu"].long().repeat_interleave(maxlen)[:T]
     band = torch.minimum(wv, pos + 1)
     lo = (pos - wv + 1).clamp(min=0)
@@ -265,10 +286,12 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         from oracle.sdpa_cpu import time_baseline
-        r = time_baseline(x_cpu, wl.k_lmk, scope, backward=wl.backward)
+        r = time_baseline(x_cpu, wl.k_lmk, scope, backward=wl.backward,
+                          train=(wl.tau_win, wl.win_edge, wl.tau_lmk) if wl.train else None)
         cpu = {"value": round(r["tokens_per_s"], 2), "unit": "tokens/s", "cores": r["threads"], "kind": "port",
                "sample": (f"full-length landmark selection (C oracle, 1 thread, {r['t_select']:.2f}s) + reference "
-                          f"masked-SDPA {'fwd+bwd' if wl.backward else 'fwd'} on the last {r['rows']} query rows x "
+                          f"{'dense training log-bias + SDPA' if wl.train else 'masked-SDPA'} "
+                          f"{'fwd+bwd' if wl.backward else 'fwd'} on the last {r['rows']} query rows x "
                           f"{H} heads x all {T} keys ({r['t_attention']:.2f}s, torch CPU, {r['threads']} threads, "
                           f"host cpu_count {r['cpu_count']})")}
 
@@ -287,7 +310,9 @@ def main():
         "data": "synthetic",
         "config": {"workload": wl.name, "batch": wl.batch, "heads": H, "seq_len": wl.seqlen, "head_dim": D,
                    "hidden": wl.hidden, "w_max": wl.w_max, "k_lmk": wl.k_lmk, "select": wl.select_mode,
-                   "backward": wl.backward, "pairs": pairs},
+                   "backward": wl.backward, "pairs": pairs,
+                   **({"variant": "train", "tau_win": wl.tau_win, "win_edge": wl.win_edge, "tau_lmk": wl.tau_lmk}
+                      if wl.train else {})},
         "roofline": roof,
         "step_roofline": {"bound": "hbm" if step_bytes / HBM_PEAK_GBS >= step_flops / (MFMA_PEAK_TFLOPS[dtn] * 1e3)
                           else "mfma", "t_roof_ms": round(t_roof * 1e3, 4),

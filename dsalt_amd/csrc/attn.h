@@ -65,13 +65,38 @@ __device__ __forceinline__ float edge_bias(const AttnParams& p, float wt, int d)
     const float fd = wt - (float)d;
     return fd >= p.edge ? 0.f : -__logf(1.f + __expf(-fd * p.tau_inv)) * p.inv_scale;
 }
-// d bias / d wt of the same key: (1 - sigmoid((wt - d) / tau)) / tau outside the core
-// (keys outside the band get a finite value; callers mask them)
-__device__ __forceinline__ float edge_grad(const AttnParams& p, float wt, int d) {
+// bias and d bias / d wt of the same key, sharing one exponential: d bias / d wt is
+// (1 - sigmoid((wt - d) / tau)) / tau outside the core, 0 inside (keys outside the band
+// get finite values; callers mask them)
+__device__ __forceinline__ void edge_terms(const AttnParams& p, float wt, int d, float& bias, float& grad) {
     const float fd = fmaxf(wt - (float)d, 0.f);
-    if (fd >= p.edge) return 0.f;
     const float e = __expf(-fd * p.tau_inv);
-    return e / (1.f + e) * p.tau_inv;
+    const bool inside = fd >= p.edge;
+    bias = inside ? 0.f : -__logf(1.f + e) * p.inv_scale;
+    grad = inside ? 0.f : e * __builtin_amdgcn_rcpf(1.f + e) * p.tau_inv;
+}
+
+// The soft edge of a row with continuous window wt covers at most ceil(win_edge) band
+// keys from the unclamped window start lo_u = i - floor(wt): key lo_u + k sits at
+// wt - d = frac(wt) + k.  For win_edge <= 4 the kernels read a row's edge terms from
+// a four-entry table built once per row (no transcendentals per key).
+constexpr int kEdgeTab = 4;
+__device__ __forceinline__ void edge_table(const AttnParams& p, float wt, float* b, float* g) {
+    const float fr = wt - floorf(wt);
+#pragma unroll
+    for (int k = 0; k < kEdgeTab; ++k) {
+        float bb, gg;
+        edge_terms(p, fr + (float)k, 0, bb, gg);
+        b[k] = bb;
+        if (g) g[k] = gg;
+    }
+}
+// table entry for key offset k from lo_u (0 from kEdgeTab on: the core)
+__device__ __forceinline__ float edge_lookup(const float* t, int k) {
+    float v = 0.f;
+#pragma unroll
+    for (int e = 0; e < kEdgeTab; ++e) v = k == e ? t[e] : v;
+    return v;
 }
 
 size_t plan_bytes(const AttnParams& p);

@@ -48,13 +48,15 @@ __device__ __forceinline__ int lower_bound_i(const int* a, int n, int x) {
 }
 
 // loads a landmark set into LDS; returns the number of valid (non -1) slots
-__device__ __forceinline__ int load_set(const AttnParams& p, int64_t set_off, int* lpos, int* nvalid_s, int tid) {
+__device__ __forceinline__ int load_set(const AttnParams& p, int64_t set_off, int* lpos, int* nvalid_s, int tid,
+                                        float* lbs = nullptr) {
     if (tid == 0) *nvalid_s = 0;
     __syncthreads();
     for (int i = tid; i < p.k_lmk; i += 256) {
         int v = p.lmk[set_off + i];
         lpos[i] = v;
         if (v >= 0 && (i + 1 == p.k_lmk || p.lmk[set_off + i + 1] < 0)) *nvalid_s = i + 1;
+        if (lbs) lbs[i] = p.lbias[set_off + i] * p.inv_scale;  // landmark bias in raw-score units
     }
     __syncthreads();
     return *nvalid_s;
@@ -77,8 +79,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) T Ks[2][KT::ELEMS];
     __shared__ __attribute__((aligned(16))) T Vs[2][KT::ELEMS];
     __shared__ int lpos[kMaxLandmarks];
-    __shared__ int red[4];
-    __shared__ int nvalid_s;
+    __shared__ __attribute__((aligned(16))) float lbs[kMaxLandmarks];
+    // block scalars live in the second K buffer until the first chunk is staged there
+    // (keeps the block at 40 KB of LDS: four blocks per CU)
+    int* red = (int*)Ks[1];
+    int& nvalid_s = red[4];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
@@ -96,7 +101,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
     const float c2 = p.c2;
     const float inv_scale = p.inv_scale;
     const bool has_bias = p.lbias != nullptr;
-    const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid);
+    const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid, has_bias ? lbs : nullptr);
 
     // this wave's rows (ordered by window start) and their bounds, from the row plan
     const int uw = uniform(wave);
@@ -107,15 +112,19 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
     const int bhi = max(max(bnd[2], bnd[6]), max(bnd[10], bnd[14]));
     const int i = r0 + p.plan_perm[tile * 64 + uw * 16 + (lane & 15)];
     const bool valid = i < len;
-    int lo = 0x7fffffff, hi = -1, cnt = 0;
+    int lo = 0x7fffffff, hi = -1, cnt = 0, lou = 0x7fffffff;
     float wt = 0.f;
     if (valid) {
         const int wi = max(p.w[st + i], 1);
         lo = max(i - wi + 1, 0);
+        lou = i - (wi - 1);
         hi = i;
         cnt = lower_bound_i(lpos, nvalid, lo);
         if (TR) wt = p.w_cont[st + i];
     }
+    // soft-edge bias and window gradient of keys lou .. lou+3 (training variant)
+    float etb[TR ? kEdgeTab : 1], etg[TR ? kEdgeTab : 1];
+    if (TR) edge_table(p, wt, etb, etg);
     const int lo_edge = TR ? wLmax + p.edge_keys : wLmax;  // keys from here on carry no edge bias
     float dwacc = 0.f;
     if (valid && g == 0 && p.cnt) p.cnt[(int64_t)(st + i) * p.n_heads + h] = cnt;
@@ -212,29 +221,36 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
                 const int tl = lo - a - lane_off, th = hi - a - lane_off;
                 if (a >= lo_edge && a + 15 <= wHmin) {
                     ci = floatx4{0.f, 0.f, 0.f, 0.f};
-                } else if (a + 15 <= wHmin) {  // below every row's diagonal: window start only
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        ci[r] = r < tl ? NEG : (TR ? edge_bias(p, wt, th - r) : 0.f);
-                        if (TR) eg[r] = r < tl ? 0.f : edge_grad(p, wt, th - r);
-                    }
                 } else {
+                    // below every row's diagonal only the window start masks; the soft
+                    // edge only reaches subtiles before lo_edge (wave-uniform tests)
+                    const bool upper = a + 15 > wHmin;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const bool out = r < tl || r > th;
-                        ci[r] = out ? NEG : (TR ? edge_bias(p, wt, th - r) : 0.f);
-                        if (TR) eg[r] = out ? 0.f : edge_grad(p, wt, th - r);
+                    for (int r = 0; r < 4; ++r) ci[r] = (r < tl || (upper && r > th)) ? NEG : 0.f;
+                    if (TR && a < lo_edge) {
+                        if (p.edge_keys <= kEdgeTab) {
+                            const int k0 = a + lane_off - lou;
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const bool out = r < tl || r > th;
+                                ci[r] = out ? NEG : edge_lookup(etb, k0 + r);
+                                eg[r] = out ? 0.f : edge_lookup(etg, k0 + r);
+                            }
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                float b, gr;
+                                edge_terms(p, wt, th - r, b, gr);
+                                const bool out = r < tl || r > th;
+                                ci[r] = out ? NEG : b;
+                                eg[r] = out ? 0.f : gr;
+                            }
+                        }
                     }
                 }
             } else {
-                floatx4 bv = floatx4{0.f, 0.f, 0.f, 0.f};
-                if (has_bias) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int sl = a + lane_off + r;
-                        bv[r] = sl < K ? p.lbias[set_off + sl] * inv_scale : 0.f;
-                    }
-                }
+                // slots past the set's valid count are masked below (a + 15 < 512)
+                const floatx4 bv = has_bias ? *(const floatx4*)(lbs + a + lane_off) : floatx4{0.f, 0.f, 0.f, 0.f};
                 if (a + 15 < wcmin) {
                     ci = bv;
                 } else {
@@ -456,7 +472,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_
                 if (kind != 1) {
                     const int4 lo4 = *(const int4*)(q.key + qs * 16 + lane_off);
                     floatx4 eb = floatx4{0.f, 0.f, 0.f, 0.f};
-                    if (TR) {
+                    // the soft edge reaches this key only for rows with jj < lo + edge_keys:
+                    // skipped unless some lane of the wave has such a row
+                    if (TR && __builtin_amdgcn_ballot_w64(jj < lo4.x + p.edge_keys || jj < lo4.y + p.edge_keys ||
+                                                          jj < lo4.z + p.edge_keys || jj < lo4.w + p.edge_keys)) {
                         const floatx4 w4 = *(const floatx4*)(q.wt + qs * 16 + lane_off);
                         const int4 i4 = *(const int4*)(q.ri + qs * 16 + lane_off);
                         eb[0] = edge_bias(p, w4[0], i4.x - jj);

@@ -131,6 +131,8 @@ struct RowGroup {
     int i, lo, hi, cnt;
     bool valid;
     float wt;  // continuous window of the row (training variant)
+    int lou;   // unclamped window start i - floor(wt) (training variant)
+    float eb[kEdgeTab];  // soft-edge bias of keys lou .. lou+3 (training variant, win_edge <= 4)
     int wlo, wLmax, whi, wHmin, wcmax, wcmin;
 };
 
@@ -151,6 +153,7 @@ __device__ __forceinline__ void plan_group(const AttnParams& p, int64_t tile0, i
     rg.cnt = 0;
     rg.valid = false;
     rg.wt = 0.f;
+    rg.lou = 0x7fffffff;
     rg.wlo = 0x7fffffff;
     rg.wLmax = (int)0x80000000;
     rg.whi = -1;
@@ -169,10 +172,27 @@ __device__ __forceinline__ void plan_group(const AttnParams& p, int64_t tile0, i
             rg.hi = rg.i;
             rg.cnt = lower_bound_lds(lpos, nvalid, rg.lo);
             if (p.w_cont) rg.wt = p.w_cont[st + rg.i];
+            rg.lou = rg.i - (wi - 1);
         }
     }
+    if (p.w_cont) edge_table(p, rg.wt, rg.eb, nullptr);
     rg.wcmax = uniform(row_max16(rg.cnt));
     rg.wcmin = uniform(row_min16(rg.valid ? rg.cnt : 0));
+}
+
+// Soft-edge bias of the lane's four keys a + lane_off + r of a band subtile (training
+// variant), masked keys (r < tl, and r past the diagonal when `upper`) left at -inf.
+__device__ __forceinline__ void band_edge(const AttnParams& p, const RowGroup& R, int a, int lane_off, int tl,
+                                          bool upper, floatx4& ci) {
+    const int th = R.hi - a - lane_off;
+    if (p.edge_keys <= kEdgeTab) {
+        const int k0 = a + lane_off - R.lou;  // key offset from the unclamped window start, r = 0
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ci[r] = (r < tl || (upper && r > th)) ? -INFINITY : edge_lookup(R.eb, k0 + r);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ci[r] = (r < tl || (upper && r > th)) ? -INFINITY : edge_bias(p, R.wt, th - r);
+    }
 }
 
 // One 256-thread block (4 waves) owns 64*RG query rows of one (head, sequence),
@@ -192,8 +212,11 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) T Ks[2][KT::ELEMS];
     __shared__ __attribute__((aligned(16))) T Vs[2][KT::ELEMS];
     __shared__ int lpos[kMaxLandmarks];
-    __shared__ int red[4];
-    __shared__ int nvalid_s;
+    __shared__ __attribute__((aligned(16))) float lbs[kMaxLandmarks];
+    // block scalars live in the second K buffer until the first chunk is staged there
+    // (keeps the block at 40 KB of LDS: four blocks per CU)
+    int* red = (int*)Ks[1];
+    int& nvalid_s = red[4];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
     const int nblk = ceil_div(p.n_tiles, RG);
@@ -220,6 +243,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
         int v = p.lmk[set_off + i];
         lpos[i] = v;
         if (v >= 0 && (i + 1 == K || p.lmk[set_off + i + 1] < 0)) nvalid_s = i + 1;
+        if (has_bias) lbs[i] = p.lbias[set_off + i] * inv_scale;  // raw-score units
     }
     __syncthreads();
     const int nvalid = nvalid_s;
@@ -333,30 +357,37 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
                 else kind = 3;
             } else {
                 if (base >= R.wcmax) kind = 0;
-                else if (!has_bias && base + BN - 1 < R.wcmin) kind = 4;
+                else if (base + BN - 1 < R.wcmin) kind = 4;
                 else kind = 5;
             }
             gact[u] = kind != 0;
 #pragma unroll
             for (int stt = 0; stt < NST; ++stt) act[u][stt] = kind != 0;
             const floatx4 zero = floatx4{0.f, 0.f, 0.f, 0.f};
-            if (kind == 1 || kind == 4) {
+            if (kind == 1 || (kind == 4 && !has_bias)) {
 #pragma unroll
                 for (int stt = 0; stt < NST; ++stt) {
                     KOp<T, D> ko;
                     ko.load(kl, KT::RS, stt * 16, lane);
                     S[u][stt] = ko.dot(qr[u], zero);
                 }
+            } else if (kind == 4) {  // every slot visible to every row, landmark bias only
+#pragma unroll
+                for (int stt = 0; stt < NST; ++stt) {
+                    KOp<T, D> ko;
+                    ko.load(kl, KT::RS, stt * 16, lane);
+                    S[u][stt] = ko.dot(qr[u], *(const floatx4*)(lbs + base + stt * 16 + lane_off));
+                }
             } else if (kind == 2) {
 #pragma unroll
                 for (int stt = 0; stt < NST; ++stt) {
-                    const int tl = R.lo - (base + stt * 16) - lane_off;
+                    const int a = base + stt * 16;
+                    const int tl = R.lo - a - lane_off;
                     floatx4 ci;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float eb = TR ? edge_bias(p, R.wt, tl - r + R.i - R.lo) : 0.f;
-                        ci[r] = r < tl ? NEG : eb;
-                    }
+                    for (int r = 0; r < 4; ++r) ci[r] = r < tl ? NEG : 0.f;
+                    if (TR && a < R.wLmax + p.edge_keys)  // the soft edge reaches this subtile
+                        band_edge(p, R, a, lane_off, tl, false, ci);
                     KOp<T, D> ko;
                     ko.load(kl, KT::RS, stt * 16, lane);
                     S[u][stt] = ko.dot(qr[u], ci);
@@ -364,13 +395,12 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
             } else if (kind == 3) {
 #pragma unroll
                 for (int stt = 0; stt < NST; ++stt) {
-                    const int tl = R.lo - (base + stt * 16) - lane_off, th = R.hi - (base + stt * 16) - lane_off;
+                    const int a = base + stt * 16;
+                    const int tl = R.lo - a - lane_off, th = R.hi - a - lane_off;
                     floatx4 ci;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float eb = TR ? edge_bias(p, R.wt, th - r) : 0.f;
-                        ci[r] = (r < tl || r > th) ? NEG : eb;
-                    }
+                    for (int r = 0; r < 4; ++r) ci[r] = (r < tl || r > th) ? NEG : 0.f;
+                    if (TR && a < R.wLmax + p.edge_keys) band_edge(p, R, a, lane_off, tl, true, ci);
                     KOp<T, D> ko;
                     ko.load(kl, KT::RS, stt * 16, lane);
                     S[u][stt] = ko.dot(qr[u], ci);
@@ -388,19 +418,11 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
                     if (band) {
                         const int tl = R.lo - a - lane_off, th = R.hi - a - lane_off;
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const float eb = TR ? edge_bias(p, R.wt, th - r) : 0.f;
-                            ci[r] = (r < tl || r > th) ? NEG : eb;
-                        }
+                        for (int r = 0; r < 4; ++r) ci[r] = (r < tl || r > th) ? NEG : 0.f;
+                        if (TR && a < R.wLmax + p.edge_keys) band_edge(p, R, a, lane_off, tl, true, ci);
                     } else {
-                        floatx4 bv = zero;
-                        if (has_bias) {
-                            float braw[4];
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) braw[r] = p.lbias[set_off + min(a + lane_off + r, K - 1)];
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) bv[r] = a + lane_off + r < K ? braw[r] * inv_scale : 0.f;
-                        }
+                        // slots past the valid count are masked below (a + 15 < 512)
+                        const floatx4 bv = has_bias ? *(const floatx4*)(lbs + a + lane_off) : zero;
                         const int tc = R.cnt - a - lane_off;
 #pragma unroll
                         for (int r = 0; r < 4; ++r) ci[r] = r < tc ? bv[r] : NEG;

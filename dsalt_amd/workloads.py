@@ -5,6 +5,8 @@ float32 and then cast, so the bits handed to the GPU and to any CPU check are id
 Draw order: q, k, v, h, window normals, upstream gradient.
 Windows: ``w_i = clamp(round_half_even(sigmoid(z_i) * w_max), 16, w_max)``.
 Landmark score: alpha = 0.5 for every head (the same ranking as z(|v|) + z(|h|)).
+Training workloads draw the same tensors and keep the windows continuous,
+``w~_i = clamp(sigmoid(z_i) * w_max, 16, w_max)``; their hard selection uses ``floor(w~)``.
 """
 from __future__ import annotations
 
@@ -29,6 +31,10 @@ class Workload:
     block_size: int = 512
     heavy_tails: bool = False    # v rows x lognormal(0,1), h rows x lognormal(0,0.5)
     seed: int = 1000
+    train: bool = False          # training variant: soft window edge, landmark log-weights
+    tau_win: float = 1.0
+    win_edge: float = 4.0
+    tau_lmk: float = 2.0
 
     @property
     def total_len(self) -> int:
@@ -45,6 +51,9 @@ WORKLOADS = {
         # forward + backward, bf16, one 32K sequence, heavy-tailed norms
         Workload("fwdbwd_bf16_h16_l32768", 1, 16, 32768, 64, 1024, torch.bfloat16, 512, 128, True,
                  heavy_tails=True, seed=1002),
+        # the same tensors through the training variant (differentiable selectors)
+        Workload("train_bf16_h16_l32768", 1, 16, 32768, 64, 1024, torch.bfloat16, 512, 128, True,
+                 heavy_tails=True, seed=1002, train=True),
         # forward (inference), bf16, 128K tokens, block-causal landmarks (512-query blocks)
         Workload("fwd_bf16_h16_l131072_block", 1, 16, 131072, 128, 2048, torch.bfloat16, 512, 256, False,
                  select_mode="block", block_size=512, seed=1003),
@@ -62,7 +71,7 @@ def generate(wl: Workload, device="cpu", seqlen: int | None = None, heads: int |
 
     ``seqlen`` / ``heads`` shrink the shape for tests while keeping the recipe.
     Keys: q, k, v [T,H,D]; h [T,hidden]; w [T] int32; cu [S+1] int32; alpha [H] fp32;
-    dout [T,H,D] (backward workloads).
+    dout [T,H,D] (backward workloads); w_cont [T] fp32 (training workloads, with w = floor).
     """
     L = seqlen or wl.seqlen
     H = heads or wl.heads
@@ -82,6 +91,9 @@ def generate(wl: Workload, device="cpu", seqlen: int | None = None, heads: int |
         cu=torch.arange(0, T + 1, L, dtype=torch.int32),
         alpha=torch.full((H,), 0.5, dtype=torch.float32),
     )
+    if wl.train:
+        out["w_cont"] = (torch.sigmoid(zw) * wl.w_max).clamp(16, wl.w_max).to(torch.float32)
+        out["w"] = out["w_cont"].floor().to(torch.int32)
     if wl.backward:
         out["dout"] = torch.randn(T, H, wl.head_dim, generator=g).to(wl.dtype)
     return {kk: vv.to(device) for kk, vv in out.items()}

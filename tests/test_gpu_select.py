@@ -108,7 +108,8 @@ def test_constant_scores_pick_lowest_indices():
     np.testing.assert_array_equal(idx.cpu().numpy()[0, 0, 0], np.arange(5, 25))
 
 
-@pytest.mark.parametrize("name", ["fwd_f32_h4_l2048", "fwdbwd_bf16_b4_h8_l8192", "fwdbwd_bf16_h16_l32768"])
+@pytest.mark.parametrize("name", ["fwd_f32_h4_l2048", "fwdbwd_bf16_b4_h8_l8192", "fwdbwd_bf16_h16_l32768",
+                                  "train_bf16_h16_l32768"])
 def test_workload_selection_bit_exact(name):
     wl = WORKLOADS[name]
     x = generate(wl)

@@ -292,3 +292,60 @@ def test_layer_training_branch_against_float64_dense():
     assert float(named["win_gate.weight"].grad.abs().max()) > 0
     assert float(named["alpha_w"].grad.abs().max()) > 0
     assert rel_err(f64(xd.grad), f64(xr.grad)) < 1e-4
+
+
+# ------------------------------------------------------------- the benchmark's training workload
+def _workload_logw(x, idx, sc, tau_lmk):
+    pos = idx[:, :, 0].long()
+    H = pos.shape[0]
+    starts = x["cu"][:-1].long()
+    s_sel = sc[starts[None, :, None] + pos.clamp(min=0), torch.arange(H, device=sc.device)[:, None, None]]
+    logw = torch.log(torch.sigmoid(s_sel / tau_lmk).clamp(min=1e-20))
+    return torch.where(pos >= 0, logw, torch.full_like(logw, float("-inf")))
+
+
+def test_train_workload_shortened_against_oracle():
+    from dsalt_amd.workloads import WORKLOADS, generate
+    wl = WORKLOADS["train_bf16_h16_l32768"]
+    x = {k: v.to(DEV) for k, v in generate(wl, seqlen=2048, heads=2).items()}
+    maxlen = 2048
+    idx, _, _, sc = ops.select_landmarks(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, max_seqlen=maxlen,
+                                         stats_scope=ops.STATS_SEQUENCE, want_scores=True)
+    logw = _workload_logw(x, idx, sc, wl.tau_lmk)
+    out, lse = ops.train_forward(x["q"], x["k"], x["v"], x["w_cont"], x["cu"], idx, logw.unsqueeze(2),
+                                 tau_win=wl.tau_win, win_edge=wl.win_edge, max_seqlen=maxlen)
+    dq, dk, dv, dlw, dw = ops.train_backward(x["dout"], x["q"], x["k"], x["v"], out, lse, x["w_cont"], x["cu"], idx,
+                                             logw.unsqueeze(2), tau_win=wl.tau_win, win_edge=wl.win_edge,
+                                             max_seqlen=maxlen)
+    torch.cuda.synchronize()
+    c = {k: v.cpu() for k, v in x.items()}
+    pos = idx[:, :, 0].cpu()
+    (ro, _), (rdq, rdk, rdv, rdw, rdlw) = _oracle(c["q"], c["k"], c["v"], c["w_cont"], c["cu"], pos, logw.cpu(),
+                                                  c["dout"], 1.0 / 8.0, wl.tau_win, wl.win_edge)
+    for name, a, b in (("out", out, ro), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv), ("d_w", dw, rdw),
+                       ("d_logw", dlw[:, :, 0], rdlw)):
+        e = rel_err(f64(a), b)
+        assert e < 2e-2, (name, e)
+
+
+def test_train_workload_full_size_without_edge_is_the_operator():
+    """At the benchmark's full shape (T=32768, H=16): with win_edge 0 the training kernels
+    give the operator's output and gradients (window floor(w~)+1, log-weights as bias)."""
+    from dsalt_amd.workloads import WORKLOADS, generate
+    wl = WORKLOADS["train_bf16_h16_l32768"]
+    x = {k: v.to(DEV) for k, v in generate(wl).items()}
+    maxlen = wl.seqlen
+    idx, _, _, sc = ops.select_landmarks(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, max_seqlen=maxlen,
+                                         stats_scope=ops.STATS_SEQUENCE, want_scores=True)
+    lw = _workload_logw(x, idx, sc, wl.tau_lmk).unsqueeze(2)
+    out, lse = ops.train_forward(x["q"], x["k"], x["v"], x["w_cont"], x["cu"], idx, lw, tau_win=1.0, win_edge=0.0,
+                                 max_seqlen=maxlen)
+    wi = x["w"] + 1
+    out2, lse2 = ops.attention_forward(x["q"], x["k"], x["v"], wi, x["cu"], idx, lw, max_seqlen=maxlen)
+    assert rel_err(f64(out), f64(out2)) < 1e-6
+    g1 = ops.train_backward(x["dout"], x["q"], x["k"], x["v"], out, lse, x["w_cont"], x["cu"], idx, lw, tau_win=1.0,
+                            win_edge=0.0, max_seqlen=maxlen)
+    g2 = ops.attention_backward(x["dout"], x["q"], x["k"], x["v"], out2, lse2, wi, x["cu"], idx, lw,
+                                max_seqlen=maxlen)
+    for a, b in zip(g1[:4], g2):
+        assert rel_err(f64(a), f64(b)) < 1e-6

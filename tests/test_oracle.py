@@ -389,3 +389,33 @@ def test_train_bwd_matches_finite_differences_in_selectors():
         lm[ix] -= eps
         fd = (loss(w_cont, lp) - loss(w_cont, lm)) / (2 * eps)
         assert abs(fd - dlogw[ix]) < 1e-6 + 1e-5 * abs(fd), ix
+
+
+def test_cpu_baseline_training_bias_rows_match_oracle():
+    from oracle.sdpa_cpu import train_bias_rows
+    rng = np.random.default_rng(61)
+    lens, H, K = (50, 41), 3, 5
+    T = sum(lens)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
+    w = torch.tensor(rng.uniform(0.0, 20.0, T))
+    w[::5] = w[::5].floor()
+    pos = torch.full((H, 2, K), -1, dtype=torch.int64)
+    for h in range(H):
+        for s, L in enumerate(lens):
+            pos[h, s, :K - 1] = torch.tensor(rng.choice(L, K - 1, replace=False))
+    logw = torch.where(pos >= 0, torch.tensor(np.log(rng.uniform(0.05, 1, pos.shape))),
+                       torch.tensor(float("-inf"), dtype=torch.float64))
+    rows = torch.arange(30, T)
+    b = train_bias_rows(w, cu, pos, logw, rows, 1.3, 4.0).numpy()
+    for h in range(H):
+        for s, L in enumerate(lens):
+            st = int(cu[s])
+            ref, _ = OT.train_bias(w[st:st + L].numpy(), pos[h, s].numpy(), logw[h, s].numpy(), 1.3, 4.0)
+            full = np.full((L, T), -np.inf)
+            full[:, st:st + L] = ref
+            sel = (rows >= st) & (rows < st + L)
+            got = b[h][sel.numpy()]
+            want = full[(rows[sel] - st).numpy()]
+            np.testing.assert_array_equal(np.isinf(got), np.isinf(want))
+            fin = np.isfinite(want)
+            assert np.abs(got[fin] - want[fin]).max() < 1e-12
