@@ -50,14 +50,14 @@ def parse():
 
 
 LABELS = ("sel_norms", "sel_sums", "sel_stats", "sel_z", "sel_scores", "sel_part", "sel_merge", "sel_topk", "gather",
-          "row_plan", "attn_fwd", "bwd_init", "bwd_dq", "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum")
+          "row_plan", "attn_fwd", "bwd_init", "bwd_dq", "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum", "train_windows", "train_dw")
 
 
 def short_kernel_name(name: str) -> str:
     """Label of a library kernel (the one dsalt_timing_report uses) from a profiler kernel name."""
     import re
     m = re.search(r"(sel_norms|sel_sums|sel_stats|sel_z|sel_scores|sel_part|sel_merge|sel_topk|gather|row_plan|fwd|bwd_init|bwd_dq|"
-                  r"bwd_dkdv|bwd_lmk_sum|"
+                  r"bwd_dkdv|bwd_lmk_sum|train_windows|train_dw|"
                   r"bwd_lmk)_kernel", name)
     if not m:
         return name
@@ -117,10 +117,11 @@ def kernel_model(wl, T, H, D, hidden, pairs, e):
     """Algorithmic bytes and flops per launch of each kernel (no recompute, no workspace)."""
     thd = T * H * D * e
     th4 = 4 * T * H
+    tr = th4 if wl.train else 0  # training variant: per-head window gradients written by bwd_dq
     return {
         "sel_norms": dict(bytes=T * hidden * e + thd, flops=0),
         "attn_fwd": dict(bytes=4 * thd + th4, flops=4 * D * pairs),
-        "bwd_dq": dict(bytes=6 * thd + 2 * th4, flops=4 * D * pairs),
+        "bwd_dq": dict(bytes=6 * thd + 2 * th4 + tr, flops=4 * D * pairs),
         "bwd_dkdv": dict(bytes=6 * thd + 2 * th4, flops=4 * D * pairs),
     }
 
