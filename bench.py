@@ -126,6 +126,102 @@ def kernel_model(wl, T, H, D, hidden, pairs, e):
     }
 
 
+def model_bench(args, wl):
+    """Whole-model prefill: a step is one forward of the decoder over B x L random token ids
+    (embedding, every layer, final norm and the LM head over all positions, as the
+    reference's forward without labels), weights random-init in bf16, no autograd."""
+    import ctypes
+
+    import torch
+
+    from dsalt_amd import _lib
+    from dsalt_amd.model import DSALTLMHeadModel
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    cfg = wl.config()
+    torch.manual_seed(wl.seed)
+    with torch.device(dev):  # parameters initialised on the GPU; the RoPE tables follow with .to
+        model = DSALTLMHeadModel.from_config(cfg).to(dev, wl.dtype).eval()
+    T = wl.batch * wl.seqlen
+    g = torch.Generator(device="cpu").manual_seed(wl.seed)
+    ids = torch.randint(0, cfg.vocab_size, (T,), generator=g).to(dev)
+    cu = torch.arange(0, T + 1, wl.seqlen, dtype=torch.int32, device=dev)
+
+    def step():
+        with torch.no_grad():
+            return model(ids, cu_seqlens=cu, max_seqlen=wl.seqlen)["logits"]
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = 1e3 * elapsed / args.steps
+
+    # second timed pass: library kernels by HIP events, and the gate/up GEMM of every FFN by
+    # torch events on the stream it runs on
+    ffns = [layer.ffn for layer in model.layers]
+    for f in ffns:
+        f.gemm_events = []
+    lib.dsalt_timing_enable(1)
+    torch.cuda.synchronize()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    buf = ctypes.create_string_buffer(1 << 16)
+    lib.dsalt_timing_report(buf, len(buf))
+    lib.dsalt_timing_enable(0)
+    kernels = {}
+    for line in buf.value.decode().splitlines():
+        name, n, tot = line.split()
+        kernels[name] = dict(launches=int(n), avg_ms=float(tot) / int(n), ms_per_step=float(tot) / args.steps)
+    gemm_ms = [a.elapsed_time(b) for f in ffns for a, b in f.gemm_events]
+    for f in ffns:
+        f.gemm_events = None
+    d, dff, V = cfg.d_model, cfg.d_ff, cfg.vocab_size
+    gu_flops = 2.0 * T * d * 2 * dff
+    gemm_avg = sum(gemm_ms) / len(gemm_ms)
+    kernels["ffn_gate_up_gemm"] = dict(launches=len(gemm_ms), avg_ms=gemm_avg, ms_per_step=sum(gemm_ms) / args.steps)
+    ach = gu_flops / (gemm_avg * 1e-3) / 1e12
+    roof = {"bound": "mfma", "kernel": "ffn_gate_up_gemm (hipBLASLt via torch)", "achieved": round(ach, 1),
+            "peak": MFMA_PEAK_TFLOPS["bf16"], "unit": "TFLOP/s", "frac": round(ach / MFMA_PEAK_TFLOPS["bf16"], 4),
+            "traffic": None, "algorithmic_flops": gu_flops}
+    kvd = cfg.n_kv_heads * (d // cfg.n_heads)
+    linear_params = cfg.n_layers * (2 * d * d + 2 * d * kvd + 3 * d * dff + d * kvd) + d * V
+    step_flops = 2.0 * T * linear_params
+    t_roof = step_flops / (MFMA_PEAK_TFLOPS["bf16"] * 1e12)
+    line = {
+        "metric": "DSALT decoder prefill tokens/sec @L=32K bf16 (1 GPU)",
+        "value": round(T * args.steps / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random token ids, random-init weights)",
+        "config": {"workload": wl.name, "batch": wl.batch, "seq_len": wl.seqlen, "layers": cfg.n_layers,
+                   "hidden": d, "heads": cfg.n_heads, "kv_heads": cfg.n_kv_heads, "d_ff": dff, "vocab": V,
+                   "w_max": cfg.n_max, "k_lmk": cfg.k_lmk, "select": cfg.select_mode, "block_size": cfg.block_size,
+                   "lm_head": "all positions"},
+        "roofline": roof,
+        "step_roofline": {"bound": "mfma", "t_roof_ms": round(t_roof * 1e3, 3), "frac": round(t_roof * 1e3 / ms_step, 4),
+                          "flops": step_flops, "note": "linear layers (incl. LM head over all positions) only"},
+        "cpu_baseline": None,
+        "kernels": {k: {kk: round(vv, 5) if isinstance(vv, float) else vv for kk, vv in v.items()}
+                    for k, v in sorted(kernels.items())},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.traffic_from:
@@ -155,8 +251,10 @@ def main():
     import torch
 
     from dsalt_amd import _lib, ops
-    from dsalt_amd.workloads import WORKLOADS, generate
+    from dsalt_amd.workloads import MODEL_WORKLOADS, WORKLOADS, generate
 
+    if args.workload in MODEL_WORKLOADS:
+        return model_bench(args, MODEL_WORKLOADS[args.workload])
     wl = WORKLOADS[args.workload]
     lib = _lib.load()
     dev = torch.device("cuda", 0)

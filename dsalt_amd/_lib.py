@@ -75,6 +75,14 @@ class TrainBwdArgs(ctypes.Structure):
     _fields_ = [("base", BwdArgs), ("w_cont", _vp), ("tau_win", _f32), ("win_edge", _f32), ("d_w", _vp)]
 
 
+class RopeArgs(ctypes.Structure):
+    _fields_ = [("total_len", _i32), ("num_seqs", _i32), ("max_seqlen", _i32), ("n_q_heads", _i32),
+                ("n_k_heads", _i32), ("head_dim", _i32), ("dtype", _i32),
+                ("q", _vp), ("q_stride_t", _i64), ("q_stride_h", _i64),
+                ("k", _vp), ("k_stride_t", _i64), ("k_stride_h", _i64),
+                ("cu_seqlens", _vp), ("cos", _vp), ("sin", _vp), ("max_pos", _i32)]
+
+
 class GatherArgs(ctypes.Structure):
     _fields_ = [("p", Problem),
                 ("k", _vp), ("k_stride_t", _i64), ("k_stride_h", _i64),
@@ -99,6 +107,7 @@ SIGNATURES = {
     "dsalt_train_fwd": ([ctypes.POINTER(TrainFwdArgs), _vp], ctypes.c_int),
     "dsalt_train_bwd_workspace_bytes": ([ctypes.POINTER(TrainBwdArgs)], _sz),
     "dsalt_train_bwd": ([ctypes.POINTER(TrainBwdArgs), _vp], ctypes.c_int),
+    "dsalt_rope_qk": ([ctypes.POINTER(RopeArgs), _vp], ctypes.c_int),
     "dsalt_timing_enable": ([ctypes.c_int], ctypes.c_int),
     "dsalt_timing_report": ([ctypes.c_char_p, _sz], ctypes.c_int),
 }

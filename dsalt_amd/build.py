@@ -23,6 +23,8 @@ SOURCES = {
     "select.hip": ["-ffp-contract=off"],
     "attn_fwd.hip": [],
     "attn_bwd.hip": [],
+    # the rotation rounds every product and sum to the tensor type: no fused multiply-adds
+    "rope.hip": ["-ffp-contract=off"],
     "capi.hip": [],
     "timing.hip": [],
 }

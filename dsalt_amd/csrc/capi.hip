@@ -6,6 +6,7 @@
 #include <string>
 
 #include "attn.h"
+#include "rope.h"
 #include "select.h"
 #include "common.h"
 
@@ -361,6 +362,41 @@ int dsalt_train_bwd(const dsalt_train_bwd_args* a, dsalt_stream_t stream) {
     if (e == hipSuccess) e = dsalt::bwd_launch(p, w + train_bwd_extra(p), (hipStream_t)stream);
     if (e == hipSuccess) e = dsalt::train_dw_launch(p, (hipStream_t)stream);
     return hip_status(e, "dsalt_train_bwd");
+}
+
+int dsalt_rope_qk(const dsalt_rope_args* a, dsalt_stream_t stream) {
+    if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
+    if (a->total_len < 0 || a->num_seqs < 1 || a->n_q_heads < 0 || a->n_k_heads < 0)
+        return fail(DSALT_ERR_INVALID, "bad shape (T=%d, S=%d, heads %d/%d)", a->total_len, a->num_seqs,
+                    a->n_q_heads, a->n_k_heads);
+    if (a->head_dim < 16 || a->head_dim > 256 || a->head_dim % 16)
+        return fail(DSALT_ERR_INVALID, "head_dim must be a multiple of 16 in [16, 256], got %d", a->head_dim);
+    if (a->dtype < 0 || a->dtype > 2) return fail(DSALT_ERR_INVALID, "unknown dtype %d", a->dtype);
+    if (a->max_seqlen < 0 || a->max_seqlen > a->max_pos)
+        return fail(DSALT_ERR_INVALID, "max_seqlen (%d) must be in [0, max_pos = %d]", a->max_seqlen, a->max_pos);
+    int rc;
+    if (a->n_q_heads && (rc = check_rows(a->q, a->q_stride_t, a->q_stride_h, a->dtype, "q"))) return rc;
+    if (a->n_k_heads && (rc = check_rows(a->k, a->k_stride_t, a->k_stride_h, a->dtype, "k"))) return rc;
+    if (!a->cu_seqlens || !a->cos || !a->sin || !aligned16(a->cos) || !aligned16(a->sin))
+        return fail(DSALT_ERR_INVALID, "cu_seqlens, cos and sin are required (cos/sin 16-byte aligned)");
+    dsalt::RopeParams p;
+    p.total_len = a->total_len;
+    p.num_seqs = a->num_seqs;
+    p.n_q_heads = a->n_q_heads;
+    p.n_k_heads = a->n_k_heads;
+    p.head_dim = a->head_dim;
+    p.dtype = a->dtype;
+    p.q = a->q;
+    p.q_st = a->q_stride_t;
+    p.q_sh = a->q_stride_h;
+    p.k = a->k;
+    p.k_st = a->k_stride_t;
+    p.k_sh = a->k_stride_h;
+    p.cu = a->cu_seqlens;
+    p.cos = a->cos;
+    p.sin = a->sin;
+    p.max_pos = a->max_pos;
+    return hip_status(dsalt::rope_launch(p, (hipStream_t)stream), "dsalt_rope_qk");
 }
 
 int dsalt_gather_landmarks(const dsalt_gather_args* a, dsalt_stream_t stream) {

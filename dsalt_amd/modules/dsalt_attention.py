@@ -3,11 +3,14 @@
 Mirrors ``DSALTAttention`` of ``dsalt/modules/dsalt_attention.py:147-704`` (constructor,
 parameters and ``forward(x, cu_seqlens, max_seqlen, rope_cs, cu_list) -> (out, aux)``).
 Inference branch of ``_packed`` (:610-634):
-  * q/k/v projections (library GEMMs), RoPE on q and k;
+  * one fused q/k/v projection GEMM (the three weights concatenated, cached until a
+    weight changes) and RoPE applied in place to its q and k columns by a HIP kernel;
+    the attention reads q, k and v through strides from that one buffer (no [T, H, D]
+    copies, no materialised GQA repeat);
   * windows ``w = floor(n_min + sigmoid(win_gate(x)) (n_max - n_min))``, at least 1
     (:277-284), and ``alpha = sigmoid(alpha_w)`` (:228, :243-244);
-  * landmark selection (``_compute_landmark_indices``) and the sparse operator with zero
-    landmark bias (:622), k/v read per kv head (no materialised GQA repeat).
+  * landmark selection (``_compute_landmark_indices``, on ``x W_V^T`` without the bias as
+    in the reference) and the sparse operator with zero landmark bias (:622).
 ``select_mode="block"`` switches to block-causal landmarks (``block_size`` query rows per
 set, statistics of the prefix), the variant of ``results/causal_landmark_check.py:150-189``.
 Batched ``[B, T, d]`` input is run as ``B`` packed sequences of length ``T``.
@@ -28,7 +31,9 @@ import math
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
+from .. import ops
 from ..kernels.dsalt_attn import dsalt_attention
 from ..kernels.dsalt_train import dsalt_train_attention
 from ..kernels.landmark_tokens_ker import hybrid_scores_per_head
@@ -68,6 +73,7 @@ class DSALTAttention(nn.Module):
         self.tau_win, self.tau_lmk, self.win_edge = 1.0, 2.0, 4
         self._last_P = None
         self._collect_last_P = False
+        self._qkv_cache = None
         cos, sin = build_rope_cache(max_seq_len, self.head_dim, torch.device("cpu"), base=rope_base, scale=yarn_scale)
         self.register_buffer("rope_cos", cos, persistent=False)
         self.register_buffer("rope_sin", sin, persistent=False)
@@ -137,7 +143,58 @@ class DSALTAttention(nn.Module):
         return dsalt_train_attention(q, k, v, lmk_pos, lmk_logw, w_cont, cu_seqlens, tau_win=self.tau_win,
                                      win_edge=float(self.win_edge), n_max=self.n_max, cu_list=cu_list)
 
+    def _fused_qkv_weight(self):
+        """Concatenated [W_q; W_k; W_v] (and biases), rebuilt when a projection changes."""
+        ps = [m.weight for m in (self.q_proj, self.k_proj, self.v_proj)]
+        bs = [m.bias for m in (self.q_proj, self.k_proj, self.v_proj)]
+        key = tuple((t.data_ptr(), t._version, t.dtype) for t in ps + [b for b in bs if b is not None])
+        if self._qkv_cache is None or self._qkv_cache[0] != key:
+            with torch.no_grad():
+                w = torch.cat(ps)
+                b = torch.cat(bs) if bs[0] is not None else None
+            self._qkv_cache = (key, w, b)
+        return self._qkv_cache[1], self._qkv_cache[2]
+
+    def _rope_tables32(self):
+        """The RoPE tables as float32 (the buffers follow the module's dtype; values already
+        rounded to a 16-bit type round to themselves again in the kernel)."""
+        c, s = self.rope_cos, self.rope_sin
+        if c.dtype == torch.float32:
+            return c, s
+        key = (c.data_ptr(), c._version, s.data_ptr(), s._version)
+        if getattr(self, "_rope32", None) is None or self._rope32[0] != key:
+            self._rope32 = (key, c.float(), s.float())
+        return self._rope32[1], self._rope32[2]
+
+    @torch.no_grad()
+    def _packed_inference(self, x, cu_seqlens, total_len, device, rope_cs=None, cu_list=None):
+        H, G, D = self.n_heads, self.n_kv_heads, self.head_dim
+        w_qkv, b_qkv = self._fused_qkv_weight()
+        qkv = F.linear(x, w_qkv, b_qkv)                                            # [T, (H + 2G) D]
+        q = qkv[:, :H * D].view(total_len, H, D)
+        k = qkv[:, H * D:(H + G) * D].view(total_len, G, D)
+        v = qkv[:, (H + G) * D:].view(total_len, G, D)
+        maxlen = ops._max_seqlen(cu_seqlens, cu_list)
+        if rope_cs is None:
+            cos, sin = self._rope_tables32()
+            ops.rope_qk_(q, k, cu_seqlens, cos, sin, max_seqlen=maxlen)
+        else:  # rows already gathered per token: token t reads row t
+            cu1 = torch.tensor([0, total_len], dtype=torch.int32, device=device)
+            ops.rope_qk_(q, k, cu1, rope_cs[0].float(), rope_cs[1].float(), max_seqlen=total_len)
+        w = self._window_sizes(x, floor=True)
+        lmk, _, _ = _compute_landmark_indices(x, self.v_proj.weight, self._alpha().float(), w, cu_seqlens, self.k_lmk,
+                                              self.n_min, total_len, cu_list, head_dim=D, select_mode=self.select_mode,
+                                              block_size=self.block_size, stats_scope=self.stats_scope)
+        idx = lmk.to(torch.int32) if lmk.dim() == 4 else lmk.to(torch.int32).unsqueeze(2)
+        mode = ops.SELECT_BLOCK if self.select_mode == "block" else ops.SELECT_GLOBAL
+        out, _ = ops.attention_forward(q, k, v, w.to(torch.int32), cu_seqlens, idx, None, max_seqlen=maxlen,
+                                       select_mode=mode, block_size=self.block_size)
+        self._last_P = None
+        return self._apply_out_proj(out.view(total_len, self.d_model)), self._aux_zero(x.device, x.dtype)
+
     def _packed(self, x, cu_seqlens, total_len, device, rope_cs=None, cu_list=None):
+        if not self.training and not torch.is_grad_enabled():
+            return self._packed_inference(x, cu_seqlens, total_len, device, rope_cs, cu_list)
         q = self.q_proj(x).view(total_len, self.n_heads, self.head_dim)
         k = self.k_proj(x).view(total_len, self.n_kv_heads, self.head_dim)
         v = self.v_proj(x).view(total_len, self.n_kv_heads, self.head_dim)

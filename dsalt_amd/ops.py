@@ -13,7 +13,7 @@ import torch
 
 from . import _lib
 from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, SELECT_BLOCK, SELECT_GLOBAL, STATS_PACKED,
-                   STATS_SEQUENCE, BwdArgs, FwdArgs, GatherArgs, Problem, SelectArgs, TrainBwdArgs,
+                   STATS_SEQUENCE, BwdArgs, FwdArgs, GatherArgs, Problem, RopeArgs, SelectArgs, TrainBwdArgs,
                    TrainFwdArgs)
 
 _DT = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
@@ -365,6 +365,41 @@ def gather_landmarks(k, v, cu_seqlens, lmk_idx, *, max_seqlen=None, select_mode=
     L = _lib.load()
     _lib.check("dsalt_gather_landmarks", L.dsalt_gather_landmarks(ctypes.byref(a), _stream(dev)))
     return lk, lv
+
+
+def rope_qk_(q, k, cu_seqlens, cos, sin, *, max_seqlen=None):
+    """Rotary embedding of q [T, Hq, D] and k [T, Hk, D] in place (either may be None);
+    cos/sin [max_pos, D] fp32 tables indexed by each token's position in its sequence.
+    q and k may be strided views of one fused projection output."""
+    dev = _gpu(q, k, cu_seqlens, cos, sin)
+    ref = q if q is not None else k
+    if ref is None:
+        return q, k
+    for t, n in ((q, "q"), (k, "k")):
+        if t is not None and (t.dim() != 3 or t.stride(2) != 1):
+            raise ValueError(f"{n} must be [T, H, D] with unit stride along D")
+    T, _, D = ref.shape
+    if k is not None and q is not None and (k.shape[0] != T or k.shape[2] != D or k.dtype != q.dtype):
+        raise ValueError("q and k must share T, D and dtype")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape or cos.dim() != 2 \
+            or cos.shape[1] != D:
+        raise ValueError("cos/sin must be float32 [max_pos, head_dim]")
+    cos, sin = cos.contiguous(), sin.contiguous()
+    cu_c = cu_seqlens.detach().to(torch.int32).contiguous()
+    maxlen = max_seqlen if max_seqlen is not None else _max_seqlen(cu_seqlens)
+    a = RopeArgs()
+    a.total_len, a.num_seqs, a.max_seqlen = T, cu_c.shape[0] - 1, maxlen
+    a.n_q_heads = q.shape[1] if q is not None else 0
+    a.n_k_heads = k.shape[1] if k is not None else 0
+    a.head_dim, a.dtype = D, dtype_code(ref.dtype)
+    if q is not None:
+        a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    if k is not None:
+        a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
+    a.cu_seqlens, a.cos, a.sin, a.max_pos = cu_c.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0]
+    L = _lib.load()
+    _lib.check("dsalt_rope_qk", L.dsalt_rope_qk(ctypes.byref(a), _stream(dev)))
+    return q, k
 
 
 def sort_landmarks(idx: torch.Tensor, bias: torch.Tensor | None = None):

@@ -97,3 +97,27 @@ def generate(wl: Workload, device="cpu", seqlen: int | None = None, heads: int |
     if wl.backward:
         out["dout"] = torch.randn(T, H, wl.head_dim, generator=g).to(wl.dtype)
     return {kk: vv.to(device) for kk, vv in out.items()}
+
+
+@dataclass(frozen=True)
+class ModelWorkload:
+    """A whole-model prefill: random-init weights of a named shape, random token ids."""
+    name: str
+    batch: int
+    seqlen: int
+    dtype: torch.dtype
+    seed: int = 2000
+
+    def config(self):
+        from .model import qwen25_3b_config
+        return qwen25_3b_config(max_seq_len=self.seqlen)
+
+
+MODEL_WORKLOADS = {
+    w.name: w
+    for w in [
+        # Qwen2.5-3B-shaped DSALT decoder (36 layers, hidden 2048, 16/2 heads, head_dim 128,
+        # SwiGLU 11008, vocab 151936), block-causal landmarks k=128, w_max=512, prefill of 32K
+        ModelWorkload("prefill_qwen3b_l32768", 1, 32768, torch.bfloat16),
+    ]
+}

@@ -183,6 +183,33 @@ typedef struct dsalt_train_bwd_args {
     float* d_w;                /* out [T]                                            */
 } dsalt_train_bwd_args;
 
+/* Rotary position embedding of the query and key heads, in place, e.g. on the
+ * output of one fused QKV projection read through strides (the attention entry
+ * points then read q, k and v from the same buffer).  Replaces the RoPE step of
+ * DSALTAttention._packed, dsalt/modules/dsalt_attention.py:566-585 (cos/sin rows
+ * gathered at each token's position in its sequence and cast to the tensor type,
+ * q * cos + rotate_half(q) * sin with rotate_half(x) = [-x2, x1], x1/x2 the two
+ * halves of the head; dsalt/kernels/window_utils.py apply_rotary_emb), with the
+ * rounding of that expression evaluated one operation at a time in the tensor type.
+ * Needs no workspace. */
+typedef struct dsalt_rope_args {
+    int32_t total_len;         /* T                                                  */
+    int32_t num_seqs;          /* S                                                  */
+    int32_t max_seqlen;        /* longest sequence (host value), <= max_pos          */
+    int32_t n_q_heads;         /* heads rotated in q (may be 0)                      */
+    int32_t n_k_heads;         /* heads rotated in k (may be 0)                      */
+    int32_t head_dim;          /* multiple of 16, <= 256                             */
+    int32_t dtype;             /* DSALT_DTYPE_*                                      */
+    void* q; int64_t q_stride_t; int64_t q_stride_h;
+    void* k; int64_t k_stride_t; int64_t k_stride_h;
+    const int32_t* cu_seqlens;
+    const float* cos;          /* [max_pos, head_dim] fp32, rows 16-byte aligned     */
+    const float* sin;          /* [max_pos, head_dim]                                */
+    int32_t max_pos;
+} dsalt_rope_args;
+
+int    dsalt_rope_qk(const dsalt_rope_args* a, dsalt_stream_t stream);
+
 size_t dsalt_select_workspace_bytes(const dsalt_select_args* a);
 int    dsalt_select(const dsalt_select_args* a, dsalt_stream_t stream);
 

@@ -48,6 +48,7 @@ STRUCTS = {
     "dsalt_gather_args": _lib.GatherArgs,
     "dsalt_train_fwd_args": _lib.TrainFwdArgs,
     "dsalt_train_bwd_args": _lib.TrainBwdArgs,
+    "dsalt_rope_args": _lib.RopeArgs,
 }
 
 
@@ -175,3 +176,24 @@ def test_train_rejects_block_sets_and_small_workspace():
     assert need >= 128 * 4 + 128 * 2 * 4
     b.base.workspace, b.base.workspace_bytes = fake, need - 16
     assert lib.dsalt_train_bwd(ctypes.byref(b), None) == 3
+
+
+def _valid_rope():
+    a = _lib.RopeArgs()
+    a.total_len, a.num_seqs, a.max_seqlen, a.n_q_heads, a.n_k_heads, a.head_dim, a.dtype = 128, 1, 128, 4, 2, 64, 1
+    fake = 1 << 20
+    a.q = a.k = a.cu_seqlens = a.cos = a.sin = fake
+    a.q_stride_t, a.q_stride_h = 512, 64
+    a.k_stride_t, a.k_stride_h = 512, 64
+    a.max_pos = 128
+    return a
+
+
+@pytest.mark.parametrize("field,value", [("head_dim", 72), ("head_dim", 512), ("dtype", 5), ("max_pos", 100),
+                                         ("num_seqs", 0), ("q_stride_h", 63), ("cos", None), ("sin", (1 << 20) + 4)])
+def test_rope_validation(field, value):
+    lib = _lib.load()
+    a = _valid_rope()
+    setattr(a, field, value)
+    assert lib.dsalt_rope_qk(ctypes.byref(a), None) == 1
+    assert lib.dsalt_last_error()

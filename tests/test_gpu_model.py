@@ -1,0 +1,138 @@
+"""Fused ingress (RoPE in place on a fused QKV projection) and the decoder stack on the GPU.
+
+RoPE: bit-exact against the oracle's emulation of the reference expression.  Layer and
+model outputs: the attention part against the float64 oracle, the rest against the same
+torch computation; tolerances are relative (max|a-b| / max|b|) and written per test.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from dsalt_amd import ops
+from oracle import rope as OR
+from tests.helpers import f64, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+NAME = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+def test_rope_in_place_on_fused_qkv_bit_exact(dt, D):
+    from dsalt_amd.kernels.window_utils import build_rope_cache
+    g = torch.Generator().manual_seed(D)
+    lens = [300, 77, 1]
+    T, H, G = sum(lens), 4, 2
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    qkv = (torch.randn(T, (H + 2 * G) * D, generator=g) * 2).to(dt)
+    cos, sin = build_rope_cache(512, D, torch.device("cpu"), base=1e6)
+    buf = qkv.to(DEV)
+    q = buf[:, :H * D].view(T, H, D)
+    k = buf[:, H * D:(H + G) * D].view(T, G, D)
+    ops.rope_qk_(q, k, cu.to(DEV), cos.to(DEV), sin.to(DEV), max_seqlen=max(lens))
+    torch.cuda.synchronize()
+    out = buf.cpu().float().numpy()
+    ref_q = OR.rope(qkv[:, :H * D].view(T, H, D).float().numpy(), cu.numpy(), cos.numpy(), sin.numpy(), NAME[dt])
+    ref_k = OR.rope(qkv[:, H * D:(H + G) * D].view(T, G, D).float().numpy(), cu.numpy(), cos.numpy(), sin.numpy(),
+                    NAME[dt])
+    np.testing.assert_array_equal(out[:, :H * D], ref_q.reshape(T, -1))
+    np.testing.assert_array_equal(out[:, H * D:(H + G) * D], ref_k.reshape(T, -1))
+    np.testing.assert_array_equal(out[:, (H + G) * D:], qkv[:, (H + G) * D:].float().numpy())  # v untouched
+
+
+def test_rope_rejects_positions_past_the_table():
+    from dsalt_amd.kernels.window_utils import build_rope_cache
+    cos, sin = build_rope_cache(64, 64, torch.device(DEV))
+    q = torch.zeros(100, 2, 64, dtype=torch.bfloat16, device=DEV)
+    cu = torch.tensor([0, 100], dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError, match="max_pos"):
+        ops.rope_qk_(q, None, cu, cos, sin)
+
+
+def _layer_both_paths(dt, mode, G=2, rope_cs=False):
+    from dsalt_amd.modules import DSALTAttention
+    torch.manual_seed(3)
+    d, H, T = 256, 4, 640
+    m = DSALTAttention(d, H, 16, 96, 12, 1024, n_kv_heads=G, qkv_bias=True, select_mode=mode,
+                       block_size=128).to(DEV).to(dt).eval()
+    x = torch.randn(T, d, device=DEV).to(dt)
+    cu = torch.tensor([0, 400, T], dtype=torch.int32, device=DEV)
+    cs = None
+    if rope_cs:
+        pos = torch.cat([torch.arange(400), torch.arange(T - 400)]).to(DEV)
+        cs = (m.rope_cos[pos], m.rope_sin[pos])
+    with torch.enable_grad():  # the separate-projection path with autograd
+        ref, _ = m(x, cu, rope_cs=cs, cu_list=[0, 400, T])
+    with torch.no_grad():      # fused QKV GEMM, RoPE kernel in place, strided attention
+        out, aux = m(x, cu, rope_cs=cs, cu_list=[0, 400, T])
+    return out, ref.detach(), aux
+
+
+@pytest.mark.parametrize("dt,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("mode", ["global", "block"])
+def test_layer_fused_inference_path_matches_projection_path(dt, tol, mode):
+    out, ref, aux = _layer_both_paths(dt, mode)
+    assert out.dtype == dt and float(aux) == 0.0
+    assert rel_err(f64(out), f64(ref)) < tol
+
+
+def test_layer_fused_path_with_gathered_rope_rows():
+    out, ref, _ = _layer_both_paths(torch.float32, "global", G=4, rope_cs=True)
+    assert rel_err(f64(out), f64(ref)) < 1e-5
+
+
+def _small_model(mode, dt=torch.float32, tie=True):
+    from dsalt_amd.model import DSALTConfig, DSALTLMHeadModel
+    cfg = DSALTConfig(vocab_size=1000, d_model=256, n_layers=2, n_heads=4, n_kv_heads=2, n_min=16, n_max=96, k_lmk=12,
+                      max_seq_len=1024, d_ff=512, qkv_bias=True, rope_base=1e6, select_mode=mode, block_size=128,
+                      tie_weights=tie, lm_head_chunk_size=128)
+    torch.manual_seed(5)
+    return DSALTLMHeadModel.from_config(cfg).to(DEV).to(dt)
+
+
+@pytest.mark.parametrize("mode", ["global", "block"])
+def test_model_inference_forward_matches_autograd_forward(mode):
+    m = _small_model(mode).eval()
+    T = 513
+    ids = torch.randint(0, 1000, (T,), device=DEV)
+    cu = torch.tensor([0, 300, T], dtype=torch.int32, device=DEV)
+    with torch.no_grad():
+        lg = m(ids, cu_seqlens=cu)["logits"]
+    lg_ref = m(ids, cu_seqlens=cu)["logits"].detach()
+    assert lg.shape == (T, 1000)
+    assert rel_err(f64(lg), f64(lg_ref)) < 1e-5
+    # batched input runs as packed sequences of equal length
+    with torch.no_grad():
+        lb = m(ids[:512].view(2, 256))["logits"]
+        lp = m(ids[:512], cu_seqlens=torch.tensor([0, 256, 512], dtype=torch.int32, device=DEV))["logits"]
+    assert rel_err(f64(lb.reshape(512, -1)), f64(lp)) < 1e-5
+
+
+def test_model_loss_is_mean_token_cross_entropy():
+    m = _small_model("global").eval()
+    T = 400
+    ids = torch.randint(0, 1000, (T,), device=DEV)
+    labels = torch.randint(0, 1000, (T,), device=DEV)
+    labels[::7] = -100
+    cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
+    with torch.no_grad():
+        loss = m(ids, cu_seqlens=cu, labels=labels)["loss"]
+        lg = m(ids, cu_seqlens=cu)["logits"]
+    ref = torch.nn.functional.cross_entropy(lg.float(), labels, ignore_index=-100)
+    assert abs(float(loss) - float(ref)) < 1e-4 * abs(float(ref))
+
+
+def test_model_training_step_reaches_every_parameter():
+    m = _small_model("global", tie=False).train()
+    T = 300
+    ids = torch.randint(0, 1000, (T,), device=DEV)
+    cu = torch.tensor([0, 180, T], dtype=torch.int32, device=DEV)
+    out = m(ids, cu_seqlens=cu, labels=torch.roll(ids, -1))
+    out["loss"].backward()
+    for n, p in m.named_parameters():
+        assert p.grad is not None and torch.isfinite(p.grad).all(), n
+        if "win_gate" in n or "alpha_w" in n or "proj" in n:
+            assert float(p.grad.abs().max()) > 0, n

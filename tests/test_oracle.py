@@ -15,6 +15,8 @@ Parity status of each oracle function (how it is pinned):
   attention.literal_mask         golden (reference _build_mask_packed + masked SDPA)
   train.train_bias / train_fwd   golden (reference _dense_logbias_from_kernel + SDPA, float64)
                                  + win_edge 0 reduces to attention_fwd with window floor(w~)+1
+  rope.rope                      torch's evaluation of the reference expression (CPU, bf16/fp16/fp32)
+                                 + rotation of 2-vectors preserves norms (fp32)
   train.train_bwd                golden (float64 autograd of the reference dense form)
                                  + central finite differences in w~ and lmk_logw
 """
@@ -28,6 +30,7 @@ import torch
 
 from oracle import attention as OA
 from oracle import select as OS
+from oracle import rope as OR
 from oracle import train as OT
 from tests.helpers import load_golden, rel_err
 
@@ -419,3 +422,22 @@ def test_cpu_baseline_training_bias_rows_match_oracle():
             np.testing.assert_array_equal(np.isinf(got), np.isinf(want))
             fin = np.isfinite(want)
             assert np.abs(got[fin] - want[fin]).max() < 1e-12
+
+
+@pytest.mark.parametrize("dt,name", [(torch.bfloat16, "bf16"), (torch.float16, "f16"), (torch.float32, "f32")])
+def test_rope_matches_reference_expression(dt, name):
+    from dsalt_amd.kernels.window_utils import apply_rotary_emb, build_rope_cache
+    g = torch.Generator().manual_seed(70)
+    lens = [37, 64, 5]
+    T, H, D = sum(lens), 3, 64
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cos, sin = build_rope_cache(80, D, torch.device("cpu"), base=1e6)
+    x = (torch.randn(T, H, D, generator=g) * 3).to(dt)
+    pos = torch.cat([torch.arange(n) for n in lens])
+    ref, _ = apply_rotary_emb(x, x, cos[pos].to(dt).unsqueeze(1), sin[pos].to(dt).unsqueeze(1))
+    got = OR.rope(x.float().numpy(), cu, cos.numpy(), sin.numpy(), name)
+    np.testing.assert_array_equal(got, ref.float().numpy())
+    if name == "f32":  # a rotation keeps the length of every (x_j, x_j+D/2) pair
+        n0 = x[..., :32] ** 2 + x[..., 32:] ** 2
+        n1 = torch.tensor(got[..., :32] ** 2 + got[..., 32:] ** 2)
+        assert torch.allclose(n0, n1, rtol=1e-5)
