@@ -25,6 +25,8 @@ SOURCES = {
     "attn_bwd.hip": [],
     # the rotation rounds every product and sum to the tensor type: no fused multiply-adds
     "rope.hip": ["-ffp-contract=off"],
+    # products rounded to the tensor type one operation at a time, as the torch expression
+    "ffn.hip": ["-ffp-contract=off"],
     "capi.hip": [],
     "timing.hip": [],
 }

@@ -6,6 +6,7 @@
 #include <string>
 
 #include "attn.h"
+#include "ffn.h"
 #include "rope.h"
 #include "select.h"
 #include "common.h"
@@ -397,6 +398,31 @@ int dsalt_rope_qk(const dsalt_rope_args* a, dsalt_stream_t stream) {
     p.sin = a->sin;
     p.max_pos = a->max_pos;
     return hip_status(dsalt::rope_launch(p, (hipStream_t)stream), "dsalt_rope_qk");
+}
+
+int dsalt_silu_mul(const dsalt_silu_mul_args* a, dsalt_stream_t stream) {
+    if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
+    if (a->rows < 0 || a->cols < 0 || a->cols % 8)
+        return fail(DSALT_ERR_INVALID, "rows >= 0 and cols a multiple of 8 required (got %d x %d)", a->rows, a->cols);
+    if (a->dtype < 0 || a->dtype > 2) return fail(DSALT_ERR_INVALID, "unknown dtype %d", a->dtype);
+    if (a->rows == 0 || a->cols == 0) return DSALT_OK;
+    const int64_t es = (int64_t)esize(a->dtype);
+    const void* ptrs[3] = {a->gate, a->up, a->out};
+    const int64_t strides[3] = {a->gate_stride, a->up_stride, a->out_stride};
+    for (int i = 0; i < 3; ++i)
+        if (!ptrs[i] || !aligned16(ptrs[i]) || strides[i] < a->cols || (strides[i] * es) % 16)
+            return fail(DSALT_ERR_INVALID, "gate, up and out need 16-byte aligned rows of at least cols elements");
+    dsalt::SiluMulParams p;
+    p.rows = a->rows;
+    p.cols = a->cols;
+    p.dtype = a->dtype;
+    p.gate = a->gate;
+    p.gate_st = a->gate_stride;
+    p.up = a->up;
+    p.up_st = a->up_stride;
+    p.out = a->out;
+    p.out_st = a->out_stride;
+    return hip_status(dsalt::silu_mul_launch(p, (hipStream_t)stream), "dsalt_silu_mul");
 }
 
 int dsalt_gather_landmarks(const dsalt_gather_args* a, dsalt_stream_t stream) {

@@ -5,7 +5,8 @@ Mirrors ``SwiGLUFFN`` and ``DSALTTransformerBlock`` of
 -> SwiGLU FFN -> residual; optional activation checkpointing), with the attention layer's
 landmark variant exposed (``select_mode``, ``block_size``, ``stats_scope``).  Without
 autograd the FFN runs its gate and up projections as one GEMM over the concatenated
-weights (same per-element arithmetic).
+weights and the gated activation as one HIP kernel over that buffer (same per-element
+arithmetic as silu(g) * u).
 """
 from __future__ import annotations
 
@@ -14,6 +15,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 import torch.utils.checkpoint
 
+from .. import ops
 from ..kernels.RMSENorm import RMSENorm
 from .dsalt_attention import DSALTAttention
 
@@ -51,7 +53,9 @@ class SwiGLUFFN(nn.Module):
             self.gemm_events.append(ev)
         else:
             gu = F.linear(x, w)
-        return self.down_proj(F.silu(gu[..., :d_ff]) * gu[..., d_ff:])
+        g2 = gu.reshape(-1, 2 * d_ff)
+        h = ops.silu_mul(g2[:, :d_ff], g2[:, d_ff:]).view(*gu.shape[:-1], d_ff)
+        return self.down_proj(h)
 
 
 class DSALTTransformerBlock(nn.Module):

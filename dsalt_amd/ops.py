@@ -13,7 +13,7 @@ import torch
 
 from . import _lib
 from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, SELECT_BLOCK, SELECT_GLOBAL, STATS_PACKED,
-                   STATS_SEQUENCE, BwdArgs, FwdArgs, GatherArgs, Problem, RopeArgs, SelectArgs, TrainBwdArgs,
+                   STATS_SEQUENCE, BwdArgs, FwdArgs, GatherArgs, Problem, RopeArgs, SelectArgs, SiluMulArgs, TrainBwdArgs,
                    TrainFwdArgs)
 
 _DT = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
@@ -400,6 +400,21 @@ def rope_qk_(q, k, cu_seqlens, cos, sin, *, max_seqlen=None):
     L = _lib.load()
     _lib.check("dsalt_rope_qk", L.dsalt_rope_qk(ctypes.byref(a), _stream(dev)))
     return q, k
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(gate) * up for 2-D [rows, cols] tensors with unit column stride (gate and up may
+    be column ranges of one buffer); a new contiguous output unless ``out`` is given."""
+    dev = _gpu(gate, up, out)
+    if gate.dim() != 2 or gate.shape != up.shape or gate.stride(1) != 1 or up.stride(1) != 1 or gate.dtype != up.dtype:
+        raise ValueError("gate and up must be [rows, cols] of one dtype with unit column stride")
+    if out is None:
+        out = torch.empty(gate.shape, dtype=gate.dtype, device=dev)
+    a = SiluMulArgs(gate.shape[0], gate.shape[1], dtype_code(gate.dtype), gate.data_ptr(), gate.stride(0),
+                    up.data_ptr(), up.stride(0), out.data_ptr(), out.stride(0))
+    L = _lib.load()
+    _lib.check("dsalt_silu_mul", L.dsalt_silu_mul(ctypes.byref(a), _stream(dev)))
+    return out
 
 
 def sort_landmarks(idx: torch.Tensor, bias: torch.Tensor | None = None):

@@ -210,6 +210,23 @@ typedef struct dsalt_rope_args {
 
 int    dsalt_rope_qk(const dsalt_rope_args* a, dsalt_stream_t stream);
 
+/* Gated activation of the SwiGLU feed-forward block, out = silu(gate) * up, where
+ * gate and up may be column ranges of one fused gate/up GEMM output.  Replaces
+ * F.silu(gate_proj(x)) * up_proj(x) of SwiGLUFFN.forward,
+ * dsalt/modules/dsalt_transformer.py:20-21 (silu in float32 as g / (1 + exp(-g))
+ * rounded to the tensor type, the product rounded to the tensor type).  rows x cols
+ * with cols a multiple of 8; every row 16-byte aligned.  Needs no workspace. */
+typedef struct dsalt_silu_mul_args {
+    int32_t rows;
+    int32_t cols;
+    int32_t dtype;              /* DSALT_DTYPE_*                                     */
+    const void* gate; int64_t gate_stride;   /* row strides in elements              */
+    const void* up;   int64_t up_stride;
+    void* out;        int64_t out_stride;
+} dsalt_silu_mul_args;
+
+int    dsalt_silu_mul(const dsalt_silu_mul_args* a, dsalt_stream_t stream);
+
 size_t dsalt_select_workspace_bytes(const dsalt_select_args* a);
 int    dsalt_select(const dsalt_select_args* a, dsalt_stream_t stream);
 

@@ -49,6 +49,7 @@ STRUCTS = {
     "dsalt_train_fwd_args": _lib.TrainFwdArgs,
     "dsalt_train_bwd_args": _lib.TrainBwdArgs,
     "dsalt_rope_args": _lib.RopeArgs,
+    "dsalt_silu_mul_args": _lib.SiluMulArgs,
 }
 
 
@@ -197,3 +198,12 @@ def test_rope_validation(field, value):
     setattr(a, field, value)
     assert lib.dsalt_rope_qk(ctypes.byref(a), None) == 1
     assert lib.dsalt_last_error()
+
+
+@pytest.mark.parametrize("field,value", [("cols", 12), ("dtype", 3), ("up", None), ("out", (1 << 20) + 2),
+                                         ("gate_stride", 8), ("out_stride", 36)])
+def test_silu_mul_validation(field, value):
+    lib = _lib.load()
+    a = _lib.SiluMulArgs(64, 32, 1, 1 << 20, 64, (1 << 20) + 64, 64, 1 << 21, 32)
+    setattr(a, field, value)
+    assert lib.dsalt_silu_mul(ctypes.byref(a), None) == 1

@@ -136,3 +136,15 @@ def test_model_training_step_reaches_every_parameter():
         assert p.grad is not None and torch.isfinite(p.grad).all(), n
         if "win_gate" in n or "alpha_w" in n or "proj" in n:
             assert float(p.grad.abs().max()) > 0, n
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+def test_silu_mul_on_fused_gate_up_matches_torch(dt):
+    g = torch.Generator().manual_seed(9)
+    T, F_ = 333, 11008
+    gu = (torch.randn(T, 2 * F_, generator=g) * 4).to(dt).to(DEV)
+    gu[0, :8] = torch.tensor([0.0, -0.0, 30.0, -30.0, 88.0, -88.0, 1e-3, -1e-3], dtype=dt)
+    out = ops.silu_mul(gu[:, :F_], gu[:, F_:])
+    ref = torch.nn.functional.silu(gu[:, :F_].contiguous()) * gu[:, F_:].contiguous()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), float((out.float() - ref.float()).abs().max())
