@@ -50,14 +50,15 @@ def parse():
 
 
 LABELS = ("sel_norms", "sel_sums", "sel_stats", "sel_z", "sel_scores", "sel_part", "sel_merge", "sel_topk", "gather",
-          "row_plan", "attn_fwd", "bwd_init", "bwd_dq", "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum", "train_windows", "train_dw")
+          "row_plan", "attn_fwd", "bwd_init", "bwd_dq", "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum", "train_windows", "train_dw",
+          "rope", "silu_mul", "probs")
 
 
 def short_kernel_name(name: str) -> str:
     """Label of a library kernel (the one dsalt_timing_report uses) from a profiler kernel name."""
     import re
     m = re.search(r"(sel_norms|sel_sums|sel_stats|sel_z|sel_scores|sel_part|sel_merge|sel_topk|gather|row_plan|fwd|bwd_init|bwd_dq|"
-                  r"bwd_dkdv|bwd_lmk_sum|train_windows|train_dw|"
+                  r"bwd_dkdv|bwd_lmk_sum|train_windows|train_dw|rope|silu_mul|probs|"
                   r"bwd_lmk)_kernel", name)
     if not m:
         return name
@@ -124,6 +125,68 @@ def kernel_model(wl, T, H, D, hidden, pairs, e):
         "bwd_dq": dict(bytes=6 * thd + 2 * th4 + tr, flops=4 * D * pairs),
         "bwd_dkdv": dict(bytes=6 * thd + 2 * th4, flops=4 * D * pairs),
     }
+
+
+def probs_bench(args, wl):
+    """Export of one sequence's attention probabilities (window band + landmark slots) after
+    a forward of the workload: a step is one dsalt_export_probs call over the whole
+    sequence, every head (the forward runs once, untimed)."""
+    import ctypes
+
+    import torch
+
+    from dsalt_amd import _lib, ops
+    from dsalt_amd.workloads import generate
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    x = {k: v.to(dev) for k, v in generate(wl).items()}
+    T, H, D = x["q"].shape
+    L = wl.seqlen
+    idx = ops.select_landmarks(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, max_seqlen=L,
+                               stats_scope=ops.STATS_SEQUENCE)
+    _, lse = ops.attention_forward(x["q"], x["k"], x["v"], x["w"], x["cu"], idx, None, max_seqlen=L)
+    w_cap = wl.w_max
+
+    def step():
+        return ops.export_probs(x["q"], x["k"], x["w"], x["cu"], idx, lse, seq=0, rows=L, w_cap=w_cap, max_seqlen=L)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    lib.dsalt_timing_enable(1)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    buf = ctypes.create_string_buffer(1 << 14)
+    lib.dsalt_timing_report(buf, len(buf))
+    lib.dsalt_timing_enable(0)
+    kernels = {}
+    for line in buf.value.decode().splitlines():
+        name, n, tot = line.split()
+        kernels[name] = dict(launches=int(n), avg_ms=float(tot) / int(n))
+    e = x["q"].element_size()
+    alg = H * L * (w_cap + wl.k_lmk) * 4 + 2 * L * H * D * e + 8 * L * H  # outputs + q, k + w, lse
+    avg = kernels["probs"]["avg_ms"] * 1e-3
+    ach = alg / avg / 1e9
+    line = {"metric": "attention-probability export rows/sec @L=32K (window band + landmark slots, all heads)",
+            "value": round(L * args.steps / elapsed, 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(1e3 * elapsed / args.steps, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32 out / bf16 in", "data": "synthetic",
+            "config": {"workload": "probs_" + wl.name, "heads": H, "seq_len": L, "head_dim": D, "w_cap": w_cap,
+                       "k_lmk": wl.k_lmk, "dense_bytes_avoided": H * L * L * 4},
+            "roofline": {"bound": "hbm", "kernel": "probs", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "algorithmic_bytes": alg},
+            "cpu_baseline": None,
+            "kernels": {k: {kk: round(vv, 5) if isinstance(vv, float) else vv for kk, vv in v.items()}
+                        for k, v in kernels.items()}}
+    print(json.dumps(line), flush=True)
 
 
 def model_bench(args, wl):
@@ -255,6 +318,8 @@ def main():
 
     if args.workload in MODEL_WORKLOADS:
         return model_bench(args, MODEL_WORKLOADS[args.workload])
+    if args.workload.startswith("probs_"):
+        return probs_bench(args, WORKLOADS[args.workload[len("probs_"):]])
     wl = WORKLOADS[args.workload]
     lib = _lib.load()
     dev = torch.device("cuda", 0)

@@ -83,6 +83,14 @@ class RopeArgs(ctypes.Structure):
                 ("cu_seqlens", _vp), ("cos", _vp), ("sin", _vp), ("max_pos", _i32)]
 
 
+class ProbsArgs(ctypes.Structure):
+    _fields_ = [("p", Problem),
+                ("q", _vp), ("q_stride_t", _i64), ("q_stride_h", _i64),
+                ("k", _vp), ("k_stride_t", _i64), ("k_stride_h", _i64),
+                ("w", _vp), ("cu_seqlens", _vp), ("lmk_idx", _vp), ("lmk_bias", _vp), ("lse", _vp),
+                ("scale", _f32), ("seq", _i32), ("rows", _i32), ("w_cap", _i32), ("p_win", _vp), ("p_lmk", _vp)]
+
+
 class SiluMulArgs(ctypes.Structure):
     _fields_ = [("rows", _i32), ("cols", _i32), ("dtype", _i32), ("gate", _vp), ("gate_stride", _i64),
                 ("up", _vp), ("up_stride", _i64), ("out", _vp), ("out_stride", _i64)]
@@ -114,6 +122,7 @@ SIGNATURES = {
     "dsalt_train_bwd": ([ctypes.POINTER(TrainBwdArgs), _vp], ctypes.c_int),
     "dsalt_rope_qk": ([ctypes.POINTER(RopeArgs), _vp], ctypes.c_int),
     "dsalt_silu_mul": ([ctypes.POINTER(SiluMulArgs), _vp], ctypes.c_int),
+    "dsalt_export_probs": ([ctypes.POINTER(ProbsArgs), _vp], ctypes.c_int),
     "dsalt_timing_enable": ([ctypes.c_int], ctypes.c_int),
     "dsalt_timing_report": ([ctypes.c_char_p, _sz], ctypes.c_int),
 }

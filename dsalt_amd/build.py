@@ -27,6 +27,7 @@ SOURCES = {
     "rope.hip": ["-ffp-contract=off"],
     # products rounded to the tensor type one operation at a time, as the torch expression
     "ffn.hip": ["-ffp-contract=off"],
+    "probs.hip": [],
     "capi.hip": [],
     "timing.hip": [],
 }

@@ -7,6 +7,7 @@
 
 #include "attn.h"
 #include "ffn.h"
+#include "probs.h"
 #include "rope.h"
 #include "select.h"
 #include "common.h"
@@ -398,6 +399,41 @@ int dsalt_rope_qk(const dsalt_rope_args* a, dsalt_stream_t stream) {
     p.sin = a->sin;
     p.max_pos = a->max_pos;
     return hip_status(dsalt::rope_launch(p, (hipStream_t)stream), "dsalt_rope_qk");
+}
+
+int dsalt_export_probs(const dsalt_probs_args* a, dsalt_stream_t stream) {
+    if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
+    int rc = check_problem(a->p, true);
+    if (rc) return rc;
+    const int dt = a->p.dtype;
+    if ((rc = check_rows(a->q, a->q_stride_t, a->q_stride_h, dt, "q"))) return rc;
+    if ((rc = check_rows(a->k, a->k_stride_t, a->k_stride_h, dt, "k"))) return rc;
+    if (!a->w || !a->cu_seqlens || !a->lse || (a->p.k_lmk > 0 && !a->lmk_idx))
+        return fail(DSALT_ERR_INVALID, "w, cu_seqlens, lse and lmk_idx are required");
+    if (a->seq < 0 || a->seq >= a->p.num_seqs) return fail(DSALT_ERR_INVALID, "seq %d out of range", a->seq);
+    if (a->rows < 0 || a->rows > a->p.max_seqlen || a->w_cap < 1)
+        return fail(DSALT_ERR_INVALID, "rows must be in [0, max_seqlen] and w_cap >= 1");
+    if (!a->p_win) return fail(DSALT_ERR_INVALID, "p_win is required");
+    if (!(a->scale > 0.f)) return fail(DSALT_ERR_INVALID, "scale must be positive");
+    dsalt::ProbsParams pp;
+    pp.a = attn_common(a->p, a->scale);
+    pp.a.q = a->q;
+    pp.a.q_st = a->q_stride_t;
+    pp.a.q_sh = a->q_stride_h;
+    pp.a.k = a->k;
+    pp.a.k_st = a->k_stride_t;
+    pp.a.k_sh = a->k_stride_h;
+    pp.a.w = a->w;
+    pp.a.cu = a->cu_seqlens;
+    pp.a.lmk = a->lmk_idx;
+    pp.a.lbias = a->lmk_bias;
+    pp.a.lse_out = (float*)a->lse;
+    pp.seq = a->seq;
+    pp.out_rows = a->rows;
+    pp.w_cap = a->w_cap;
+    pp.p_win = a->p_win;
+    pp.p_lmk = a->p.k_lmk > 0 ? a->p_lmk : nullptr;
+    return hip_status(dsalt::probs_launch(pp, (hipStream_t)stream), "dsalt_export_probs");
 }
 
 int dsalt_silu_mul(const dsalt_silu_mul_args* a, dsalt_stream_t stream) {

@@ -22,8 +22,12 @@ continuous windows ``w~ = n_min + sigmoid(win_gate(x)) (n_max - n_min)`` (gradie
 ``alpha_w``, ``x`` and ``v_proj``) -- feed the training attention kernels.  Global landmark
 sets only, as in the reference.
 
-Not provided here: the dense ``_last_P`` rebuild for the metrics (``:636-702``), which stays
-``None``.
+Analysis export (:636-702): with ``_collect_last_P`` set (off by default: it costs a kernel
+and O(L (w + k)) memory per layer), eval-mode inference stores the first sequence's
+attention probabilities as ``_last_P_sparse`` (``kernels.attention_probs``: window band +
+landmark slots, the probabilities the forward used) and, for sequences up to
+``last_P_dense_max`` tokens, the dense ``[H, L, L]`` matrix as ``_last_P`` for callers that
+index it like the reference's.
 """
 from __future__ import annotations
 
@@ -74,6 +78,8 @@ class DSALTAttention(nn.Module):
         self._last_P = None
         self._collect_last_P = False
         self._qkv_cache = None
+        self._last_P_sparse = None
+        self.last_P_dense_max = 4096
         cos, sin = build_rope_cache(max_seq_len, self.head_dim, torch.device("cpu"), base=rope_base, scale=yarn_scale)
         self.register_buffer("rope_cos", cos, persistent=False)
         self.register_buffer("rope_sin", sin, persistent=False)
@@ -187,10 +193,26 @@ class DSALTAttention(nn.Module):
                                               block_size=self.block_size, stats_scope=self.stats_scope)
         idx = lmk.to(torch.int32) if lmk.dim() == 4 else lmk.to(torch.int32).unsqueeze(2)
         mode = ops.SELECT_BLOCK if self.select_mode == "block" else ops.SELECT_GLOBAL
-        out, _ = ops.attention_forward(q, k, v, w.to(torch.int32), cu_seqlens, idx, None, max_seqlen=maxlen,
-                                       select_mode=mode, block_size=self.block_size)
-        self._last_P = None
+        w32 = w.to(torch.int32)
+        out, lse = ops.attention_forward(q, k, v, w32, cu_seqlens, idx, None, max_seqlen=maxlen, select_mode=mode,
+                                         block_size=self.block_size)
+        self._last_P = self._last_P_sparse = None
+        if self._collect_last_P:
+            self._export_last_P(q, k, w32, cu_seqlens, idx, lse, maxlen, mode, cu_list)
         return self._apply_out_proj(out.view(total_len, self.d_model)), self._aux_zero(x.device, x.dtype)
+
+    def _export_last_P(self, q, k, w32, cu_seqlens, idx, lse, maxlen, mode, cu_list):
+        """Attention probabilities of the first sequence (sparse; dense when short)."""
+        from ..kernels.attention_probs import SparseAttentionProbs
+        cu_h = list(cu_list) if cu_list is not None else cu_seqlens.detach().to("cpu").tolist()
+        n0 = cu_h[1] - cu_h[0]
+        p_win, p_lmk = ops.export_probs(q, k, w32, cu_seqlens, idx, lse, seq=0, rows=n0,
+                                        w_cap=max(1, min(n0, self.n_max + 1)), max_seqlen=maxlen, select_mode=mode,
+                                        block_size=self.block_size)
+        sp = SparseAttentionProbs(p_win, p_lmk, idx[:, 0].long(), self.block_size if mode == ops.SELECT_BLOCK else 0)
+        self._last_P_sparse = sp
+        if n0 <= self.last_P_dense_max:
+            self._last_P = sp.to_dense()
 
     def _packed(self, x, cu_seqlens, total_len, device, rope_cs=None, cu_list=None):
         if not self.training and not torch.is_grad_enabled():

@@ -13,7 +13,8 @@ import torch
 
 from . import _lib
 from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, SELECT_BLOCK, SELECT_GLOBAL, STATS_PACKED,
-                   STATS_SEQUENCE, BwdArgs, FwdArgs, GatherArgs, Problem, RopeArgs, SelectArgs, SiluMulArgs, TrainBwdArgs,
+                   STATS_SEQUENCE, BwdArgs, FwdArgs, GatherArgs, Problem, ProbsArgs, RopeArgs, SelectArgs, SiluMulArgs,
+                   TrainBwdArgs,
                    TrainFwdArgs)
 
 _DT = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
@@ -400,6 +401,50 @@ def rope_qk_(q, k, cu_seqlens, cos, sin, *, max_seqlen=None):
     L = _lib.load()
     _lib.check("dsalt_rope_qk", L.dsalt_rope_qk(ctypes.byref(a), _stream(dev)))
     return q, k
+
+
+def export_probs(q, k, w, cu_seqlens, lmk_idx, lse, lmk_bias=None, *, seq=0, rows=None, w_cap=None, scale=None,
+                 max_seqlen=None, select_mode=SELECT_GLOBAL, block_size=512, want_lmk=True):
+    """(p_win [H, rows, w_cap], p_lmk [H, rows, K] or None), fp32: the probabilities the
+    forward used for sequence ``seq`` (``lse`` from attention_forward on the same inputs),
+    window keys as p_win[h, i, c] = P(i, i - c), landmark slots as p_lmk[h, i, slot]."""
+    dev = _gpu(q, k, w, cu_seqlens, lmk_idx, lse, lmk_bias)
+    q, k = _rows3(q, "q"), _rows3(k, "k")
+    T, H, D = q.shape
+    S = cu_seqlens.shape[0] - 1
+    maxlen = max_seqlen if max_seqlen is not None else _max_seqlen(cu_seqlens)
+    if rows is None or w_cap is None:
+        cu_h = cu_seqlens.detach().to("cpu").tolist()
+        n = cu_h[seq + 1] - cu_h[seq]
+        rows = n if rows is None else rows
+        if w_cap is None:
+            w_cap = int(w[cu_h[seq]:cu_h[seq + 1]].max().item()) if n else 1
+            w_cap = max(1, min(w_cap, n))
+    K = lmk_idx.shape[-1]
+    if lmk_idx.dim() != 4 or lmk_idx.shape[:2] != (H, S) or lmk_idx.shape[2] != n_sets(select_mode, maxlen, block_size):
+        raise ValueError(f"lmk_idx must be [H, S, n_sets, K], got {tuple(lmk_idx.shape)}")
+    w_c = w.detach().to(torch.int32).contiguous()
+    cu_c = cu_seqlens.detach().to(torch.int32).contiguous()
+    li = lmk_idx.to(torch.int32).contiguous()
+    lb = lmk_bias.detach().to(torch.float32).contiguous() if lmk_bias is not None else None
+    lse_c = lse.detach().to(torch.float32).contiguous()
+    p_win = torch.zeros((H, rows, w_cap), dtype=torch.float32, device=dev)
+    p_lmk = torch.zeros((H, rows, K), dtype=torch.float32, device=dev) if want_lmk and K else None
+    a = ProbsArgs()
+    a.p = _problem(T, S, maxlen, H, k.shape[1], D, K, select_mode, block_size, dtype_code(q.dtype))
+    a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
+    a.w, a.cu_seqlens = w_c.data_ptr(), cu_c.data_ptr()
+    a.lmk_idx = li.data_ptr() if li.numel() else None
+    a.lmk_bias = lb.data_ptr() if lb is not None and lb.numel() else None
+    a.lse = lse_c.data_ptr()
+    a.scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    a.seq, a.rows, a.w_cap = seq, rows, w_cap
+    a.p_win = p_win.data_ptr()
+    a.p_lmk = p_lmk.data_ptr() if p_lmk is not None else None
+    L = _lib.load()
+    _lib.check("dsalt_export_probs", L.dsalt_export_probs(ctypes.byref(a), _stream(dev)))
+    return p_win, p_lmk
 
 
 def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:

@@ -210,6 +210,33 @@ typedef struct dsalt_rope_args {
 
 int    dsalt_rope_qk(const dsalt_rope_args* a, dsalt_stream_t stream);
 
+/* Attention probabilities of one sequence over the keys each row attends, in banded
+ * form (O(L (w + k)) memory).  Replaces the dense [H, L, L] rebuild of _last_P for the
+ * analysis metrics, dsalt/modules/dsalt_attention.py:636-702 (consumer
+ * dsalt/training/trainer.py:88-135): p_win[h][i][c] = P(i, i - c) for window keys
+ * c < min(w_i, i + 1) and 0 up to w_cap; p_lmk[h][i][slot] = P(i, landmark of the slot)
+ * when the row sees it, else 0.  P = exp(scale * q_i . k_j + bias - lse_i) with the LSE
+ * the forward returned, i.e. the probabilities the forward used (rows of the dense
+ * matrix are the two parts scattered to their key columns).  Needs no workspace. */
+typedef struct dsalt_probs_args {
+    dsalt_problem p;
+    const void* q;  int64_t q_stride_t; int64_t q_stride_h;
+    const void* k;  int64_t k_stride_t; int64_t k_stride_h;
+    const int32_t* w;
+    const int32_t* cu_seqlens;
+    const int32_t* lmk_idx;
+    const float* lmk_bias;     /* or NULL                                           */
+    const float* lse;          /* [T, n_heads] as returned by dsalt_fwd              */
+    float scale;
+    int32_t seq;               /* the exported sequence                             */
+    int32_t rows;              /* rows of the outputs (its length)                  */
+    int32_t w_cap;             /* columns of p_win, >= the largest window of its rows */
+    float* p_win;              /* [n_heads, rows, w_cap]                             */
+    float* p_lmk;              /* [n_heads, rows, k_lmk] or NULL                     */
+} dsalt_probs_args;
+
+int    dsalt_export_probs(const dsalt_probs_args* a, dsalt_stream_t stream);
+
 /* Gated activation of the SwiGLU feed-forward block, out = silu(gate) * up, where
  * gate and up may be column ranges of one fused gate/up GEMM output.  Replaces
  * F.silu(gate_proj(x)) * up_proj(x) of SwiGLUFFN.forward,

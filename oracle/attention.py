@@ -29,6 +29,7 @@ import numpy as np
 
 __all__ = [
     "attention_fwd",
+    "attention_probs",
     "attention_bwd",
     "dense_mask_kernel",
     "dense_attention",
@@ -111,6 +112,35 @@ def attention_fwd(q, k, v, w, cu, lmk_idx, scale, lmk_bias=None, block_size=None
                 out[st + i0:st + i1, h] = o / l[:, None]
                 lse[st + i0:st + i1, h] = m + np.log(l)
     return out, lse
+
+
+def attention_probs(q, k, w, cu, lmk_idx, scale, seq=0, lmk_bias=None, block_size=None):
+    """Dense [H, L, L] float64 attention probabilities of sequence ``seq`` (the matrix the
+    reference rebuilds as ``_last_P``, dsalt/modules/dsalt_attention.py:636-702, here with
+    the kernel semantics above: window band and the landmarks left of it)."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    T, H, D = q.shape
+    rep = H // k.shape[1]
+    st, L = int(cu[seq]), int(cu[seq + 1] - cu[seq])
+    P = np.zeros((H, L, L))
+    for h in range(H):
+        qh, kh = q[:, h], k[:, h // rep]
+        for i0, i1 in _row_blocks(L, block_size):
+            b = _set_of_row(i0, block_size)
+            pos = lmk_idx[h, seq, b].astype(np.int64)
+            pos = np.where(pos < L, pos, -1)
+            bias = None if lmk_bias is None else lmk_bias[h, seq, b].astype(np.float64)
+            kr0, sb, sl, _, _ = _block_logits(qh, kh, w, st, i0, i1, pos, bias, scale)
+            m = np.maximum(sb.max(1), sl.max(1) if sl.shape[1] else -np.inf)
+            pb = np.exp(sb - m[:, None])
+            pl = np.exp(sl - m[:, None])
+            l = (pb.sum(1) + pl.sum(1))[:, None]
+            P[h, i0:i1, kr0:i1] = pb / l
+            for slot, p in enumerate(pos.tolist()):
+                if p >= 0:
+                    P[h, i0:i1, p] += pl[:, slot] / l[:, 0]
+    return P
 
 
 def attention_bwd(q, k, v, w, cu, lmk_idx, scale, dout, lmk_bias=None, block_size=None, out=None):

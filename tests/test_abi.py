@@ -50,6 +50,7 @@ STRUCTS = {
     "dsalt_train_bwd_args": _lib.TrainBwdArgs,
     "dsalt_rope_args": _lib.RopeArgs,
     "dsalt_silu_mul_args": _lib.SiluMulArgs,
+    "dsalt_probs_args": _lib.ProbsArgs,
 }
 
 
@@ -207,3 +208,18 @@ def test_silu_mul_validation(field, value):
     a = _lib.SiluMulArgs(64, 32, 1, 1 << 20, 64, (1 << 20) + 64, 64, 1 << 21, 32)
     setattr(a, field, value)
     assert lib.dsalt_silu_mul(ctypes.byref(a), None) == 1
+
+
+@pytest.mark.parametrize("field,value", [("seq", 1), ("seq", -1), ("rows", 129), ("w_cap", 0), ("p_win", None),
+                                         ("lse", None), ("scale", 0.0)])
+def test_export_probs_validation(field, value):
+    lib = _lib.load()
+    a = _lib.ProbsArgs()
+    a.p = _lib.Problem(128, 1, 128, 2, 2, 64, 8, 0, 0, _lib.DTYPE_BF16)
+    fake = 1 << 20
+    a.q = a.k = a.w = a.cu_seqlens = a.lmk_idx = a.lse = a.p_win = a.p_lmk = fake
+    a.q_stride_t = a.k_stride_t = 128
+    a.q_stride_h = a.k_stride_h = 64
+    a.scale, a.seq, a.rows, a.w_cap = 0.125, 0, 128, 64
+    setattr(a, field, value)
+    assert lib.dsalt_export_probs(ctypes.byref(a), None) == 1

@@ -13,6 +13,8 @@ Parity status of each oracle function (how it is pinned):
                                  causal-SDPA and O=V special cases + no-double-count
   attention.attention_bwd        central finite differences + torch autograd of the dense form
   attention.literal_mask         golden (reference _build_mask_packed + masked SDPA)
+  attention.attention_probs      P @ V reproduces attention_fwd's output for random V; rows sum
+                                 to 1; zero off the dense kernel mask
   train.train_bias / train_fwd   golden (reference _dense_logbias_from_kernel + SDPA, float64)
                                  + win_edge 0 reduces to attention_fwd with window floor(w~)+1
   rope.rope                      torch's evaluation of the reference expression (CPU, bf16/fp16/fp32)
@@ -441,3 +443,21 @@ def test_rope_matches_reference_expression(dt, name):
         n0 = x[..., :32] ** 2 + x[..., 32:] ** 2
         n1 = torch.tensor(got[..., :32] ** 2 + got[..., 32:] ** 2)
         assert torch.allclose(n0, n1, rtol=1e-5)
+
+
+@pytest.mark.parametrize("block", [None, 16])
+def test_attention_probs_reproduce_forward(block):
+    q, k, v, w, cu, idx = _attn_case(41, lens=(40, 27), H=2, G=1, K=5)
+    if block:
+        idx = np.repeat(idx, 3, axis=2)
+        idx[:, :, 0] = -1  # the first block sees no landmark
+    bias = np.random.default_rng(42).standard_normal(idx.shape)
+    o, _ = OA.attention_fwd(q, k, v, w, cu, idx, 0.37, lmk_bias=bias, block_size=block)
+    m = OA.dense_mask_kernel(w, cu, idx, block_size=block)
+    for s in range(2):
+        st, en = cu[s], cu[s + 1]
+        P = OA.attention_probs(q, k, w, cu, idx, 0.37, seq=s, lmk_bias=bias, block_size=block)
+        np.testing.assert_allclose(P.sum(-1), 1.0, atol=1e-12)
+        assert np.all(P[~m[:, st:en, st:en]] == 0)
+        got = np.einsum("hij,jhd->ihd", P, v[st:en, :1].repeat(2, axis=1))
+        np.testing.assert_allclose(got, o[st:en], atol=1e-12)
