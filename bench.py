@@ -51,14 +51,14 @@ def parse():
 
 LABELS = ("sel_norms", "sel_sums", "sel_stats", "sel_z", "sel_scores", "sel_part", "sel_merge", "sel_topk", "gather",
           "row_plan", "attn_fwd", "bwd_init", "bwd_dq", "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum", "train_windows", "train_dw",
-          "rope", "silu_mul", "probs")
+          "rope", "silu_mul", "probs", "ce_rows")
 
 
 def short_kernel_name(name: str) -> str:
     """Label of a library kernel (the one dsalt_timing_report uses) from a profiler kernel name."""
     import re
     m = re.search(r"(sel_norms|sel_sums|sel_stats|sel_z|sel_scores|sel_part|sel_merge|sel_topk|gather|row_plan|fwd|bwd_init|bwd_dq|"
-                  r"bwd_dkdv|bwd_lmk_sum|train_windows|train_dw|rope|silu_mul|probs|"
+                  r"bwd_dkdv|bwd_lmk_sum|train_windows|train_dw|rope|silu_mul|probs|ce|"
                   r"bwd_lmk)_kernel", name)
     if not m:
         return name
@@ -183,6 +183,80 @@ def probs_bench(args, wl):
                        "k_lmk": wl.k_lmk, "dense_bytes_avoided": H * L * L * 4},
             "roofline": {"bound": "hbm", "kernel": "probs", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "algorithmic_bytes": alg},
+            "cpu_baseline": None,
+            "kernels": {k: {kk: round(vv, 5) if isinstance(vv, float) else vv for kk, vv in v.items()}
+                        for k, v in kernels.items()}}
+    print(json.dumps(line), flush=True)
+
+
+def ce_bench(args):
+    """LM-head loss of the Qwen2.5-3B shape: hidden states [32768, 2048] bf16, vocabulary
+    151936, tied weight; a step is loss + gradients (input and weight) by the fused linear
+    cross-entropy.  The reference's default path (torch logits per 2048-row chunk +
+    F.cross_entropy, autograd backward) is timed beside it on the same GPU."""
+    import ctypes
+
+    import torch
+
+    from dsalt_amd import _lib
+    from dsalt_amd.kernels.cross_entropy import LigerFusedLinearCrossEntropyFunction
+    from dsalt_amd.model.dsalt_lm import _chunked_cross_entropy
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    BT, H, V = 32768, 2048, 151936
+    g = torch.Generator(device="cpu").manual_seed(3000)
+    x = (torch.randn(BT, H, generator=g) * 0.5).to(torch.bfloat16).to(dev).requires_grad_(True)
+    w = (torch.randn(V, H, generator=g) * 0.02).to(torch.bfloat16).to(dev).requires_grad_(True)
+    t = torch.randint(0, V, (BT,), generator=g).to(dev)
+
+    def fused():
+        x.grad = w.grad = None
+        LigerFusedLinearCrossEntropyFunction.apply(x, w, t)[0].backward()
+
+    def chunked():
+        x.grad = w.grad = None
+        _chunked_cross_entropy(x, w, t, 2048).backward()
+
+    def timed(fn, n):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n
+
+    t_fused = timed(fused, args.steps)
+    t_ref = timed(chunked, max(1, args.steps // 2))
+    lib.dsalt_timing_enable(1)
+    for _ in range(args.steps):
+        fused()
+    torch.cuda.synchronize()
+    buf = ctypes.create_string_buffer(1 << 14)
+    lib.dsalt_timing_report(buf, len(buf))
+    lib.dsalt_timing_enable(0)
+    kernels = {}
+    for line in buf.value.decode().splitlines():
+        name, n, tot = line.split()
+        kernels[name] = dict(launches=int(n), avg_ms=float(tot) / int(n), ms_per_step=float(tot) / args.steps)
+    ce = kernels["ce_rows"]
+    rows_per_launch = BT / (ce["launches"] / args.steps)
+    alg = rows_per_launch * V * 2 * 2 + rows_per_launch * 16  # logits read, gradient written, targets/loss
+    ach = alg / (ce["avg_ms"] * 1e-3) / 1e9
+    flops = 6.0 * BT * H * V
+    line = {"metric": "fused linear cross-entropy tokens/sec (loss + input and weight gradients), V=151936 bf16",
+            "value": round(BT / t_fused, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(t_fused * 1e3, 3), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "ce_qwen3b_l32768", "rows": BT, "hidden": H, "vocab": V},
+            "roofline": {"bound": "hbm", "kernel": "ce_rows", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "algorithmic_bytes": alg},
+            "step_roofline": {"bound": "mfma", "flops": flops, "t_roof_ms": round(flops / 2.5e15 * 1e3, 3),
+                              "frac": round(flops / 2.5e15 / t_fused, 4)},
+            "torch_chunked_same_gpu": {"ms_per_step": round(t_ref * 1e3, 3), "tokens_per_s": round(BT / t_ref, 1)},
             "cpu_baseline": None,
             "kernels": {k: {kk: round(vv, 5) if isinstance(vv, float) else vv for kk, vv in v.items()}
                         for k, v in kernels.items()}}
@@ -318,6 +392,8 @@ def main():
 
     if args.workload in MODEL_WORKLOADS:
         return model_bench(args, MODEL_WORKLOADS[args.workload])
+    if args.workload == "ce_qwen3b_l32768":
+        return ce_bench(args)
     if args.workload.startswith("probs_"):
         return probs_bench(args, WORKLOADS[args.workload[len("probs_"):]])
     wl = WORKLOADS[args.workload]

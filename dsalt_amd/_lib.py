@@ -91,6 +91,14 @@ class ProbsArgs(ctypes.Structure):
                 ("scale", _f32), ("seq", _i32), ("rows", _i32), ("w_cap", _i32), ("p_win", _vp), ("p_lmk", _vp)]
 
 
+class CeArgs(ctypes.Structure):
+    _fields_ = [("rows", _i32), ("n_cols", _i32), ("dtype", _i32), ("logits", _vp), ("logits_stride", _i64),
+                ("target", _vp), ("ce_weight", _vp), ("loss", _vp), ("z_loss", _vp), ("accuracy", _vp),
+                ("predicted", _vp), ("ignore_index", _i64), ("n_non_ignore", _f32), ("sum_non_ignore_weight", _f32),
+                ("weight_sum", _f32), ("lse_square_scale", _f32), ("label_smoothing", _f32), ("softcap", _f32),
+                ("reduction", _i32), ("want_grad", _i32), ("token_scaling", _i32)]
+
+
 class SiluMulArgs(ctypes.Structure):
     _fields_ = [("rows", _i32), ("cols", _i32), ("dtype", _i32), ("gate", _vp), ("gate_stride", _i64),
                 ("up", _vp), ("up_stride", _i64), ("out", _vp), ("out_stride", _i64)]
@@ -123,6 +131,7 @@ SIGNATURES = {
     "dsalt_rope_qk": ([ctypes.POINTER(RopeArgs), _vp], ctypes.c_int),
     "dsalt_silu_mul": ([ctypes.POINTER(SiluMulArgs), _vp], ctypes.c_int),
     "dsalt_export_probs": ([ctypes.POINTER(ProbsArgs), _vp], ctypes.c_int),
+    "dsalt_cross_entropy_rows": ([ctypes.POINTER(CeArgs), _vp], ctypes.c_int),
     "dsalt_timing_enable": ([ctypes.c_int], ctypes.c_int),
     "dsalt_timing_report": ([ctypes.c_char_p, _sz], ctypes.c_int),
 }

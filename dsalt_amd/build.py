@@ -28,6 +28,7 @@ SOURCES = {
     # products rounded to the tensor type one operation at a time, as the torch expression
     "ffn.hip": ["-ffp-contract=off"],
     "probs.hip": [],
+    "ce.hip": [],
     "capi.hip": [],
     "timing.hip": [],
 }

@@ -6,6 +6,7 @@
 #include <string>
 
 #include "attn.h"
+#include "ce.h"
 #include "ffn.h"
 #include "probs.h"
 #include "rope.h"
@@ -434,6 +435,46 @@ int dsalt_export_probs(const dsalt_probs_args* a, dsalt_stream_t stream) {
     pp.p_win = a->p_win;
     pp.p_lmk = a->p.k_lmk > 0 ? a->p_lmk : nullptr;
     return hip_status(dsalt::probs_launch(pp, (hipStream_t)stream), "dsalt_export_probs");
+}
+
+int dsalt_cross_entropy_rows(const dsalt_ce_args* a, dsalt_stream_t stream) {
+    if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
+    if (a->rows < 0 || a->n_cols < 8 || a->n_cols % 8)
+        return fail(DSALT_ERR_INVALID, "rows >= 0 and n_cols a positive multiple of 8 required (got %d, %d)", a->rows,
+                    a->n_cols);
+    if (a->dtype < 0 || a->dtype > 2) return fail(DSALT_ERR_INVALID, "unknown dtype %d", a->dtype);
+    if (a->reduction < 0 || a->reduction > 2) return fail(DSALT_ERR_INVALID, "reduction must be 0, 1 or 2");
+    if (a->rows == 0) return DSALT_OK;
+    if (!a->logits || !aligned16(a->logits) || a->logits_stride < a->n_cols ||
+        (a->logits_stride * (int64_t)esize(a->dtype)) % 16)
+        return fail(DSALT_ERR_INVALID, "logits need 16-byte aligned rows of at least n_cols elements");
+    if (!a->target || !a->loss) return fail(DSALT_ERR_INVALID, "target and loss are required");
+    if (!(a->label_smoothing >= 0.f && a->label_smoothing <= 1.f))
+        return fail(DSALT_ERR_INVALID, "label_smoothing must be in [0, 1]");
+    if (!(a->softcap >= 0.f)) return fail(DSALT_ERR_INVALID, "softcap must be >= 0 (0: none)");
+    dsalt::CeParams p;
+    p.rows = a->rows;
+    p.n_cols = a->n_cols;
+    p.dtype = a->dtype;
+    p.x = a->logits;
+    p.x_st = a->logits_stride;
+    p.target = a->target;
+    p.ce_weight = a->ce_weight;
+    p.loss = a->loss;
+    p.z_loss = a->z_loss;
+    p.accuracy = a->accuracy;
+    p.predicted = a->predicted;
+    p.ignore_index = a->ignore_index;
+    p.n_non_ignore = a->n_non_ignore;
+    p.sum_non_ignore_weight = a->sum_non_ignore_weight;
+    p.weight_sum = a->weight_sum;
+    p.lse_square_scale = a->lse_square_scale;
+    p.label_smoothing = a->label_smoothing;
+    p.softcap = a->softcap;
+    p.reduction = a->reduction;
+    p.grads = a->want_grad;
+    p.token_scaling = a->token_scaling;
+    return hip_status(dsalt::ce_launch(p, (hipStream_t)stream), "dsalt_cross_entropy_rows");
 }
 
 int dsalt_silu_mul(const dsalt_silu_mul_args* a, dsalt_stream_t stream) {

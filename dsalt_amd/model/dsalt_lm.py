@@ -3,7 +3,7 @@
 Mirrors ``DSALTLMHeadModel`` of ``dsalt/model/dsalt_lm.py:64-284``: token embedding, a stack
 of ``DSALTTransformerBlock``, final RMSNorm and an LM head (tied to the embedding by
 default); packed input (``cu_seqlens``) or batched ``[B, T]``; with ``labels`` the loss
-(chunked cross-entropy, :19-39), without them the logits of every position (:280).
+(chunked cross-entropy, :19-39, or the fused linear cross-entropy), without them the logits of every position (:280).
 Initialisation as :164-172.  Per forward the RoPE rows are gathered once for all layers
 and ``cu_seqlens`` is copied to the host once (:220-235).
 """
@@ -77,11 +77,16 @@ class DSALTLMHeadModel(nn.Module):
                     nn.init.zeros_(module.bias)
 
     def _compute_loss(self, x, labels):
-        if self.loss_fn == "liger":
-            raise RuntimeError("loss_fn='liger' (fused linear cross-entropy) is not available in this build; "
-                               "use loss_fn='chunked'")
-        return _chunked_cross_entropy(x.view(-1, self.d_model), self.lm_head.weight, labels.view(-1).long(),
-                                      self.lm_head_chunk_size)
+        """"chunked": torch logits per row chunk + F.cross_entropy (:19-39); "liger" and "auto":
+        the fused linear cross-entropy (HIP row kernel between the chunk GEMMs, :42-51; the
+        reference's "auto" measures both once, here the fused path is taken)."""
+        flat_x = x.view(-1, self.d_model)
+        flat_labels = labels.view(-1).long()
+        if self.loss_fn in ("liger", "auto"):
+            from ..kernels.cross_entropy import LigerFusedLinearCrossEntropyFunction
+            return LigerFusedLinearCrossEntropyFunction.apply(flat_x.contiguous(), self.lm_head.weight,
+                                                              flat_labels.contiguous())[0]
+        return _chunked_cross_entropy(flat_x, self.lm_head.weight, flat_labels, self.lm_head_chunk_size)
 
     @staticmethod
     def _to_autocast_dtype(x):

@@ -13,7 +13,8 @@ import torch
 
 from . import _lib
 from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, SELECT_BLOCK, SELECT_GLOBAL, STATS_PACKED,
-                   STATS_SEQUENCE, BwdArgs, FwdArgs, GatherArgs, Problem, ProbsArgs, RopeArgs, SelectArgs, SiluMulArgs,
+                   STATS_SEQUENCE, BwdArgs, CeArgs, FwdArgs, GatherArgs, Problem, ProbsArgs, RopeArgs, SelectArgs,
+                   SiluMulArgs,
                    TrainBwdArgs,
                    TrainFwdArgs)
 
@@ -445,6 +446,55 @@ def export_probs(q, k, w, cu_seqlens, lmk_idx, lse, lmk_bias=None, *, seq=0, row
     L = _lib.load()
     _lib.check("dsalt_export_probs", L.dsalt_export_probs(ctypes.byref(a), _stream(dev)))
     return p_win, p_lmk
+
+
+_REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
+
+
+def cross_entropy_rows(logits, target, *, ce_weight=None, ignore_index=-100, n_non_ignore=None,
+                       sum_non_ignore_weight=None, weight_sum=None, lse_square_scale=0.0, label_smoothing=0.0,
+                       softcap=None, reduction="mean", want_grad=True, token_scaling=False, want_z=False,
+                       want_accuracy=False, want_predicted=False):
+    """Row losses of ``logits`` [rows, V] against ``target`` [rows] (int64), and with
+    ``want_grad`` the gradient wrt the logits written over them.  The batch totals of the
+    "mean" reduction default to this call's rows.  Returns (loss [rows] fp32, z [rows] in the
+    logits' type or None, accuracy [rows] or None, predicted [rows] int64 or None)."""
+    dev = _gpu(logits, target, ce_weight)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [rows, V] with unit column stride")
+    rows, V = logits.shape
+    tgt = target.detach().to(torch.int64).contiguous()
+    cw = ce_weight.detach().to(torch.float32).contiguous() if ce_weight is not None else None
+    keep = tgt != ignore_index
+    if n_non_ignore is None:
+        n_non_ignore = float(keep.sum().item())
+    if sum_non_ignore_weight is None:
+        sum_non_ignore_weight = float(cw[tgt[keep]].sum().item()) if cw is not None else n_non_ignore
+    if weight_sum is None:
+        weight_sum = float(cw.sum().item()) if cw is not None else 0.0
+    loss = torch.empty(rows, dtype=torch.float32, device=dev)
+    z = torch.empty(rows, dtype=logits.dtype, device=dev) if want_z else None
+    acc = torch.empty(rows, dtype=torch.float32, device=dev) if want_accuracy else None
+    pred = torch.empty(rows, dtype=torch.int64, device=dev) if want_predicted else None
+    a = CeArgs()
+    a.rows, a.n_cols, a.dtype = rows, V, dtype_code(logits.dtype)
+    a.logits, a.logits_stride = logits.data_ptr(), logits.stride(0)
+    a.target = tgt.data_ptr()
+    a.ce_weight = cw.data_ptr() if cw is not None else None
+    a.loss = loss.data_ptr()
+    a.z_loss = z.data_ptr() if z is not None else None
+    a.accuracy = acc.data_ptr() if acc is not None else None
+    a.predicted = pred.data_ptr() if pred is not None else None
+    a.ignore_index = int(ignore_index)
+    a.n_non_ignore, a.sum_non_ignore_weight, a.weight_sum = n_non_ignore, sum_non_ignore_weight, weight_sum
+    a.lse_square_scale, a.label_smoothing = float(lse_square_scale), float(label_smoothing)
+    a.softcap = float(softcap) if softcap is not None else 0.0
+    if reduction not in _REDUCTIONS:
+        raise ValueError(f"reduction must be one of {list(_REDUCTIONS)}")
+    a.reduction, a.want_grad, a.token_scaling = _REDUCTIONS[reduction], int(want_grad), int(token_scaling)
+    L = _lib.load()
+    _lib.check("dsalt_cross_entropy_rows", L.dsalt_cross_entropy_rows(ctypes.byref(a), _stream(dev)))
+    return loss, z, acc, pred
 
 
 def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:

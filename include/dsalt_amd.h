@@ -237,6 +237,41 @@ typedef struct dsalt_probs_args {
 
 int    dsalt_export_probs(const dsalt_probs_args* a, dsalt_stream_t stream);
 
+/* Row cross-entropy of the fused linear cross-entropy: for each row of a chunk of logits
+ * (x W^T of the LM head), the loss and, in place over the logits, the gradient of the
+ * loss with respect to them.  Replaces liger_cross_entropy_kernel,
+ * dsalt/kernels/cross_entropy.py:133-310 (ignore_index, class weights, label smoothing,
+ * z-loss lse_square_scale * lse^2, softcap, reductions none/mean/sum, token accuracy and
+ * predicted tokens), plus the token scaling of its driver (:420-446): every output of a
+ * row times the row's probability of its target.  n_non_ignore / sum_non_ignore_weight /
+ * weight_sum are the batch totals the "mean" reduction divides by.  Targets must be
+ * ignore_index or in [0, n_cols); n_cols a multiple of 8; rows 16-byte aligned.  The
+ * GEMMs around it (logits, grad_input, grad_weight) are the caller's. */
+typedef struct dsalt_ce_args {
+    int32_t rows;
+    int32_t n_cols;            /* vocabulary size V                                  */
+    int32_t dtype;             /* DSALT_DTYPE_* of the logits                        */
+    void* logits; int64_t logits_stride;   /* [rows, V]; gradient written in place    */
+    const int64_t* target;     /* [rows]                                             */
+    const float* ce_weight;    /* [V] class weights or NULL                          */
+    float* loss;               /* [rows] per-row loss (z-loss included)              */
+    void* z_loss;              /* [rows] in the logits' type, or NULL                */
+    float* accuracy;           /* [rows] 1 when the argmax is the target, or NULL    */
+    int64_t* predicted;        /* [rows] argmax (first index), -1 for ignored rows   */
+    int64_t ignore_index;
+    float n_non_ignore;
+    float sum_non_ignore_weight;
+    float weight_sum;
+    float lse_square_scale;
+    float label_smoothing;
+    float softcap;             /* 0: none                                            */
+    int32_t reduction;         /* 0 none, 1 mean, 2 sum                              */
+    int32_t want_grad;         /* write the gradient over the logits                 */
+    int32_t token_scaling;
+} dsalt_ce_args;
+
+int    dsalt_cross_entropy_rows(const dsalt_ce_args* a, dsalt_stream_t stream);
+
 /* Gated activation of the SwiGLU feed-forward block, out = silu(gate) * up, where
  * gate and up may be column ranges of one fused gate/up GEMM output.  Replaces
  * F.silu(gate_proj(x)) * up_proj(x) of SwiGLUFFN.forward,

@@ -51,6 +51,7 @@ STRUCTS = {
     "dsalt_rope_args": _lib.RopeArgs,
     "dsalt_silu_mul_args": _lib.SiluMulArgs,
     "dsalt_probs_args": _lib.ProbsArgs,
+    "dsalt_ce_args": _lib.CeArgs,
 }
 
 
@@ -223,3 +224,16 @@ def test_export_probs_validation(field, value):
     a.scale, a.seq, a.rows, a.w_cap = 0.125, 0, 128, 64
     setattr(a, field, value)
     assert lib.dsalt_export_probs(ctypes.byref(a), None) == 1
+
+
+@pytest.mark.parametrize("field,value", [("n_cols", 100), ("dtype", 4), ("reduction", 3), ("logits", (1 << 20) + 8),
+                                         ("logits_stride", 64), ("target", None), ("label_smoothing", 1.5),
+                                         ("softcap", -1.0)])
+def test_cross_entropy_validation(field, value):
+    lib = _lib.load()
+    a = _lib.CeArgs()
+    a.rows, a.n_cols, a.dtype, a.logits, a.logits_stride = 16, 128, 1, 1 << 20, 128
+    a.target = a.loss = 1 << 21
+    a.ignore_index, a.n_non_ignore, a.reduction, a.want_grad = -100, 16.0, 1, 1
+    setattr(a, field, value)
+    assert lib.dsalt_cross_entropy_rows(ctypes.byref(a), None) == 1

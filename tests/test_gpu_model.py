@@ -148,3 +148,91 @@ def test_silu_mul_on_fused_gate_up_matches_torch(dt):
     ref = torch.nn.functional.silu(gu[:, :F_].contiguous()) * gu[:, F_:].contiguous()
     torch.cuda.synchronize()
     assert torch.equal(out, ref), float((out.float() - ref.float()).abs().max())
+
+
+# ------------------------------------------------------------------ fused linear cross-entropy
+@pytest.mark.parametrize("opts", [dict(), dict(label_smoothing=0.1, lse_square_scale=1e-3), dict(softcap=20.0),
+                                  dict(ce_weight=True, label_smoothing=0.05, reduction="sum"),
+                                  dict(use_token_scaling=True), dict(reduction="none")])
+def test_row_kernel_matches_oracle(opts):
+    from oracle import cross_entropy as OCE
+    g = torch.Generator().manual_seed(90)
+    N, V = 96, 4000
+    x = torch.randn(N, V, generator=g) * 3
+    t = torch.randint(0, V, (N,), generator=g)
+    t[::6] = -100
+    opts = dict(opts)
+    cw = torch.rand(V, generator=g) + 0.2 if opts.pop("ce_weight", False) else None
+    red = opts.pop("reduction", "mean")
+    scaling = opts.pop("use_token_scaling", False)
+    zs, ls, cap = opts.get("lse_square_scale", 0.0), opts.get("label_smoothing", 0.0), opts.get("softcap")
+    logits = x.to(DEV)
+    loss, z, acc, pred = ops.cross_entropy_rows(logits, t.to(DEV), ce_weight=cw.to(DEV) if cw is not None else None,
+                                                reduction=red, token_scaling=scaling, lse_square_scale=zs,
+                                                label_smoothing=ls, softcap=cap, want_z=True, want_accuracy=True,
+                                                want_predicted=True)
+    torch.cuda.synchronize()
+    rl, rz, rg, am, _ = OCE.ce_rows(x.double().numpy(), t.numpy(), None if cw is None else cw.double().numpy(),
+                                    -100, zs, ls, red, cap, scaling)
+    assert rel_err(f64(loss), rl) < 1e-5
+    assert rel_err(f64(logits), rg) < 1e-5
+    if zs:
+        assert rel_err(f64(z), rz) < 1e-5
+    keep = (t != -100).numpy()
+    assert np.array_equal(pred.cpu().numpy()[keep], am[keep]) and np.all(pred.cpu().numpy()[~keep] == -1)
+    assert np.array_equal(acc.cpu().numpy(), (am == t.numpy()).astype(np.float32) * keep)
+
+
+def test_row_kernel_token_scaling_matches_oracle():
+    from oracle import cross_entropy as OCE
+    g = torch.Generator().manual_seed(91)
+    N, V = 64, 1024
+    x = torch.randn(N, V, generator=g)
+    t = torch.randint(0, V, (N,), generator=g)
+    logits = x.to(DEV)
+    loss, _, _, _ = ops.cross_entropy_rows(logits, t.to(DEV), token_scaling=True, label_smoothing=0.1)
+    rl, _, rg, _, _ = OCE.ce_rows(x.double().numpy(), t.numpy(), label_smoothing=0.1, use_token_scaling=True)
+    assert rel_err(f64(loss), rl) < 1e-5 and rel_err(f64(logits), rg) < 1e-5
+
+
+@pytest.mark.parametrize("dt,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_fused_linear_cross_entropy_matches_autograd(dt, tol):
+    from dsalt_amd.kernels.cross_entropy import LigerFusedLinearCrossEntropyFunction
+    g = torch.Generator().manual_seed(92)
+    BT, H, V = 700, 256, 5000
+    x = (torch.randn(BT, H, generator=g)).to(dt).to(DEV).requires_grad_(True)
+    w = (torch.randn(V, H, generator=g) * 0.05).to(dt).to(DEV).requires_grad_(True)
+    b = (torch.randn(V, generator=g) * 0.1).to(dt).to(DEV).requires_grad_(True)
+    t = torch.randint(0, V, (BT,), generator=g).to(DEV)
+    t[::9] = -100
+    loss, z, acc, _ = LigerFusedLinearCrossEntropyFunction.apply(x, w, t, b, None, -100, 1e-4, 0.1, "mean", None,
+                                                                 True, None, False, True, False)
+    (loss * 2.0).backward()
+    xr, wr, br = (a.detach().double().requires_grad_(True) for a in (x, w, b))
+    lg = xr @ wr.T + br
+    keep = t != -100
+    lr = torch.nn.functional.cross_entropy(lg, t, ignore_index=-100, label_smoothing=0.1)
+    lr = lr + 1e-4 * (torch.logsumexp(lg, -1) ** 2 * keep).sum() / keep.sum()
+    (lr * 2.0).backward()
+    assert abs(loss.item() - lr.item()) < tol * abs(lr.item())
+    for a, r in ((x.grad, xr.grad), (w.grad, wr.grad), (b.grad, br.grad)):
+        assert rel_err(f64(a), f64(r)) < tol
+    assert 0.0 <= float(acc) <= 1.0
+
+
+def test_model_fused_loss_matches_chunked():
+    m = _small_model("global").train()
+    T = 400
+    ids = torch.randint(0, 1000, (T,), device=DEV)
+    labels = torch.roll(ids, -1)
+    cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
+    m.loss_fn = "chunked"
+    l1 = m(ids, cu_seqlens=cu, labels=labels)["loss"]
+    l1.backward()
+    g1 = m.embed_tokens.weight.grad.clone()
+    m.zero_grad()
+    m.loss_fn = "liger"
+    l2 = m(ids, cu_seqlens=cu, labels=labels)["loss"]
+    l2.backward()
+    assert abs(float(l1) - float(l2)) < 1e-5 * abs(float(l1))
+    assert rel_err(f64(m.embed_tokens.weight.grad), f64(g1)) < 1e-4

@@ -17,6 +17,9 @@ Parity status of each oracle function (how it is pinned):
                                  to 1; zero off the dense kernel mask
   train.train_bias / train_fwd   golden (reference _dense_logbias_from_kernel + SDPA, float64)
                                  + win_edge 0 reduces to attention_fwd with window floor(w~)+1
+  cross_entropy.ce_rows          torch F.cross_entropy + autograd (ignore_index, class weights, label
+                                 smoothing, mean/sum/none), softcap and z-loss and token scaling
+                                 through torch autograd of their definitions
   rope.rope                      torch's evaluation of the reference expression (CPU, bf16/fp16/fp32)
                                  + rotation of 2-vectors preserves norms (fp32)
   train.train_bwd                golden (float64 autograd of the reference dense form)
@@ -32,6 +35,7 @@ import torch
 
 from oracle import attention as OA
 from oracle import select as OS
+from oracle import cross_entropy as OCE
 from oracle import rope as OR
 from oracle import train as OT
 from tests.helpers import load_golden, rel_err
@@ -461,3 +465,44 @@ def test_attention_probs_reproduce_forward(block):
         assert np.all(P[~m[:, st:en, st:en]] == 0)
         got = np.einsum("hij,jhd->ihd", P, v[st:en, :1].repeat(2, axis=1))
         np.testing.assert_allclose(got, o[st:en], atol=1e-12)
+
+
+def _ce_torch(x, t, w, ii, ls, red, softcap=None, zs=0.0, scaling=False):
+    xt = torch.tensor(x, requires_grad=True)
+    xc = softcap * torch.tanh(xt / softcap) if softcap is not None else xt
+    wt = torch.tensor(w) if w is not None else None
+    rows = torch.nn.functional.cross_entropy(xc, torch.tensor(t), weight=wt, ignore_index=ii, reduction="none",
+                                             label_smoothing=ls)
+    keep = torch.tensor(t) != ii
+    lse = torch.logsumexp(xc, -1)
+    z = zs * lse ** 2 * keep
+    denom_l = (wt[torch.tensor(t)[keep]].sum() if wt is not None else keep.sum()).double()
+    if red == "mean":
+        rows, z = rows / denom_l, z / keep.sum()
+    if scaling:
+        p = torch.softmax(xc, -1).gather(1, torch.tensor(t).clamp(min=0)[:, None])[:, 0].detach() * keep
+        rows, z = rows * p, z * p
+    tot = rows + z
+    (tot.sum() if red != "none" else tot.sum()).backward()
+    return tot.detach().numpy(), xt.grad.numpy()
+
+
+@pytest.mark.parametrize("cw,ls,red,softcap,zs,scaling", [
+    (False, 0.0, "mean", None, 0.0, False), (True, 0.0, "mean", None, 0.0, False),
+    (False, 0.1, "mean", None, 0.0, False), (True, 0.2, "sum", None, 0.0, False),
+    (False, 0.0, "none", None, 0.0, False), (False, 0.0, "mean", 7.0, 0.0, False),
+    (True, 0.1, "mean", None, 1e-3, False), (False, 0.1, "mean", 5.0, 1e-2, True)])
+def test_ce_rows_match_torch(cw, ls, red, softcap, zs, scaling):
+    rng = np.random.default_rng(80)
+    N, V = 40, 97
+    x = rng.standard_normal((N, V)) * 3
+    t = rng.integers(0, V, N)
+    t[::5] = -100
+    w = rng.uniform(0.2, 2.0, V) if cw else None
+    loss, z, g, am, _ = OCE.ce_rows(x, t, w, -100, zs, ls, red, softcap, scaling)
+    ref_l, ref_g = _ce_torch(x, t, w, -100, ls, red, softcap, zs, scaling)
+    np.testing.assert_allclose(loss, ref_l, rtol=1e-10, atol=1e-13)
+    np.testing.assert_allclose(g, ref_g, rtol=1e-9, atol=1e-13)
+    keep = t != -100
+    xs = softcap * np.tanh(x / softcap) if softcap else x
+    assert np.all(am[keep] == xs[keep].argmax(1)) and np.all(am[~keep] == -1)
