@@ -62,7 +62,7 @@ def short_kernel_name(name: str) -> str:
                   r"bwd_lmk)_kernel", name)
     if not m:
         return name
-    return "attn_fwd" if m.group(1) == "fwd" else m.group(1)
+    return {"fwd": "attn_fwd", "ce": "ce_rows"}.get(m.group(1), m.group(1))
 
 
 def read_pmc(root: str) -> dict:
@@ -150,7 +150,8 @@ def probs_bench(args, wl):
     w_cap = wl.w_max
 
     def step():
-        return ops.export_probs(x["q"], x["k"], x["w"], x["cu"], idx, lse, seq=0, rows=L, w_cap=w_cap, max_seqlen=L)
+        return ops.export_probs(x["q"], x["k"], x["w"], x["cu"], idx, lse, seq=0, rows=L, w_cap=w_cap, max_seqlen=L,
+                                seq_len=L)
 
     for _ in range(args.warmup):
         step()

@@ -206,7 +206,7 @@ class DSALTAttention(nn.Module):
         from ..kernels.attention_probs import SparseAttentionProbs
         cu_h = list(cu_list) if cu_list is not None else cu_seqlens.detach().to("cpu").tolist()
         n0 = cu_h[1] - cu_h[0]
-        p_win, p_lmk = ops.export_probs(q, k, w32, cu_seqlens, idx, lse, seq=0, rows=n0,
+        p_win, p_lmk = ops.export_probs(q, k, w32, cu_seqlens, idx, lse, seq=0, rows=n0, seq_len=n0,
                                         w_cap=max(1, min(n0, self.n_max + 1)), max_seqlen=maxlen, select_mode=mode,
                                         block_size=self.block_size)
         sp = SparseAttentionProbs(p_win, p_lmk, idx[:, 0].long(), self.block_size if mode == ops.SELECT_BLOCK else 0)

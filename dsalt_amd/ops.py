@@ -405,10 +405,12 @@ def rope_qk_(q, k, cu_seqlens, cos, sin, *, max_seqlen=None):
 
 
 def export_probs(q, k, w, cu_seqlens, lmk_idx, lse, lmk_bias=None, *, seq=0, rows=None, w_cap=None, scale=None,
-                 max_seqlen=None, select_mode=SELECT_GLOBAL, block_size=512, want_lmk=True):
+                 max_seqlen=None, select_mode=SELECT_GLOBAL, block_size=512, want_lmk=True, seq_len=None):
     """(p_win [H, rows, w_cap], p_lmk [H, rows, K] or None), fp32: the probabilities the
     forward used for sequence ``seq`` (``lse`` from attention_forward on the same inputs),
-    window keys as p_win[h, i, c] = P(i, i - c), landmark slots as p_lmk[h, i, slot]."""
+    window keys as p_win[h, i, c] = P(i, i - c), landmark slots as p_lmk[h, i, slot].
+    ``seq_len`` (the sequence's length, when the caller knows it) lets the outputs skip their
+    zero fill."""
     dev = _gpu(q, k, w, cu_seqlens, lmk_idx, lse, lmk_bias)
     q, k = _rows3(q, "q"), _rows3(k, "k")
     T, H, D = q.shape
@@ -417,6 +419,7 @@ def export_probs(q, k, w, cu_seqlens, lmk_idx, lse, lmk_bias=None, *, seq=0, row
     if rows is None or w_cap is None:
         cu_h = cu_seqlens.detach().to("cpu").tolist()
         n = cu_h[seq + 1] - cu_h[seq]
+        seq_len = n
         rows = n if rows is None else rows
         if w_cap is None:
             w_cap = int(w[cu_h[seq]:cu_h[seq + 1]].max().item()) if n else 1
@@ -429,8 +432,9 @@ def export_probs(q, k, w, cu_seqlens, lmk_idx, lse, lmk_bias=None, *, seq=0, row
     li = lmk_idx.to(torch.int32).contiguous()
     lb = lmk_bias.detach().to(torch.float32).contiguous() if lmk_bias is not None else None
     lse_c = lse.detach().to(torch.float32).contiguous()
-    p_win = torch.zeros((H, rows, w_cap), dtype=torch.float32, device=dev)
-    p_lmk = torch.zeros((H, rows, K), dtype=torch.float32, device=dev) if want_lmk and K else None
+    alloc = torch.empty if rows == seq_len else torch.zeros  # the kernel writes every row of the sequence
+    p_win = alloc((H, rows, w_cap), dtype=torch.float32, device=dev)
+    p_lmk = alloc((H, rows, K), dtype=torch.float32, device=dev) if want_lmk and K else None
     a = ProbsArgs()
     a.p = _problem(T, S, maxlen, H, k.shape[1], D, K, select_mode, block_size, dtype_code(q.dtype))
     a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
