@@ -190,32 +190,45 @@ __global__ __launch_bounds__(256) void sel_sums_kernel(SelectParams p, const flo
 
 // stats[(r * nsig + sig) * 2] = {mean, std} of the block-causal prefixes: r
 // indexes (sequence, block) sets, statistics over the blocks before it.
+// one thread per (sequence, signal, block): the block's prefix sums are accumulated in block
+// order (the same additions, in the same order, for every block), then its mean and std
 __global__ void sel_stats_kernel(SelectParams p, const double* sums, double* stats) {
     const int nsig = 1 + p.n_kv_heads;
     const int id = blockIdx.x * blockDim.x + threadIdx.x;
-    {
-        if (id >= p.num_seqs * nsig) return;
-        int s = id / nsig, sig = id % nsig;
-        int st, len;
-        seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
-        double p1 = 0.0, p2 = 0.0;
-        for (int b = 0; b < p.n_sets; ++b) {
-            int64_t o = ((int64_t)(s * p.n_sets + b) * nsig + sig) * 2;
-            int b0 = b * p.block_size;
-            double m = 0.0, sd = 1.0;
-            if (b0 >= 2 && b0 < len) mean_std(p1, p2, b0, m, sd);
-            stats[o] = m;
-            stats[o + 1] = sd;
-            if (b0 < len) {
-                p1 = __dadd_rn(p1, sums[o]);
-                p2 = __dadd_rn(p2, sums[o + 1]);
-            }
-        }
+    if (id >= p.num_seqs * nsig * p.n_sets) return;
+    const int b = id % p.n_sets;
+    const int sig = (id / p.n_sets) % nsig;
+    const int s = id / (p.n_sets * nsig);
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
+    double p1 = 0.0, p2 = 0.0;
+    for (int bb = 0; bb < b; ++bb) {
+        if (bb * p.block_size >= len) break;
+        const int64_t o = ((int64_t)(s * p.n_sets + bb) * nsig + sig) * 2;
+        p1 = __dadd_rn(p1, sums[o]);
+        p2 = __dadd_rn(p2, sums[o + 1]);
     }
+    const int64_t o = ((int64_t)(s * p.n_sets + b) * nsig + sig) * 2;
+    const int b0 = b * p.block_size;
+    double m = 0.0, sd = 1.0;
+    if (b0 >= 2 && b0 < len) mean_std(p1, p2, b0, m, sd);
+    stats[o] = m;
+    stats[o + 1] = sd;
 }
 
 __device__ __forceinline__ float zscore(float a, double mean, double sd) {
     return (float)__ddiv_rn(__dadd_rn((double)a, -mean), sd);
+}
+
+// zscore from a precomputed reciprocal rsd = 1/sd (rounded): q = (a - mean) * rsd is within
+// 2^-51 (relative) of the quotient, so when q widened by 2^-48 either way rounds to one fp32
+// value, that value is the quotient's rounding; otherwise (q within 2^-48 of an fp32
+// rounding midpoint, about once in 2^24 draws) the division decides.  Same result as zscore.
+__device__ __forceinline__ float zscore_rcp(float a, double mean, double sd, double rsd) {
+    const double d = __dadd_rn((double)a, -mean);
+    const double q = __dmul_rn(d, rsd);
+    const float lo = (float)__dmul_rn(q, 1.0 - 0x1p-48), hi = (float)__dmul_rn(q, 1.0 + 0x1p-48);
+    return lo == hi ? lo : (float)__ddiv_rn(d, sd);
 }
 
 __device__ __forceinline__ float mix_score(float alpha, float zv, float zx) {
@@ -294,7 +307,7 @@ struct KeyFn {
     float alpha;
     bool block;
     const float *zx, *zv, *nx, *nv;
-    double mx, sx, mv, sv;
+    double mx, sx, mv, sv, rsx, rsv;
     __device__ __forceinline__ unsigned long long operator()(int j) const {
         if (j < w[st + j]) return 0ull;
         float zxj, zvj;
@@ -302,13 +315,15 @@ struct KeyFn {
             zxj = zx[st + j];
             zvj = zv[(int64_t)rep_g * total_len + st + j];
         } else {
-            zxj = zscore(nx[st + j], mx, sx);
-            zvj = zscore(nv[(int64_t)rep_g * total_len + st + j], mv, sv);
+            zxj = zscore_rcp(nx[st + j], mx, sx, rsx);
+            zvj = zscore_rcp(nv[(int64_t)rep_g * total_len + st + j], mv, sv, rsv);
         }
         uint32_t u = order_key(mix_score(alpha, zvj, zxj));
         return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)j);
     }
 };
+
+
 
 // bitonic sorts of n (a power of two) LDS elements by NT threads
 template <int NT>
@@ -507,9 +522,12 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
                                                                const double* stats, int border_cap) {
     __shared__ TopkShared sh;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int set = blockIdx.x % p.n_sets;
-    const int s = (blockIdx.x / p.n_sets) % p.num_seqs;
-    const int h = blockIdx.x / (p.n_sets * p.num_seqs);
+    // later blocks scan longer prefixes: dispatch them first (largest sets first balances
+    // the tail); every (head, sequence) of one set index is adjacent
+    const int hs = p.n_heads * p.num_seqs;
+    const int set = p.n_sets - 1 - (int)(blockIdx.x / hs);
+    const int s = (blockIdx.x % hs) % p.num_seqs;
+    const int h = (blockIdx.x % hs) / p.num_seqs;
     const int K = p.k_lmk;
     int32_t* out = p.lmk_idx + (((int64_t)h * p.num_seqs + s) * p.n_sets + set) * K;
     int st, len;
@@ -541,6 +559,8 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
         key.sx = sr[1];
         key.mv = sr[2 * (key.rep_g + 1)];
         key.sv = sr[2 * (key.rep_g + 1) + 1];
+        key.rsx = __ddiv_rn(1.0, key.sx);
+        key.rsv = __ddiv_rn(1.0, key.sv);
     }
     const int cap = min(border_cap, kBorderCap);
 
@@ -756,8 +776,8 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
                 DSALT_LAUNCH("sel_scores", sel_scores_kernel, dim3(ceil_div(p.max_seqlen, 256), p.num_seqs),
                              dim3(256), 0, stream, p, nx, nv, stats);
         } else {
-            DSALT_LAUNCH("sel_stats", sel_stats_kernel, dim3(ceil_div(p.num_seqs * nsig, 64)), dim3(64), 0, stream,
-                         p, sums, stats);
+            DSALT_LAUNCH("sel_stats", sel_stats_kernel, dim3(ceil_div(p.num_seqs * nsig * p.n_sets, 64)), dim3(64), 0,
+                         stream, p, sums, stats);
         }
     }
     const int nsets_total = p.n_heads * p.num_seqs * p.n_sets;
