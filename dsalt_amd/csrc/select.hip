@@ -21,9 +21,13 @@
 //     global:   sel_part sorts the keys of each part of a set's candidates in
 //               LDS and keeps its best k; sel_merge sorts the survivors of up
 //               to G parts per block, level by level, and writes the indices.
-//     block:    sel_topk, one 1024-thread block per landmark set: radix select
-//               8 bits per pass until the boundary bin fits in LDS, then a
-//               bitonic sort of that bin.
+//     block:    sel_topk, one 1024-thread block per landmark set (largest sets
+//               first).  Sets of 8192+ candidates: a threshold key from a sorted
+//               strided sample of 4096, one pass screening every candidate with a
+//               float32 affine form of its score (exact keys only near the
+//               threshold), a sort of the survivors; when the sample misplaces the
+//               threshold, and for smaller sets: radix select 8 bits per pass until
+//               the boundary bin fits in LDS, then a bitonic sort of that bin.
 // The arithmetic order above is the canonical one that the CPU oracle
 // restates; this file is compiled with -ffp-contract=off.
 #include "common.h"
@@ -244,6 +248,10 @@ __device__ __forceinline__ uint32_t order_key(float s) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+__device__ __forceinline__ float from_order_key(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 // global variant: z per (token, signal), head-major zv for the selection, API outputs
 __global__ __launch_bounds__(256) void sel_z_kernel(SelectParams p, const float* nx, const float* nv,
                                                     const double* stats, float* zx, float* zv) {
@@ -288,9 +296,12 @@ __global__ __launch_bounds__(256) void sel_scores_kernel(SelectParams p, const f
 }
 
 // ------------------------------------------------------------------ top-k
+constexpr int kSample = 4096;      // candidates sampled for the threshold of large block-causal sets
+constexpr int kSampleMin = 8192;   // sets of fewer candidates take the radix path directly
+
 struct TopkShared {
     uint32_t hist[kSelWaves][256];
-    unsigned long long border[kBorderCap];
+    unsigned long long border[kBorderCap > kSample ? kBorderCap : kSample];
     int sel[kMaxLandmarks];
     uint32_t total;
     int digit;
@@ -331,7 +342,7 @@ __device__ void bitonic_desc_u64(unsigned long long* a, int n, int tid) {
     for (int size = 2; size <= n; size <<= 1)
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             for (int i = tid; i < (n >> 1); i += NT) {
-                int lo = (i / stride) * 2 * stride + (i % stride), hi = lo + stride;
+                int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1)), hi = lo + stride;  // stride: a power of two
                 bool desc = (lo & size) == 0;
                 unsigned long long x = a[lo], y = a[hi];
                 if ((x < y) == desc) {
@@ -348,7 +359,7 @@ __device__ void bitonic_asc_i32(int* a, int n, int tid) {
     for (int size = 2; size <= n; size <<= 1)
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             for (int i = tid; i < (n >> 1); i += NT) {
-                int lo = (i / stride) * 2 * stride + (i % stride), hi = lo + stride;
+                int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1)), hi = lo + stride;  // stride: a power of two
                 bool asc = (lo & size) == 0;
                 int x = a[lo], y = a[hi];
                 if ((x > y) == asc) {
@@ -563,6 +574,95 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
         key.rsv = __ddiv_rn(1.0, key.sv);
     }
     const int cap = min(border_cap, kBorderCap);
+
+    // Large sets: a threshold from an evenly strided sample of the candidates, then one pass
+    // that keeps every key at or above it.  When that keeps between K and cap keys, their
+    // top K are the set's top K; otherwise (an unrepresentative sample) the radix path
+    // below runs from scratch.
+    if (n >= kSampleMin && border_cap >= kBorderCap) {
+        const int stride = n / kSample;
+        for (int i = tid; i < kSample; i += kSelThreads) sh.border[i] = key(i * stride);
+        __syncthreads();
+        bitonic_desc_u64<kSelThreads>(sh.border, kSample, tid);
+        // aim at about 1.6 K + 128 keys above the threshold (the sample's spread leaves
+        // fewer than K above it in a small fraction of the sets: those take the radix path)
+        const long long want = ((long long)K * 16 / 10 + 128) * kSample / n;
+        const int rank = (int)min((long long)kSample - 1, max(want, 1ll));
+        const unsigned long long thr = sh.border[rank];
+        __syncthreads();
+        if (tid == 0) sh.nborder = 0u;
+        __syncthreads();
+        if (thr != 0ull) {
+            // Screen with the score as one float32 affine form of the two norms,
+            // s' = A nv + B nx + C; it differs from the canonical score by less than
+            // 16 * 2^-24 * M (M: the magnitudes of the terms), so keys at or above the
+            // threshold all pass s' + 2^-19 M >= thr_score and only those get exact keys.
+            const float thr_s = from_order_key((uint32_t)(thr >> 32));
+            float A = 0.f, B = 0.f, Cv = 0.f, Cx = 0.f;
+            if (block) {
+                const double al = (double)key.alpha, om = 1.0 - al;
+                A = (float)(al / key.sv);
+                B = (float)(om / key.sx);
+                Cv = (float)(al * key.mv / key.sv);
+                Cx = (float)(om * key.mx / key.sx);
+            }
+            // U candidates per thread per step, all loads issued before any screen
+            constexpr int U = 4;
+            const float* nvg = nv + (int64_t)key.rep_g * p.total_len + st;
+            const float* nxs = nx + st;
+            const float C = -(Cv + Cx), Cm = fabsf(Cv) + fabsf(Cx);
+            for (int j0 = tid; j0 < n; j0 += kSelThreads * U) {
+                float av[U], bv[U];
+                if (block) {
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const int j = min(j0 + u * kSelThreads, n - 1);
+                        av[u] = nxs[j];
+                        bv[u] = nvg[j];
+                    }
+                }
+                uint32_t pass = 0u;
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int j = j0 + u * kSelThreads;
+                    bool maybe = j < n;
+                    if (block && maybe) {
+                        const float sa = fmaf(A, bv[u], fmaf(B, av[u], C));
+                        const float M = fabsf(A * bv[u]) + fabsf(B * av[u]) + Cm;
+                        maybe = sa + 0x1p-19f * M >= thr_s;
+                    }
+                    pass |= maybe ? 1u << u : 0u;
+                }
+                while (pass) {  // exact keys of the few survivors (one copy of the key code)
+                    const int u = __builtin_ctz(pass);
+                    pass &= pass - 1u;
+                    const unsigned long long kj = key(j0 + u * kSelThreads);
+                    if (kj >= thr) {
+                        const uint32_t slot = atomicAdd(&sh.nborder, 1u);
+                        if (slot < (uint32_t)cap) sh.border[slot] = kj;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        const int nb = (int)sh.nborder;
+        if (thr != 0ull && nb >= K && nb <= cap) {
+            int nb2 = 1;
+            while (nb2 < nb) nb2 <<= 1;
+            for (int i = nb + tid; i < nb2; i += kSelThreads) sh.border[i] = 0ull;
+            __syncthreads();
+            bitonic_desc_u64<kSelThreads>(sh.border, nb2, tid);
+            int ns2 = 1;
+            while (ns2 < K) ns2 <<= 1;
+            for (int i = tid; i < ns2; i += kSelThreads)
+                sh.sel[i] = i < K ? (int)(0xffffffffu - (uint32_t)(sh.border[i] & 0xffffffffull)) : 0x7fffffff;
+            __syncthreads();
+            bitonic_asc_i32<kSelThreads>(sh.sel, ns2, tid);
+            for (int i = tid; i < K; i += kSelThreads) out[i] = sh.sel[i];
+            return;
+        }
+        __syncthreads();
+    }
 
     unsigned long long prefix = 0ull;
     int plen = 0;

@@ -125,3 +125,12 @@ def test_block_workload_selection_bit_exact_shortened():
     idx, ridx = _run(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, ops.SELECT_BLOCK, 512,
                      ops.STATS_SEQUENCE, want=False)
     np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
+def test_block_workload_selection_bit_exact_long_prefixes():
+    # prefixes of up to 64K candidates take the sampled-threshold path
+    wl = WORKLOADS["fwd_bf16_h16_l131072_block"]
+    x = generate(wl, seqlen=65536, heads=2)
+    idx, ridx = _run(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, ops.SELECT_BLOCK, 512,
+                     ops.STATS_SEQUENCE, want=False)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
