@@ -1,0 +1,106 @@
+"""Edge cases of the operator on the GPU against the oracle: empty and one-token sequences in a
+packed batch, no landmarks, the largest landmark sets, every landmark slot empty, the GQA ratio
+of the 3B decoder, and windows covering whole sequences.  Indices bit-exact; outputs and
+gradients relative max|a-b| / max|b| within 1e-5 (fp32) or 2e-2 (bf16)."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from dsalt_amd import ops
+from oracle import attention as OA
+from oracle import select as OS
+from tests.helpers import bits, f64, oracle_dtype, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+
+
+def _case(lens, H, G, D, K, wmax, dt, seed, hidden=128):
+    g = torch.Generator().manual_seed(seed)
+    T = sum(lens)
+    x = {"q": torch.randn(T, H, D, generator=g).to(dt), "k": torch.randn(T, G, D, generator=g).to(dt),
+         "v": torch.randn(T, G, D, generator=g).to(dt), "h": torch.randn(T, hidden, generator=g).to(dt),
+         "w": torch.randint(1, wmax + 1, (T,), generator=g, dtype=torch.int32),
+         "do": torch.randn(T, H, D, generator=g).to(dt),
+         "cu": torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32),
+         "alpha": torch.rand(H, generator=g)}
+    return x
+
+
+def _run(x, K, mode=ops.SELECT_GLOBAL, block=64, backward=True):
+    dt = x["q"].dtype
+    H, G = x["q"].shape[1], x["k"].shape[1]
+    maxlen = max(1, int((x["cu"][1:] - x["cu"][:-1]).max()))
+    d = {k: v.to(DEV) for k, v in x.items()}
+    idx = ops.select_landmarks(d["h"], d["v"], d["alpha"], d["w"], d["cu"], K, max_seqlen=maxlen, select_mode=mode,
+                               block_size=block, stats_scope=ops.STATS_SEQUENCE)
+    ridx = OS.select(bits(x["h"]), bits(x["v"]), x["alpha"].numpy(), x["w"].numpy(), x["cu"].numpy(), K,
+                     oracle_dtype(dt), mode=mode, block_size=block, stats_scope=OS.STATS_SEQUENCE)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    scale = 1.0 / math.sqrt(x["q"].shape[-1])
+    out, lse = ops.attention_forward(d["q"], d["k"], d["v"], d["w"], d["cu"], idx, None, scale=scale,
+                                     max_seqlen=maxlen, select_mode=mode, block_size=block)
+    bs = block if mode == ops.SELECT_BLOCK else None
+    ro, rl = OA.attention_fwd(f64(x["q"]), f64(x["k"]), f64(x["v"]), x["w"].numpy(), x["cu"].numpy(), ridx, scale,
+                              block_size=bs)
+    assert rel_err(f64(out), ro) < TOL[dt]
+    if not backward:
+        return
+    kk, vv = d["k"], d["v"]
+    if G != H:
+        kk, vv = kk.repeat_interleave(H // G, 1), vv.repeat_interleave(H // G, 1)
+    dq, dk, dv, _ = ops.attention_backward(d["do"], d["q"], kk, vv, out, lse, d["w"], d["cu"], idx, max_seqlen=maxlen)
+    rdq, rdk, rdv, _ = OA.attention_bwd(f64(x["q"]), f64(x["k"]), f64(x["v"]), x["w"].numpy(), x["cu"].numpy(),
+                                        ridx, scale, f64(x["do"]))
+    if G != H:
+        dk = dk.view(dk.shape[0], G, H // G, -1).float().sum(2)
+        dv = dv.view(dv.shape[0], G, H // G, -1).float().sum(2)
+    for name, a, b in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        assert rel_err(f64(a), b) < TOL[dt], name
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_empty_and_single_token_sequences(dt):
+    _run(_case([100, 0, 1, 0, 130], 2, 2, 64, 8, 40, dt, seed=200), 8)
+
+
+def test_empty_sequences_block_causal():
+    _run(_case([0, 300, 0, 1, 70], 2, 2, 64, 8, 40, torch.bfloat16, seed=201), 8, mode=ops.SELECT_BLOCK,
+         block=64, backward=False)
+
+
+def test_no_landmarks():
+    _run(_case([257, 190], 4, 4, 64, 0, 90, torch.bfloat16, seed=202), 0)
+
+
+def test_largest_landmark_sets():
+    _run(_case([1200, 700], 2, 2, 128, 512, 300, torch.bfloat16, seed=203), 512)
+
+
+def test_gqa_ratio_of_the_3b_decoder():
+    _run(_case([640, 333], 16, 2, 128, 32, 200, torch.bfloat16, seed=204), 32)
+
+
+def test_windows_covering_whole_sequences():
+    _run(_case([300, 77], 2, 2, 64, 16, 5000, torch.float32, seed=205), 16)
+
+
+def test_all_landmark_slots_empty():
+    x = _case([200, 130], 2, 2, 64, 8, 30, torch.float32, seed=206)
+    d = {k: v.to(DEV) for k, v in x.items()}
+    idx = torch.full((2, 2, 1, 8), -1, dtype=torch.int32, device=DEV)
+    out, lse = ops.attention_forward(d["q"], d["k"], d["v"], d["w"], d["cu"], idx, None, max_seqlen=200)
+    ro, _ = OA.attention_fwd(f64(x["q"]), f64(x["k"]), f64(x["v"]), x["w"].numpy(), x["cu"].numpy(),
+                             idx.cpu().numpy(), 1 / 8.0)
+    assert rel_err(f64(out), ro) < 1e-5
+    dq, dk, dv, db = ops.attention_backward(d["do"], d["q"], d["k"], d["v"], out, lse, d["w"], d["cu"], idx,
+                                            torch.zeros(2, 2, 1, 8, device=DEV), max_seqlen=200)
+    assert torch.all(db == 0)
+    rdq, _, _, _ = OA.attention_bwd(f64(x["q"]), f64(x["k"]), f64(x["v"]), x["w"].numpy(), x["cu"].numpy(),
+                                    idx.cpu().numpy(), 1 / 8.0, f64(x["do"]))
+    assert rel_err(f64(dq), rdq) < 1e-5
