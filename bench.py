@@ -57,7 +57,9 @@ LABELS = ("sel_norms", "sel_sums", "sel_stats", "sel_z", "sel_scores", "sel_part
 def short_kernel_name(name: str) -> str:
     """Label of a library kernel (the one dsalt_timing_report uses) from a profiler kernel name."""
     import re
-    m = re.search(r"(sel_norms|sel_sums|sel_stats|sel_z|sel_scores|sel_part|sel_merge|sel_topk|gather|row_plan|fwd|bwd_init|bwd_dq|"
+    # the label must start the identifier (a mangled length prefix, "::" or the start): no
+    # match inside library names such as reduce_kernel or vectorized_gather_kernel
+    m = re.search(r"(?<![A-Za-z_])(sel_norms|sel_sums|sel_stats|sel_z|sel_scores|sel_part|sel_merge|sel_topk|gather|row_plan|fwd|bwd_init|bwd_dq|"
                   r"bwd_dkdv|bwd_lmk_sum|train_windows|train_dw|rope|silu_mul|probs|ce|"
                   r"bwd_lmk)_kernel", name)
     if not m:
