@@ -30,9 +30,13 @@ constexpr int kRowChunk = 1024;
 constexpr int kSeg = 512;  // rows compacted at a time in the dK/dV sweep
 
 template <typename T, int D> struct BwdShape;
-template <> struct BwdShape<bf16, 64> { static constexpr int BN = 64, BQ = 64; };
+// BN: keys per staged chunk of the query-parallel dQ kernel (32 for 16-bit head_dim 64:
+// the shorter chunk brings the kernel to 78 registers, six waves per SIMD, and the
+// kernel is bound by the latency of its chunk loop, not by issue); BQ: query rows per
+// staged chunk of the key-parallel kernels
+template <> struct BwdShape<bf16, 64> { static constexpr int BN = 32, BQ = 64; };
 template <> struct BwdShape<bf16, 128> { static constexpr int BN = 32, BQ = 32; };
-template <> struct BwdShape<f16, 64> { static constexpr int BN = 64, BQ = 64; };
+template <> struct BwdShape<f16, 64> { static constexpr int BN = 32, BQ = 64; };
 template <> struct BwdShape<f16, 128> { static constexpr int BN = 32, BQ = 32; };
 template <> struct BwdShape<float, 64> { static constexpr int BN = 32, BQ = 32; };
 template <> struct BwdShape<float, 128> { static constexpr int BN = 16, BQ = 16; };
@@ -71,7 +75,7 @@ __global__ void bwd_init_kernel(AttnParams p) {
 // TR: training variant -- band keys near the window start carry the soft edge bias,
 // and the lane also sums dS * d(bias)/d(w~) of its row into dw_h.
 template <typename T, int D, bool TR>
-__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (TR ? 5 : 6) : 2) void bwd_dq_kernel(AttnParams p) {
     constexpr int BN = BwdShape<T, D>::BN;
     constexpr int NST = BN / 16;
     constexpr bool kHalf = sizeof(T) == 2;
@@ -81,7 +85,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(AttnParams p) {
     __shared__ int lpos[kMaxLandmarks];
     __shared__ __attribute__((aligned(16))) float lbs[kMaxLandmarks];
     // block scalars live in the second K buffer until the first chunk is staged there
-    // (keeps the block at 40 KB of LDS: four blocks per CU)
     int* red = (int*)Ks[1];
     int& nvalid_s = red[4];
 
