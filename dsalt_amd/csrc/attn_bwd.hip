@@ -826,12 +826,28 @@ __global__ __launch_bounds__(256) void bwd_lmk_sum_kernel(AttnParams p) {
     const int pos = p.lmk[(((int64_t)h * p.num_seqs + s) * p.n_sets) * K + sl];
     int st, len;
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
+    // chunk partials summed in chunk order; eight chunks' loads in flight at a time
     float sk = 0.f, sv = 0.f, sb = 0.f;
-    for (int ch = 0; ch < p.n_chunks; ++ch) {
-        const int64_t pr = ((int64_t)ch * p.n_heads + h) * p.num_seqs * K + (int64_t)s * K + sl;
-        sk += p.part_k[pr * D + d];
-        sv += p.part_v[pr * D + d];
-        if (d == 0) sb += p.part_b[pr];
+    const int64_t cstride = (int64_t)p.n_heads * p.num_seqs * K;
+    const int64_t pr0 = (int64_t)h * p.num_seqs * K + (int64_t)s * K + sl;
+    constexpr int U = 8;
+    for (int ch0 = 0; ch0 < p.n_chunks; ch0 += U) {
+        float ak[U], av[U], ab[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int ch = min(ch0 + u, p.n_chunks - 1);
+            const int64_t pr = ch * cstride + pr0;
+            ak[u] = p.part_k[pr * D + d];
+            av[u] = p.part_v[pr * D + d];
+            ab[u] = d == 0 ? p.part_b[pr] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (ch0 + u < p.n_chunks) {
+                sk += ak[u];
+                sv += av[u];
+                sb += ab[u];
+            }
     }
     if (d == 0 && p.d_bias) p.d_bias[(((int64_t)h * p.num_seqs + s) * p.n_sets) * K + sl] = sb;
     if (pos < 0 || pos >= len) return;

@@ -50,7 +50,7 @@ __device__ __forceinline__ int lower_bound_lds(const int* a, int n, int x) {
 // recorded, and, when seq_wmax is set, the largest clamped window of each
 // sequence (bounding the key-parallel backward sweep).
 __global__ __launch_bounds__(64) void row_plan_kernel(AttnParams p) {
-    __shared__ int sp[64];
+    __shared__ int sp[64], slo[64];
     const int l = threadIdx.x;
     const int tile = blockIdx.x;  // s * n_tiles + t
     const int s = tile / p.n_tiles, t = tile % p.n_tiles;
@@ -73,6 +73,7 @@ __global__ __launch_bounds__(64) void row_plan_kernel(AttnParams p) {
         rank += (jhi < khi || (jhi == khi && jlo < klo)) ? 1 : 0;
     }
     sp[rank] = l;
+    slo[l] = lo;
     __syncthreads();
     const int pl = sp[l];  // row offset at sorted position l
     p.plan_perm[(int64_t)tile * 64 + l] = (uint8_t)pl;
@@ -80,7 +81,7 @@ __global__ __launch_bounds__(64) void row_plan_kernel(AttnParams p) {
     const bool rv = ri < len;
     int rlo = 0x7fffffff, rlmax = (int)0x80000000, rhi = -1, rhmin = 0x7fffffff;
     if (rv) {
-        rlo = max(ri - max(p.w[st + ri], 1) + 1, 0);
+        rlo = slo[pl];
         rlmax = rlo;
         rhi = ri;
         rhmin = ri;
