@@ -33,13 +33,15 @@ template <typename T, int D> struct BwdShape;
 // BN: keys per staged chunk of the query-parallel dQ kernel (32 for 16-bit head_dim 64:
 // the shorter chunk brings the kernel to 78 registers, six waves per SIMD, and the
 // kernel is bound by the latency of its chunk loop, not by issue); BQ: query rows per
-// staged chunk of the key-parallel kernels
-template <> struct BwdShape<bf16, 64> { static constexpr int BN = 32, BQ = 64; };
-template <> struct BwdShape<bf16, 128> { static constexpr int BN = 32, BQ = 32; };
-template <> struct BwdShape<f16, 64> { static constexpr int BN = 32, BQ = 64; };
-template <> struct BwdShape<f16, 128> { static constexpr int BN = 32, BQ = 32; };
-template <> struct BwdShape<float, 64> { static constexpr int BN = 32, BQ = 32; };
-template <> struct BwdShape<float, 128> { static constexpr int BN = 16, BQ = 16; };
+// staged chunk of the key-parallel dK/dV kernel (32 for 16-bit head_dim 64: four waves
+// per SIMD without spills, also in the training variant); BL: the same for the landmark
+// kernel
+template <> struct BwdShape<bf16, 64> { static constexpr int BN = 32, BQ = 32, BL = 64; };
+template <> struct BwdShape<bf16, 128> { static constexpr int BN = 32, BQ = 32, BL = 32; };
+template <> struct BwdShape<f16, 64> { static constexpr int BN = 32, BQ = 32, BL = 64; };
+template <> struct BwdShape<f16, 128> { static constexpr int BN = 32, BQ = 32, BL = 32; };
+template <> struct BwdShape<float, 64> { static constexpr int BN = 32, BQ = 32, BL = 32; };
+template <> struct BwdShape<float, 128> { static constexpr int BN = 16, BQ = 16, BL = 16; };
 
 __device__ __forceinline__ int lower_bound_i(const int* a, int n, int x) {
     int lo = 0, hi = n;
@@ -375,7 +377,7 @@ struct QLoader {
 //     partial rows j0 < lo_i <= j0+63   (see keys >= lo_i: one-sided mask);
 // rows with lo_i > j0 + 63 are skipped.  List order is row order, so the sum
 // order is fixed and results are deterministic.
-// four waves per SIMD for 16-bit head_dim 64 (at a few spilled registers), two otherwise.
+// four waves per SIMD for 16-bit head_dim 64 (32-row stages keep it free of spills), two otherwise.
 // TR: training variant -- fully visible rows must also see every key of the block
 // past their edge_keys edge-bias keys; other rows add the soft edge bias.
 template <typename T, int D, bool TR>
@@ -652,7 +654,7 @@ constexpr int kLmkGroup = 64 * kLmkSub;
 
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
-    constexpr int BQ = BwdShape<T, D>::BQ;
+    constexpr int BQ = BwdShape<T, D>::BL;
     constexpr int NQS = BQ / 16;
     constexpr bool kHalf = sizeof(T) == 2;
     typedef QStage<T, D, BQ> QS;
