@@ -22,12 +22,15 @@
 //               LDS and keeps its best k; sel_merge sorts the survivors of up
 //               to G parts per block, level by level, and writes the indices.
 //     block:    sel_topk, one 1024-thread block per landmark set (largest sets
-//               first).  Sets of 8192+ candidates: a threshold key from a sorted
-//               strided sample of 4096, one pass screening every candidate with a
-//               float32 affine form of its score (exact keys only near the
-//               threshold), a sort of the survivors; when the sample misplaces the
-//               threshold, and for smaller sets: radix select 8 bits per pass until
-//               the boundary bin fits in LDS, then a bitonic sort of that bin.
+//               first).  Sets of 8192+ candidates: a threshold key, the order
+//               statistic of a strided sample of 4096 found by radix passes
+//               (kth_desc), one pass screening every candidate with a float32 affine
+//               form of its score (exact keys only near the threshold; bf16 inputs
+//               read both norms from one packed word), then the K-th largest survivor
+//               by the same radix passes and the K survivors at or above it, output
+//               in index order by ranks; when the sample misplaces the threshold,
+//               and for smaller sets: radix select 8 bits per pass until the boundary
+//               bin fits in LDS, then a bitonic sort of that bin.
 // The arithmetic order above is the canonical one that the CPU oracle
 // restates; this file is compiled with -ffp-contract=off.
 #include "common.h"
@@ -50,8 +53,17 @@ __device__ __forceinline__ int pow2ceil64(int n) {
 constexpr int kNormTPW = 1;              // tokens per wave
 constexpr int kNormTB = 4 * kNormTPW;    // tokens per 256-thread block
 
+// bf16 inputs: the norms are bf16 values, so a token's |h| and |v_g| pack losslessly into
+// one word, pk[g][t] = bf16(|v_g|) << 16 | bf16(|h|); the block-causal top-k reads that
+// word (half the bytes of the two fp32 arrays) in its prefix scans
+__device__ __forceinline__ uint32_t pack_norms(float nx, float nv) {
+    return (__float_as_uint(nv) & 0xffff0000u) | (__float_as_uint(nx) >> 16);
+}
+__device__ __forceinline__ float packed_nx(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float packed_nv(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
 template <typename T>
-__global__ __launch_bounds__(256) void sel_norms_kernel(SelectParams p, float* nx, float* nv) {
+__global__ __launch_bounds__(256) void sel_norms_kernel(SelectParams p, float* nx, float* nv, uint32_t* pk) {
     constexpr int VW = 16 / (int)sizeof(T);
     typedef uint32_t u4 __attribute__((ext_vector_type(4)));
     extern __shared__ double ss[];  // [kNormTB][1 + n_kv] sums of squares
@@ -105,6 +117,8 @@ __global__ __launch_bounds__(256) void sel_norms_kernel(SelectParams p, float* n
         const float nr = round_norm<T>((float)canon_sqrt64(ss[idx]));
         if (sig == 0) nx[t] = nr;
         else nv[(int64_t)(sig - 1) * p.total_len + t] = nr;
+        if (pk && sig > 0)
+            pk[(int64_t)(sig - 1) * p.total_len + t] = pack_norms(round_norm<T>((float)canon_sqrt64(ss[tl * nsig])), nr);
     }
 }
 
@@ -299,16 +313,112 @@ __global__ __launch_bounds__(256) void sel_scores_kernel(SelectParams p, const f
 constexpr int kSample = 4096;      // candidates sampled for the threshold of large block-causal sets
 constexpr int kSampleMin = 8192;   // sets of fewer candidates take the radix path directly
 
+constexpr int kKthCand = 64;       // radix passes of kth_desc stop once the bin holds at most this many keys
+
 struct TopkShared {
     uint32_t hist[kSelWaves][256];
     unsigned long long border[kBorderCap > kSample ? kBorderCap : kSample];
     int sel[kMaxLandmarks];
+    unsigned long long cand[kKthCand];
+    unsigned long long kth;
     uint32_t total;
     int digit;
     uint32_t above;
     uint32_t nsure;
     uint32_t nborder;
+    uint32_t ncand;
 };
+
+// The r-th largest (0-based) of the n keys a[0..n) in LDS, for the whole block: radix
+// passes over 8-bit digits from the top (per-wave LDS histograms, as in the selection
+// below) narrow the keys to one digit prefix until at most kKthCand remain; those are
+// gathered and the answer is the candidate c with #{> c} <= r < #{>= c} (equal keys all
+// qualify and write the same value).  Exact for any keys; replaces a full sort where only
+// one order statistic is needed.
+__device__ unsigned long long kth_desc(TopkShared& sh, const unsigned long long* a, int n, int r, int tid) {
+    const int wave = tid >> 6, lane = tid & 63;
+    unsigned long long prefix = 0ull;
+    int plen = 0;
+    uint32_t rem = (uint32_t)r;
+    for (;;) {
+        for (int i = tid; i < kSelWaves * 256; i += kSelThreads) (&sh.hist[0][0])[i] = 0u;
+        __syncthreads();
+        const int shift = 56 - plen;
+        for (int i = tid; i < n; i += kSelThreads) {
+            const unsigned long long k = a[i];
+            if (plen > 0 && (k >> (64 - plen)) != prefix) continue;
+            atomicAdd(&sh.hist[wave][(uint32_t)(k >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid < 256) {
+            uint32_t c = 0;
+            for (int w2 = 0; w2 < kSelWaves; ++w2) c += sh.hist[w2][tid];
+            sh.hist[0][tid] = c;
+        }
+        __syncthreads();
+        if (wave == 0) {  // the digit whose bin holds rank rem, counting from the top bin
+            const uint32_t c0 = sh.hist[0][4 * lane], c1 = sh.hist[0][4 * lane + 1];
+            const uint32_t c2 = sh.hist[0][4 * lane + 2], c3 = sh.hist[0][4 * lane + 3];
+            const uint32_t loc = c0 + c1 + c2 + c3;
+            uint32_t suf = loc;
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t o = __shfl_down(suf, off, 64);
+                if (lane + off < 64) suf += o;
+            }
+            const uint32_t cs[4] = {c0, c1, c2, c3};
+            uint32_t above = suf - loc;  // keys in bins >= 4 lane + 4
+            for (int b = 3; b >= 0; --b) {
+                if (above <= rem && rem < above + cs[b]) {
+                    sh.digit = 4 * lane + b;
+                    sh.above = above;
+                }
+                above += cs[b];
+            }
+        }
+        __syncthreads();
+        const int d = sh.digit;
+        const uint32_t inbin = sh.hist[0][d];
+        rem -= sh.above;
+        prefix = (prefix << 8) | (unsigned long long)d;
+        plen += 8;
+        if (plen == 64) return prefix;  // every bit fixed
+        if (inbin <= (uint32_t)kKthCand) break;
+        __syncthreads();  // hist and digit are rewritten by the next pass
+    }
+    if (tid == 0) sh.ncand = 0u;
+    __syncthreads();
+    for (int i = tid; i < n; i += kSelThreads) {
+        const unsigned long long k = a[i];
+        if ((k >> (64 - plen)) == prefix) sh.cand[atomicAdd(&sh.ncand, 1u)] = k;
+    }
+    __syncthreads();
+    const int m = (int)sh.ncand;
+    if (tid < m) {
+        const unsigned long long c = sh.cand[tid];
+        uint32_t gt = 0u, ge = 0u;
+        for (int u = 0; u < m; ++u) {
+            const unsigned long long o = sh.cand[u];
+            gt += o > c ? 1u : 0u;
+            ge += o >= c ? 1u : 0u;
+        }
+        if (gt <= rem && rem < ge) sh.kth = c;
+    }
+    __syncthreads();
+    const unsigned long long res = sh.kth;
+    __syncthreads();
+    return res;
+}
+
+// out[0..m) = the m distinct values v[0..m) (LDS) in ascending order: each value's rank
+// is the number of smaller values (m <= kMaxLandmarks, one thread per value)
+__device__ void rank_sort_asc(const int* v, int m, int32_t* out, int tid) {
+    for (int t = tid; t < m; t += kSelThreads) {
+        const int x = v[t];
+        int rank = 0;
+        for (int u = 0; u < m; ++u) rank += v[u] < x ? 1 : 0;
+        out[rank] = x;
+    }
+}
 
 // key of candidate j_rel, or 0 when j_rel is not a candidate
 struct KeyFn {
@@ -318,6 +428,7 @@ struct KeyFn {
     float alpha;
     bool block;
     const float *zx, *zv, *nx, *nv;
+    const uint32_t* pk;  // packed norms (bf16 inputs), or null
     double mx, sx, mv, sv, rsx, rsv;
     __device__ __forceinline__ unsigned long long operator()(int j) const {
         if (j < w[st + j]) return 0ull;
@@ -325,6 +436,10 @@ struct KeyFn {
         if (!block) {
             zxj = zx[st + j];
             zvj = zv[(int64_t)rep_g * total_len + st + j];
+        } else if (pk) {
+            const uint32_t wd = pk[(int64_t)rep_g * total_len + st + j];
+            zxj = zscore_rcp(packed_nx(wd), mx, sx, rsx);
+            zvj = zscore_rcp(packed_nv(wd), mv, sv, rsv);
         } else {
             zxj = zscore_rcp(nx[st + j], mx, sx, rsx);
             zvj = zscore_rcp(nv[(int64_t)rep_g * total_len + st + j], mv, sv, rsv);
@@ -446,6 +561,7 @@ __device__ __forceinline__ KeyFn global_key(const SelectParams& p, const float* 
     key.zv = zv;
     key.nx = nullptr;
     key.nv = nullptr;
+    key.pk = nullptr;
     key.mx = key.sx = key.mv = key.sv = 0.0;
     return key;
 }
@@ -529,7 +645,7 @@ __global__ __launch_bounds__(kSortThreads) void sel_merge_kernel(SelectParams p,
 }
 
 __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, const float* zx, const float* zv,
-                                                               const float* nx, const float* nv,
+                                                               const float* nx, const float* nv, const uint32_t* pk,
                                                                const double* stats, int border_cap) {
     __shared__ TopkShared sh;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -557,6 +673,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
     key.zv = zv;
     key.nx = nx;
     key.nv = nv;
+    key.pk = pk;
     if (block) {
         int b0 = set * p.block_size;
         if (b0 < 2 || b0 >= len) {
@@ -583,13 +700,11 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
         const int stride = n / kSample;
         for (int i = tid; i < kSample; i += kSelThreads) sh.border[i] = key(i * stride);
         __syncthreads();
-        bitonic_desc_u64<kSelThreads>(sh.border, kSample, tid);
         // aim at about 1.6 K + 128 keys above the threshold (the sample's spread leaves
         // fewer than K above it in a small fraction of the sets: those take the radix path)
         const long long want = ((long long)K * 16 / 10 + 128) * kSample / n;
         const int rank = (int)min((long long)kSample - 1, max(want, 1ll));
-        const unsigned long long thr = sh.border[rank];
-        __syncthreads();
+        const unsigned long long thr = kth_desc(sh, sh.border, kSample, rank, tid);
         if (tid == 0) sh.nborder = 0u;
         __syncthreads();
         if (thr != 0ull) {
@@ -607,9 +722,10 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
                 Cx = (float)(om * key.mx / key.sx);
             }
             // U candidates per thread per step, all loads issued before any screen
-            constexpr int U = 4;
+            constexpr int U = 8;
             const float* nvg = nv + (int64_t)key.rep_g * p.total_len + st;
             const float* nxs = nx + st;
+            const uint32_t* pkg = pk ? pk + (int64_t)key.rep_g * p.total_len + st : nullptr;
             const float C = -(Cv + Cx), Cm = fabsf(Cv) + fabsf(Cx);
             for (int j0 = tid; j0 < n; j0 += kSelThreads * U) {
                 float av[U], bv[U];
@@ -617,8 +733,14 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
                         const int j = min(j0 + u * kSelThreads, n - 1);
-                        av[u] = nxs[j];
-                        bv[u] = nvg[j];
+                        if (pkg) {
+                            const uint32_t wd = pkg[j];
+                            av[u] = packed_nx(wd);
+                            bv[u] = packed_nv(wd);
+                        } else {
+                            av[u] = nxs[j];
+                            bv[u] = nvg[j];
+                        }
                     }
                 }
                 uint32_t pass = 0u;
@@ -647,18 +769,17 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
         __syncthreads();
         const int nb = (int)sh.nborder;
         if (thr != 0ull && nb >= K && nb <= cap) {
-            int nb2 = 1;
-            while (nb2 < nb) nb2 <<= 1;
-            for (int i = nb + tid; i < nb2; i += kSelThreads) sh.border[i] = 0ull;
+            // the survivors' keys are distinct (one per candidate index): the K at or above
+            // the K-th largest are the set, output by ascending index
+            const unsigned long long kk = kth_desc(sh, sh.border, nb, K - 1, tid);
+            if (tid == 0) sh.nsure = 0u;
             __syncthreads();
-            bitonic_desc_u64<kSelThreads>(sh.border, nb2, tid);
-            int ns2 = 1;
-            while (ns2 < K) ns2 <<= 1;
-            for (int i = tid; i < ns2; i += kSelThreads)
-                sh.sel[i] = i < K ? (int)(0xffffffffu - (uint32_t)(sh.border[i] & 0xffffffffull)) : 0x7fffffff;
+            for (int i = tid; i < nb; i += kSelThreads) {
+                const unsigned long long kj = sh.border[i];
+                if (kj >= kk) sh.sel[atomicAdd(&sh.nsure, 1u)] = (int)(0xffffffffu - (uint32_t)(kj & 0xffffffffull));
+            }
             __syncthreads();
-            bitonic_asc_i32<kSelThreads>(sh.sel, ns2, tid);
-            for (int i = tid; i < K; i += kSelThreads) out[i] = sh.sel[i];
+            rank_sort_asc(sh.sel, K, out, tid);
             return;
         }
         __syncthreads();
@@ -829,6 +950,8 @@ size_t select_workspace_cap(const SelectParams& p, int border_cap) {
     b += align256(sizeof(float) * (size_t)p.total_len * nsig);           // norms
     b += align256(sizeof(double) * 2 * (size_t)nranges * nsig);          // sums
     b += align256(sizeof(double) * 2 * (size_t)nranges * nsig);          // stats
+    if (p.select_mode != DSALT_SELECT_GLOBAL && p.dtype == DSALT_DTYPE_BF16)
+        b += align256(sizeof(uint32_t) * (size_t)p.total_len * p.n_kv_heads);  // packed norms
     if (p.select_mode == DSALT_SELECT_GLOBAL) {
         b += align256(sizeof(float) * (size_t)p.total_len * nsig);       // z
         if (p.k_lmk > 0) {
@@ -851,6 +974,11 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
     w += align256(sizeof(double) * 2 * (size_t)nranges * nsig);
     double* stats = (double*)w;
     w += align256(sizeof(double) * 2 * (size_t)nranges * nsig);
+    uint32_t* pk = nullptr;
+    if (!global && p.dtype == DSALT_DTYPE_BF16) {
+        pk = (uint32_t*)w;
+        w += align256(sizeof(uint32_t) * (size_t)p.total_len * p.n_kv_heads);
+    }
     float* zx = nullptr;
     float* zv = nullptr;
     if (global) {
@@ -862,11 +990,11 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
         const int blocks = ceil_div(p.total_len, kNormTB);
         const size_t shm = sizeof(double) * kNormTB * nsig;
         if (p.dtype == DSALT_DTYPE_BF16)
-            DSALT_LAUNCH("sel_norms", sel_norms_kernel<bf16>, dim3(blocks), dim3(256), shm, stream, p, nx, nv);
+            DSALT_LAUNCH("sel_norms", sel_norms_kernel<bf16>, dim3(blocks), dim3(256), shm, stream, p, nx, nv, pk);
         else if (p.dtype == DSALT_DTYPE_F16)
-            DSALT_LAUNCH("sel_norms", sel_norms_kernel<f16>, dim3(blocks), dim3(256), shm, stream, p, nx, nv);
+            DSALT_LAUNCH("sel_norms", sel_norms_kernel<f16>, dim3(blocks), dim3(256), shm, stream, p, nx, nv, nullptr);
         else
-            DSALT_LAUNCH("sel_norms", sel_norms_kernel<float>, dim3(blocks), dim3(256), shm, stream, p, nx, nv);
+            DSALT_LAUNCH("sel_norms", sel_norms_kernel<float>, dim3(blocks), dim3(256), shm, stream, p, nx, nv, nullptr);
         DSALT_LAUNCH("sel_sums", sel_sums_kernel, dim3(nranges, nsig), dim3(256), 0, stream, p, nx, nv, sums,
                      global ? stats : nullptr);
         if (global) {
@@ -884,7 +1012,7 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
     if (nsets_total == 0 || p.k_lmk == 0) return hipGetLastError();
     if (!global) {
         DSALT_LAUNCH("sel_topk", sel_topk_kernel, dim3(nsets_total), dim3(kSelThreads), 0, stream, p, zx, zv, nx, nv,
-                     stats, border_cap);
+                     pk, stats, border_cap);
         return hipGetLastError();
     }
     const TopkPlan t = topk_plan(p, border_cap);
