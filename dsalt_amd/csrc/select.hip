@@ -18,9 +18,11 @@
 //               (token, signal); sel_scores the optional per-head scores.
 //   top-k on the 64-bit key (order(score) << 32 | ~index), so ties go to the
 //   lower index; output ascending indices:
-//     global:   sel_part sorts the keys of each part of a set's candidates in
-//               LDS and keeps its best k; sel_merge sorts the survivors of up
-//               to G parts per block, level by level, and writes the indices.
+//     global:   sel_part keeps the best pow2(k) keys of each part of a set's
+//               candidates (the order statistic by radix passes, kth_desc);
+//               sel_merge does the same over the survivors of up to G parts per
+//               block, level by level, and the last level writes the indices in
+//               ascending order (by ranks).
 //     block:    sel_topk, one 1024-thread block per landmark set (largest sets
 //               first).  Sets of 8192+ candidates: a threshold key, the order
 //               statistic of a strided sample of 4096 found by radix passes
@@ -329,13 +331,24 @@ struct TopkShared {
     uint32_t ncand;
 };
 
+// LDS of kth_desc alone (the global top-k parts and merges)
+struct KthShared {
+    uint32_t hist[kSelWaves][256];
+    unsigned long long cand[kKthCand];
+    unsigned long long kth;
+    int digit;
+    uint32_t above;
+    uint32_t ncand;
+};
+
 // The r-th largest (0-based) of the n keys a[0..n) in LDS, for the whole block: radix
 // passes over 8-bit digits from the top (per-wave LDS histograms, as in the selection
 // below) narrow the keys to one digit prefix until at most kKthCand remain; those are
 // gathered and the answer is the candidate c with #{> c} <= r < #{>= c} (equal keys all
 // qualify and write the same value).  Exact for any keys; replaces a full sort where only
 // one order statistic is needed.
-__device__ unsigned long long kth_desc(TopkShared& sh, const unsigned long long* a, int n, int r, int tid) {
+template <class Sh>
+__device__ unsigned long long kth_desc(Sh& sh, const unsigned long long* a, int n, int r, int tid) {
     const int wave = tid >> 6, lane = tid & 63;
     unsigned long long prefix = 0ull;
     int plen = 0;
@@ -486,67 +499,9 @@ __device__ void bitonic_asc_i32(int* a, int n, int tid) {
         }
 }
 
-// Descending bitonic sort of N = NT*E 64-bit keys held E per thread (element
-// i = tid*E + e): partners within a thread swap in registers, partners in
-// another lane of the wave through lane shuffles, others through LDS (`lds`
-// holds N keys, stored key-slot-major so that a wave's accesses fall in
-// distinct banks).
-template <int NT, int E>
-__device__ void block_sort_desc(unsigned long long (&k)[E], unsigned long long* lds, int tid) {
-    constexpr int N = NT * E;
-#pragma unroll
-    for (int size = 2; size <= N; size <<= 1) {
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            if (stride < E) {
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    const int f = e ^ stride;
-                    if (f > e) {
-                        const bool desc = ((tid * E + e) & size) == 0;
-                        const unsigned long long x = k[e], y = k[f];
-                        const bool sw = desc ? (x < y) : (x > y);
-                        k[e] = sw ? y : x;
-                        k[f] = sw ? x : y;
-                    }
-                }
-            } else if (stride / E < 64) {  // partner lane in the same wave
-                const int m = stride / E;
-                const bool lower = (tid & m) == 0;
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    const int i = tid * E + e;
-                    const unsigned long long x = k[e];
-                    const uint32_t ylo = (uint32_t)__shfl_xor((int)(uint32_t)x, m, 64);
-                    const uint32_t yhi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), m, 64);
-                    const unsigned long long y = ((unsigned long long)yhi << 32) | ylo;
-                    const bool desc = (i & size) == 0;
-                    const unsigned long long hi = x > y ? x : y, lo = x > y ? y : x;
-                    k[e] = (lower == desc) ? hi : lo;
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < E; ++e) lds[e * NT + tid] = k[e];
-                __syncthreads();
-                const int pt = tid ^ (stride / E);
-                const bool lower = (tid & (stride / E)) == 0;
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    const int i = tid * E + e;
-                    const unsigned long long x = k[e], y = lds[e * NT + pt];
-                    const bool desc = (i & size) == 0;
-                    const unsigned long long hi = x > y ? x : y, lo = x > y ? y : x;
-                    k[e] = (lower == desc) ? hi : lo;
-                }
-                __syncthreads();
-            }
-        }
-    }
-}
-
 // ------------------------------------------- global variant: parts + merges
-constexpr int kPartMax = 2048;   // candidates per part (keys sorted in LDS)
-constexpr int kMergeMax = 4096;  // keys sorted per merge block (1024 threads x 4)
+constexpr int kPartMax = 2048;   // candidates per part (keys in LDS)
+constexpr int kMergeMax = 4096;  // keys per merge block
 
 __device__ __forceinline__ KeyFn global_key(const SelectParams& p, const float* zx, const float* zv, int st, int h) {
     KeyFn key;
@@ -566,14 +521,32 @@ __device__ __forceinline__ KeyFn global_key(const SelectParams& p, const float* 
     return key;
 }
 
-// part q of set (h, s): candidates [q*psize, (q+1)*psize); writes its kpad best
-// keys, descending (zero keys where it has fewer)
-constexpr int kSortThreads = 1024;
+// Writes the kpad largest of the n keys a[0..n) (LDS) to o, in no particular order: the keys
+// above the kpad-th largest, then copies of it (several only when it is 0, the key of no
+// candidate); with n <= kpad, every key and zeros after them.
+__device__ void keep_largest(KthShared& sh, const unsigned long long* a, int n, int kpad, unsigned long long* o,
+                             int tid) {
+    if (n <= kpad) {
+        for (int i = tid; i < kpad; i += kSelThreads) o[i] = i < n ? a[i] : 0ull;
+        return;
+    }
+    const unsigned long long kk = kth_desc(sh, a, n, kpad - 1, tid);
+    if (tid == 0) sh.ncand = 0u;
+    __syncthreads();
+    for (int i = tid; i < n; i += kSelThreads)
+        if (a[i] > kk) o[atomicAdd(&sh.ncand, 1u)] = a[i];
+    __syncthreads();
+    for (int i = (int)sh.ncand + tid; i < kpad; i += kSelThreads) o[i] = kk;
+}
+
+// part q of set (h, s): candidates [q*psize, (q+1)*psize); writes its kpad best keys
+// (zero keys where it has fewer)
+constexpr int kSortThreads = kSelThreads;
 
 __global__ __launch_bounds__(kSortThreads) void sel_part_kernel(SelectParams p, const float* zx, const float* zv,
                                                                 int psize, int nparts, int kpad,
                                                                 unsigned long long* out) {
-    constexpr int E = kPartMax / kSortThreads;
+    __shared__ KthShared sh;
     __shared__ unsigned long long keys[kPartMax];
     const int tid = threadIdx.x;
     const int part = blockIdx.x % nparts, sidx = blockIdx.x / nparts;
@@ -582,66 +555,47 @@ __global__ __launch_bounds__(kSortThreads) void sel_part_kernel(SelectParams p, 
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     const KeyFn key = global_key(p, zx, zv, st, h);
     const int j0 = part * psize;
-    unsigned long long kr[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int i = tid * E + e, j = j0 + i;
-        kr[e] = (i < psize && j < len) ? key(j) : 0ull;
-    }
-    block_sort_desc<kSortThreads, E>(kr, keys, tid);
-    unsigned long long* o = out + ((int64_t)sidx * nparts + part) * kpad;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int i = tid * E + e;
-        if (i < kpad) o[i] = kr[e];
-    }
+    const int n = max(0, min(psize, len - j0));
+    for (int i = tid; i < n; i += kSortThreads) keys[i] = key(j0 + i);
+    __syncthreads();
+    keep_largest(sh, keys, n, kpad, out + ((int64_t)sidx * nparts + part) * kpad, tid);
 }
 
-// merge parts [op*G, op*G+G) of set sidx (E keys per thread, 1024*E >= G*kpad):
-// with `out`, keep the kpad best keys; without, write the set's landmark
-// indices (ascending, -1 padded)
-template <int E>
+// merge parts [op*G, op*G+G) of set sidx (G*kpad <= kMergeMax keys): with `out`, keep
+// the kpad best keys; without, write the set's landmark indices (ascending, -1 padded)
 __global__ __launch_bounds__(kSortThreads) void sel_merge_kernel(SelectParams p, const unsigned long long* in,
                                                                  int nin, int G, int kpad, unsigned long long* out,
                                                                  int nout) {
-    __shared__ unsigned long long keys[kSortThreads * E];
+    __shared__ KthShared sh;
+    __shared__ unsigned long long keys[kMergeMax];
     __shared__ int sel[kMaxLandmarks];
     const int tid = threadIdx.x;
     const int op = blockIdx.x % nout, sidx = blockIdx.x / nout;
     const int q0 = op * G, q1 = min(nin, q0 + G);
     const int m = (q1 - q0) * kpad;
     const unsigned long long* src = in + ((int64_t)sidx * nin + q0) * kpad;
-    unsigned long long kr[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int i = tid * E + e;
-        kr[e] = i < m ? src[i] : 0ull;
-    }
-    block_sort_desc<kSortThreads, E>(kr, keys, tid);
+    for (int i = tid; i < m; i += kSortThreads) keys[i] = src[i];
+    __syncthreads();
     if (out) {
-        unsigned long long* o = out + ((int64_t)sidx * nout + op) * kpad;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const int i = tid * E + e;
-            if (i < kpad) o[i] = kr[e];
-        }
+        keep_largest(sh, keys, m, kpad, out + ((int64_t)sidx * nout + op) * kpad, tid);
         return;
     }
+    // the K largest keys: those above the K-th largest, and it when it is a candidate's
+    // key (keys of candidates are distinct; fewer than K candidates leave it 0)
     const int K = p.k_lmk;
-    int ks = 1;
-    while (ks < K) ks <<= 1;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int i = tid * E + e;
-        if (i < ks) {
-            const unsigned long long kj = i < K ? kr[e] : 0ull;
-            sel[i] = kj ? (int)(0xffffffffu - (uint32_t)(kj & 0xffffffffull)) : 0x7fffffff;
-        }
+    const unsigned long long kk = kth_desc(sh, keys, m, K - 1, tid);
+    if (tid == 0) sh.ncand = 0u;
+    __syncthreads();
+    for (int i = tid; i < m; i += kSortThreads) {
+        const unsigned long long kj = keys[i];
+        if (kj > kk || (kj == kk && kk != 0ull))
+            sel[atomicAdd(&sh.ncand, 1u)] = (int)(0xffffffffu - (uint32_t)(kj & 0xffffffffull));
     }
     __syncthreads();
-    bitonic_asc_i32<kSortThreads>(sel, ks, tid);
+    const int nsel = (int)sh.ncand;
     int32_t* o = p.lmk_idx + (int64_t)sidx * K;
-    for (int i = tid; i < K; i += kSortThreads) o[i] = sel[i] == 0x7fffffff ? -1 : sel[i];
+    rank_sort_asc(sel, nsel, o, tid);
+    for (int i = nsel + tid; i < K; i += kSortThreads) o[i] = -1;
 }
 
 __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, const float* zx, const float* zv,
@@ -1021,16 +975,10 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
     unsigned long long* kb2 = (unsigned long long*)(w + kb);
     DSALT_LAUNCH("sel_part", sel_part_kernel, dim3(nsets_total * t.nparts), dim3(kSortThreads), 0, stream, p, zx, zv,
                  t.psize, t.nparts, t.kpad, ka);
-    // keys per merge block <= kMergeMax; sort width from the largest group
+    // keys per merge block <= kMergeMax
     auto merge = [&](int nin, unsigned long long* out, int nout) {
-        const int keysn = min(nin, t.G) * t.kpad;
-        const dim3 grid(nsets_total * nout), blk(kSortThreads);
-        if (keysn <= kSortThreads)
-            DSALT_LAUNCH("sel_merge", sel_merge_kernel<1>, grid, blk, 0, stream, p, ka, nin, t.G, t.kpad, out, nout);
-        else if (keysn <= 2 * kSortThreads)
-            DSALT_LAUNCH("sel_merge", sel_merge_kernel<2>, grid, blk, 0, stream, p, ka, nin, t.G, t.kpad, out, nout);
-        else
-            DSALT_LAUNCH("sel_merge", sel_merge_kernel<4>, grid, blk, 0, stream, p, ka, nin, t.G, t.kpad, out, nout);
+        DSALT_LAUNCH("sel_merge", sel_merge_kernel, dim3(nsets_total * nout), dim3(kSortThreads), 0, stream, p, ka,
+                     nin, t.G, t.kpad, out, nout);
     };
     int nin = t.nparts;
     while (nin > t.G) {
