@@ -32,7 +32,7 @@
 //               by the same radix passes and the K survivors at or above it, output
 //               in index order by ranks; when the sample misplaces the threshold,
 //               and for smaller sets: radix select 8 bits per pass until the boundary
-//               bin fits in LDS, then a bitonic sort of that bin.
+//               bin fits in LDS, then its order statistic by kth_desc.
 // The arithmetic order above is the canonical one that the CPU oracle
 // restates; this file is compiled with -ffp-contract=off.
 #include "common.h"
@@ -464,41 +464,6 @@ struct KeyFn {
 
 
 
-// bitonic sorts of n (a power of two) LDS elements by NT threads
-template <int NT>
-__device__ void bitonic_desc_u64(unsigned long long* a, int n, int tid) {
-    for (int size = 2; size <= n; size <<= 1)
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = tid; i < (n >> 1); i += NT) {
-                int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1)), hi = lo + stride;  // stride: a power of two
-                bool desc = (lo & size) == 0;
-                unsigned long long x = a[lo], y = a[hi];
-                if ((x < y) == desc) {
-                    a[lo] = y;
-                    a[hi] = x;
-                }
-            }
-            __syncthreads();
-        }
-}
-
-template <int NT>
-__device__ void bitonic_asc_i32(int* a, int n, int tid) {
-    for (int size = 2; size <= n; size <<= 1)
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = tid; i < (n >> 1); i += NT) {
-                int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1)), hi = lo + stride;  // stride: a power of two
-                bool asc = (lo & size) == 0;
-                int x = a[lo], y = a[hi];
-                if ((x > y) == asc) {
-                    a[lo] = y;
-                    a[hi] = x;
-                }
-            }
-            __syncthreads();
-        }
-}
-
 // ------------------------------------------- global variant: parts + merges
 constexpr int kPartMax = 2048;   // candidates per part (keys in LDS)
 constexpr int kMergeMax = 4096;  // keys per merge block
@@ -813,24 +778,20 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
         else if (top == prefix) sh.border[atomicAdd(&sh.nborder, 1u)] = kj;
     }
     __syncthreads();
-    int nsel = (int)sh.nsure;
     if (!all_sure) {
-        int nb = (int)sh.nborder, nb2 = 1;
-        while (nb2 < nb) nb2 <<= 1;
-        for (int i = nb + tid; i < nb2; i += kSelThreads) sh.border[i] = 0ull;
-        __syncthreads();
-        bitonic_desc_u64<kSelThreads>(sh.border, nb2, tid);
-        for (int i = tid; i < (int)k_rem; i += kSelThreads)
-            sh.sel[nsel + i] = (int)(0xffffffffu - (uint32_t)(sh.border[i] & 0xffffffffull));
-        nsel += (int)k_rem;
+        // the k_rem largest of the boundary bin (distinct candidate keys): at or above its
+        // k_rem-th largest
+        const int nb = (int)sh.nborder;
+        const unsigned long long kk = kth_desc(sh, sh.border, nb, (int)k_rem - 1, tid);
+        for (int i = tid; i < nb; i += kSelThreads) {
+            const unsigned long long kj = sh.border[i];
+            if (kj >= kk) sh.sel[atomicAdd(&sh.nsure, 1u)] = (int)(0xffffffffu - (uint32_t)(kj & 0xffffffffull));
+        }
         __syncthreads();
     }
-    int ns2 = 1;
-    while (ns2 < nsel) ns2 <<= 1;
-    for (int i = nsel + tid; i < ns2; i += kSelThreads) sh.sel[i] = 0x7fffffff;
-    __syncthreads();
-    bitonic_asc_i32<kSelThreads>(sh.sel, ns2, tid);
-    for (int i = tid; i < K; i += kSelThreads) out[i] = i < nsel ? sh.sel[i] : -1;
+    const int nsel = (int)sh.nsure;
+    rank_sort_asc(sh.sel, nsel, out, tid);
+    for (int i = nsel + tid; i < K; i += kSelThreads) out[i] = -1;
 }
 
 // --------------------------------------------------------------- gather
