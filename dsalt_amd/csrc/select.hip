@@ -55,14 +55,28 @@ __device__ __forceinline__ int pow2ceil64(int n) {
 constexpr int kNormTPW = 1;              // tokens per wave
 constexpr int kNormTB = 4 * kNormTPW;    // tokens per 256-thread block
 
-// bf16 inputs: the norms are bf16 values, so a token's |h| and |v_g| pack losslessly into
-// one word, pk[g][t] = bf16(|v_g|) << 16 | bf16(|h|); the block-causal top-k reads that
-// word (half the bytes of the two fp32 arrays) in its prefix scans
-__device__ __forceinline__ uint32_t pack_norms(float nx, float nv) {
-    return (__float_as_uint(nv) & 0xffff0000u) | (__float_as_uint(nx) >> 16);
+// bf16 inputs: the norms are non-negative bf16 values, so a token's |h| and |v_g| pack
+// losslessly into one word, pk[g][t] = bf16(|v_g|) << 16 | bf16(|h|), whose bit 15 (the
+// sign of |h|) instead flags a token that is never a candidate (its own window reaches
+// its sequence start, j_rel < w_j).  The block-causal top-k reads only that word per
+// candidate in its prefix scans: no window load, and exact keys straight from it.
+constexpr uint32_t kExcluded = 0x8000u;
+__device__ __forceinline__ uint32_t pack_norms(float nx, float nv, bool excluded) {
+    return (__float_as_uint(nv) & 0xffff0000u) | (__float_as_uint(nx) >> 16) | (excluded ? kExcluded : 0u);
 }
-__device__ __forceinline__ float packed_nx(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float packed_nx(uint32_t w) { return __uint_as_float((w << 16) & 0x7fff0000u); }
 __device__ __forceinline__ float packed_nv(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// sequence of packed token t: the last s whose (clamped) start is <= t
+__device__ __forceinline__ int seq_of(const SelectParams& p, int t) {
+    int lo = 0, hi = p.num_seqs - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (min(max(p.cu[mid], 0), p.total_len) <= t) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
 
 template <typename T>
 __global__ __launch_bounds__(256) void sel_norms_kernel(SelectParams p, float* nx, float* nv, uint32_t* pk) {
@@ -112,6 +126,12 @@ __global__ __launch_bounds__(256) void sel_norms_kernel(SelectParams p, float* n
             if (sub == 0 && g < p.n_kv_heads) ss[tl * nsig + 1 + g] = a2;
         }
     }
+    __shared__ bool excl[kNormTB];
+    if (pk && threadIdx.x < kNormTB && t0 + (int)threadIdx.x < p.total_len) {
+        const int t = t0 + threadIdx.x;
+        const int st = min(max(p.cu[seq_of(p, t)], 0), p.total_len);
+        excl[threadIdx.x] = t - st < p.w[t];
+    }
     __syncthreads();
     for (int idx = threadIdx.x; idx < kNormTB * nsig; idx += 256) {
         const int tl = idx / nsig, sig = idx % nsig, t = t0 + tl;
@@ -120,7 +140,8 @@ __global__ __launch_bounds__(256) void sel_norms_kernel(SelectParams p, float* n
         if (sig == 0) nx[t] = nr;
         else nv[(int64_t)(sig - 1) * p.total_len + t] = nr;
         if (pk && sig > 0)
-            pk[(int64_t)(sig - 1) * p.total_len + t] = pack_norms(round_norm<T>((float)canon_sqrt64(ss[tl * nsig])), nr);
+            pk[(int64_t)(sig - 1) * p.total_len + t] =
+                pack_norms(round_norm<T>((float)canon_sqrt64(ss[tl * nsig])), nr, excl[tl]);
     }
 }
 
@@ -444,21 +465,26 @@ struct KeyFn {
     const uint32_t* pk;  // packed norms (bf16 inputs), or null
     double mx, sx, mv, sv, rsx, rsv;
     __device__ __forceinline__ unsigned long long operator()(int j) const {
+        if (block && pk) return packed(j, pk[(int64_t)rep_g * total_len + st + j]);
         if (j < w[st + j]) return 0ull;
         float zxj, zvj;
         if (!block) {
             zxj = zx[st + j];
             zvj = zv[(int64_t)rep_g * total_len + st + j];
-        } else if (pk) {
-            const uint32_t wd = pk[(int64_t)rep_g * total_len + st + j];
-            zxj = zscore_rcp(packed_nx(wd), mx, sx, rsx);
-            zvj = zscore_rcp(packed_nv(wd), mv, sv, rsv);
         } else {
             zxj = zscore_rcp(nx[st + j], mx, sx, rsx);
             zvj = zscore_rcp(nv[(int64_t)rep_g * total_len + st + j], mv, sv, rsv);
         }
-        uint32_t u = order_key(mix_score(alpha, zvj, zxj));
-        return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)j);
+        return of_score(j, mix_score(alpha, zvj, zxj));
+    }
+    // block-causal key of candidate j from its packed norms word
+    __device__ __forceinline__ unsigned long long packed(int j, uint32_t wd) const {
+        if (wd & kExcluded) return 0ull;
+        return of_score(j, mix_score(alpha, zscore_rcp(packed_nv(wd), mv, sv, rsv),
+                                     zscore_rcp(packed_nx(wd), mx, sx, rsx)));
+    }
+    __device__ __forceinline__ static unsigned long long of_score(int j, float sc) {
+        return ((unsigned long long)order_key(sc) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)j);
     }
 };
 
@@ -648,15 +674,17 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
             const float C = -(Cv + Cx), Cm = fabsf(Cv) + fabsf(Cx);
             for (int j0 = tid; j0 < n; j0 += kSelThreads * U) {
                 float av[U], bv[U];
+                uint32_t wds[U];
                 if (block) {
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
                         const int j = min(j0 + u * kSelThreads, n - 1);
                         if (pkg) {
-                            const uint32_t wd = pkg[j];
-                            av[u] = packed_nx(wd);
-                            bv[u] = packed_nv(wd);
+                            wds[u] = pkg[j];
+                            av[u] = packed_nx(wds[u]);
+                            bv[u] = packed_nv(wds[u]);
                         } else {
+                            wds[u] = 0u;
                             av[u] = nxs[j];
                             bv[u] = nvg[j];
                         }
@@ -667,6 +695,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
                 for (int u = 0; u < U; ++u) {
                     const int j = j0 + u * kSelThreads;
                     bool maybe = j < n;
+                    if (pkg) maybe = maybe && !(wds[u] & kExcluded);
                     if (block && maybe) {
                         const float sa = fmaf(A, bv[u], fmaf(B, av[u], C));
                         const float M = fabsf(A * bv[u]) + fabsf(B * av[u]) + Cm;
@@ -677,7 +706,11 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
                 while (pass) {  // exact keys of the few survivors (one copy of the key code)
                     const int u = __builtin_ctz(pass);
                     pass &= pass - 1u;
-                    const unsigned long long kj = key(j0 + u * kSelThreads);
+                    const int j = j0 + u * kSelThreads;
+                    uint32_t wd = 0u;
+#pragma unroll
+                    for (int v = 0; v < U; ++v) wd = v == u ? wds[v] : wd;
+                    const unsigned long long kj = pkg ? key.packed(j, wd) : key(j);
                     if (kj >= thr) {
                         const uint32_t slot = atomicAdd(&sh.nborder, 1u);
                         if (slot < (uint32_t)cap) sh.border[slot] = kj;
