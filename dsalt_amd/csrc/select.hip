@@ -594,12 +594,13 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
                                                                const double* stats, int border_cap) {
     __shared__ TopkShared sh;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    // later blocks scan longer prefixes: dispatch them first (largest sets first balances
-    // the tail); every (head, sequence) of one set index is adjacent
-    const int hs = p.n_heads * p.num_seqs;
-    const int set = p.n_sets - 1 - (int)(blockIdx.x / hs);
-    const int s = (blockIdx.x % hs) % p.num_seqs;
-    const int h = (blockIdx.x % hs) / p.num_seqs;
+    // blocks of one (head, sequence) are contiguous in the XCD-swizzled order, so each XCD's
+    // L2 holds the norms of few heads; within them later sets, which scan longer prefixes,
+    // come first (largest sets first balances the tail)
+    const int Lb = xcd_swizzle(blockIdx.x, p.n_heads * p.num_seqs * p.n_sets);
+    const int set = p.n_sets - 1 - Lb % p.n_sets;
+    const int s = (Lb / p.n_sets) % p.num_seqs;
+    const int h = (Lb / p.n_sets) / p.num_seqs;
     const int K = p.k_lmk;
     int32_t* out = p.lmk_idx + (((int64_t)h * p.num_seqs + s) * p.n_sets + set) * K;
     int st, len;
