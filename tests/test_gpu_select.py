@@ -134,3 +134,12 @@ def test_block_workload_selection_bit_exact_long_prefixes():
     idx, ridx = _run(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, ops.SELECT_BLOCK, 512,
                      ops.STATS_SEQUENCE, want=False)
     np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
+def test_block_sampled_path_packed_sequences_gqa():
+    # several sequences (one empty) whose later sets hold 8192+ candidates: the sampled
+    # threshold, packed norms with their exclusion flags and the order statistics run at
+    # nonzero sequence starts, with two query heads per value head
+    h, v, alpha, w, cu = _case([20000, 0, 17000], 128, 2, 64, 4, torch.bfloat16, 300, seed=5)
+    idx, ridx = _run(h, v, alpha, w, cu, 64, ops.SELECT_BLOCK, 512, ops.STATS_SEQUENCE, want=False)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
