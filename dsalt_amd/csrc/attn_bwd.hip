@@ -26,7 +26,7 @@
 namespace dsalt {
 
 constexpr float kLog2eB = 1.4426950408889634f;
-constexpr int kRowChunk = 1024;
+constexpr int kRowChunk = 1024;  // rows per landmark-backward block (ceil(max_seqlen / kRowChunk) blocks share a sequence)
 constexpr int kSeg = 512;  // rows compacted at a time in the dK/dV sweep
 
 template <typename T, int D> struct BwdShape;
@@ -647,8 +647,11 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_
 }
 
 // -------------------------------------------------------- landmark dK/dV
-// Block = (head, sequence, 1024-row chunk, group of 64*kLmkSub slots); wave w
-// owns slots grp*64*kLmkSub + 16*kLmkSub*w .. as kLmkSub 16-slot subtiles.
+// Block = (head, sequence, chunk c, group of 64*kLmkSub slots); wave w owns slots
+// grp*64*kLmkSub + 16*kLmkSub*w .. as kLmkSub 16-slot subtiles.  Chunk c takes the
+// BQ-row tiles c, c + n_chunks, c + 2 n_chunks, ... of the sequence: a row sees more
+// landmarks the later it is, so strided tiles give every block the same work (the
+// kernel lasts as long as its longest block).
 constexpr int kLmkSub = 1;
 constexpr int kLmkGroup = 64 * kLmkSub;
 
@@ -680,7 +683,6 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     const int64_t set_off = (((int64_t)h * p.num_seqs + s) * p.n_sets) * K;
     const float c2 = p.c2;
     const float inv_scale = p.inv_scale;
-    const int rbeg = chunk * kRowChunk, rend = min(len, rbeg + kRowChunk);
     const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid);
 
     // slots of this lane (kLmkSub subtiles)
@@ -713,22 +715,26 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     const T* db = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
     const float NEG = -INFINITY;
     const int lane_off = 4 * g;
-    // first row with any visible landmark: lo_i > lpos[0]  =>  i > lpos[0]
+    // first row with any visible landmark: lo_i > lpos[0]  =>  i > lpos[0]; tiles wholly
+    // before it are skipped
     const int first_row = nvalid > 0 ? lpos[0] + 1 : 0x7fffffff;
-    const int istart = max(rbeg, (first_row / BQ) * BQ);
+    const int ntile = ceil_div(len, BQ);
+    int t0 = chunk;
+    if (nvalid > 0 && t0 < first_row / BQ) t0 += ceil_div(first_row / BQ - t0, p.n_chunks) * p.n_chunks;
     // the loop bound is uniform over the block (every wave reaches each barrier);
     // waves whose slots are all empty skip their products through act[] below
     const bool any_slot = grp * kLmkGroup < nvalid;
     QLoader<T, D, BQ> ld(p, tid);
     // rows staged in LDS; visible landmark counts come from the dQ pass
-    for (int i0 = istart; any_slot && i0 < rend; i0 += BQ) {
-        ld.load(p, qb, db, i0, rend, tid);
+    for (int t = t0; any_slot && t < ntile; t += p.n_chunks) {
+        const int i0 = t * BQ;
+        ld.load(p, qb, db, i0, len, tid);
         __syncthreads();
         ld.store(q, tid);
         if (tid < BQ) {
             const int i = i0 + tid;
             int c = 0;
-            if (i < rend) {
+            if (i < len) {
                 c = p.cnt[(int64_t)(st + i) * p.n_heads + h];
                 q.lse2[tid] = p.lse[(int64_t)(st + i) * p.n_heads + h] * kLog2eB;
                 q.dlt[tid] = p.delta[(int64_t)(st + i) * p.n_heads + h];
