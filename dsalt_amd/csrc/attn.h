@@ -49,8 +49,9 @@ struct AttnParams {
     uint8_t* plan_perm;      // [S * n_tiles * 64] row offset within the tile
     int* plan_bounds;        // [S * n_tiles * 4 * 4]
     // backward workspace
-    float* delta;            // [T, H]
-    int* cnt;                // [T, H] landmarks visible to each row (written by the dQ pass)
+    float* delta;            // [H, T] rowsum(O * dO), head-major (written by the dQ pass)
+    int* cnt;                // [H, T] landmarks visible to each row (written by the dQ pass)
+    float* lse2t;            // [H, T] LSE * log2(e), head-major (written by the dQ pass)
     int* seq_wmax;           // [S] max clamped window per sequence
     float* part_k;           // [n_chunks, H, S, K, D] landmark dK partials
     float* part_v;           // [n_chunks, H, S, K, D]

@@ -132,7 +132,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (TR ? 5 : 6) : 2
     if (TR) edge_table(p, wt, etb, etg);
     const int lo_edge = TR ? wLmax + p.edge_keys : wLmax;  // keys from here on carry no edge bias
     float dwacc = 0.f;
-    if (valid && g == 0 && p.cnt) p.cnt[(int64_t)(st + i) * p.n_heads + h] = cnt;
+    // per-row data of the key-parallel passes, head-major: a head's rows are contiguous
+    const int64_t hrow = (int64_t)h * p.total_len + st + i;
+    if (valid && g == 0 && p.cnt) p.cnt[hrow] = cnt;
     const int wcmax = uniform(row_max16(cnt)), wcmin = uniform(row_min16(valid ? cnt : 0));
     if (lane == 0) red[uw] = wcmax;
     __syncthreads();
@@ -163,7 +165,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (TR ? 5 : 6) : 2
     float lse2 = 0.f;
     if (valid) {
         lse2 = p.lse[(int64_t)(st + i) * p.n_heads + h] * kLog2eB;
-        if (g == 0) p.delta[(int64_t)(st + i) * p.n_heads + h] = dlt;
+        if (g == 0) {
+            p.delta[hrow] = dlt;
+            p.lse2t[hrow] = lse2;
+        }
     }
 
     const T* kbase = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)kvh * p.k_sh;
@@ -418,16 +423,16 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_
     const T* qb = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
     const T* db = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
     const int* wrow = p.w + st;
-    const float* lrow = p.lse + (int64_t)st * p.n_heads + h;
-    const float* drow = p.delta + (int64_t)st * p.n_heads + h;
+    const float* lrow = p.lse2t + (int64_t)h * p.total_len + st;
+    const float* drow = p.delta + (int64_t)h * p.total_len + st;
     QLoader<T, D, BQ> ld(p, tid);
     // per-row data of staged row i (or of no row when !ok)
     auto stage_row = [&](QS& q, int r, int i, bool ok) {
         if (ok) {
             const int wi = max(wrow[i], 1);
             q.key[r] = max(i - wi + 1, 0);
-            q.lse2[r] = lrow[(int64_t)i * p.n_heads] * kLog2eB;
-            q.dlt[r] = drow[(int64_t)i * p.n_heads];
+            q.lse2[r] = lrow[i];
+            q.dlt[r] = drow[i];
             if (TR) {
                 q.wt[r] = p.w_cont[st + i];
                 q.ri[r] = i;
@@ -735,9 +740,10 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
             const int i = i0 + tid;
             int c = 0;
             if (i < len) {
-                c = p.cnt[(int64_t)(st + i) * p.n_heads + h];
-                q.lse2[tid] = p.lse[(int64_t)(st + i) * p.n_heads + h] * kLog2eB;
-                q.dlt[tid] = p.delta[(int64_t)(st + i) * p.n_heads + h];
+                const int64_t hr = (int64_t)h * p.total_len + st + i;
+                c = p.cnt[hr];
+                q.lse2[tid] = p.lse2t[hr];
+                q.dlt[tid] = p.delta[hr];
             } else {
                 q.lse2[tid] = 0.f;
                 q.dlt[tid] = 0.f;
@@ -888,6 +894,7 @@ size_t bwd_workspace(const AttnParams& p) {
     size_t b = plan_bytes(p);
     b += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
     b += al(sizeof(int) * (size_t)p.total_len * p.n_heads);
+    b += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
     b += al(sizeof(int) * (size_t)p.num_seqs);
     b += 2 * al(sizeof(float) * (size_t)nch * p.n_heads * p.num_seqs * p.k_lmk * p.head_dim);
     b += al(sizeof(float) * (size_t)nch * p.n_heads * p.num_seqs * p.k_lmk);
@@ -925,6 +932,8 @@ hipError_t bwd_launch(AttnParams p, void* ws, hipStream_t stream) {
     w += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
     p.cnt = (int*)w;
     w += al(sizeof(int) * (size_t)p.total_len * p.n_heads);
+    p.lse2t = (float*)w;
+    w += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
     p.seq_wmax = (int*)w;
     w += al(sizeof(int) * (size_t)p.num_seqs);
     const size_t npart = (size_t)p.n_chunks * p.n_heads * p.num_seqs * p.k_lmk;
