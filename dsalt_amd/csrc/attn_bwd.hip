@@ -26,7 +26,7 @@
 namespace dsalt {
 
 constexpr float kLog2eB = 1.4426950408889634f;
-constexpr int kRowChunk = 1024;  // rows per landmark-backward block (ceil(max_seqlen / kRowChunk) blocks share a sequence)
+constexpr int kRowChunk = 1024;  // rows per landmark-backward block, at most
 constexpr int kSeg = 512;  // rows compacted at a time in the dK/dV sweep
 
 template <typename T, int D> struct BwdShape;
@@ -888,9 +888,19 @@ hipError_t train_dw_launch(const AttnParams& p, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------- launch
+// blocks of the landmark backward per (head, sequence, slot group): at most kRowChunk rows
+// each, and more (down to one 64-row tile each) until the launch has about four blocks per
+// CU, since a block's rows are one dependent chain of staged tiles
+static int lmk_chunks(const AttnParams& p) {
+    const int ngrp = ceil_div(p.k_lmk, kLmkGroup);
+    const int sets = max(1, p.n_heads * p.num_seqs * ngrp);
+    const int fill = ceil_div(1024, sets);
+    return max(ceil_div(p.max_seqlen, kRowChunk), min(fill, ceil_div(p.max_seqlen, 64)));
+}
+
 size_t bwd_workspace(const AttnParams& p) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    const int nch = ceil_div(p.max_seqlen, kRowChunk);
+    const int nch = lmk_chunks(p);
     size_t b = plan_bytes(p);
     b += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
     b += al(sizeof(int) * (size_t)p.total_len * p.n_heads);
@@ -925,7 +935,7 @@ static void bwd_run(const AttnParams& p, hipStream_t stream) {
 
 hipError_t bwd_launch(AttnParams p, void* ws, hipStream_t stream) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    p.n_chunks = ceil_div(p.max_seqlen, kRowChunk);
+    p.n_chunks = lmk_chunks(p);
     char* w = (char*)ws;
     plan_carve(p, w);
     p.delta = (float*)w;
