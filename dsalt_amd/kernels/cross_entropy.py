@@ -142,6 +142,8 @@ class LigerFusedLinearCrossEntropyFunction(torch.autograd.Function):
             return_z_loss=return_z_loss, accum_dtype=accum_dtype, use_token_scaling=use_token_scaling,
             return_token_accuracy=return_token_accuracy, return_predicted_tokens=return_predicted_tokens)
         ctx.save_for_backward(gi, gw, gb)
+        if acc is not None:
+            ctx.mark_non_differentiable(acc)  # a count ratio: no gradient flows through it
         return loss, z_loss, acc, pred
 
     @staticmethod
