@@ -290,6 +290,12 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
         koff[n] = KT::row_offset(tid, n, krb);
         voff[n] = KT::row_offset(tid, n, vrb);
     }
+    // landmark rows: 32-bit offsets into resources over the sequence's rows when the
+    // sequence spans less than 2 GiB of K and of V, else 64-bit row addresses (always
+    // for fp32 D128, where the offsets would cost a wave of occupancy)
+    const uint32_t kext = gather_extent(len, krb, D * sizeof(T)), vext = gather_extent(len, vrb, D * sizeof(T));
+    const bool lmk32 = (D == 64 || sizeof(T) == 2) && kext != 0u && vext != 0u;
+    const rsrc_t krs = make_rsrc(kbase, kext), vrs = make_rsrc(vbase, vext);
     KT kt, vt;
     auto load_chunk = [&](int c) {
         if (c < nband) {
@@ -303,10 +309,17 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
                 const int q = sl < bcm ? lpos[sl] : -1;
                 return q < len ? q : -1;
             };
-            kt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr; },
-                    kbase);
-            vt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr; },
-                    vbase);
+            if (lmk32) {
+                uint32_t ko[KT::NV], vo[KT::NV];
+                KT::gather_offsets(tid, pos, krb, vrb, ko, vo);
+                kt.load_rows(krs, ko);
+                vt.load_rows(vrs, vo);
+            } else {
+                kt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr; },
+                        kbase);
+                vt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr; },
+                        vbase);
+            }
         }
     };
     if (nchunks > 0) {

@@ -44,6 +44,15 @@ __device__ __forceinline__ rsrc_t rows_rsrc(const void* base, int rows, uint32_t
     return make_rsrc(base, n);
 }
 
+// Gathered-row offset of a missing row: beyond every resource of at most 2^31 bytes.
+constexpr uint32_t kNoRow = 0x80000000u;
+// Byte extent of `rows` token rows (stride row_bytes, row_len bytes used), or 0 when
+// it exceeds 2^31 - 1 and gathered rows must take 64-bit addresses instead.
+__device__ __forceinline__ uint32_t gather_extent(int rows, uint32_t row_bytes, uint32_t row_len) {
+    const int64_t n = rows > 0 ? (int64_t)(rows - 1) * row_bytes + row_len : 0;
+    return n <= 0x7fffffff ? (uint32_t)n : 0u;
+}
+
 template <typename T, int D, int ROWS>
 struct Tile {
     static constexpr int VW = 16 / (int)sizeof(T);  // elements per 16-byte vector
@@ -71,7 +80,21 @@ struct Tile {
         const int vi = tid + 256 * n;
         return (uint32_t)(vi / CPR) * row_bytes + (uint32_t)(vi % CPR) * 16u;
     }
-    // consecutive rows through a buffer resource (zero past its bound)
+    // byte offsets of this thread's vectors for gathered rows of two tensors (row
+    // strides rb0, rb1): row(rr) is the token row of tile row rr, or -1 for a zero
+    // row, which gets kNoRow (past any resource of at most 2^31 bytes)
+    template <typename RowFn>
+    __device__ __forceinline__ static void gather_offsets(int tid, RowFn row, uint32_t rb0, uint32_t rb1,
+                                                          uint32_t (&o0)[NV], uint32_t (&o1)[NV]) {
+#pragma unroll
+        for (int n = 0; n < NV; ++n) {
+            const int vi = tid + 256 * n, rr = vi / CPR, c = vi % CPR;
+            const int j = row(rr);
+            o0[n] = j >= 0 ? (uint32_t)j * rb0 + (uint32_t)c * 16u : kNoRow;
+            o1[n] = j >= 0 ? (uint32_t)j * rb1 + (uint32_t)c * 16u : kNoRow;
+        }
+    }
+    // rows through a buffer resource at per-thread offsets (zero past its bound)
     __device__ __forceinline__ void load_rows(rsrc_t rs, const uint32_t (&off)[NV]) {
 #pragma unroll
         for (int n = 0; n < NV; ++n) r[n] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[n], 0, 0);
