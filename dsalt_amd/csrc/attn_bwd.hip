@@ -747,20 +747,20 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     for (int t = t0; any_slot && t < ntile; t += p.n_chunks) {
         const int i0 = t * BQ;
         ld.load(p, qb, db, i0, len, tid);
+        // per-row data loaded with the tile (one memory latency per tile)
+        int c = 0;
+        float rl = 0.f, rd = 0.f;
+        if (tid < BQ && i0 + tid < len) {
+            const int64_t hr = (int64_t)h * p.total_len + st + i0 + tid;
+            c = p.cnt[hr];
+            rl = p.lse2t[hr];
+            rd = p.delta[hr];
+        }
         __syncthreads();
         ld.store(q, tid);
         if (tid < BQ) {
-            const int i = i0 + tid;
-            int c = 0;
-            if (i < len) {
-                const int64_t hr = (int64_t)h * p.total_len + st + i;
-                c = p.cnt[hr];
-                q.lse2[tid] = p.lse2t[hr];
-                q.dlt[tid] = p.delta[hr];
-            } else {
-                q.lse2[tid] = 0.f;
-                q.dlt[tid] = 0.f;
-            }
+            q.lse2[tid] = rl;
+            q.dlt[tid] = rd;
             q.key[tid] = c;
             const int mn = row_min16(c), mx = row_max16(c);
             if ((tid & 15) == 0) {
