@@ -145,3 +145,41 @@ def test_bwd_long_windows(dt):
 
 def test_bwd_long_windows_d128():
     _bwd_check(torch.bfloat16, [1500, 90], 2, 128, 8, 1500, seed=15, bias=True)
+
+
+@pytest.mark.parametrize("T", [2000, 2100])
+def test_landmark_rows_far_apart_in_memory(T):
+    """K and V rows 1 MiB apart (strided views of wide buffers; the largest token stride
+    the boundary accepts): 2000 rows span just under 2 GiB, so landmark rows are reached
+    through 32-bit offsets close to their limit; 2100 rows span more and take 64-bit row
+    addresses.  Forward and backward must equal the
+    contiguous layout bit for bit."""
+    H, D, K = 2, 64, 32
+    dt = torch.bfloat16
+    q, k, v, w, cu, idx, _, maxlen = _inputs([T], H, H, D, K, 300, dt, seed=31)
+    g = torch.Generator().manual_seed(32)
+    dout = torch.randn(T, H, D, generator=g).to(dt)
+    dev = [t.to(DEV) for t in (q, k, v, w, cu, idx, dout)]
+    q_d, k_d, v_d, w_d, cu_d, idx_d, do_d = dev
+    row = 1 << 19  # elements per row of the wide buffers (1 MiB in bf16)
+    kw = torch.zeros(T, row, dtype=dt, device=DEV)
+    vw = torch.zeros(T, row, dtype=dt, device=DEV)
+    k_s = kw[:, :H * D].view(T, H, D)
+    v_s = vw[:, :H * D].view(T, H, D)
+    k_s.copy_(k_d)
+    v_s.copy_(v_d)
+    assert k_s.stride(0) == row and ((T - 1) * row * 2 < 2 ** 31) == (T == 2000)
+    res = []
+    for kk, vv in ((k_d, v_d), (k_s, v_s)):
+        out, lse = ops.attention_forward(q_d, kk, vv, w_d, cu_d, idx_d, None, max_seqlen=maxlen)
+        dq, dk, dv, _ = ops.attention_backward(do_d, q_d, kk, vv, out, lse, w_d, cu_d, idx_d, None,
+                                               max_seqlen=maxlen, want_dbias=False)
+        torch.cuda.synchronize()
+        res.append([t.cpu() for t in (out, lse, dq, dk, dv)])
+    del kw, vw, k_s, v_s
+    torch.cuda.empty_cache()
+    for name, a, b in zip(("out", "lse", "dq", "dk", "dv"), *res):
+        assert torch.equal(a, b), name
+    # and the contiguous result is the operator's (oracle at the bf16 tolerance)
+    ro, _ = OA.attention_fwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), 1.0 / math.sqrt(D))
+    assert rel_err(f64(res[0][0]), ro) < TOL[dt]
