@@ -49,7 +49,8 @@ def parse():
     return ap.parse_args()
 
 
-LABELS = ("sel_norms", "sel_sums", "sel_stats", "sel_z", "sel_scores", "sel_part", "sel_merge", "sel_topk", "gather",
+LABELS = ("sel_norms", "sel_sums", "sel_stats", "sel_z", "sel_scores", "sel_part", "sel_merge", "sel_prune_hist",
+          "sel_prune_prefix", "sel_prune_mark", "sel_prune_list", "sel_topk", "gather",
           "row_plan", "attn_fwd", "bwd_init", "bwd_dq", "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum", "train_windows", "train_dw",
           "rope", "silu_mul", "probs", "ce_rows")
 
@@ -59,7 +60,8 @@ def short_kernel_name(name: str) -> str:
     import re
     # the label must start the identifier (a mangled length prefix, "::" or the start): no
     # match inside library names such as reduce_kernel or vectorized_gather_kernel
-    m = re.search(r"(?<![A-Za-z_])(sel_norms|sel_sums|sel_stats|sel_z|sel_scores|sel_part|sel_merge|sel_topk|gather|row_plan|fwd|bwd_init|bwd_dq|"
+    m = re.search(r"(?<![A-Za-z_])(sel_norms|sel_sums|sel_stats|sel_z|sel_scores|sel_part|sel_merge|sel_prune_hist|"
+                  r"sel_prune_prefix|sel_prune_mark|sel_prune_list|sel_topk|gather|row_plan|fwd|bwd_init|bwd_dq|"
                   r"bwd_dkdv|bwd_lmk_sum|train_windows|train_dw|rope|silu_mul|probs|ce|"
                   r"bwd_lmk)_kernel", name)
     if not m:

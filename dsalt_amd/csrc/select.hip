@@ -490,6 +490,171 @@ struct KeyFn {
 
 
 
+// ------------------------------------------------ block-causal pruning
+// With bf16 norms, a candidate t that at least k earlier candidates q dominate
+// (bf16 |v_q| >= |v_t| and |h_q| >= |h_t|, q < t) is in no set's top k: for alpha in
+// [0, 1] the key's score is non-decreasing in both norms (zscore_rcp and mix_score are
+// compositions of monotone roundings) and an equal score goes to the lower index, and
+// every set holding t holds its earlier candidates.  The dominators are counted from
+// below: tokens of earlier kPruneSB-token super-blocks whose bins (monotone in each norm)
+// are strictly higher in both.  Survivors are listed per (kv head, sequence) in token
+// order; a set scans the prefix of that list instead of its whole prefix.
+constexpr int kPruneSB = 4096;  // tokens per super-block
+constexpr int kPruneNB = 32;    // bins per norm: quarter standard deviations, clamped
+constexpr int kPruneRS = kPruneNB + 1;  // LDS row stride of the bin table
+
+struct PruneBins {
+    float mx, ix, mv, iv;
+    // z-scaled bins of the sequence's longest prefix statistics (any monotone binning
+    // is exact; these spread the tokens)
+    __device__ PruneBins(const SelectParams& p, const double* stats, int s, int g, int len) {
+        const int nsig = 1 + p.n_kv_heads;
+        const int b = min(max((len - 1) / p.block_size, 0), p.n_sets - 1);
+        const double* sr = stats + (int64_t)(s * p.n_sets + b) * nsig * 2;
+        auto inv = [](double sd) { return (sd > 1e-30 && sd < 1e30) ? (float)(4.0 / sd) : 0.f; };
+        mx = (float)sr[0];
+        ix = inv(sr[1]);
+        mv = (float)sr[2 * (g + 1)];
+        iv = inv(sr[2 * (g + 1) + 1]);
+        if (!(mx == mx) || !(mv == mv)) ix = iv = mx = mv = 0.f;
+    }
+    // in [0, kPruneNB) for every input (NaN -> 0: still monotone, it arises only at a == m)
+    __device__ static int bin(float a, float m, float i) {
+        const float z = floorf(__fmul_rn(__fsub_rn(a, m), i));
+        if (!(z >= -(float)(kPruneNB / 2))) return 0;
+        if (z >= (float)(kPruneNB / 2)) return kPruneNB - 1;
+        return (int)z + kPruneNB / 2;
+    }
+    __device__ int v(uint32_t wd) const { return bin(packed_nv(wd), mv, iv); }
+    __device__ int x(uint32_t wd) const { return bin(packed_nx(wd), mx, ix); }
+};
+
+// per (super-block, sequence, kv head): 2D histogram of the candidates' bins
+__global__ __launch_bounds__(256) void sel_prune_hist_kernel(SelectParams p, const uint32_t* pk, const double* stats,
+                                                             uint32_t* hist) {
+    __shared__ uint32_t hs[kPruneNB * kPruneNB];
+    const int M = blockIdx.x, s = blockIdx.y, g = blockIdx.z, tid = threadIdx.x;
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
+    for (int i = tid; i < kPruneNB * kPruneNB; i += 256) hs[i] = 0u;
+    __syncthreads();
+    const int t0 = M * kPruneSB;
+    if (t0 < len) {
+        const PruneBins bins(p, stats, s, g, len);
+        const uint32_t* w = pk + (int64_t)g * p.total_len + st;
+        for (int t = t0 + tid; t < min(len, t0 + kPruneSB); t += 256) {
+            const uint32_t wd = w[t];
+            if (!(wd & kExcluded)) atomicAdd(&hs[bins.v(wd) * kPruneNB + bins.x(wd)], 1u);
+        }
+    }
+    __syncthreads();
+    uint32_t* o = hist + (((int64_t)g * p.num_seqs + s) * gridDim.x + M) * (kPruneNB * kPruneNB);
+    for (int i = tid; i < kPruneNB * kPruneNB; i += 256) o[i] = hs[i];
+}
+
+// per (bin group, sequence, kv head), in place: each bin's count becomes the sum over the
+// earlier super-blocks (exclusive prefix along the super-blocks)
+__global__ __launch_bounds__(256) void sel_prune_prefix_kernel(SelectParams p, uint32_t* hist, int nsb) {
+    constexpr int NB2 = kPruneNB * kPruneNB, U = 8;
+    const int bin = blockIdx.x * 256 + threadIdx.x, s = blockIdx.y, g = blockIdx.z;
+    uint32_t* h = hist + ((int64_t)g * p.num_seqs + s) * nsb * NB2 + bin;
+    uint32_t run = 0u;
+    for (int m0 = 0; m0 < nsb; m0 += U) {
+        uint32_t c[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) c[u] = m0 + u < nsb ? h[(int64_t)(m0 + u) * NB2] : 0u;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (m0 + u < nsb) h[(int64_t)(m0 + u) * NB2] = run;
+            run += c[u];
+        }
+    }
+}
+
+// per (super-block, sequence, kv head): keep flag of each token (a candidate whose lower
+// bound of earlier dominators is below k) and the super-block's survivor count; hist
+// holds the earlier super-blocks' sums by now
+__global__ __launch_bounds__(256) void sel_prune_mark_kernel(SelectParams p, const uint32_t* pk, const double* stats,
+                                                             const uint32_t* hist, uint8_t* keep, int* cnt) {
+    __shared__ uint32_t sf[kPruneNB * kPruneRS];
+    __shared__ int wsum[4];
+    const int M = blockIdx.x, s = blockIdx.y, g = blockIdx.z, tid = threadIdx.x;
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
+    const int64_t gs = (int64_t)g * p.num_seqs + s;
+    const uint32_t* h0 = hist + (gs * gridDim.x + M) * (kPruneNB * kPruneNB);  // earlier super-blocks' sums
+    for (int i = tid; i < kPruneNB * kPruneNB; i += 256) sf[(i / kPruneNB) * kPruneRS + i % kPruneNB] = h0[i];
+    __syncthreads();
+    // inclusive suffix sums along x, then along v: sf[a][b] = tokens in bins >= a, >= b
+    if (tid < kPruneNB) {
+        uint32_t r = 0u;
+        for (int b = kPruneNB - 1; b >= 0; --b) r = sf[tid * kPruneRS + b] += r;
+    }
+    __syncthreads();
+    if (tid < kPruneNB) {
+        uint32_t r = 0u;
+        for (int a = kPruneNB - 1; a >= 0; --a) r = sf[a * kPruneRS + tid] += r;
+    }
+    __syncthreads();
+    const int t0 = M * kPruneSB;
+    int n = 0;
+    if (t0 < len) {
+        const PruneBins bins(p, stats, s, g, len);
+        const uint32_t* w = pk + (int64_t)g * p.total_len + st;
+        uint8_t* kp = keep + (int64_t)g * p.total_len + st;
+        for (int t = t0 + tid; t < min(len, t0 + kPruneSB); t += 256) {
+            const uint32_t wd = w[t];
+            bool k = false;
+            if (!(wd & kExcluded)) {
+                const int a = bins.v(wd), b = bins.x(wd);
+                const uint32_t dom = (a + 1 < kPruneNB && b + 1 < kPruneNB) ? sf[(a + 1) * kPruneRS + b + 1] : 0u;
+                k = dom < (uint32_t)p.k_lmk;
+            }
+            kp[t] = k ? 1 : 0;
+            n += k ? 1 : 0;
+        }
+    }
+    for (int off = 32; off >= 1; off >>= 1) n += __shfl_xor(n, off);
+    if ((tid & 63) == 0) wsum[tid >> 6] = n;
+    __syncthreads();
+    if (tid == 0) cnt[gs * gridDim.x + M] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+}
+
+// per (super-block, sequence, kv head): the survivors' in-sequence indices, in token order,
+// at the super-block's offset of the (kv head, sequence) list, and at every 16th token of
+// the sequence the number of survivors below it
+__global__ __launch_bounds__(256) void sel_prune_list_kernel(SelectParams p, const uint8_t* keep, const int* cnt,
+                                                             int32_t* list, int32_t* below) {
+    __shared__ int wsum[4];
+    const int M = blockIdx.x, s = blockIdx.y, g = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
+    const int t0 = M * kPruneSB;
+    if (t0 >= len) return;
+    const int64_t gs = (int64_t)g * p.num_seqs + s;
+    int off = 0;
+    for (int m = 0; m < M; ++m) off += cnt[gs * gridDim.x + m];
+    // thread tid takes tokens t0 + 16 tid .. + 15: counts, block exclusive scan, writes
+    constexpr int PER = kPruneSB / 256;
+    const uint8_t* kp = keep + (int64_t)g * p.total_len + st;
+    const int a = t0 + PER * tid, e = min(len, a + PER);
+    int c = 0;
+    for (int t = a; t < e; ++t) c += kp[t];
+    int inc = c;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(inc, o);
+        if (lane >= o) inc += y;
+    }
+    if (lane == 63) wsum[wave] = inc;
+    __syncthreads();
+    int base = off + inc - c;
+    for (int w2 = 0; w2 < wave; ++w2) base += wsum[w2];
+    int32_t* lo = list + (int64_t)g * p.total_len + st;
+    if (a < len) below[(int64_t)g * p.total_len + st + a] = base;  // survivors below token a
+    for (int t = a; t < e; ++t)
+        if (kp[t]) lo[base++] = t;
+}
+
 // ------------------------------------------- global variant: parts + merges
 constexpr int kPartMax = 2048;   // candidates per part (keys in LDS)
 constexpr int kMergeMax = 4096;  // keys per merge block
@@ -591,7 +756,9 @@ __global__ __launch_bounds__(kSortThreads) void sel_merge_kernel(SelectParams p,
 
 __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, const float* zx, const float* zv,
                                                                const float* nx, const float* nv, const uint32_t* pk,
-                                                               const double* stats, int border_cap) {
+                                                               const double* stats, int border_cap,
+                                                               const int32_t* plist, const int* pcnt,
+                                                               const int32_t* pbelow, int nsb) {
     __shared__ TopkShared sh;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // blocks of one (head, sequence) are contiguous in the XCD-swizzled order, so each XCD's
@@ -636,15 +803,37 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
         key.rsx = __ddiv_rn(1.0, key.sx);
         key.rsv = __ddiv_rn(1.0, key.sv);
     }
+    // candidates e < n are the in-sequence indices cand(e): the pruned survivor list's
+    // entries below b0 where it applies to this head (alpha in [0, 1]), else 0 .. b0-1
+    const int32_t* cl = nullptr;
+    if (block && plist && key.alpha >= 0.f && key.alpha <= 1.f) {
+        cl = plist + (int64_t)key.rep_g * p.total_len + st;
+        if (n % 16 == 0) {
+            n = pbelow[(int64_t)key.rep_g * p.total_len + st + n];
+        } else {
+            const int64_t gs = (int64_t)key.rep_g * p.num_seqs + s;
+            const int Mb = n / kPruneSB;  // entries of earlier super-blocks all lie below b0
+            int off = 0;
+            for (int m = 0; m < Mb; ++m) off += pcnt[gs * nsb + m];
+            int lo = off, hi = off + pcnt[gs * nsb + Mb];
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (cl[mid] < n) lo = mid + 1;
+                else hi = mid;
+            }
+            n = lo;
+        }
+    }
+    auto cand = [&](int e) { return cl ? cl[e] : e; };
     const int cap = min(border_cap, kBorderCap);
 
     // Large sets: a threshold from an evenly strided sample of the candidates, then one pass
     // that keeps every key at or above it.  When that keeps between K and cap keys, their
     // top K are the set's top K; otherwise (an unrepresentative sample) the radix path
     // below runs from scratch.
-    if (n >= kSampleMin && border_cap >= kBorderCap) {
-        const int stride = n / kSample;
-        for (int i = tid; i < kSample; i += kSelThreads) sh.border[i] = key(i * stride);
+    // (a pruned list takes it from kSample candidates: its candidates are all near the top)
+    if (n >= (cl ? kSample : kSampleMin) && border_cap >= kBorderCap) {
+        for (int i = tid; i < kSample; i += kSelThreads) sh.border[i] = key(cand((int)((int64_t)i * n / kSample)));
         __syncthreads();
         // aim at about 1.6 K + 128 keys above the threshold (the sample's spread leaves
         // fewer than K above it in a small fraction of the sets: those take the radix path)
@@ -679,7 +868,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
                 if (block) {
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
-                        const int j = min(j0 + u * kSelThreads, n - 1);
+                        const int j = cand(min(j0 + u * kSelThreads, n - 1));
                         if (pkg) {
                             wds[u] = pkg[j];
                             av[u] = packed_nx(wds[u]);
@@ -711,7 +900,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
                     uint32_t wd = 0u;
 #pragma unroll
                     for (int v = 0; v < U; ++v) wd = v == u ? wds[v] : wd;
-                    const unsigned long long kj = pkg ? key.packed(j, wd) : key(j);
+                    const unsigned long long kj = pkg ? key.packed(cand(j), wd) : key(cand(j));
                     if (kj >= thr) {
                         const uint32_t slot = atomicAdd(&sh.nborder, 1u);
                         if (slot < (uint32_t)cap) sh.border[slot] = kj;
@@ -747,7 +936,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
         __syncthreads();
         const int shift = 56 - plen;
         for (int j = tid; j < n; j += kSelThreads) {
-            unsigned long long kj = key(j);
+            unsigned long long kj = key(cand(j));
             if (kj == 0ull) continue;
             if (plen > 0 && (kj >> (64 - plen)) != prefix) continue;
             atomicAdd(&sh.hist[wave][(uint32_t)(kj >> shift) & 255u], 1u);
@@ -800,7 +989,8 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
         sh.nborder = 0u;
     }
     __syncthreads();
-    for (int j = tid; j < n; j += kSelThreads) {
+    for (int e = tid; e < n; e += kSelThreads) {
+        const int j = cand(e);
         unsigned long long kj = key(j);
         if (kj == 0ull) continue;
         if (all_sure) {
@@ -899,8 +1089,14 @@ size_t select_workspace_cap(const SelectParams& p, int border_cap) {
     b += align256(sizeof(float) * (size_t)p.total_len * nsig);           // norms
     b += align256(sizeof(double) * 2 * (size_t)nranges * nsig);          // sums
     b += align256(sizeof(double) * 2 * (size_t)nranges * nsig);          // stats
-    if (p.select_mode != DSALT_SELECT_GLOBAL && p.dtype == DSALT_DTYPE_BF16)
-        b += align256(sizeof(uint32_t) * (size_t)p.total_len * p.n_kv_heads);  // packed norms
+    if (p.select_mode != DSALT_SELECT_GLOBAL && p.dtype == DSALT_DTYPE_BF16) {
+        const size_t tg = (size_t)p.total_len * p.n_kv_heads;
+        const size_t gsb = (size_t)p.n_kv_heads * p.num_seqs * ceil_div(p.max_seqlen, kPruneSB);
+        b += align256(sizeof(uint32_t) * tg);                            // packed norms
+        b += align256(sizeof(uint32_t) * gsb * kPruneNB * kPruneNB);     // pruning histograms
+        b += align256(tg) + align256(sizeof(int) * gsb);                 // keep flags, survivor counts
+        b += 2 * align256(sizeof(int32_t) * tg);                         // survivor lists, counts below
+    }
     if (p.select_mode == DSALT_SELECT_GLOBAL) {
         b += align256(sizeof(float) * (size_t)p.total_len * nsig);       // z
         if (p.k_lmk > 0) {
@@ -924,9 +1120,27 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
     double* stats = (double*)w;
     w += align256(sizeof(double) * 2 * (size_t)nranges * nsig);
     uint32_t* pk = nullptr;
+    uint32_t* phist = nullptr;
+    uint8_t* pkeep = nullptr;
+    int* pcnt = nullptr;
+    int32_t* plist = nullptr;
+    int32_t* pbelow = nullptr;
+    const int nsb = ceil_div(p.max_seqlen, kPruneSB);
     if (!global && p.dtype == DSALT_DTYPE_BF16) {
+        const size_t tg = (size_t)p.total_len * p.n_kv_heads;
+        const size_t gsb = (size_t)p.n_kv_heads * p.num_seqs * nsb;
         pk = (uint32_t*)w;
-        w += align256(sizeof(uint32_t) * (size_t)p.total_len * p.n_kv_heads);
+        w += align256(sizeof(uint32_t) * tg);
+        phist = (uint32_t*)w;
+        w += align256(sizeof(uint32_t) * gsb * kPruneNB * kPruneNB);
+        pkeep = (uint8_t*)w;
+        w += align256(tg);
+        pcnt = (int*)w;
+        w += align256(sizeof(int) * gsb);
+        plist = (int32_t*)w;
+        w += align256(sizeof(int32_t) * tg);
+        pbelow = (int32_t*)w;
+        w += align256(sizeof(int32_t) * tg);
     }
     float* zx = nullptr;
     float* zv = nullptr;
@@ -960,8 +1174,19 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
     const int nsets_total = p.n_heads * p.num_seqs * p.n_sets;
     if (nsets_total == 0 || p.k_lmk == 0) return hipGetLastError();
     if (!global) {
+        const bool prune = pk && p.total_len > 0 && nsb > 1;
+        if (prune) {
+            const dim3 pg(nsb, p.num_seqs, p.n_kv_heads);
+            DSALT_LAUNCH("sel_prune_hist", sel_prune_hist_kernel, pg, dim3(256), 0, stream, p, pk, stats, phist);
+            DSALT_LAUNCH("sel_prune_prefix", sel_prune_prefix_kernel, dim3(kPruneNB * kPruneNB / 256, p.num_seqs,
+                         p.n_kv_heads), dim3(256), 0, stream, p, phist, nsb);
+            DSALT_LAUNCH("sel_prune_mark", sel_prune_mark_kernel, pg, dim3(256), 0, stream, p, pk, stats, phist, pkeep,
+                         pcnt);
+            DSALT_LAUNCH("sel_prune_list", sel_prune_list_kernel, pg, dim3(256), 0, stream, p, pkeep, pcnt, plist,
+                         pbelow);
+        }
         DSALT_LAUNCH("sel_topk", sel_topk_kernel, dim3(nsets_total), dim3(kSelThreads), 0, stream, p, zx, zv, nx, nv,
-                     pk, stats, border_cap);
+                     pk, stats, border_cap, prune ? plist : nullptr, pcnt, pbelow, nsb);
         return hipGetLastError();
     }
     const TopkPlan t = topk_plan(p, border_cap);
