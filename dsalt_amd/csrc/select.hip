@@ -827,6 +827,25 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
     auto cand = [&](int e) { return cl ? cl[e] : e; };
     const int cap = min(border_cap, kBorderCap);
 
+    // Sets of at most kSample candidates: every key in LDS, the K-th largest by kth_desc,
+    // the keys at or above it (zero keys, of excluded tokens, never) by ascending index.
+    if (n <= kSample && border_cap >= kBorderCap) {
+        for (int i = tid; i < n; i += kSelThreads) sh.border[i] = key(cand(i));
+        __syncthreads();
+        const unsigned long long kk = n > K ? kth_desc(sh, sh.border, n, K - 1, tid) : 0ull;
+        if (tid == 0) sh.nsure = 0u;
+        __syncthreads();
+        for (int i = tid; i < n; i += kSelThreads) {
+            const unsigned long long kj = sh.border[i];
+            if (kj != 0ull && kj >= kk) sh.sel[atomicAdd(&sh.nsure, 1u)] = (int)(0xffffffffu - (uint32_t)(kj & 0xffffffffull));
+        }
+        __syncthreads();
+        const int nsel = (int)sh.nsure;
+        rank_sort_asc(sh.sel, nsel, out, tid);
+        for (int i = nsel + tid; i < K; i += kSelThreads) out[i] = -1;
+        return;
+    }
+
     // Large sets: a threshold from an evenly strided sample of the candidates, then one pass
     // that keeps every key at or above it.  When that keeps between K and cap keys, their
     // top K are the set's top K; otherwise (an unrepresentative sample) the radix path
