@@ -502,6 +502,9 @@ struct KeyFn {
 constexpr int kPruneSB = 4096;  // tokens per super-block
 constexpr int kPruneNB = 32;    // bins per norm: quarter standard deviations, clamped
 constexpr int kPruneRS = kPruneNB + 1;  // LDS row stride of the bin table
+// Pruning pays from this sequence length on (its four launches cost ~45 us; at 32768
+// tokens the scans it saves are shorter than that, at 131072 it saves ~190 us)
+constexpr int kPruneMinLen = 65536;
 
 struct PruneBins {
     float mx, ix, mv, iv;
@@ -1193,7 +1196,8 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
     const int nsets_total = p.n_heads * p.num_seqs * p.n_sets;
     if (nsets_total == 0 || p.k_lmk == 0) return hipGetLastError();
     if (!global) {
-        const bool prune = pk && p.total_len > 0 && nsb > 1;
+        const bool prune = pk && p.total_len > 0 && nsb > 1 &&
+                           (p.max_seqlen >= kPruneMinLen || border_cap == DSALT_SELECT_FORCE_PRUNE);
         if (prune) {
             const dim3 pg(nsb, p.num_seqs, p.n_kv_heads);
             DSALT_LAUNCH("sel_prune_hist", sel_prune_hist_kernel, pg, dim3(256), 0, stream, p, pk, stats, phist);

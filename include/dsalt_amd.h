@@ -312,7 +312,11 @@ int    dsalt_train_bwd(const dsalt_train_bwd_args* a, dsalt_stream_t stream);
  * Global sets: candidates sorted per part and parts merged per merge block
  * limited by `border_cap` (many parts, several merge levels).  dsalt_select is
  * this call with the full capacity; the workspace it needs is
- * dsalt_select_workspace_bytes_cap(a, border_cap). */
+ * dsalt_select_workspace_bytes_cap(a, border_cap).  border_cap ==
+ * DSALT_SELECT_FORCE_PRUNE is the full capacity with the block-causal candidate
+ * pruning (bf16 inputs) run whatever the sequence length; dsalt_select runs it
+ * for sequences of 65536 tokens or more. */
+#define DSALT_SELECT_FORCE_PRUNE 0x3fffffff
 int    dsalt_select_with_border_cap(const dsalt_select_args* a, dsalt_stream_t stream, int border_cap);
 size_t dsalt_select_workspace_bytes_cap(const dsalt_select_args* a, int border_cap);
 

@@ -143,3 +143,30 @@ def test_block_sampled_path_packed_sequences_gqa():
     h, v, alpha, w, cu = _case([20000, 0, 17000], 128, 2, 64, 4, torch.bfloat16, 300, seed=5)
     idx, ridx = _run(h, v, alpha, w, cu, 64, ops.SELECT_BLOCK, 512, ops.STATS_SEQUENCE, want=False)
     np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
+# Block-causal candidate pruning (a candidate that k earlier candidates dominate in both
+# norms is dropped before the sets' scans) forced on short sequences: the selection must
+# stay bit-exact against the oracle, which never prunes.
+def test_block_pruned_packed_sequences_gqa():
+    h, v, alpha, w, cu = _case([20000, 0, 17000], 128, 2, 64, 4, torch.bfloat16, 300, seed=5)
+    idx, ridx = _run(h, v, alpha, w, cu, 64, ops.SELECT_BLOCK, 512, ops.STATS_SEQUENCE, want=False,
+                     border_cap=ops.SELECT_FORCE_PRUNE)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
+def test_block_pruned_alpha_outside_unit_interval():
+    # heads with alpha outside [0, 1] (a norm weighted negatively) must scan whole prefixes
+    h, v, alpha, w, cu = _case([12000, 9000], 128, 2, 64, 4, torch.bfloat16, 300, seed=9, scale_tails=True)
+    alpha[0], alpha[1], alpha[2] = 1.5, -0.25, 1.0
+    idx, ridx = _run(h, v, alpha, w, cu, 32, ops.SELECT_BLOCK, 512, ops.STATS_SEQUENCE, want=False,
+                     border_cap=ops.SELECT_FORCE_PRUNE)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
+def test_block_pruned_workload_shortened():
+    wl = WORKLOADS["fwd_bf16_h16_l131072_block"]
+    x = generate(wl, seqlen=16384, heads=4)
+    idx, ridx = _run(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, ops.SELECT_BLOCK, 512,
+                     ops.STATS_SEQUENCE, want=False, border_cap=ops.SELECT_FORCE_PRUNE)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
