@@ -23,8 +23,14 @@
 //               sel_merge does the same over the survivors of up to G parts per
 //               block, level by level, and the last level writes the indices in
 //               ascending order (by ranks).
-//     block:    sel_topk, one 1024-thread block per landmark set (largest sets
-//               first).  Sets of 8192+ candidates: a threshold key, the order
+//     block:    (bf16, sequences of 65536+ tokens) sel_prune_* list per kv head
+//               the candidates that fewer than k earlier candidates can dominate
+//               in both norms (a lower bound from 2D bin histograms); the others
+//               are in no set's top k.  sel_topk, one 1024-thread block per
+//               landmark set (largest sets first), scans the listed candidates
+//               below the set's start (or the whole prefix).  Sets of at most 4096:
+//               every key in LDS and one order statistic.  Larger sets (8192+
+//               unlisted candidates): a threshold key, the order
 //               statistic of a strided sample of 4096 found by radix passes
 //               (kth_desc), one pass screening every candidate with a float32 affine
 //               form of its score (exact keys only near the threshold; bf16 inputs
