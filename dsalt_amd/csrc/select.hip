@@ -341,6 +341,7 @@ __global__ __launch_bounds__(256) void sel_scores_kernel(SelectParams p, const f
 // ------------------------------------------------------------------ top-k
 constexpr int kSample = 4096;      // candidates sampled for the threshold of large block-causal sets
 constexpr int kSampleMin = 8192;   // sets of fewer candidates take the radix path directly
+constexpr int kSampleList = 1024;  // sample of a pruned list (its candidates are near the top)
 
 constexpr int kKthCand = 64;       // radix passes of kth_desc stop once the bin holds at most this many keys
 
@@ -860,14 +861,15 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
     // top K are the set's top K; otherwise (an unrepresentative sample) the radix path
     // below runs from scratch.
     // (a pruned list takes it from kSample candidates: its candidates are all near the top)
+    const int ns = cl ? kSampleList : kSample;
     if (n >= (cl ? kSample : kSampleMin) && border_cap >= kBorderCap) {
-        for (int i = tid; i < kSample; i += kSelThreads) sh.border[i] = key(cand((int)((int64_t)i * n / kSample)));
+        for (int i = tid; i < ns; i += kSelThreads) sh.border[i] = key(cand((int)((int64_t)i * n / ns)));
         __syncthreads();
         // aim at about 1.6 K + 128 keys above the threshold (the sample's spread leaves
         // fewer than K above it in a small fraction of the sets: those take the radix path)
-        const long long want = ((long long)K * 16 / 10 + 128) * kSample / n;
-        const int rank = (int)min((long long)kSample - 1, max(want, 1ll));
-        const unsigned long long thr = kth_desc(sh, sh.border, kSample, rank, tid);
+        const long long want = ((long long)K * 16 / 10 + 128) * ns / n;
+        const int rank = (int)min((long long)ns - 1, max(want, 1ll));
+        const unsigned long long thr = kth_desc(sh, sh.border, ns, rank, tid);
         if (tid == 0) sh.nborder = 0u;
         __syncthreads();
         if (thr != 0ull) {
