@@ -263,6 +263,38 @@ __global__ void sel_stats_kernel(SelectParams p, const double* sums, double* sta
     stats[o + 1] = sd;
 }
 
+// One block per (sequence, signal) when the sets fit in LDS: the block sums staged once,
+// then each thread adds the prefix of its sets in block order (the order above: same bits).
+constexpr int kStatsLdsSets = 2048;
+__global__ __launch_bounds__(256) void sel_stats_lds_kernel(SelectParams p, const double* sums, double* stats) {
+    extern __shared__ double bs[];  // [n_sets][2]
+    const int nsig = 1 + p.n_kv_heads;
+    const int sig = blockIdx.x % nsig, s = blockIdx.x / nsig;
+    int st, len;
+    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
+    const int nb = min(p.n_sets, ceil_div(len, p.block_size));  // blocks holding tokens
+    for (int b = threadIdx.x; b < nb; b += 256) {
+        const int64_t o = ((int64_t)(s * p.n_sets + b) * nsig + sig) * 2;
+        bs[2 * b] = sums[o];
+        bs[2 * b + 1] = sums[o + 1];
+    }
+    __syncthreads();
+    for (int b = threadIdx.x; b < p.n_sets; b += 256) {
+        double p1 = 0.0, p2 = 0.0;
+        const int e = min(b, nb);
+        for (int bb = 0; bb < e; ++bb) {
+            p1 = __dadd_rn(p1, bs[2 * bb]);
+            p2 = __dadd_rn(p2, bs[2 * bb + 1]);
+        }
+        const int64_t o = ((int64_t)(s * p.n_sets + b) * nsig + sig) * 2;
+        const int b0 = b * p.block_size;
+        double m = 0.0, sd = 1.0;
+        if (b0 >= 2 && b0 < len) mean_std(p1, p2, b0, m, sd);
+        stats[o] = m;
+        stats[o + 1] = sd;
+    }
+}
+
 __device__ __forceinline__ float zscore(float a, double mean, double sd) {
     return (float)__ddiv_rn(__dadd_rn((double)a, -mean), sd);
 }
@@ -1197,8 +1229,12 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
                 DSALT_LAUNCH("sel_scores", sel_scores_kernel, dim3(ceil_div(p.max_seqlen, 256), p.num_seqs),
                              dim3(256), 0, stream, p, nx, nv, stats);
         } else {
-            DSALT_LAUNCH("sel_stats", sel_stats_kernel, dim3(ceil_div(p.num_seqs * nsig * p.n_sets, 64)), dim3(64), 0,
-                         stream, p, sums, stats);
+            if (p.n_sets <= kStatsLdsSets)
+                DSALT_LAUNCH("sel_stats", sel_stats_lds_kernel, dim3(p.num_seqs * nsig), dim3(256),
+                             sizeof(double) * 2 * p.n_sets, stream, p, sums, stats);
+            else
+                DSALT_LAUNCH("sel_stats", sel_stats_kernel, dim3(ceil_div(p.num_seqs * nsig * p.n_sets, 64)), dim3(64),
+                             0, stream, p, sums, stats);
         }
     }
     const int nsets_total = p.n_heads * p.num_seqs * p.n_sets;
