@@ -28,10 +28,10 @@
 //               in both norms (a lower bound from 2D bin histograms); the others
 //               are in no set's top k.  sel_topk, one 1024-thread block per
 //               landmark set (largest sets first), scans the listed candidates
-//               below the set's start (or the whole prefix).  Sets of at most 4096:
+//               below the set's start (or the whole prefix).  Sets of at most 2048:
 //               every key in LDS and one order statistic.  Larger sets (8192+
 //               unlisted candidates): a threshold key, the order
-//               statistic of a strided sample of 4096 found by radix passes
+//               statistic of a strided sample of 2048 (1024 of a list) found by radix passes
 //               (kth_desc), one pass screening every candidate with a float32 affine
 //               form of its score (exact keys only near the threshold; bf16 inputs
 //               read both norms from one packed word), then the K-th largest survivor
@@ -371,7 +371,7 @@ __global__ __launch_bounds__(256) void sel_scores_kernel(SelectParams p, const f
 }
 
 // ------------------------------------------------------------------ top-k
-constexpr int kSample = 4096;      // candidates sampled for the threshold of large block-causal sets
+constexpr int kSample = 2048;      // candidates sampled for the threshold of large block-causal sets
 constexpr int kSampleMin = 8192;   // sets of fewer candidates take the radix path directly
 constexpr int kSampleList = 1024;  // sample of a pruned list (its candidates are near the top)
 
