@@ -584,10 +584,16 @@ __global__ __launch_bounds__(256) void sel_prune_hist_kernel(SelectParams p, con
     if (t0 < len) {
         const PruneBins bins(p, stats, s, g, len);
         const uint32_t* w = pk + (int64_t)g * p.total_len + st;
-        for (int t = t0 + tid; t < min(len, t0 + kPruneSB); t += 256) {
-            const uint32_t wd = w[t];
-            if (!(wd & kExcluded)) atomicAdd(&hs[bins.v(wd) * kPruneNB + bins.x(wd)], 1u);
+        constexpr int PER = kPruneSB / 256;
+        uint32_t wd[PER];  // all of the thread's words in flight before any bin
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int t = t0 + tid + 256 * u;
+            wd[u] = t < len ? w[t] : kExcluded;
         }
+#pragma unroll
+        for (int u = 0; u < PER; ++u)
+            if (!(wd[u] & kExcluded)) atomicAdd(&hs[bins.v(wd[u]) * kPruneNB + bins.x(wd[u])], 1u);
     }
     __syncthreads();
     uint32_t* o = hist + (((int64_t)g * p.num_seqs + s) * gridDim.x + M) * (kPruneNB * kPruneNB);
@@ -644,15 +650,23 @@ __global__ __launch_bounds__(256) void sel_prune_mark_kernel(SelectParams p, con
         const PruneBins bins(p, stats, s, g, len);
         const uint32_t* w = pk + (int64_t)g * p.total_len + st;
         uint8_t* kp = keep + (int64_t)g * p.total_len + st;
-        for (int t = t0 + tid; t < min(len, t0 + kPruneSB); t += 256) {
-            const uint32_t wd = w[t];
+        constexpr int PER = kPruneSB / 256;
+        uint32_t wd[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int t = t0 + tid + 256 * u;
+            wd[u] = t < len ? w[t] : kExcluded;
+        }
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int t = t0 + tid + 256 * u;
             bool k = false;
-            if (!(wd & kExcluded)) {
-                const int a = bins.v(wd), b = bins.x(wd);
+            if (!(wd[u] & kExcluded)) {
+                const int a = bins.v(wd[u]), b = bins.x(wd[u]);
                 const uint32_t dom = (a + 1 < kPruneNB && b + 1 < kPruneNB) ? sf[(a + 1) * kPruneRS + b + 1] : 0u;
                 k = dom < (uint32_t)p.k_lmk;
             }
-            kp[t] = k ? 1 : 0;
+            if (t < len) kp[t] = k ? 1 : 0;
             n += k ? 1 : 0;
         }
     }
@@ -667,34 +681,44 @@ __global__ __launch_bounds__(256) void sel_prune_mark_kernel(SelectParams p, con
 // the sequence the number of survivors below it
 __global__ __launch_bounds__(256) void sel_prune_list_kernel(SelectParams p, const uint8_t* keep, const int* cnt,
                                                              int32_t* list, int32_t* below) {
-    __shared__ int wsum[4];
+    __shared__ int wsum[4], woff[4];
     const int M = blockIdx.x, s = blockIdx.y, g = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int st, len;
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     const int t0 = M * kPruneSB;
     if (t0 >= len) return;
     const int64_t gs = (int64_t)g * p.num_seqs + s;
-    int off = 0;
-    for (int m = 0; m < M; ++m) off += cnt[gs * gridDim.x + m];
-    // thread tid takes tokens t0 + 16 tid .. + 15: counts, block exclusive scan, writes
+    // thread tid takes tokens t0 + 16 tid .. + 15 (flags loaded together): counts, block
+    // exclusive scan, writes; the earlier super-blocks' counts are summed by the block
     constexpr int PER = kPruneSB / 256;
     const uint8_t* kp = keep + (int64_t)g * p.total_len + st;
-    const int a = t0 + PER * tid, e = min(len, a + PER);
+    const int a = t0 + PER * tid;
+    uint8_t kb[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) kb[u] = a + u < len ? kp[a + u] : (uint8_t)0;
+    int prev = 0;
+    for (int m = tid; m < M; m += 256) prev += cnt[gs * gridDim.x + m];
     int c = 0;
-    for (int t = a; t < e; ++t) c += kp[t];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) c += kb[u];
+    for (int o = 32; o >= 1; o >>= 1) prev += __shfl_xor(prev, o);
     int inc = c;
     for (int o = 1; o < 64; o <<= 1) {
         const int y = __shfl_up(inc, o);
         if (lane >= o) inc += y;
     }
-    if (lane == 63) wsum[wave] = inc;
+    if (lane == 63) {
+        wsum[wave] = inc;
+        woff[wave] = prev;
+    }
     __syncthreads();
-    int base = off + inc - c;
+    int base = woff[0] + woff[1] + woff[2] + woff[3] + inc - c;
     for (int w2 = 0; w2 < wave; ++w2) base += wsum[w2];
     int32_t* lo = list + (int64_t)g * p.total_len + st;
     if (a < len) below[(int64_t)g * p.total_len + st + a] = base;  // survivors below token a
-    for (int t = a; t < e; ++t)
-        if (kp[t]) lo[base++] = t;
+#pragma unroll
+    for (int u = 0; u < PER; ++u)
+        if (kb[u]) lo[base++] = a + u;
 }
 
 // ------------------------------------------- global variant: parts + merges
