@@ -49,6 +49,8 @@ namespace dsalt {
 
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / kWave;
+constexpr int kTopkThreads = 512;  // block-causal sets (sel_topk): more sets in flight per CU
+constexpr int kTopkWaves = kTopkThreads / kWave;
 constexpr int kBorderCap = 2048;
 
 __device__ __forceinline__ int pow2ceil64(int n) {
@@ -378,7 +380,8 @@ constexpr int kSampleList = 1024;  // sample of a pruned list (its candidates ar
 constexpr int kKthCand = 64;       // radix passes of kth_desc stop once the bin holds at most this many keys
 
 struct TopkShared {
-    uint32_t hist[kSelWaves][256];
+    static constexpr int NT = kTopkThreads;
+    uint32_t hist[kTopkWaves][256];
     unsigned long long border[kBorderCap > kSample ? kBorderCap : kSample];
     int sel[kMaxLandmarks];
     unsigned long long cand[kKthCand];
@@ -393,6 +396,7 @@ struct TopkShared {
 
 // LDS of kth_desc alone (the global top-k parts and merges)
 struct KthShared {
+    static constexpr int NT = kSelThreads;
     uint32_t hist[kSelWaves][256];
     unsigned long long cand[kKthCand];
     unsigned long long kth;
@@ -414,10 +418,10 @@ __device__ unsigned long long kth_desc(Sh& sh, const unsigned long long* a, int 
     int plen = 0;
     uint32_t rem = (uint32_t)r;
     for (;;) {
-        for (int i = tid; i < kSelWaves * 256; i += kSelThreads) (&sh.hist[0][0])[i] = 0u;
+        for (int i = tid; i < (Sh::NT / kWave) * 256; i += Sh::NT) (&sh.hist[0][0])[i] = 0u;
         __syncthreads();
         const int shift = 56 - plen;
-        for (int i = tid; i < n; i += kSelThreads) {
+        for (int i = tid; i < n; i += Sh::NT) {
             const unsigned long long k = a[i];
             if (plen > 0 && (k >> (64 - plen)) != prefix) continue;
             atomicAdd(&sh.hist[wave][(uint32_t)(k >> shift) & 255u], 1u);
@@ -425,7 +429,7 @@ __device__ unsigned long long kth_desc(Sh& sh, const unsigned long long* a, int 
         __syncthreads();
         if (tid < 256) {
             uint32_t c = 0;
-            for (int w2 = 0; w2 < kSelWaves; ++w2) c += sh.hist[w2][tid];
+            for (int w2 = 0; w2 < (Sh::NT / kWave); ++w2) c += sh.hist[w2][tid];
             sh.hist[0][tid] = c;
         }
         __syncthreads();
@@ -460,7 +464,7 @@ __device__ unsigned long long kth_desc(Sh& sh, const unsigned long long* a, int 
     }
     if (tid == 0) sh.ncand = 0u;
     __syncthreads();
-    for (int i = tid; i < n; i += kSelThreads) {
+    for (int i = tid; i < n; i += Sh::NT) {
         const unsigned long long k = a[i];
         if ((k >> (64 - plen)) == prefix) sh.cand[atomicAdd(&sh.ncand, 1u)] = k;
     }
@@ -484,8 +488,9 @@ __device__ unsigned long long kth_desc(Sh& sh, const unsigned long long* a, int 
 
 // out[0..m) = the m distinct values v[0..m) (LDS) in ascending order: each value's rank
 // is the number of smaller values (m <= kMaxLandmarks, one thread per value)
+template <int NT>
 __device__ void rank_sort_asc(const int* v, int m, int32_t* out, int tid) {
-    for (int t = tid; t < m; t += kSelThreads) {
+    for (int t = tid; t < m; t += NT) {
         const int x = v[t];
         int rank = 0;
         for (int u = 0; u < m; ++u) rank += v[u] < x ? 1 : 0;
@@ -816,11 +821,11 @@ __global__ __launch_bounds__(kSortThreads) void sel_merge_kernel(SelectParams p,
     __syncthreads();
     const int nsel = (int)sh.ncand;
     int32_t* o = p.lmk_idx + (int64_t)sidx * K;
-    rank_sort_asc(sel, nsel, o, tid);
+    rank_sort_asc<kSelThreads>(sel, nsel, o, tid);
     for (int i = nsel + tid; i < K; i += kSortThreads) o[i] = -1;
 }
 
-__global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, const float* zx, const float* zv,
+__global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, const float* zx, const float* zv,
                                                                const float* nx, const float* nv, const uint32_t* pk,
                                                                const double* stats, int border_cap,
                                                                const int32_t* plist, const int* pcnt,
@@ -856,7 +861,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
     if (block) {
         int b0 = set * p.block_size;
         if (b0 < 2 || b0 >= len) {
-            for (int i = tid; i < K; i += kSelThreads) out[i] = -1;
+            for (int i = tid; i < K; i += kTopkThreads) out[i] = -1;
             return;
         }
         n = b0;
@@ -896,19 +901,19 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
     // Sets of at most kSample candidates: every key in LDS, the K-th largest by kth_desc,
     // the keys at or above it (zero keys, of excluded tokens, never) by ascending index.
     if (n <= kSample && border_cap >= kBorderCap) {
-        for (int i = tid; i < n; i += kSelThreads) sh.border[i] = key(cand(i));
+        for (int i = tid; i < n; i += kTopkThreads) sh.border[i] = key(cand(i));
         __syncthreads();
         const unsigned long long kk = n > K ? kth_desc(sh, sh.border, n, K - 1, tid) : 0ull;
         if (tid == 0) sh.nsure = 0u;
         __syncthreads();
-        for (int i = tid; i < n; i += kSelThreads) {
+        for (int i = tid; i < n; i += kTopkThreads) {
             const unsigned long long kj = sh.border[i];
             if (kj != 0ull && kj >= kk) sh.sel[atomicAdd(&sh.nsure, 1u)] = (int)(0xffffffffu - (uint32_t)(kj & 0xffffffffull));
         }
         __syncthreads();
         const int nsel = (int)sh.nsure;
-        rank_sort_asc(sh.sel, nsel, out, tid);
-        for (int i = nsel + tid; i < K; i += kSelThreads) out[i] = -1;
+        rank_sort_asc<kTopkThreads>(sh.sel, nsel, out, tid);
+        for (int i = nsel + tid; i < K; i += kTopkThreads) out[i] = -1;
         return;
     }
 
@@ -919,7 +924,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
     // (a pruned list takes it from kSample candidates: its candidates are all near the top)
     const int ns = cl ? kSampleList : kSample;
     if (n >= (cl ? kSample : kSampleMin) && border_cap >= kBorderCap) {
-        for (int i = tid; i < ns; i += kSelThreads) sh.border[i] = key(cand((int)((int64_t)i * n / ns)));
+        for (int i = tid; i < ns; i += kTopkThreads) sh.border[i] = key(cand((int)((int64_t)i * n / ns)));
         __syncthreads();
         // aim at about 1.6 K + 128 keys above the threshold (the sample's spread leaves
         // fewer than K above it in a small fraction of the sets: those take the radix path)
@@ -948,13 +953,13 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
             const float* nxs = nx + st;
             const uint32_t* pkg = pk ? pk + (int64_t)key.rep_g * p.total_len + st : nullptr;
             const float C = -(Cv + Cx), Cm = fabsf(Cv) + fabsf(Cx);
-            for (int j0 = tid; j0 < n; j0 += kSelThreads * U) {
+            for (int j0 = tid; j0 < n; j0 += kTopkThreads * U) {
                 float av[U], bv[U];
                 uint32_t wds[U];
                 if (block) {
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
-                        const int j = cand(min(j0 + u * kSelThreads, n - 1));
+                        const int j = cand(min(j0 + u * kTopkThreads, n - 1));
                         if (pkg) {
                             wds[u] = pkg[j];
                             av[u] = packed_nx(wds[u]);
@@ -969,7 +974,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
                 uint32_t pass = 0u;
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    const int j = j0 + u * kSelThreads;
+                    const int j = j0 + u * kTopkThreads;
                     bool maybe = j < n;
                     if (pkg) maybe = maybe && !(wds[u] & kExcluded);
                     if (block && maybe) {
@@ -982,7 +987,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
                 while (pass) {  // exact keys of the few survivors (one copy of the key code)
                     const int u = __builtin_ctz(pass);
                     pass &= pass - 1u;
-                    const int j = j0 + u * kSelThreads;
+                    const int j = j0 + u * kTopkThreads;
                     uint32_t wd = 0u;
 #pragma unroll
                     for (int v = 0; v < U; ++v) wd = v == u ? wds[v] : wd;
@@ -1002,12 +1007,12 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
             const unsigned long long kk = kth_desc(sh, sh.border, nb, K - 1, tid);
             if (tid == 0) sh.nsure = 0u;
             __syncthreads();
-            for (int i = tid; i < nb; i += kSelThreads) {
+            for (int i = tid; i < nb; i += kTopkThreads) {
                 const unsigned long long kj = sh.border[i];
                 if (kj >= kk) sh.sel[atomicAdd(&sh.nsure, 1u)] = (int)(0xffffffffu - (uint32_t)(kj & 0xffffffffull));
             }
             __syncthreads();
-            rank_sort_asc(sh.sel, K, out, tid);
+            rank_sort_asc<kTopkThreads>(sh.sel, K, out, tid);
             return;
         }
         __syncthreads();
@@ -1018,10 +1023,10 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
     uint32_t k_rem = (uint32_t)K;
     bool all_sure = false;
     for (;;) {
-        for (int i = tid; i < kSelWaves * 256; i += kSelThreads) (&sh.hist[0][0])[i] = 0u;
+        for (int i = tid; i < kTopkWaves * 256; i += kTopkThreads) (&sh.hist[0][0])[i] = 0u;
         __syncthreads();
         const int shift = 56 - plen;
-        for (int j = tid; j < n; j += kSelThreads) {
+        for (int j = tid; j < n; j += kTopkThreads) {
             unsigned long long kj = key(cand(j));
             if (kj == 0ull) continue;
             if (plen > 0 && (kj >> (64 - plen)) != prefix) continue;
@@ -1030,7 +1035,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
         __syncthreads();
         if (tid < 256) {
             uint32_t c = 0;
-            for (int w2 = 0; w2 < kSelWaves; ++w2) c += sh.hist[w2][tid];
+            for (int w2 = 0; w2 < kTopkWaves; ++w2) c += sh.hist[w2][tid];
             sh.hist[0][tid] = c;
         }
         __syncthreads();
@@ -1075,7 +1080,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
         sh.nborder = 0u;
     }
     __syncthreads();
-    for (int e = tid; e < n; e += kSelThreads) {
+    for (int e = tid; e < n; e += kTopkThreads) {
         const int j = cand(e);
         unsigned long long kj = key(j);
         if (kj == 0ull) continue;
@@ -1093,15 +1098,15 @@ __global__ __launch_bounds__(kSelThreads) void sel_topk_kernel(SelectParams p, c
         // k_rem-th largest
         const int nb = (int)sh.nborder;
         const unsigned long long kk = kth_desc(sh, sh.border, nb, (int)k_rem - 1, tid);
-        for (int i = tid; i < nb; i += kSelThreads) {
+        for (int i = tid; i < nb; i += kTopkThreads) {
             const unsigned long long kj = sh.border[i];
             if (kj >= kk) sh.sel[atomicAdd(&sh.nsure, 1u)] = (int)(0xffffffffu - (uint32_t)(kj & 0xffffffffull));
         }
         __syncthreads();
     }
     const int nsel = (int)sh.nsure;
-    rank_sort_asc(sh.sel, nsel, out, tid);
-    for (int i = nsel + tid; i < K; i += kSelThreads) out[i] = -1;
+    rank_sort_asc<kTopkThreads>(sh.sel, nsel, out, tid);
+    for (int i = nsel + tid; i < K; i += kTopkThreads) out[i] = -1;
 }
 
 // --------------------------------------------------------------- gather
@@ -1276,7 +1281,7 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
             DSALT_LAUNCH("sel_prune_list", sel_prune_list_kernel, pg, dim3(256), 0, stream, p, pkeep, pcnt, plist,
                          pbelow);
         }
-        DSALT_LAUNCH("sel_topk", sel_topk_kernel, dim3(nsets_total), dim3(kSelThreads), 0, stream, p, zx, zv, nx, nv,
+        DSALT_LAUNCH("sel_topk", sel_topk_kernel, dim3(nsets_total), dim3(kTopkThreads), 0, stream, p, zx, zv, nx, nv,
                      pk, stats, border_cap, prune ? plist : nullptr, pcnt, pbelow, nsb);
         return hipGetLastError();
     }
