@@ -49,8 +49,11 @@ namespace dsalt {
 
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / kWave;
-constexpr int kTopkThreads = 512;  // block-causal sets (sel_topk): more sets in flight per CU
-constexpr int kTopkWaves = kTopkThreads / kWave;
+// block-causal sets (sel_topk): blocks smaller than the global top-k's put more sets in
+// flight per CU; 256 threads when the sets scan pruned lists (a few thousand candidates
+// each), 512 for whole prefixes
+constexpr int kTopkThreads = 512;
+constexpr int kTopkThreadsPruned = 256;
 constexpr int kBorderCap = 2048;
 
 __device__ __forceinline__ int pow2ceil64(int n) {
@@ -379,9 +382,10 @@ constexpr int kSampleList = 1024;  // sample of a pruned list (its candidates ar
 
 constexpr int kKthCand = 64;       // radix passes of kth_desc stop once the bin holds at most this many keys
 
+template <int NT_>
 struct TopkShared {
-    static constexpr int NT = kTopkThreads;
-    uint32_t hist[kTopkWaves][256];
+    static constexpr int NT = NT_;
+    uint32_t hist[NT_ / kWave][256];
     unsigned long long border[kBorderCap > kSample ? kBorderCap : kSample];
     int sel[kMaxLandmarks];
     unsigned long long cand[kKthCand];
@@ -825,12 +829,13 @@ __global__ __launch_bounds__(kSortThreads) void sel_merge_kernel(SelectParams p,
     for (int i = nsel + tid; i < K; i += kSortThreads) o[i] = -1;
 }
 
-__global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, const float* zx, const float* zv,
+template <int NT>
+__global__ __launch_bounds__(NT) void sel_topk_kernel(SelectParams p, const float* zx, const float* zv,
                                                                const float* nx, const float* nv, const uint32_t* pk,
                                                                const double* stats, int border_cap,
                                                                const int32_t* plist, const int* pcnt,
                                                                const int32_t* pbelow, int nsb) {
-    __shared__ TopkShared sh;
+    __shared__ TopkShared<NT> sh;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // blocks of one (head, sequence) are contiguous in the XCD-swizzled order, so each XCD's
     // L2 holds the norms of few heads; within them later sets, which scan longer prefixes,
@@ -861,7 +866,7 @@ __global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, 
     if (block) {
         int b0 = set * p.block_size;
         if (b0 < 2 || b0 >= len) {
-            for (int i = tid; i < K; i += kTopkThreads) out[i] = -1;
+            for (int i = tid; i < K; i += NT) out[i] = -1;
             return;
         }
         n = b0;
@@ -901,19 +906,19 @@ __global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, 
     // Sets of at most kSample candidates: every key in LDS, the K-th largest by kth_desc,
     // the keys at or above it (zero keys, of excluded tokens, never) by ascending index.
     if (n <= kSample && border_cap >= kBorderCap) {
-        for (int i = tid; i < n; i += kTopkThreads) sh.border[i] = key(cand(i));
+        for (int i = tid; i < n; i += NT) sh.border[i] = key(cand(i));
         __syncthreads();
         const unsigned long long kk = n > K ? kth_desc(sh, sh.border, n, K - 1, tid) : 0ull;
         if (tid == 0) sh.nsure = 0u;
         __syncthreads();
-        for (int i = tid; i < n; i += kTopkThreads) {
+        for (int i = tid; i < n; i += NT) {
             const unsigned long long kj = sh.border[i];
             if (kj != 0ull && kj >= kk) sh.sel[atomicAdd(&sh.nsure, 1u)] = (int)(0xffffffffu - (uint32_t)(kj & 0xffffffffull));
         }
         __syncthreads();
         const int nsel = (int)sh.nsure;
-        rank_sort_asc<kTopkThreads>(sh.sel, nsel, out, tid);
-        for (int i = nsel + tid; i < K; i += kTopkThreads) out[i] = -1;
+        rank_sort_asc<NT>(sh.sel, nsel, out, tid);
+        for (int i = nsel + tid; i < K; i += NT) out[i] = -1;
         return;
     }
 
@@ -924,7 +929,7 @@ __global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, 
     // (a pruned list takes it from kSample candidates: its candidates are all near the top)
     const int ns = cl ? kSampleList : kSample;
     if (n >= (cl ? kSample : kSampleMin) && border_cap >= kBorderCap) {
-        for (int i = tid; i < ns; i += kTopkThreads) sh.border[i] = key(cand((int)((int64_t)i * n / ns)));
+        for (int i = tid; i < ns; i += NT) sh.border[i] = key(cand((int)((int64_t)i * n / ns)));
         __syncthreads();
         // aim at about 1.6 K + 128 keys above the threshold (the sample's spread leaves
         // fewer than K above it in a small fraction of the sets: those take the radix path)
@@ -953,13 +958,13 @@ __global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, 
             const float* nxs = nx + st;
             const uint32_t* pkg = pk ? pk + (int64_t)key.rep_g * p.total_len + st : nullptr;
             const float C = -(Cv + Cx), Cm = fabsf(Cv) + fabsf(Cx);
-            for (int j0 = tid; j0 < n; j0 += kTopkThreads * U) {
+            for (int j0 = tid; j0 < n; j0 += NT * U) {
                 float av[U], bv[U];
                 uint32_t wds[U];
                 if (block) {
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
-                        const int j = cand(min(j0 + u * kTopkThreads, n - 1));
+                        const int j = cand(min(j0 + u * NT, n - 1));
                         if (pkg) {
                             wds[u] = pkg[j];
                             av[u] = packed_nx(wds[u]);
@@ -974,7 +979,7 @@ __global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, 
                 uint32_t pass = 0u;
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    const int j = j0 + u * kTopkThreads;
+                    const int j = j0 + u * NT;
                     bool maybe = j < n;
                     if (pkg) maybe = maybe && !(wds[u] & kExcluded);
                     if (block && maybe) {
@@ -987,7 +992,7 @@ __global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, 
                 while (pass) {  // exact keys of the few survivors (one copy of the key code)
                     const int u = __builtin_ctz(pass);
                     pass &= pass - 1u;
-                    const int j = j0 + u * kTopkThreads;
+                    const int j = j0 + u * NT;
                     uint32_t wd = 0u;
 #pragma unroll
                     for (int v = 0; v < U; ++v) wd = v == u ? wds[v] : wd;
@@ -1007,12 +1012,12 @@ __global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, 
             const unsigned long long kk = kth_desc(sh, sh.border, nb, K - 1, tid);
             if (tid == 0) sh.nsure = 0u;
             __syncthreads();
-            for (int i = tid; i < nb; i += kTopkThreads) {
+            for (int i = tid; i < nb; i += NT) {
                 const unsigned long long kj = sh.border[i];
                 if (kj >= kk) sh.sel[atomicAdd(&sh.nsure, 1u)] = (int)(0xffffffffu - (uint32_t)(kj & 0xffffffffull));
             }
             __syncthreads();
-            rank_sort_asc<kTopkThreads>(sh.sel, K, out, tid);
+            rank_sort_asc<NT>(sh.sel, K, out, tid);
             return;
         }
         __syncthreads();
@@ -1023,10 +1028,10 @@ __global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, 
     uint32_t k_rem = (uint32_t)K;
     bool all_sure = false;
     for (;;) {
-        for (int i = tid; i < kTopkWaves * 256; i += kTopkThreads) (&sh.hist[0][0])[i] = 0u;
+        for (int i = tid; i < (NT / kWave) * 256; i += NT) (&sh.hist[0][0])[i] = 0u;
         __syncthreads();
         const int shift = 56 - plen;
-        for (int j = tid; j < n; j += kTopkThreads) {
+        for (int j = tid; j < n; j += NT) {
             unsigned long long kj = key(cand(j));
             if (kj == 0ull) continue;
             if (plen > 0 && (kj >> (64 - plen)) != prefix) continue;
@@ -1035,7 +1040,7 @@ __global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, 
         __syncthreads();
         if (tid < 256) {
             uint32_t c = 0;
-            for (int w2 = 0; w2 < kTopkWaves; ++w2) c += sh.hist[w2][tid];
+            for (int w2 = 0; w2 < (NT / kWave); ++w2) c += sh.hist[w2][tid];
             sh.hist[0][tid] = c;
         }
         __syncthreads();
@@ -1080,7 +1085,7 @@ __global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, 
         sh.nborder = 0u;
     }
     __syncthreads();
-    for (int e = tid; e < n; e += kTopkThreads) {
+    for (int e = tid; e < n; e += NT) {
         const int j = cand(e);
         unsigned long long kj = key(j);
         if (kj == 0ull) continue;
@@ -1098,15 +1103,15 @@ __global__ __launch_bounds__(kTopkThreads) void sel_topk_kernel(SelectParams p, 
         // k_rem-th largest
         const int nb = (int)sh.nborder;
         const unsigned long long kk = kth_desc(sh, sh.border, nb, (int)k_rem - 1, tid);
-        for (int i = tid; i < nb; i += kTopkThreads) {
+        for (int i = tid; i < nb; i += NT) {
             const unsigned long long kj = sh.border[i];
             if (kj >= kk) sh.sel[atomicAdd(&sh.nsure, 1u)] = (int)(0xffffffffu - (uint32_t)(kj & 0xffffffffull));
         }
         __syncthreads();
     }
     const int nsel = (int)sh.nsure;
-    rank_sort_asc<kTopkThreads>(sh.sel, nsel, out, tid);
-    for (int i = nsel + tid; i < K; i += kTopkThreads) out[i] = -1;
+    rank_sort_asc<NT>(sh.sel, nsel, out, tid);
+    for (int i = nsel + tid; i < K; i += NT) out[i] = -1;
 }
 
 // --------------------------------------------------------------- gather
@@ -1281,8 +1286,12 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
             DSALT_LAUNCH("sel_prune_list", sel_prune_list_kernel, pg, dim3(256), 0, stream, p, pkeep, pcnt, plist,
                          pbelow);
         }
-        DSALT_LAUNCH("sel_topk", sel_topk_kernel, dim3(nsets_total), dim3(kTopkThreads), 0, stream, p, zx, zv, nx, nv,
-                     pk, stats, border_cap, prune ? plist : nullptr, pcnt, pbelow, nsb);
+        if (prune)
+            DSALT_LAUNCH("sel_topk", sel_topk_kernel<kTopkThreadsPruned>, dim3(nsets_total), dim3(kTopkThreadsPruned), 0,
+                         stream, p, zx, zv, nx, nv, pk, stats, border_cap, plist, pcnt, pbelow, nsb);
+        else
+            DSALT_LAUNCH("sel_topk", sel_topk_kernel<kTopkThreads>, dim3(nsets_total), dim3(kTopkThreads), 0, stream, p,
+                         zx, zv, nx, nv, pk, stats, border_cap, nullptr, pcnt, pbelow, nsb);
         return hipGetLastError();
     }
     const TopkPlan t = topk_plan(p, border_cap);
