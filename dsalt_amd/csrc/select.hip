@@ -26,7 +26,7 @@
 //     block:    (bf16, sequences of 65536+ tokens) sel_prune_* list per kv head
 //               the candidates that fewer than k earlier candidates can dominate
 //               in both norms (a lower bound from 2D bin histograms); the others
-//               are in no set's top k.  sel_topk, one 1024-thread block per
+//               are in no set's top k.  sel_topk, one 256/512-thread block per
 //               landmark set (largest sets first), scans the listed candidates
 //               below the set's start (or the whole prefix).  Sets of at most 2048:
 //               every key in LDS and one order statistic.  Larger sets (8192+
