@@ -833,8 +833,7 @@ template <int NT>
 __global__ __launch_bounds__(NT) void sel_topk_kernel(SelectParams p, const float* zx, const float* zv,
                                                                const float* nx, const float* nv, const uint32_t* pk,
                                                                const double* stats, int border_cap,
-                                                               const int32_t* plist, const int* pcnt,
-                                                               const int32_t* pbelow, int nsb) {
+                                                               const int32_t* plist, const int32_t* pbelow) {
     __shared__ TopkShared<NT> sh;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // blocks of one (head, sequence) are contiguous in the XCD-swizzled order, so each XCD's
@@ -883,22 +882,9 @@ __global__ __launch_bounds__(NT) void sel_topk_kernel(SelectParams p, const floa
     // entries below b0 where it applies to this head (alpha in [0, 1]), else 0 .. b0-1
     const int32_t* cl = nullptr;
     if (block && plist && key.alpha >= 0.f && key.alpha <= 1.f) {
+        // b0 is a multiple of 16 (block_size is a multiple of 64, checked at the boundary)
         cl = plist + (int64_t)key.rep_g * p.total_len + st;
-        if (n % 16 == 0) {
-            n = pbelow[(int64_t)key.rep_g * p.total_len + st + n];
-        } else {
-            const int64_t gs = (int64_t)key.rep_g * p.num_seqs + s;
-            const int Mb = n / kPruneSB;  // entries of earlier super-blocks all lie below b0
-            int off = 0;
-            for (int m = 0; m < Mb; ++m) off += pcnt[gs * nsb + m];
-            int lo = off, hi = off + pcnt[gs * nsb + Mb];
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (cl[mid] < n) lo = mid + 1;
-                else hi = mid;
-            }
-            n = lo;
-        }
+        n = pbelow[(int64_t)key.rep_g * p.total_len + st + n];
     }
     auto cand = [&](int e) { return cl ? cl[e] : e; };
     const int cap = min(border_cap, kBorderCap);
@@ -1288,10 +1274,10 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
         }
         if (prune)
             DSALT_LAUNCH("sel_topk", sel_topk_kernel<kTopkThreadsPruned>, dim3(nsets_total), dim3(kTopkThreadsPruned), 0,
-                         stream, p, zx, zv, nx, nv, pk, stats, border_cap, plist, pcnt, pbelow, nsb);
+                         stream, p, zx, zv, nx, nv, pk, stats, border_cap, plist, pbelow);
         else
             DSALT_LAUNCH("sel_topk", sel_topk_kernel<kTopkThreads>, dim3(nsets_total), dim3(kTopkThreads), 0, stream, p,
-                         zx, zv, nx, nv, pk, stats, border_cap, nullptr, pcnt, pbelow, nsb);
+                         zx, zv, nx, nv, pk, stats, border_cap, nullptr, nullptr);
         return hipGetLastError();
     }
     const TopkPlan t = topk_plan(p, border_cap);

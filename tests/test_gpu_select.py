@@ -170,3 +170,12 @@ def test_block_pruned_workload_shortened():
     idx, ridx = _run(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, ops.SELECT_BLOCK, 512,
                      ops.STATS_SEQUENCE, want=False, border_cap=ops.SELECT_FORCE_PRUNE)
     np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
+@pytest.mark.parametrize("block", [64, 128])
+def test_block_pruned_block_sizes(block):
+    # the smallest block sizes (many sets, each reading its survivor count at its start)
+    h, v, alpha, w, cu = _case([9000, 6000], 128, 2, 64, 4, torch.bfloat16, 300, seed=11, scale_tails=True)
+    idx, ridx = _run(h, v, alpha, w, cu, 32, ops.SELECT_BLOCK, block, ops.STATS_SEQUENCE, want=False,
+                     border_cap=ops.SELECT_FORCE_PRUNE)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
