@@ -30,6 +30,30 @@ MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}  # dense
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 
+def kernel_source_sha() -> str:
+    """Hash of the HIP sources and the C header: a traffic record measured on other sources is stale."""
+    import hashlib
+    hs = hashlib.sha256()
+    for d in (os.path.join(HERE, "dsalt_amd", "csrc"), os.path.join(HERE, "include")):
+        for fn in sorted(os.listdir(d)):
+            with open(os.path.join(d, fn), "rb") as f:
+                hs.update(fn.encode() + b"\0" + f.read())
+    return hs.hexdigest()[:16]
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu "Model name", read from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -107,7 +131,8 @@ def traffic_from(root: str, wl_name: str, copy_mib: int = 1024) -> dict:
     w_fac = known / copy_reading("copy_write", "WRITE_SIZE")
     fetch = read_pmc(os.path.join(root, "fetch"))
     write = read_pmc(os.path.join(root, "write"))
-    res = {"_calibration": {"copy_bytes": known, "fetch_factor": f_fac, "write_factor": w_fac}}
+    res = {"_calibration": {"copy_bytes": known, "fetch_factor": f_fac, "write_factor": w_fac},
+           "_sources": kernel_source_sha()}
     for k in sorted(set(fetch) & set(write) & set(LABELS)):
         fb = fetch[k]["FETCH_SIZE"] * 1024.0 * f_fac
         wb = write[k]["WRITE_SIZE"] * 1024.0 * w_fac
@@ -118,16 +143,19 @@ def traffic_from(root: str, wl_name: str, copy_mib: int = 1024) -> dict:
     return res
 
 
-def kernel_model(wl, T, H, D, hidden, pairs, e):
-    """Algorithmic bytes and flops per launch of each kernel (no recompute, no workspace)."""
+def kernel_model(wl, T, H, D, hidden, pairs, e, G=None):
+    """Algorithmic bytes and flops per launch of each kernel (no recompute, no workspace);
+    K and V (and dK, dV) count their own G heads when they are read unexpanded."""
+    G = G or H
     thd = T * H * D * e
+    tgd = T * G * D * e
     th4 = 4 * T * H
     tr = th4 if wl.train else 0  # training variant: per-head window gradients written by bwd_dq
     return {
-        "sel_norms": dict(bytes=T * hidden * e + thd, flops=0),
-        "attn_fwd": dict(bytes=4 * thd + th4, flops=4 * D * pairs),
-        "bwd_dq": dict(bytes=6 * thd + 2 * th4 + tr, flops=4 * D * pairs),
-        "bwd_dkdv": dict(bytes=6 * thd + 2 * th4, flops=4 * D * pairs),
+        "sel_norms": dict(bytes=T * hidden * e + tgd, flops=0),
+        "attn_fwd": dict(bytes=2 * thd + 2 * tgd + th4, flops=4 * D * pairs),
+        "bwd_dq": dict(bytes=4 * thd + 2 * tgd + 2 * th4 + tr, flops=4 * D * pairs),
+        "bwd_dkdv": dict(bytes=2 * thd + 4 * tgd + 2 * th4, flops=4 * D * pairs),
     }
 
 
@@ -418,6 +446,7 @@ def main():
     x_cpu = generate(wl)
     x = {k: v.to(dev) for k, v in x_cpu.items()}
     T, H, D = x["q"].shape
+    G = x["k"].shape[1]
     mode = ops.SELECT_GLOBAL if wl.select_mode == "global" else ops.SELECT_BLOCK
     scope = ops.STATS_SEQUENCE
     maxlen = wl.seqlen
@@ -502,7 +531,7 @@ def main():
         name, n, tot = line.split()
         kernels[name] = dict(launches=int(n), avg_ms=float(tot) / int(n), ms_per_step=float(tot) / args.steps)
 
-    model = kernel_model(wl, T, H, D, wl.hidden, pairs, e)
+    model = kernel_model(wl, T, H, D, wl.hidden, pairs, e, G)
     dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
     roof = None
     if dom in model:
@@ -512,7 +541,10 @@ def main():
         tpath = os.path.join(HERE, "profiles", f"traffic_{wl.name}.json")
         if os.path.exists(tpath):
             with open(tpath) as f:
-                traffic = (json.load(f).get(dom) or {}).get("bytes")
+                rec = json.load(f)
+            # only a record measured on the current kernel sources counts
+            if rec.get("_sources") == kernel_source_sha():
+                traffic = (rec.get(dom) or {}).get("bytes")
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "algorithmic_bytes": model[dom]["bytes"],
@@ -522,9 +554,10 @@ def main():
     # unique algorithmic traffic of a step: q, k, v, o (+ h for the selection) and the LSE in
     # the forward; q, k, v, o, dO, dq, dk, dv and the LSE in the backward
     thd = T * H * D * e
-    step_bytes = 4 * thd + T * wl.hidden * e + 4 * T * H
+    tgd = T * G * D * e
+    step_bytes = 2 * thd + 2 * tgd + T * wl.hidden * e + 4 * T * H
     if wl.backward:
-        step_bytes += 8 * thd + 4 * T * H
+        step_bytes += 4 * thd + 4 * tgd + 4 * T * H
     step_flops = (4 + (8 if wl.backward else 0)) * D * pairs
     t_roof = max(step_bytes / (HBM_PEAK_GBS * 1e9), step_flops / (MFMA_PEAK_TFLOPS[dtn] * 1e12))
 
@@ -534,6 +567,7 @@ def main():
         r = time_baseline(x_cpu, wl.k_lmk, scope, backward=wl.backward,
                           train=(wl.tau_win, wl.win_edge, wl.tau_lmk) if wl.train else None)
         cpu = {"value": round(r["tokens_per_s"], 2), "unit": "tokens/s", "cores": r["threads"], "kind": "port",
+               "cpu_model": cpu_model(), "torch_threads": r["threads"], "cpu_count": r["cpu_count"],
                "sample": (f"full-length landmark selection (C oracle, 1 thread, {r['t_select']:.2f}s) + reference "
                           f"{'dense training log-bias + SDPA' if wl.train else 'masked-SDPA'} "
                           f"{'fwd+bwd' if wl.backward else 'fwd'} on the last {r['rows']} query rows x "
@@ -553,7 +587,8 @@ def main():
         "vs_baseline": None,
         "dtype": dtn,
         "data": "synthetic",
-        "config": {"workload": wl.name, "batch": wl.batch, "heads": H, "seq_len": wl.seqlen, "head_dim": D,
+        "config": {"workload": wl.name, "batch": wl.batch, "heads": H, "kv_heads": G, "seq_len": wl.seqlen,
+                   "head_dim": D,
                    "hidden": wl.hidden, "w_max": wl.w_max, "k_lmk": wl.k_lmk, "select": wl.select_mode,
                    "backward": wl.backward, "pairs": pairs,
                    **({"variant": "train", "tau_win": wl.tau_win, "win_edge": wl.win_edge, "tau_lmk": wl.tau_lmk}

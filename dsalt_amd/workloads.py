@@ -4,7 +4,8 @@ Each workload is generated on the CPU with ``torch.Generator().manual_seed(seed)
 float32 and then cast, so the bits handed to the GPU and to any CPU check are identical.
 Draw order: q, k, v, h, window normals, upstream gradient.
 Windows: ``w_i = clamp(round_half_even(sigmoid(z_i) * w_max), 16, w_max)``.
-Landmark score: alpha = 0.5 for every head (the same ranking as z(|v|) + z(|h|)).
+Landmark score: alpha = 0.5 for every head (the same ranking as z(|v|) + z(|h|)) unless the
+workload states another value.
 Training workloads draw the same tensors and keep the windows continuous,
 ``w~_i = clamp(sigmoid(z_i) * w_max, 16, w_max)``; their hard selection uses ``floor(w~)``.
 """
@@ -35,6 +36,12 @@ class Workload:
     tau_win: float = 1.0
     win_edge: float = 4.0
     tau_lmk: float = 2.0
+    kv_heads: int = 0            # key/value heads (0: as many as query heads)
+    alpha: float = 0.5           # landmark score weight of every head
+
+    @property
+    def n_kv(self) -> int:
+        return self.kv_heads or self.heads
 
     @property
     def total_len(self) -> int:
@@ -57,6 +64,12 @@ WORKLOADS = {
         # forward (inference), bf16, 128K tokens, block-causal landmarks (512-query blocks)
         Workload("fwd_bf16_h16_l131072_block", 1, 16, 131072, 128, 2048, torch.bfloat16, 512, 256, False,
                  select_mode="block", block_size=512, seed=1003),
+        # forward (inference) of one decoder layer's attention shaped like the Qwen2.5-3B
+        # graft: 16 query heads, 2 key/value heads (GQA, read in place), head_dim 128,
+        # hidden 2048, block-causal landmarks k=128 in 512-query blocks, alpha 0.6 (the
+        # layer's initial value)
+        Workload("fwd_bf16_h16kv2_l32768_block", 1, 16, 32768, 128, 2048, torch.bfloat16, 512, 128, False,
+                 select_mode="block", block_size=512, seed=1004, kv_heads=2, alpha=0.6),
     ]
 }
 
@@ -70,26 +83,27 @@ def generate(wl: Workload, device="cpu", seqlen: int | None = None, heads: int |
     """Inputs of a workload as a dict of tensors on ``device``.
 
     ``seqlen`` / ``heads`` shrink the shape for tests while keeping the recipe.
-    Keys: q, k, v [T,H,D]; h [T,hidden]; w [T] int32; cu [S+1] int32; alpha [H] fp32;
+    Keys: q [T,H,D]; k, v [T,n_kv,D]; h [T,hidden]; w [T] int32; cu [S+1] int32; alpha [H] fp32;
     dout [T,H,D] (backward workloads); w_cont [T] fp32 (training workloads, with w = floor).
     """
     L = seqlen or wl.seqlen
     H = heads or wl.heads
+    G = max(1, H * wl.n_kv // wl.heads)
     T = wl.batch * L
     g = torch.Generator().manual_seed(wl.seed)
     q = torch.randn(T, H, wl.head_dim, generator=g)
-    k = torch.randn(T, H, wl.head_dim, generator=g)
-    v = torch.randn(T, H, wl.head_dim, generator=g)
+    k = torch.randn(T, G, wl.head_dim, generator=g)
+    v = torch.randn(T, G, wl.head_dim, generator=g)
     h = torch.randn(T, wl.hidden, generator=g)
     zw = torch.randn(T, generator=g)
     if wl.heavy_tails:
-        v = v * torch.exp(torch.randn(T, H, 1, generator=g))
+        v = v * torch.exp(torch.randn(T, G, 1, generator=g))
         h = h * torch.exp(0.5 * torch.randn(T, 1, generator=g))
     out = dict(
         q=q.to(wl.dtype), k=k.to(wl.dtype), v=v.to(wl.dtype), h=h.to(wl.dtype),
         w=make_windows(zw, wl.w_max),
         cu=torch.arange(0, T + 1, L, dtype=torch.int32),
-        alpha=torch.full((H,), 0.5, dtype=torch.float32),
+        alpha=torch.full((H,), wl.alpha, dtype=torch.float32),
     )
     if wl.train:
         out["w_cont"] = (torch.sigmoid(zw) * wl.w_max).clamp(16, wl.w_max).to(torch.float32)

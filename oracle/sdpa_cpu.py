@@ -128,7 +128,12 @@ def time_baseline(x: dict, k_lmk: int, stats_scope: int, target_s: float = 12.0,
     Returns a dict with tokens_per_s, threads, rows and the timing split.
     """
     threads = torch.get_num_threads()
-    T = x["q"].shape[0]
+    T, H = x["q"].shape[:2]
+    rep = H // x["k"].shape[1]
+    # grouped K/V heads are repeated per query head, as the reference's fallback does
+    # (dsalt/modules/dsalt_attention.py:254-268)
+    kx = x["k"].repeat_interleave(rep, dim=1) if rep > 1 else x["k"]
+    vx = x["v"].repeat_interleave(rep, dim=1) if rep > 1 else x["v"]
     t0 = time.perf_counter()
     res = OS.select(_bits(x["h"]), _bits(x["v"]), x["alpha"].numpy(), x["w"].numpy(), x["cu"].numpy(), k_lmk,
                     _odt(x["h"].dtype), stats_scope=stats_scope, want_scores=train is not None)
@@ -150,17 +155,17 @@ def time_baseline(x: dict, k_lmk: int, stats_scope: int, target_s: float = 12.0,
         for r0 in range(T - nrows, T, chunk):
             rows = torch.arange(r0, min(T, r0 + chunk))
             if train is not None:
-                _train_attention_rows(x["q"][rows], x["k"], x["v"], x["dout"][rows], x["w_cont"], logw, x["cu"],
+                _train_attention_rows(x["q"][rows], kx, vx, x["dout"][rows], x["w_cont"], logw, x["cu"],
                                       pos, rows, train[0], train[1])
                 continue
             m = literal_mask_rows(x["w"], x["cu"], idx, rows)
             if backward:
-                _attention_rows(x["q"][rows], x["k"], x["v"], x["dout"][rows], m)
+                _attention_rows(x["q"][rows], kx, vx, x["dout"][rows], m)
             else:
                 with torch.no_grad():
                     additive = torch.zeros(m.shape, dtype=x["q"].dtype).masked_fill(~m, float("-inf"))[None, None]
-                    F.scaled_dot_product_attention(x["q"][rows].transpose(0, 1)[None], x["k"].transpose(0, 1)[None],
-                                                   x["v"].transpose(0, 1)[None], attn_mask=additive)
+                    F.scaled_dot_product_attention(x["q"][rows].transpose(0, 1)[None], kx.transpose(0, 1)[None],
+                                                   vx.transpose(0, 1)[None], attn_mask=additive)
         return time.perf_counter() - t1
 
     probe = min(T, 256)
