@@ -61,6 +61,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="fwdbwd_bf16_h16_l32768")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--variant", type=int, default=0, help="tile variant bits (DSALT_VARIANT_*) of the attention kernels")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy (negate) a MIB-MiB device buffer five times (HBM counter calibration) and exit")
     ap.add_argument("--traffic-from", metavar="DIR",
@@ -75,7 +76,7 @@ def parse():
 
 LABELS = ("sel_norms", "sel_sums", "sel_stats", "sel_z", "sel_scores", "sel_part", "sel_merge", "sel_prune_hist",
           "sel_prune_prefix", "sel_prune_mark", "sel_prune_list", "sel_topk", "gather",
-          "row_plan", "attn_fwd", "bwd_init", "bwd_dq", "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum", "train_windows", "train_dw",
+          "row_plan", "attn_fwd", "bwd_prep", "bwd_dq", "bwd_dkdv", "bwd_lmk", "bwd_lmk_sum", "train_windows", "train_dw",
           "rope", "silu_mul", "probs", "ce_rows")
 
 
@@ -85,7 +86,7 @@ def short_kernel_name(name: str) -> str:
     # the label must start the identifier (a mangled length prefix, "::" or the start): no
     # match inside library names such as reduce_kernel or vectorized_gather_kernel
     m = re.search(r"(?<![A-Za-z_])(sel_norms|sel_sums|sel_stats|sel_z|sel_scores|sel_part|sel_merge|sel_prune_hist|"
-                  r"sel_prune_prefix|sel_prune_mark|sel_prune_list|sel_topk|gather|row_plan|fwd|bwd_init|bwd_dq|"
+                  r"sel_prune_prefix|sel_prune_mark|sel_prune_list|sel_topk|gather|row_plan|fwd|bwd_prep|bwd_dq|"
                   r"bwd_dkdv|bwd_lmk_sum|train_windows|train_dw|rope|silu_mul|probs|ce|"
                   r"bwd_lmk)_kernel", name)
     if not m:
@@ -472,14 +473,20 @@ def main():
                                tau_win=tau_win, win_edge=win_edge, max_seqlen=maxlen)
             return idx
     else:
+        plan = None
+
         def step():
+            nonlocal plan
             idx = ops.select_landmarks(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, max_seqlen=maxlen,
                                        select_mode=mode, block_size=wl.block_size, stats_scope=scope)
+            if plan is None and wl.backward:  # the forward's row plan, reused by the backward
+                plan = ops.new_plan(x["q"], x["k"], x["cu"], idx, max_seqlen=maxlen)
             out, lse = ops.attention_forward(x["q"], x["k"], x["v"], x["w"], x["cu"], idx, None, max_seqlen=maxlen,
-                                             select_mode=mode, block_size=wl.block_size)
+                                             select_mode=mode, block_size=wl.block_size, plan=plan,
+                                             variant=args.variant)
             if wl.backward:
                 ops.attention_backward(x["dout"], x["q"], x["k"], x["v"], out, lse, x["w"], x["cu"], idx, None,
-                                       max_seqlen=maxlen, want_dbias=False)
+                                       max_seqlen=maxlen, want_dbias=False, plan=plan, variant=args.variant)
             return idx
 
     for _ in range(args.warmup):

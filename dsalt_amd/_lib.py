@@ -17,6 +17,9 @@ DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 SELECT_GLOBAL, SELECT_BLOCK = 0, 1
 STATS_PACKED, STATS_SEQUENCE = 0, 1
 ERR_NAMES = {1: "invalid argument", 2: "unsupported", 3: "workspace", 4: "HIP error"}
+ABI_VERSION = 2
+# tile variants of the attention kernels (DSALT_VARIANT_*)
+VARIANT_DEFAULT, VARIANT_FWD_BN32, VARIANT_FWD_RG2, VARIANT_DQ_BN64, VARIANT_LMK_SHORT = 0, 1, 2, 4, 8
 
 _i32, _i64, _vp, _sz, _f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float
 
@@ -52,7 +55,7 @@ class FwdArgs(ctypes.Structure):
                 ("w", _vp), ("cu_seqlens", _vp), ("lmk_idx", _vp), ("lmk_bias", _vp),
                 ("out", _vp), ("o_stride_t", _i64), ("o_stride_h", _i64),
                 ("lse", _vp), ("scale", _f32),
-                ("workspace", _vp), ("workspace_bytes", _sz)]
+                ("workspace", _vp), ("workspace_bytes", _sz), ("plan", _vp), ("variant", _i32)]
 
 
 class BwdArgs(ctypes.Structure):
@@ -64,7 +67,7 @@ class BwdArgs(ctypes.Structure):
                 ("dout", _vp), ("do_stride_t", _i64), ("do_stride_h", _i64),
                 ("lse", _vp), ("w", _vp), ("cu_seqlens", _vp), ("lmk_idx", _vp), ("lmk_bias", _vp),
                 ("dq", _vp), ("dk", _vp), ("dv", _vp), ("d_bias", _vp), ("scale", _f32),
-                ("workspace", _vp), ("workspace_bytes", _sz)]
+                ("workspace", _vp), ("workspace_bytes", _sz), ("plan", _vp), ("variant", _i32)]
 
 
 class TrainFwdArgs(ctypes.Structure):
@@ -119,6 +122,7 @@ SIGNATURES = {
     "dsalt_select": ([ctypes.POINTER(SelectArgs), _vp], ctypes.c_int),
     "dsalt_select_with_border_cap": ([ctypes.POINTER(SelectArgs), _vp, ctypes.c_int], ctypes.c_int),
     "dsalt_select_workspace_bytes_cap": ([ctypes.POINTER(SelectArgs), ctypes.c_int], _sz),
+    "dsalt_plan_bytes": ([ctypes.POINTER(Problem)], _sz),
     "dsalt_fwd_workspace_bytes": ([ctypes.POINTER(FwdArgs)], _sz),
     "dsalt_fwd": ([ctypes.POINTER(FwdArgs), _vp], ctypes.c_int),
     "dsalt_bwd_workspace_bytes": ([ctypes.POINTER(BwdArgs)], _sz),
@@ -155,7 +159,7 @@ def load(path: str | None = None):
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = res
-    if lib.dsalt_abi_version() != 1:
+    if lib.dsalt_abi_version() != ABI_VERSION:
         raise ImportError(f"{p}: unexpected ABI version {lib.dsalt_abi_version()}")
     if path is None:
         _LIB = lib

@@ -8,6 +8,8 @@
 
 namespace dsalt {
 
+constexpr int kNoOwner = 0x7fffffff;  // lmk_owner of a row that is no landmark
+
 struct AttnParams {
     int total_len, num_seqs, max_seqlen, n_heads, n_kv_heads, head_dim, k_lmk;
     int n_sets, block_size;  // block_size 0 in the global variant
@@ -48,6 +50,8 @@ struct AttnParams {
     // rows ordered by window start, and per 16-row group {min lo, max lo, max i, min i}
     uint8_t* plan_perm;      // [S * n_tiles * 64] row offset within the tile
     int* plan_bounds;        // [S * n_tiles * 4 * 4]
+    int* tile_wmax;          // [S * n_tiles] largest clamped window of the tile's rows
+    int variant;             // DSALT_VARIANT_* bits
     // backward workspace
     float* delta;            // [H, T] rowsum(O * dO), head-major (written by the dQ pass)
     int* cnt;                // [H, T] landmarks visible to each row (written by the dQ pass)
@@ -56,6 +60,9 @@ struct AttnParams {
     float* part_k;           // [n_chunks, H, S, K, D] landmark dK partials
     float* part_v;           // [n_chunks, H, S, K, D]
     float* part_b;           // [n_chunks, H, S, K]
+    float* lmk_stage;        // [2, H, S, K, D] fp32 band dK / dV of landmark rows (dK/dV pass)
+    int* lmk_owner;          // [n_kv, T] h * K + slot of the first (head, slot) of the key/value
+                             // head's group holding the row as a landmark, kNoOwner elsewhere
     int n_chunks;            // row chunks of the landmark backward
 };
 
@@ -101,13 +108,15 @@ __device__ __forceinline__ float edge_lookup(const float* t, int k) {
 }
 
 size_t plan_bytes(const AttnParams& p);
-void plan_carve(AttnParams& p, char*& ws);  // assigns plan_perm / plan_bounds from a workspace
+void plan_carve(AttnParams& p, char*& ws);  // assigns plan_perm / plan_bounds / tile_wmax from a buffer
 hipError_t plan_launch(const AttnParams& p, hipStream_t stream);
-hipError_t fwd_launch(AttnParams p, void* ws, hipStream_t stream);
+// plan: a caller buffer of plan_bytes() that receives the row plan, or null (workspace)
+hipError_t fwd_launch(AttnParams p, void* ws, void* plan, hipStream_t stream);
 // training variant: integer windows floor(w~) + 1 written into `w_int` ([T] int32)
 hipError_t train_windows_launch(const AttnParams& p, int* w_int, hipStream_t stream);
 size_t bwd_workspace(const AttnParams& p);
-hipError_t bwd_launch(AttnParams p, void* ws, hipStream_t stream);
+// plan: the row plan the forward wrote for the same rows, or null (computed here)
+hipError_t bwd_launch(AttnParams p, void* ws, const void* plan, hipStream_t stream);
 // training variant: d_w[t] = sum over heads of dw_h[t, h], in head order
 hipError_t train_dw_launch(const AttnParams& p, hipStream_t stream);
 

@@ -3,7 +3,8 @@
 // Replaces _dsalt_bwd_preprocess and _dsalt_bwd_kernel
 // (dsalt/kernels/dsalt_triton_bwd.py:17-216), which accumulate dK/dV with
 // atomic_add.  Here every output element has exactly one writer:
-//   bwd_init     clears the per-sequence largest window.
+//   bwd_prep     clears the landmark-row owners and sets each sequence's
+//                largest window (from the forward's row plan when reused).
 //   bwd_dq       query-parallel, like the forward (64 rows per block, one row
 //                per lane): delta = rowsum(O dO) from the stored O (:44),
 //                dQ = scale * dS K over the band and the landmark slots
@@ -14,8 +15,11 @@
 //                dV = P^T dO, dK = scale * dS^T Q (:198-199).
 //   bwd_lmk      landmark slots x 1024-row chunks: partial dK/dV/d_bias of each
 //                (head, sequence, slot) (:150-155).
-//   bwd_lmk_sum  sums the partials in chunk order and adds them into the dK/dV
-//                rows at the landmark positions.
+//   bwd_lmk_sum  per landmark row: the band sums the dK/dV pass left in fp32
+//                plus the partials of every head holding the row, in head and
+//                chunk order, rounded once into the dK/dV row.
+// Grouped heads: dQ and the landmark pass run per query head; the dK/dV pass
+// runs per key/value head and sweeps the group's query heads in order.
 // P = exp(q.k * scale + bias - LSE) is recomputed in base 2 from the forward's
 // LSE; dS = P (dP - delta), dP = dO V^T.  Products over tokens read their
 // transposed operand from the row-major tiles with ds_read_b64_tr_b16.
@@ -68,17 +72,34 @@ __device__ __forceinline__ int load_set(const AttnParams& p, int64_t set_off, in
     return *nvalid_s;
 }
 
-__global__ void bwd_init_kernel(AttnParams p) {
-    const int s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s < p.num_seqs) p.seq_wmax[s] = 1;
+// Clears the landmark-row owners; per sequence, the largest window: from the forward's
+// row plan when it is reused (plan_given), else a start value that row_plan raises.
+__global__ __launch_bounds__(256) void bwd_prep_kernel(AttnParams p, int plan_given) {
+    if (p.lmk_owner) {
+        const int64_t n = (int64_t)p.n_kv_heads * p.total_len;
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+            p.lmk_owner[i] = kNoOwner;
+    }
+    if ((int)blockIdx.x >= p.num_seqs) return;
+    const int s = blockIdx.x;
+    if (!plan_given) {
+        if (threadIdx.x == 0) p.seq_wmax[s] = 1;
+        return;
+    }
+    __shared__ int red[4];
+    int m = 1;
+    for (int t = threadIdx.x; t < p.n_tiles; t += 256) m = max(m, p.tile_wmax[(int64_t)s * p.n_tiles + t]);
+    for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) p.seq_wmax[s] = max(max(red[0], red[1]), max(red[2], red[3]));
 }
 
 // -------------------------------------------------------------------- dQ
 // TR: training variant -- band keys near the window start carry the soft edge bias,
 // and the lane also sums dS * d(bias)/d(w~) of its row into dw_h.
-template <typename T, int D, bool TR>
-__global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (TR ? 5 : 6) : 2) void bwd_dq_kernel(AttnParams p) {
-    constexpr int BN = BwdShape<T, D>::BN;
+template <typename T, int D, int BN, bool TR>
+__global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR ? 5 : 6) : 4) : 2) void bwd_dq_kernel(AttnParams p) {
     constexpr int NST = BN / 16;
     constexpr bool kHalf = sizeof(T) == 2;
     typedef Tile<T, D, BN> KT;
@@ -107,6 +128,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (TR ? 5 : 6) : 2
     const float inv_scale = p.inv_scale;
     const bool has_bias = p.lbias != nullptr;
     const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid, has_bias ? lbs : nullptr);
+    // landmark rows of this tile: the first (head, slot) of the group holding a row owns it
+    // (integer minimum: the same owner whatever the order of the updates)
+    if (p.lmk_owner)
+        for (int sl = tid; sl < nvalid; sl += 256) {
+            const int q = lpos[sl];
+            if (q >= r0 && q < min(r0 + 64, len)) atomicMin(p.lmk_owner + (int64_t)kvh * p.total_len + st + q, h * K + sl);
+        }
 
     // this wave's rows (ordered by window start) and their bounds, from the row plan
     const int uw = uniform(wave);
@@ -395,11 +423,14 @@ struct QLoader {
 //     partial rows j0 < lo_i <= j0+63   (see keys >= lo_i: one-sided mask);
 // rows with lo_i > j0 + 63 are skipped.  List order is row order, so the sum
 // order is fixed and results are deterministic.
-// four waves per SIMD for 16-bit head_dim 64 (32-row stages keep it free of spills), two otherwise.
+// four waves per SIMD for 16-bit head_dim 64 (32-row stages keep it free of spills; three with
+// grouped heads, whose head loop needs more registers), two otherwise.
 // TR: training variant -- fully visible rows must also see every key of the block
 // past their edge_keys edge-bias keys; other rows add the soft edge bias.
-template <typename T, int D, bool TR>
-__global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_dkdv_kernel(AttnParams p) {
+// GQA: the key/value head has several query heads (swept in order); without it the
+// sweep is straight-line code for one head.
+template <typename T, int D, bool TR, bool GQA>
+__global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (GQA ? 3 : 4) : 2) void bwd_dkdv_kernel(AttnParams p) {
     constexpr int BQ = BwdShape<T, D>::BQ;
     constexpr int NQS = BQ / 16;
     constexpr int NDIAG = 64 / BQ;
@@ -411,11 +442,12 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_
     __shared__ int wcnt[4][8];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
-    const int total = p.n_heads * p.num_seqs * p.n_tiles;
+    const int total = p.n_kv_heads * p.num_seqs * p.n_tiles;
     const int L = xcd_swizzle(blockIdx.x, total);
     const int t = L % p.n_tiles;
     const int s = (L / p.n_tiles) % p.num_seqs;
-    const int h = L / (p.n_tiles * p.num_seqs);
+    const int kvh = L / (p.n_tiles * p.num_seqs);
+    const int rep = GQA ? p.n_heads / p.n_kv_heads : 1;
     int st, len;
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     const int j0 = t * 64;
@@ -426,19 +458,31 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_
     const int j = wj0 + (lane & 15);
     const bool jvalid = j < len;
     const int jj = jvalid ? j : -1;  // below every window start when past the end
-    const T* khead = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)h * p.k_sh;
-    const T* vhead = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)h * p.v_sh;
+    const T* khead = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)kvh * p.k_sh;
+    const T* vhead = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)kvh * p.v_sh;
     RowReg<T, D> kr, vr;
     kr.load(jvalid ? khead + (int64_t)j * p.k_st : nullptr, khead, g);
     vr.load(jvalid ? vhead + (int64_t)j * p.v_st : nullptr, vhead, g);
 
     const int iend = uniform(min(len, j0 + 63 + p.seq_wmax[s]));
+    const int* wrow = p.w + st;
+    QLoader<T, D, BQ> ld(p, tid);
+    floatx4 adk[D / 16], adv[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+        adk[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        adv[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float NEG = -INFINITY;
+    const int lane_off = 4 * g;
+    // the query heads of this key/value head are swept one after the other (head order),
+    // all adding into the same dK/dV registers
+    for (int hh = 0; hh < rep; ++hh) {
+    const int h = kvh * rep + hh;
     const T* qb = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
     const T* db = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
-    const int* wrow = p.w + st;
     const float* lrow = p.lse2t + (int64_t)h * p.total_len + st;
     const float* drow = p.delta + (int64_t)h * p.total_len + st;
-    QLoader<T, D, BQ> ld(p, tid);
     // per-row data of staged row i (or of no row when !ok)
     auto stage_row = [&](QS& q, int r, int i, bool ok) {
         if (ok) {
@@ -460,15 +504,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_
             }
         }
     };
-
-    floatx4 adk[D / 16], adv[D / 16];
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-        adk[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-        adv[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
-    const float NEG = -INFINITY;
-    const int lane_off = 4 * g;
 
     // one staged chunk; kind 0: diagonal rows from i0, 1: full rows, 2: partial rows.
     // Query subtiles are taken in the groups one accumulation consumes (two 16-row
@@ -641,10 +676,26 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_
             __syncthreads();
         }
     }
+    }  // query heads of the group
 
+    if (jvalid && p.lmk_owner) {
+        // a landmark row: its band sums go to the landmark pass's final sum in fp32, which
+        // rounds the total once (and writes the row)
+        const int own = p.lmk_owner[(int64_t)kvh * p.total_len + st + j];
+        if (own != kNoOwner) {
+            const int64_t so = (((int64_t)(own / p.k_lmk) * p.num_seqs + s) * p.k_lmk + own % p.k_lmk) * D;
+            const int64_t half = (int64_t)p.n_heads * p.num_seqs * p.k_lmk * D;
+#pragma unroll
+            for (int dt = 0; dt < D / 16; ++dt) {
+                *(floatx4*)(p.lmk_stage + so + dt * 16 + lane_off) = adk[dt] * p.scale;
+                *(floatx4*)(p.lmk_stage + half + so + dt * 16 + lane_off) = adv[dt];
+            }
+            return;
+        }
+    }
     if (jvalid) {
-        T* kd = (T*)p.dk + (int64_t)(st + j) * p.n_heads * D + (int64_t)h * D;
-        T* vd = (T*)p.dv + (int64_t)(st + j) * p.n_heads * D + (int64_t)h * D;
+        T* kd = (T*)p.dk + (int64_t)(st + j) * p.n_kv_heads * D + (int64_t)kvh * D;
+        T* vd = (T*)p.dv + (int64_t)(st + j) * p.n_kv_heads * D + (int64_t)kvh * D;
 #pragma unroll
         for (int dt = 0; dt < D / 16; ++dt) {
             T ok[4], ov[4];
@@ -839,6 +890,23 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     }
 }
 
+// Position of `pos` in a landmark set (ascending, -1 padding after the valid slots), or -1.
+__device__ __forceinline__ int find_slot(const int32_t* set, int K, int pos) {
+    int lo = 0, hi = K;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        const int v = set[mid];
+        if (v >= 0 && v < pos) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo < K && set[lo] == pos ? lo : -1;
+}
+
+// One thread per (head, sequence, slot, column): d_bias from the slot's chunk partials in
+// chunk order; the owner of a landmark row (the first (head, slot) of the key/value head's
+// group holding it) writes the row's dK/dV once: its band sums from the dK/dV pass, then
+// the chunk partials of every head of the group holding the row, heads and chunks in
+// order, rounded to the output type once.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void bwd_lmk_sum_kernel(AttnParams p) {
     const int K = p.k_lmk;
@@ -850,39 +918,60 @@ __global__ __launch_bounds__(256) void bwd_lmk_sum_kernel(AttnParams p) {
     const int sl = (int)(row % K);
     const int s = (int)((row / K) % p.num_seqs);
     const int h = (int)(row / ((int64_t)K * p.num_seqs));
-    const int pos = p.lmk[(((int64_t)h * p.num_seqs + s) * p.n_sets) * K + sl];
+    const int rep = p.n_heads / p.n_kv_heads, kvh = h / rep;
+    const int32_t* set = p.lmk + (((int64_t)h * p.num_seqs + s) * p.n_sets) * K;
+    const int pos = set[sl];
     int st, len;
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
-    // chunk partials summed in chunk order; eight chunks' loads in flight at a time
-    float sk = 0.f, sv = 0.f, sb = 0.f;
     const int64_t cstride = (int64_t)p.n_heads * p.num_seqs * K;
-    const int64_t pr0 = (int64_t)h * p.num_seqs * K + (int64_t)s * K + sl;
-    constexpr int U = 8;
-    for (int ch0 = 0; ch0 < p.n_chunks; ch0 += U) {
-        float ak[U], av[U], ab[U];
+    auto prow = [&](int hh, int slot) { return (int64_t)hh * p.num_seqs * K + (int64_t)s * K + slot; };
+    if (d == 0 && p.d_bias) {
+        float sb = 0.f;
+        constexpr int U = 8;  // eight chunks' loads in flight at a time, summed in chunk order
+        for (int ch0 = 0; ch0 < p.n_chunks; ch0 += U) {
+            float ab[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int ch = min(ch0 + u, p.n_chunks - 1);
-            const int64_t pr = ch * cstride + pr0;
-            ak[u] = p.part_k[pr * D + d];
-            av[u] = p.part_v[pr * D + d];
-            ab[u] = d == 0 ? p.part_b[pr] : 0.f;
+            for (int u = 0; u < U; ++u) ab[u] = p.part_b[min(ch0 + u, p.n_chunks - 1) * cstride + prow(h, sl)];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (ch0 + u < p.n_chunks) sb += ab[u];
         }
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-            if (ch0 + u < p.n_chunks) {
-                sk += ak[u];
-                sv += av[u];
-                sb += ab[u];
-            }
+        p.d_bias[(((int64_t)h * p.num_seqs + s) * p.n_sets) * K + sl] = sb;
     }
-    if (d == 0 && p.d_bias) p.d_bias[(((int64_t)h * p.num_seqs + s) * p.n_sets) * K + sl] = sb;
     if (pos < 0 || pos >= len) return;
-    const int64_t o = (int64_t)(st + pos) * p.n_heads * D + (int64_t)h * D + d;
-    T* dk = (T*)p.dk;
-    T* dv = (T*)p.dv;
-    dk[o] = from_float<T>(to_float(dk[o]) + sk);
-    dv[o] = from_float<T>(to_float(dv[o]) + sv);
+    if (p.lmk_owner[(int64_t)kvh * p.total_len + st + pos] != h * K + sl) return;
+    const int64_t half = (int64_t)p.n_heads * p.num_seqs * K * D;
+    const int64_t so = prow(h, sl) * D + d;
+    float sk = p.lmk_stage[so], sv = p.lmk_stage[half + so];
+    for (int hh = h; hh < (kvh + 1) * rep; ++hh) {
+        const int32_t* hset = p.lmk + (((int64_t)hh * p.num_seqs + s) * p.n_sets) * K;
+        // a set may repeat a position (each copy counts, as in the forward): its copies
+        // are adjacent in the ascending set
+        for (int slot = hh == h ? sl : find_slot(hset, K, pos); slot >= 0 && slot < K && hset[slot] == pos; ++slot) {
+            const int64_t pr0 = prow(hh, slot);
+            // chunk partials in chunk order; eight chunks' loads in flight at a time
+            constexpr int U = 8;
+            for (int ch0 = 0; ch0 < p.n_chunks; ch0 += U) {
+                float ak[U], av[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int ch = min(ch0 + u, p.n_chunks - 1);
+                    const int64_t pr = ch * cstride + pr0;
+                    ak[u] = p.part_k[pr * D + d];
+                    av[u] = p.part_v[pr * D + d];
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (ch0 + u < p.n_chunks) {
+                        sk += ak[u];
+                        sv += av[u];
+                    }
+            }
+        }
+    }
+    const int64_t o = (int64_t)(st + pos) * p.n_kv_heads * D + (int64_t)kvh * D + d;
+    ((T*)p.dk)[o] = from_float<T>(sk);
+    ((T*)p.dv)[o] = from_float<T>(sv);
 }
 
 // training variant: d w~ per token, the per-head sums added in head order
@@ -908,7 +997,8 @@ static int lmk_chunks(const AttnParams& p) {
     const int ngrp = ceil_div(p.k_lmk, kLmkGroup);
     const int sets = max(1, p.n_heads * p.num_seqs * ngrp);
     const int fill = ceil_div(1024, sets);
-    return max(ceil_div(p.max_seqlen, kRowChunk), min(fill, ceil_div(p.max_seqlen, 64)));
+    const int rows = (p.variant & DSALT_VARIANT_LMK_SHORT) ? kRowChunk / 2 : kRowChunk;
+    return max(ceil_div(p.max_seqlen, rows), min(fill, ceil_div(p.max_seqlen, 64)));
 }
 
 size_t bwd_workspace(const AttnParams& p) {
@@ -921,20 +1011,34 @@ size_t bwd_workspace(const AttnParams& p) {
     b += al(sizeof(int) * (size_t)p.num_seqs);
     b += 2 * al(sizeof(float) * (size_t)nch * p.n_heads * p.num_seqs * p.k_lmk * p.head_dim);
     b += al(sizeof(float) * (size_t)nch * p.n_heads * p.num_seqs * p.k_lmk);
+    b += al(sizeof(float) * 2 * (size_t)p.n_heads * p.num_seqs * p.k_lmk * p.head_dim);
+    b += al(sizeof(int) * (size_t)p.n_kv_heads * p.total_len);
     return b;
 }
 
 template <typename T, int D>
-static void bwd_run(const AttnParams& p, hipStream_t stream) {
+static hipError_t bwd_run(const AttnParams& p, bool plan_given, hipStream_t stream) {
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
-    DSALT_LAUNCH("bwd_init", bwd_init_kernel, dim3(ceil_div(p.num_seqs, 256)), dim3(256), 0, stream, p);
-    plan_launch(p, stream);
-    if (p.w_cont) {
-        DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, true>), dim3(total), dim3(256), 0, stream, p);
-        DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D, true>), dim3(total), dim3(256), 0, stream, p);
+    const int total_kv = p.n_kv_heads * p.num_seqs * p.n_tiles;
+    const int64_t nown = p.lmk_owner ? (int64_t)p.n_kv_heads * p.total_len : 0;
+    const int nprep = max(p.num_seqs, (int)(nown < 262144 ? (nown + 255) / 256 : 1024));
+    DSALT_LAUNCH("bwd_prep", bwd_prep_kernel, dim3(nprep), dim3(256), 0, stream, p, plan_given ? 1 : 0);
+    if (!plan_given) plan_launch(p, stream);
+    constexpr int BN = BwdShape<T, D>::BN;
+    const bool bn64 = sizeof(T) == 2 && D == 64 && (p.variant & DSALT_VARIANT_DQ_BN64);
+    if (bn64) {
+        if (p.w_cont) DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, 64, true>), dim3(total), dim3(256), 0, stream, p);
+        else DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, 64, false>), dim3(total), dim3(256), 0, stream, p);
     } else {
-        DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, false>), dim3(total), dim3(256), 0, stream, p);
-        DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D, false>), dim3(total), dim3(256), 0, stream, p);
+        if (p.w_cont) DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, BN, true>), dim3(total), dim3(256), 0, stream, p);
+        else DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, BN, false>), dim3(total), dim3(256), 0, stream, p);
+    }
+    if (p.n_kv_heads != p.n_heads) {
+        if (p.w_cont) DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D, true, true>), dim3(total_kv), dim3(256), 0, stream, p);
+        else DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D, false, true>), dim3(total_kv), dim3(256), 0, stream, p);
+    } else {
+        if (p.w_cont) DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D, true, false>), dim3(total_kv), dim3(256), 0, stream, p);
+        else DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D, false, false>), dim3(total_kv), dim3(256), 0, stream, p);
     }
     if (p.k_lmk > 0) {
         const int ngrp = ceil_div(p.k_lmk, kLmkGroup);
@@ -944,13 +1048,20 @@ static void bwd_run(const AttnParams& p, hipStream_t stream) {
         DSALT_LAUNCH("bwd_lmk_sum", (bwd_lmk_sum_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                      stream, p);
     }
+    return hipGetLastError();
 }
 
-hipError_t bwd_launch(AttnParams p, void* ws, hipStream_t stream) {
+hipError_t bwd_launch(AttnParams p, void* ws, const void* plan, hipStream_t stream) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     p.n_chunks = lmk_chunks(p);
     char* w = (char*)ws;
-    plan_carve(p, w);
+    if (plan) {
+        char* pw = (char*)const_cast<void*>(plan);  // read only: bwd_prep and the kernels never write it
+        plan_carve(p, pw);
+        w += plan_bytes(p);
+    } else {
+        plan_carve(p, w);
+    }
     p.delta = (float*)w;
     w += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
     p.cnt = (int*)w;
@@ -965,18 +1076,15 @@ hipError_t bwd_launch(AttnParams p, void* ws, hipStream_t stream) {
     p.part_v = (float*)w;
     w += al(sizeof(float) * npart * p.head_dim);
     p.part_b = (float*)w;
+    w += al(sizeof(float) * npart);
+    p.lmk_stage = (float*)w;
+    w += al(sizeof(float) * 2 * (size_t)p.n_heads * p.num_seqs * p.k_lmk * p.head_dim);
+    p.lmk_owner = p.k_lmk > 0 ? (int*)w : nullptr;
     if (p.total_len == 0 || p.num_seqs == 0) return hipSuccess;
-    if (p.dtype == DSALT_DTYPE_BF16) {
-        if (p.head_dim == 64) bwd_run<bf16, 64>(p, stream);
-        else bwd_run<bf16, 128>(p, stream);
-    } else if (p.dtype == DSALT_DTYPE_F16) {
-        if (p.head_dim == 64) bwd_run<f16, 64>(p, stream);
-        else bwd_run<f16, 128>(p, stream);
-    } else {
-        if (p.head_dim == 64) bwd_run<float, 64>(p, stream);
-        else bwd_run<float, 128>(p, stream);
-    }
-    return hipGetLastError();
+    const bool pg = plan != nullptr;
+    if (p.dtype == DSALT_DTYPE_BF16) return p.head_dim == 64 ? bwd_run<bf16, 64>(p, pg, stream) : bwd_run<bf16, 128>(p, pg, stream);
+    if (p.dtype == DSALT_DTYPE_F16) return p.head_dim == 64 ? bwd_run<f16, 64>(p, pg, stream) : bwd_run<f16, 128>(p, pg, stream);
+    return p.head_dim == 64 ? bwd_run<float, 64>(p, pg, stream) : bwd_run<float, 128>(p, pg, stream);
 }
 
 }  // namespace dsalt

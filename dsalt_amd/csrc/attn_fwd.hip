@@ -47,8 +47,9 @@ __device__ __forceinline__ int lower_bound_lds(const int* a, int n, int x) {
 // rows past the end last), so the 16 rows a wave takes have close window
 // starts: the wave's key range [min lo, max i] and its count of masked
 // subtiles shrink.  Each 16-row group's {min lo, max lo, max i, min i} is
-// recorded, and, when seq_wmax is set, the largest clamped window of each
-// sequence (bounding the key-parallel backward sweep).
+// recorded, with the tile's largest clamped window, and, when seq_wmax is set,
+// the largest clamped window of each sequence (bounding the key-parallel
+// backward sweep).
 __global__ __launch_bounds__(64) void row_plan_kernel(AttnParams p) {
     __shared__ int sp[64], slo[64];
     const int l = threadIdx.x;
@@ -97,16 +98,17 @@ __global__ __launch_bounds__(64) void row_plan_kernel(AttnParams p) {
         b[2] = rhi;
         b[3] = rhmin;
     }
-    if (p.seq_wmax) {
-        const int m = row_max16(wcl);
-        if ((l & 15) == 0 && m > 0) atomicMax(p.seq_wmax + s, m);
-    }
+    const int m = row_max16(wcl);
+    const int tm = max(max(__builtin_amdgcn_readlane(m, 0), __builtin_amdgcn_readlane(m, 16)),
+                       max(__builtin_amdgcn_readlane(m, 32), __builtin_amdgcn_readlane(m, 48)));
+    if (l == 0) p.tile_wmax[tile] = tm;
+    if (p.seq_wmax && l == 0 && tm > 0) atomicMax(p.seq_wmax + s, tm);
 }
 
 size_t plan_bytes(const AttnParams& p) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const size_t tiles = (size_t)p.num_seqs * p.n_tiles;
-    return al(tiles * 64) + al(tiles * 16 * sizeof(int));
+    return al(tiles * 64) + al(tiles * 16 * sizeof(int)) + al(tiles * sizeof(int));
 }
 
 void plan_carve(AttnParams& p, char*& ws) {
@@ -116,6 +118,8 @@ void plan_carve(AttnParams& p, char*& ws) {
     ws += al(tiles * 64);
     p.plan_bounds = (int*)ws;
     ws += al(tiles * 16 * sizeof(int));
+    p.tile_wmax = (int*)ws;
+    ws += al(tiles * sizeof(int));
 }
 
 hipError_t plan_launch(const AttnParams& p, hipStream_t stream) {
@@ -204,9 +208,8 @@ __device__ __forceinline__ void band_edge(const AttnParams& p, const RowGroup& R
 // TR: the training variant -- band keys near a row's window start carry the soft
 // edge bias (edge_bias), so chunks classed "every row sees every key" must also
 // lie past every row's first edge_keys band keys.
-template <typename T, int D, int RG, bool TR>
+template <typename T, int D, int BN, int RG, bool TR>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
-    constexpr int BN = FwdShape<T, D>::BN;
     constexpr int NST = BN / 16;
     constexpr bool kHalf = sizeof(T) == 2;
     typedef Tile<T, D, BN> KT;
@@ -534,25 +537,29 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     }
 }
 
-// two row groups per wave where the registers allow (16-bit, head_dim 64) and a
-// block of 128 rows stays within one landmark set (block_size a multiple of 128)
-constexpr int kFwdGroups = 1;
-template <typename T, int D>
-static int fwd_groups(const AttnParams& p) {
-    return (kFwdGroups == 2 && sizeof(T) == 2 && D == 64 && (p.block_size == 0 || p.block_size % 128 == 0)) ? 2 : 1;
-}
-
+// Tilings (DSALT_VARIANT_* bits): for 16-bit head_dim 64, 32-key chunks instead of 64
+// (FWD_BN32) and two 16-row groups per wave (FWD_RG2, 128 rows per block: the block must
+// stay within one landmark set, block_size a multiple of 128); other shapes take their
+// single compiled tiling.
 template <typename T, int D, bool TR>
 static void fwd_run(const AttnParams& p, hipStream_t stream) {
-    const int rg = fwd_groups<T, D>(p);
-    const int total = p.n_heads * p.num_seqs * ceil_div(p.n_tiles, rg);
-    if constexpr (sizeof(T) == 2 && D == 64 && kFwdGroups == 2) {
-        if (rg == 2) {
-            DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 2, TR>), dim3(total), dim3(256), 0, stream, p);
+    constexpr int BN = FwdShape<T, D>::BN;
+    if constexpr (sizeof(T) == 2 && D == 64) {
+        const bool bn32 = (p.variant & DSALT_VARIANT_FWD_BN32) != 0;
+        const bool rg2 = (p.variant & DSALT_VARIANT_FWD_RG2) != 0 && (p.block_size == 0 || p.block_size % 128 == 0);
+        const int total = p.n_heads * p.num_seqs * ceil_div(p.n_tiles, rg2 ? 2 : 1);
+        if (rg2) {
+            if (bn32) DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 32, 2, TR>), dim3(total), dim3(256), 0, stream, p);
+            else DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, BN, 2, TR>), dim3(total), dim3(256), 0, stream, p);
+            return;
+        }
+        if (bn32) {
+            DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 32, 1, TR>), dim3(total), dim3(256), 0, stream, p);
             return;
         }
     }
-    DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 1, TR>), dim3(total), dim3(256), 0, stream, p);
+    const int total = p.n_heads * p.num_seqs * p.n_tiles;
+    DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, BN, 1, TR>), dim3(total), dim3(256), 0, stream, p);
 }
 
 template <typename T>
@@ -589,8 +596,8 @@ hipError_t train_windows_launch(const AttnParams& p, int* w_int, hipStream_t str
     return hipGetLastError();
 }
 
-hipError_t fwd_launch(AttnParams p, void* ws, hipStream_t stream) {
-    char* w = (char*)ws;
+hipError_t fwd_launch(AttnParams p, void* ws, void* plan, hipStream_t stream) {
+    char* w = (char*)(plan ? plan : ws);
     plan_carve(p, w);
     p.seq_wmax = nullptr;
     if (p.dtype == DSALT_DTYPE_BF16) return fwd_dispatch<bf16>(p, stream);

@@ -213,6 +213,8 @@ static int fwd_params(const dsalt_fwd_args* a, bool need_w, dsalt::AttnParams* o
     p.cu = a->cu_seqlens;
     p.lmk = a->lmk_idx;
     p.lbias = a->lmk_bias;
+    if (a->variant & ~DSALT_VARIANT_MASK) return fail(DSALT_ERR_INVALID, "unknown variant bits 0x%x", a->variant);
+    p.variant = a->variant;
     *out = p;
     return DSALT_OK;
 }
@@ -232,6 +234,11 @@ static int train_params(const float* w_cont, float tau_win, float win_edge, dsal
 
 static size_t wint_bytes(const dsalt::AttnParams& p) { return ((size_t)p.total_len * sizeof(int) + 255) & ~(size_t)255; }
 
+size_t dsalt_plan_bytes(const dsalt_problem* p) {
+    if (!p || check_problem(*p, true)) return 0;
+    return dsalt::plan_bytes(attn_common(*p, 1.0f));
+}
+
 size_t dsalt_fwd_workspace_bytes(const dsalt_fwd_args* a) {
     if (!a || check_problem(a->p, true)) return 0;
     return dsalt::plan_bytes(attn_common(a->p, 1.0f));
@@ -244,7 +251,7 @@ int dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream) {
     const size_t need = dsalt::plan_bytes(p);
     if (!a->workspace || a->workspace_bytes < need)
         return fail(DSALT_ERR_WORKSPACE, "forward needs %zu workspace bytes, got %zu", need, a->workspace_bytes);
-    return hip_status(dsalt::fwd_launch(p, a->workspace, (hipStream_t)stream), "dsalt_fwd");
+    return hip_status(dsalt::fwd_launch(p, a->workspace, a->plan, (hipStream_t)stream), "dsalt_fwd");
 }
 
 size_t dsalt_train_fwd_workspace_bytes(const dsalt_train_fwd_args* a) {
@@ -266,7 +273,8 @@ int dsalt_train_fwd(const dsalt_train_fwd_args* a, dsalt_stream_t stream) {
     int* w_int = (int*)a->base.workspace;
     p.w = w_int;
     hipError_t e = dsalt::train_windows_launch(p, w_int, (hipStream_t)stream);
-    if (e == hipSuccess) e = dsalt::fwd_launch(p, (char*)a->base.workspace + wint_bytes(p), (hipStream_t)stream);
+    if (e == hipSuccess)
+        e = dsalt::fwd_launch(p, (char*)a->base.workspace + wint_bytes(p), a->base.plan, (hipStream_t)stream);
     return hip_status(e, "dsalt_train_fwd");
 }
 
@@ -276,8 +284,6 @@ static int bwd_params(const dsalt_bwd_args* a, dsalt::AttnParams* out, bool need
     if (rc) return rc;
     if (a->p.select_mode != DSALT_SELECT_GLOBAL)
         return fail(DSALT_ERR_UNSUPPORTED, "backward of the block-causal variant is not implemented");
-    if (a->p.n_kv_heads != a->p.n_heads)
-        return fail(DSALT_ERR_UNSUPPORTED, "backward needs n_kv_heads == n_heads (expand GQA heads first)");
     const int dt = a->p.dtype;
     if ((rc = check_rows(a->q, a->q_stride_t, a->q_stride_h, dt, "q"))) return rc;
     if ((rc = check_rows(a->k, a->k_stride_t, a->k_stride_h, dt, "k"))) return rc;
@@ -314,6 +320,8 @@ static int bwd_params(const dsalt_bwd_args* a, dsalt::AttnParams* out, bool need
     p.dk = a->dk;
     p.dv = a->dv;
     p.d_bias = a->d_bias;
+    if (a->variant & ~DSALT_VARIANT_MASK) return fail(DSALT_ERR_INVALID, "unknown variant bits 0x%x", a->variant);
+    p.variant = a->variant;
     *out = p;
     return DSALT_OK;
 }
@@ -331,7 +339,7 @@ int dsalt_bwd(const dsalt_bwd_args* a, dsalt_stream_t stream) {
     size_t need = dsalt::bwd_workspace(p);
     if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
         return fail(DSALT_ERR_WORKSPACE, "backward needs %zu workspace bytes, got %zu", need, a->workspace_bytes);
-    return hip_status(dsalt::bwd_launch(p, a->workspace, (hipStream_t)stream), "dsalt_bwd");
+    return hip_status(dsalt::bwd_launch(p, a->workspace, a->plan, (hipStream_t)stream), "dsalt_bwd");
 }
 
 // training backward workspace: integer windows, per-head d w~, then the operator's
@@ -362,7 +370,7 @@ int dsalt_train_bwd(const dsalt_train_bwd_args* a, dsalt_stream_t stream) {
     p.dw_h = (float*)(w + wint_bytes(p));
     p.d_w = a->d_w;
     hipError_t e = dsalt::train_windows_launch(p, w_int, (hipStream_t)stream);
-    if (e == hipSuccess) e = dsalt::bwd_launch(p, w + train_bwd_extra(p), (hipStream_t)stream);
+    if (e == hipSuccess) e = dsalt::bwd_launch(p, w + train_bwd_extra(p), a->base.plan, (hipStream_t)stream);
     if (e == hipSuccess) e = dsalt::train_dw_launch(p, (hipStream_t)stream);
     return hip_status(e, "dsalt_train_bwd");
 }

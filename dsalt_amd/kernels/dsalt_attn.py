@@ -7,7 +7,8 @@ holding values rounded to the input dtype (the reference returns ``out.float()``
 for q, k, v and lmk_bias.  Differences, all deliberate:
   * float32 inputs are computed in float32 (the reference silently casts them to float16,
     :266-269);
-  * k/v may carry fewer heads than q (grouped-query attention read in place);
+  * k/v may carry fewer heads than q (grouped-query attention read in place, forward and
+    backward: each key/value head's gradient sums its query heads inside the kernels);
   * landmark indices may come in any order: each set is sorted before the kernels, which
     need ascending positions, and d_bias is returned in the caller's order;
   * the backward is deterministic (no float atomics);
@@ -41,10 +42,11 @@ class DSALTAttentionFunction(torch.autograd.Function):
         w_i = w_sizes.detach().clamp(min=1).to(torch.int32)
         cu_i = cu_seqlens.detach().to(torch.int32)
         scale = 1.0 / math.sqrt(q.shape[-1])
+        plan = ops.new_plan(q, k, cu_i, idx_s, max_seqlen=max_seqlen, select_mode=mode, block_size=block_size)
         out, lse = ops.attention_forward(q, k, v, w_i, cu_i, idx_s, bias_s, scale=scale, max_seqlen=max_seqlen,
-                                         select_mode=mode, block_size=block_size)
+                                         select_mode=mode, block_size=block_size, plan=plan)
         ctx.save_for_backward(q, k, v, out, lse, idx_s, bias_s if bias_s is not None else torch.empty(0),
-                              perm, w_i, cu_i)
+                              perm, w_i, cu_i, plan)
         ctx.has_bias = bias_s is not None
         ctx.mode, ctx.max_seqlen, ctx.scale = mode, max_seqlen, scale
         ctx.bias_dtype = lmk_bias.dtype if lmk_bias is not None else None
@@ -52,21 +54,13 @@ class DSALTAttentionFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out):
-        q, k, v, out, lse, idx_s, bias_s, perm, w_i, cu_i = ctx.saved_tensors
+        q, k, v, out, lse, idx_s, bias_s, perm, w_i, cu_i, plan = ctx.saved_tensors
         if ctx.mode == ops.SELECT_BLOCK:
             raise NotImplementedError("the backward of the block-causal landmark variant is not implemented")
-        H, G = q.shape[1], k.shape[1]
-        kk, vv = k, v
-        if G != H:  # grouped heads: expand for the kernels, sum the group gradients back
-            kk = k.repeat_interleave(H // G, dim=1)
-            vv = v.repeat_interleave(H // G, dim=1)
-        dq, dk, dv, db = ops.attention_backward(grad_out.to(q.dtype), q, kk, vv, out, lse, w_i, cu_i, idx_s,
+        dq, dk, dv, db = ops.attention_backward(grad_out.to(q.dtype), q, k, v, out, lse, w_i, cu_i, idx_s,
                                                 bias_s if ctx.has_bias else None, scale=ctx.scale,
-                                                max_seqlen=ctx.max_seqlen, want_dbias=ctx.needs_input_grad[4])
-        if G != H:
-            T, _, D = dk.shape
-            dk = dk.view(T, G, H // G, D).float().sum(2).to(k.dtype)
-            dv = dv.view(T, G, H // G, D).float().sum(2).to(v.dtype)
+                                                max_seqlen=ctx.max_seqlen, want_dbias=ctx.needs_input_grad[4],
+                                                plan=plan)
         d_bias = None
         if ctx.needs_input_grad[4] and db is not None:
             d_bias = torch.zeros_like(db).scatter_(-1, perm, db)[:, :, 0].to(ctx.bias_dtype)

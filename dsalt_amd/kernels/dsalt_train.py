@@ -13,7 +13,8 @@ Per query i with continuous window w~ = w_cont[i] the row attends to
     ``lmk_logw[h, s, slot]``.
 Differences, all deliberate:
   * float32 inputs are computed in float32 (the reference casts them to float16, :608-611);
-  * k/v may carry fewer heads than q (expanded for the backward, gradients summed back);
+  * k/v may carry fewer heads than q (grouped-query attention read in place; each key/value
+    head's gradient sums its query heads inside the kernels, without a materialised repeat);
   * landmark slots may come in any order (sorted for the kernels, d_logw returned in the
     caller's order);
   * ``n_max`` is accepted and not needed: the key-parallel backward bounds its query scan
@@ -42,9 +43,10 @@ class DSALTTrainFunction(torch.autograd.Function):
         cu_i = cu_seqlens.detach().to(torch.int32)
         w_c = w_cont.detach().to(torch.float32).contiguous()
         scale = 1.0 / math.sqrt(q.shape[-1])
+        plan = ops.new_plan(q, k, cu_i, idx_s, max_seqlen=max_seqlen)
         out, lse = ops.train_forward(q, k, v, w_c, cu_i, idx_s, logw_s, tau_win=float(tau_win),
-                                     win_edge=float(win_edge), scale=scale, max_seqlen=max_seqlen)
-        ctx.save_for_backward(q, k, v, out, lse, idx_s, logw_s, perm, w_c, cu_i)
+                                     win_edge=float(win_edge), scale=scale, max_seqlen=max_seqlen, plan=plan)
+        ctx.save_for_backward(q, k, v, out, lse, idx_s, logw_s, perm, w_c, cu_i, plan)
         ctx.max_seqlen, ctx.scale = max_seqlen, scale
         ctx.tau_win, ctx.win_edge = float(tau_win), float(win_edge)
         ctx.logw_dtype, ctx.w_dtype = lmk_logw.dtype, w_cont.dtype
@@ -52,20 +54,11 @@ class DSALTTrainFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out):
-        q, k, v, out, lse, idx_s, logw_s, perm, w_c, cu_i = ctx.saved_tensors
-        H, G = q.shape[1], k.shape[1]
-        kk, vv = k, v
-        if G != H:  # grouped heads: expand for the kernels, sum the group gradients back
-            kk = k.repeat_interleave(H // G, dim=1)
-            vv = v.repeat_interleave(H // G, dim=1)
+        q, k, v, out, lse, idx_s, logw_s, perm, w_c, cu_i, plan = ctx.saved_tensors
         dq, dk, dv, dlogw, d_w = ops.train_backward(
-            grad_out.to(q.dtype), q, kk, vv, out, lse, w_c, cu_i, idx_s, logw_s, tau_win=ctx.tau_win,
+            grad_out.to(q.dtype), q, k, v, out, lse, w_c, cu_i, idx_s, logw_s, tau_win=ctx.tau_win,
             win_edge=ctx.win_edge, scale=ctx.scale, max_seqlen=ctx.max_seqlen,
-            want_dlogw=ctx.needs_input_grad[4])
-        if G != H:
-            T, _, D = dk.shape
-            dk = dk.view(T, G, H // G, D).float().sum(2).to(k.dtype)
-            dv = dv.view(T, G, H // G, D).float().sum(2).to(v.dtype)
+            want_dlogw=ctx.needs_input_grad[4], plan=plan)
         d_logw = None
         if ctx.needs_input_grad[4] and dlogw is not None:
             d_logw = torch.zeros_like(dlogw).scatter_(-1, perm, dlogw)[:, :, 0].to(ctx.logw_dtype)

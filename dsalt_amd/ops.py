@@ -13,7 +13,8 @@ import torch
 
 from . import _lib
 from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, SELECT_BLOCK, SELECT_GLOBAL, STATS_PACKED,
-                   STATS_SEQUENCE, BwdArgs, CeArgs, FwdArgs, GatherArgs, Problem, ProbsArgs, RopeArgs, SelectArgs,
+                   STATS_SEQUENCE, VARIANT_DEFAULT, VARIANT_DQ_BN64, VARIANT_FWD_BN32, VARIANT_FWD_RG2,
+                   VARIANT_LMK_SHORT, BwdArgs, CeArgs, FwdArgs, GatherArgs, Problem, ProbsArgs, RopeArgs, SelectArgs,
                    SiluMulArgs,
                    TrainBwdArgs,
                    TrainFwdArgs)
@@ -203,12 +204,38 @@ def _fwd_args(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias, scale, max_seqlen, sele
     return a, out, lse, (q, k, v, w_c, cu_c, li, lb)
 
 
+def new_plan(q: torch.Tensor, k: torch.Tensor, cu_seqlens: torch.Tensor, lmk_idx: torch.Tensor, *,
+             max_seqlen=None, select_mode=SELECT_GLOBAL, block_size=512) -> torch.Tensor:
+    """An empty row-plan buffer (uint8) for attention_forward(plan=...) / attention_backward(plan=...)."""
+    T, H, D = q.shape
+    S = cu_seqlens.shape[0] - 1
+    maxlen = max_seqlen if max_seqlen is not None else _max_seqlen(cu_seqlens)
+    prob = _problem(T, S, maxlen, H, k.shape[1], D, lmk_idx.shape[-1], select_mode, block_size,
+                    dtype_code(q.dtype))
+    n = _lib.load().dsalt_plan_bytes(ctypes.byref(prob))
+    return torch.empty(max(n, 1), dtype=torch.uint8, device=q.device)
+
+
+def _check_plan(plan, a) -> int:
+    if plan is None:
+        return 0
+    need = _lib.load().dsalt_plan_bytes(ctypes.byref(a.p))
+    if plan.dtype != torch.uint8 or not plan.is_contiguous() or plan.numel() < need or plan.device.type != "cuda":
+        raise ValueError(f"plan must be a contiguous uint8 device tensor of at least {need} bytes (ops.new_plan)")
+    return plan.data_ptr()
+
+
 def attention_forward(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias=None, *, scale=None,
-                      max_seqlen=None, select_mode=SELECT_GLOBAL, block_size=512):
+                      max_seqlen=None, select_mode=SELECT_GLOBAL, block_size=512, plan=None,
+                      variant=VARIANT_DEFAULT):
     """(out [T,H,D] in q.dtype, lse [T,H] fp32).  lmk_idx [H,S,n_sets,K] int32 ascending with
-    -1 padding at the end of each set (as select_landmarks returns)."""
+    -1 padding at the end of each set (as select_landmarks returns; a position may repeat, each
+    copy counts).  ``plan`` (ops.new_plan) receives the row plan for attention_backward of the
+    same rows; ``variant`` picks a tiling (VARIANT_* bits, kernels.autotune)."""
     a, out, lse, keep = _fwd_args(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias, scale, max_seqlen, select_mode,
                                   block_size)
+    a.plan = _check_plan(plan, a) or None
+    a.variant = int(variant)
     if q.shape[0] == 0:
         return out, lse
     dev = out.device
@@ -226,12 +253,14 @@ def _w_cont(w_cont: torch.Tensor, T: int) -> torch.Tensor:
 
 
 def train_forward(q, k, v, w_cont, cu_seqlens, lmk_idx, lmk_logw, *, tau_win=1.0, win_edge=4.0, scale=None,
-                  max_seqlen=None):
+                  max_seqlen=None, plan=None, variant=VARIANT_DEFAULT):
     """Training variant: (out [T,H,D] in q.dtype, lse [T,H] fp32).  w_cont [T] continuous
     windows; lmk_idx [H,S,1,K] ascending with -1 last; lmk_logw [H,S,1,K] landmark log-weights
     (-inf or any value in -1 slots)."""
     a, out, lse, keep = _fwd_args(q, k, v, w_cont, cu_seqlens, lmk_idx, lmk_logw, scale, max_seqlen,
                                   SELECT_GLOBAL, 0, need_w=False)
+    a.plan = _check_plan(plan, a) or None
+    a.variant = int(variant)
     if q.shape[0] == 0:
         return out, lse
     dev = out.device
@@ -256,12 +285,11 @@ def _bwd_args(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias, scale, 
     if dout.dtype != q.dtype:
         dout = dout.to(q.dtype)
     T, H, D = q.shape
+    G = k.shape[1]
     S = cu_seqlens.shape[0] - 1
     _check_tokens(q, k, v, w, cu_seqlens)
     if tuple(out.shape) != (T, H, D) or tuple(dout.shape) != (T, H, D) or tuple(lse.shape) != (T, H):
         raise ValueError("out / dout must be [T, H, D] and lse [T, H]")
-    if k.shape[1] != H:
-        raise ValueError("the backward needs n_kv_heads == n_heads (expand grouped heads first)")
     maxlen = max_seqlen if max_seqlen is not None else _max_seqlen(cu_seqlens)
     K = lmk_idx.shape[-1]
     if lmk_idx.dim() != 4 or lmk_idx.shape[:3] != (H, S, 1):
@@ -275,11 +303,11 @@ def _bwd_args(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias, scale, 
     lb = lmk_bias.detach().to(torch.float32).contiguous() if lmk_bias is not None else None
     lse = lse.detach().to(torch.float32).contiguous()
     dq = torch.empty((T, H, D), dtype=q.dtype, device=dev)
-    dk = torch.empty((T, H, D), dtype=q.dtype, device=dev)
-    dv = torch.empty((T, H, D), dtype=q.dtype, device=dev)
+    dk = torch.empty((T, G, D), dtype=q.dtype, device=dev)
+    dv = torch.empty((T, G, D), dtype=q.dtype, device=dev)
     db = torch.empty(tuple(lmk_idx.shape), dtype=torch.float32, device=dev) if want_dbias else None
     a = BwdArgs()
-    a.p = _problem(T, S, maxlen, H, k.shape[1], D, K, SELECT_GLOBAL, 0, dt)
+    a.p = _problem(T, S, maxlen, H, G, D, K, SELECT_GLOBAL, 0, dt)
     a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
     a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
     a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
@@ -296,11 +324,15 @@ def _bwd_args(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias, scale, 
 
 
 def attention_backward(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias=None, *,
-                       scale=None, max_seqlen=None, want_dbias=True):
-    """(dq, dk, dv) in q.dtype, [T,H,D], and d_bias [H,S,1,K] fp32 (or None).
-    Global selection variant, n_kv_heads == n_heads."""
+                       scale=None, max_seqlen=None, want_dbias=True, plan=None, variant=VARIANT_DEFAULT):
+    """(dq [T,H,D], dk, dv [T,n_kv,D]) in q.dtype and d_bias [H,S,1,K] fp32 (or None).
+    Global selection variant; grouped key/value heads are read in place and their gradients
+    summed over the group inside the kernels.  ``plan``: the buffer attention_forward filled
+    for the same rows (skips recomputing the row plan)."""
     a, dq, dk, dv, db, keep = _bwd_args(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias, scale,
                                         max_seqlen, want_dbias)
+    a.plan = _check_plan(plan, a) or None
+    a.variant = int(variant)
     if q.shape[0] == 0:
         return dq.zero_(), dk.zero_(), dv.zero_(), db
     dev = dq.device
@@ -315,11 +347,13 @@ def attention_backward(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, lmk_bias
 
 
 def train_backward(dout, q, k, v, out, lse, w_cont, cu_seqlens, lmk_idx, lmk_logw, *, tau_win=1.0,
-                   win_edge=4.0, scale=None, max_seqlen=None, want_dlogw=True):
-    """Training variant: (dq, dk, dv) in q.dtype, d_logw [H,S,1,K] fp32 (or None) and
-    d_w [T] fp32, the window gradient summed over heads.  n_kv_heads == n_heads."""
+                   win_edge=4.0, scale=None, max_seqlen=None, want_dlogw=True, plan=None, variant=VARIANT_DEFAULT):
+    """Training variant: (dq [T,H,D], dk, dv [T,n_kv,D]) in q.dtype, d_logw [H,S,1,K] fp32 (or
+    None) and d_w [T] fp32, the window gradient summed over heads."""
     a, dq, dk, dv, db, keep = _bwd_args(dout, q, k, v, out, lse, w_cont, cu_seqlens, lmk_idx, lmk_logw, scale,
                                         max_seqlen, want_dlogw, need_w=False)
+    a.plan = _check_plan(plan, a) or None
+    a.variant = int(variant)
     T = q.shape[0]
     d_w = torch.zeros(T, dtype=torch.float32, device=dq.device)
     if T == 0:

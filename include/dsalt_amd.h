@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DSALT_ABI_VERSION 1
+#define DSALT_ABI_VERSION 2
 
 /* element types of token tensors */
 #define DSALT_DTYPE_F32  0
@@ -118,13 +118,24 @@ typedef struct dsalt_fwd_args {
     float* lse;                /* [T, H] contiguous                                 */
     float scale;               /* logit scale, 1/sqrt(D) in the reference           */
     void* workspace; size_t workspace_bytes;
+    /* Optional (NULL: none): a buffer of dsalt_plan_bytes(&p) bytes that receives
+     * the row plan (per 64-row tile: rows ordered by window start, 16-row group
+     * bounds, largest window) so dsalt_bwd of the same w / cu_seqlens / shape can
+     * reuse it instead of recomputing it. */
+    void* plan;
+    /* Tile variant (DSALT_VARIANT_*; 0 = the library's default for the shape).  The
+     * variants compute the same result with different tilings; which is fastest
+     * depends on the shape (the autotune of dsalt/kernels/autotune.py:55-238). */
+    int32_t variant;
 } dsalt_fwd_args;
 
 /* Attention backward.  Replaces _dsalt_bwd_preprocess + _dsalt_bwd_kernel and
  * dsalt_triton_backward, dsalt/kernels/dsalt_triton_bwd.py:17-324.
- * Deterministic: no floating-point atomics.  dq/dk/dv are [T, H, D] contiguous
- * in dtype (n_kv_heads must equal n_heads); d_bias (optional) is fp32
- * [H, S, n_sets, k_lmk].  Global selection variant only. */
+ * Deterministic: no floating-point atomics.  dq/dk/dv are contiguous
+ * in dtype with dq [T, H, D] and dk/dv [T, n_kv_heads, D] (grouped heads: each
+ * key/value head's gradient sums its query heads in head order, inside the
+ * kernels); d_bias (optional) is fp32 [H, S, n_sets, k_lmk].  Global selection
+ * variant only. */
 typedef struct dsalt_bwd_args {
     dsalt_problem p;
     const void* q;    int64_t q_stride_t;  int64_t q_stride_h;
@@ -141,6 +152,9 @@ typedef struct dsalt_bwd_args {
     float* d_bias;             /* or NULL                                           */
     float scale;
     void* workspace; size_t workspace_bytes;
+    const void* plan;          /* or NULL: the row plan dsalt_fwd wrote for the same
+                                  w / cu_seqlens / shape (dsalt_fwd_args.plan)      */
+    int32_t variant;           /* DSALT_VARIANT_* (0 = default)                     */
 } dsalt_bwd_args;
 
 /* Landmark K/V gather.  Replaces _build_landmark_kv, dsalt/kernels/selectors.py:137-159:
@@ -288,6 +302,18 @@ typedef struct dsalt_silu_mul_args {
 } dsalt_silu_mul_args;
 
 int    dsalt_silu_mul(const dsalt_silu_mul_args* a, dsalt_stream_t stream);
+
+/* Tile variants of the attention kernels (dsalt_fwd_args.variant, dsalt_bwd_args.variant).
+ * Bits are independent; a bit a shape cannot use is ignored. */
+#define DSALT_VARIANT_DEFAULT    0
+#define DSALT_VARIANT_FWD_BN32   1  /* forward: 32-key chunks (16-bit types, head_dim 64)        */
+#define DSALT_VARIANT_FWD_RG2    2  /* forward: two 16-row groups per wave (16-bit, head_dim 64)  */
+#define DSALT_VARIANT_DQ_BN64    4  /* backward dQ: 64-key chunks (16-bit types, head_dim 64)     */
+#define DSALT_VARIANT_LMK_SHORT  8  /* backward landmark pass: 512-row chunks                    */
+#define DSALT_VARIANT_MASK       15
+
+/* Bytes of the row-plan buffer of dsalt_fwd_args.plan / dsalt_bwd_args.plan. */
+size_t dsalt_plan_bytes(const dsalt_problem* p);
 
 size_t dsalt_select_workspace_bytes(const dsalt_select_args* a);
 int    dsalt_select(const dsalt_select_args* a, dsalt_stream_t stream);

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_function():
     for n in names:
         assert hasattr(lib, n), n
     assert set(_lib.SIGNATURES) == names
-    assert lib.dsalt_abi_version() == 1
+    assert lib.dsalt_abi_version() == _lib.ABI_VERSION == 2
 
 
 STRUCTS = {
@@ -112,10 +112,26 @@ def test_backward_rejects_unsupported_variants():
     lib = _lib.load()
     a = _lib.BwdArgs()
     a.p = _lib.Problem(256, 1, 256, 4, 2, 64, 8, 0, 0, _lib.DTYPE_BF16)
-    assert lib.dsalt_bwd(ctypes.byref(a), None) == 2  # GQA backward
+    assert lib.dsalt_bwd(ctypes.byref(a), None) == 1  # GQA is accepted; the null tensors are not
     a.p = _lib.Problem(256, 1, 256, 4, 4, 64, 8, 1, 128, _lib.DTYPE_BF16)
     assert lib.dsalt_bwd(ctypes.byref(a), None) == 2  # block-causal backward
     assert b"block" in lib.dsalt_last_error()
+
+
+def test_unknown_variant_bits_and_plan_size():
+    lib = _lib.load()
+    a = _valid_fwd()
+    a.variant = _lib.VARIANT_FWD_BN32 | _lib.VARIANT_FWD_RG2
+    a.workspace, a.workspace_bytes = 0, 0
+    assert lib.dsalt_fwd(ctypes.byref(a), None) == 3  # variant accepted, workspace missing
+    a.variant = 64
+    assert lib.dsalt_fwd(ctypes.byref(a), None) == 1
+    assert b"variant" in lib.dsalt_last_error()
+    p = _lib.Problem(1000, 2, 600, 4, 2, 64, 16, 0, 0, _lib.DTYPE_BF16)
+    tiles = 2 * 10  # sequences x 64-row tiles of the longest
+    assert lib.dsalt_plan_bytes(ctypes.byref(p)) >= tiles * (64 + 16 * 4 + 4)
+    p.head_dim = 96
+    assert lib.dsalt_plan_bytes(ctypes.byref(p)) == 0
 
 
 def test_workspace_sizes_and_small_workspace():

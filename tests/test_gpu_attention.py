@@ -183,3 +183,92 @@ def test_landmark_rows_far_apart_in_memory(T):
     # and the contiguous result is the operator's (oracle at the bf16 tolerance)
     ro, _ = OA.attention_fwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), 1.0 / math.sqrt(D))
     assert rel_err(f64(res[0][0]), ro) < TOL[dt]
+
+
+# ------------------------------------------------ grouped heads, plan reuse, repeats
+def _bwd_gqa_case(H, G, D, dt, seed, lens=(700, 333), K=32, wmax=260):
+    q, k, v, w, cu, idx, lb, maxlen = _inputs(list(lens), H, G, D, K, wmax, dt, seed, bias=True)
+    g = torch.Generator().manual_seed(seed + 7)
+    do = torch.randn(q.shape, generator=g).to(dt)
+    return q, k, v, w, cu, idx, lb, maxlen, do
+
+
+@pytest.mark.parametrize("H,G,D,dt", [(16, 2, 64, torch.bfloat16), (8, 2, 128, torch.bfloat16),
+                                      (8, 2, 64, torch.float32), (6, 3, 64, torch.float16)])
+def test_bwd_grouped_heads_native(H, G, D, dt):
+    """dK/dV of each key/value head sum its query heads inside the kernels (no repeat)."""
+    q, k, v, w, cu, idx, lb, maxlen, do = _bwd_gqa_case(H, G, D, dt, seed=40 + H + D)
+    scale = 1.0 / math.sqrt(D)
+    dev = [t.to(DEV) for t in (q, k, v, w, cu, idx, lb, do)]
+    out, lse = ops.attention_forward(*dev[:6], dev[6], scale=scale, max_seqlen=maxlen)
+    res = ops.attention_backward(dev[7], dev[0], dev[1], dev[2], out, lse, dev[3], dev[4], dev[5], dev[6],
+                                 scale=scale, max_seqlen=maxlen)
+    torch.cuda.synchronize()
+    assert res[1].shape == (q.shape[0], G, D) and res[2].shape == (q.shape[0], G, D)
+    ref = OA.attention_bwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale, f64(do),
+                           lmk_bias=lb.double().numpy())
+    for name, a, b in zip(("dq", "dk", "dv", "dbias"), res, ref):
+        e = rel_err(f64(a), b)
+        assert e < TOL[dt], (name, e)
+    res2 = ops.attention_backward(dev[7], dev[0], dev[1], dev[2], out, lse, dev[3], dev[4], dev[5], dev[6],
+                                  scale=scale, max_seqlen=maxlen)
+    for a, b in zip(res, res2):
+        assert torch.equal(a, b)
+
+
+def test_bwd_grouped_heads_shared_landmarks():
+    """Heads of one group selecting the same positions: each landmark row's gradient is the
+    sum over the group's heads (one writer per row)."""
+    q, k, v, w, cu, idx, lb, maxlen, do = _bwd_gqa_case(8, 2, 64, torch.bfloat16, seed=47)
+    idx[1::2] = idx[0::2]  # heads 2i and 2i+1 (same group) share their sets
+    scale = 0.125
+    dev = [t.to(DEV) for t in (q, k, v, w, cu, idx, lb, do)]
+    out, lse = ops.attention_forward(*dev[:6], dev[6], scale=scale, max_seqlen=maxlen)
+    res = ops.attention_backward(dev[7], dev[0], dev[1], dev[2], out, lse, dev[3], dev[4], dev[5], dev[6],
+                                 scale=scale, max_seqlen=maxlen)
+    torch.cuda.synchronize()
+    ref = OA.attention_bwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale, f64(do),
+                           lmk_bias=lb.double().numpy())
+    for name, a, b in zip(("dq", "dk", "dv", "dbias"), res, ref):
+        assert rel_err(f64(a), b) < 2e-2, name
+
+
+def test_repeated_landmark_positions_count_each_copy():
+    """A set that repeats a position: the forward counts every copy and the backward sums
+    every copy's gradient (the oracle's semantics), deterministically."""
+    q, k, v, w, cu, idx, lb, maxlen, do = _bwd_gqa_case(4, 4, 64, torch.float32, seed=48, K=24)
+    for hh in range(4):
+        for s in range(2):
+            row = idx[hh, s, 0]
+            n = int((row >= 0).sum())
+            if n >= 4:
+                row[1] = row[0]
+                row[3] = row[2]
+    scale = 0.125
+    dev = [t.to(DEV) for t in (q, k, v, w, cu, idx, lb, do)]
+    out, lse = ops.attention_forward(*dev[:6], dev[6], scale=scale, max_seqlen=maxlen)
+    res = ops.attention_backward(dev[7], dev[0], dev[1], dev[2], out, lse, dev[3], dev[4], dev[5], dev[6],
+                                 scale=scale, max_seqlen=maxlen)
+    torch.cuda.synchronize()
+    ro, _ = OA.attention_fwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale,
+                             lmk_bias=lb.double().numpy())
+    assert rel_err(f64(out), ro) < 1e-5
+    ref = OA.attention_bwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale, f64(do),
+                           lmk_bias=lb.double().numpy())
+    for name, a, b in zip(("dq", "dk", "dv", "dbias"), res, ref):
+        assert rel_err(f64(a), b) < 1e-5, name
+
+
+@pytest.mark.parametrize("G", [4, 2])
+def test_backward_reusing_the_forward_plan_is_bit_identical(G):
+    q, k, v, w, cu, idx, lb, maxlen, do = _bwd_gqa_case(4, G, 64, torch.bfloat16, seed=49)
+    dev = [t.to(DEV) for t in (q, k, v, w, cu, idx, lb, do)]
+    plan = ops.new_plan(dev[0], dev[1], dev[4], dev[5], max_seqlen=maxlen)
+    out, lse = ops.attention_forward(*dev[:6], dev[6], max_seqlen=maxlen, plan=plan)
+    a = ops.attention_backward(dev[7], dev[0], dev[1], dev[2], out, lse, dev[3], dev[4], dev[5], dev[6],
+                               max_seqlen=maxlen)
+    b = ops.attention_backward(dev[7], dev[0], dev[1], dev[2], out, lse, dev[3], dev[4], dev[5], dev[6],
+                               max_seqlen=maxlen, plan=plan)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
