@@ -23,6 +23,8 @@
 // P = exp(q.k * scale + bias - LSE) is recomputed in base 2 from the forward's
 // LSE; dS = P (dP - delta), dP = dO V^T.  Products over tokens read their
 // transposed operand from the row-major tiles with ds_read_b64_tr_b16.
+#include <type_traits>
+
 #include "attn.h"
 #include "tiles.h"
 #include "timing.h"
@@ -216,32 +218,42 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     const bool lmk32 = (D == 64) && kext != 0u && vext != 0u;
     const rsrc_t krs = make_rsrc(kbase, kext), vrs = make_rsrc(vbase, vext);
     KT kt, vt;
-    auto load_chunk = [&](int c) {
-        if (c < nband) {
-            const int j0 = cs + c * BN;
-            const int rows = min(BN, bhi + 1 - j0);
-            kt.load_rows(rows_rsrc(kbase + (int64_t)j0 * p.k_st, rows, krb, D * sizeof(T)), koff);
-            vt.load_rows(rows_rsrc(vbase + (int64_t)j0 * p.v_st, rows, vrb, D * sizeof(T)), voff);
-        } else {
-            auto pos = [&](int rr) -> int {
-                const int sl = (c - nband) * BN + rr;
-                const int q = sl < bcm ? lpos[sl] : -1;
-                return q < len ? q : -1;
-            };
-            if (lmk32) {
-                uint32_t ko[KT::NV], vo[KT::NV];
-                KT::gather_offsets(tid, pos, krb, vrb, ko, vo);
-                kt.load_rows(krs, ko);
-                vt.load_rows(vrs, vo);
-            } else {
-                kt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr; },
-                        kbase);
-                vt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr; },
-                        vbase);
-            }
+    // band rows [cs, bhi]: one resource per tensor over the whole band (rows past bhi read
+    // zero), chunk c at byte offset c * BN * row bytes -- no per-chunk address arithmetic
+    const rsrc_t kband = rows_rsrc(kbase + (int64_t)cs * p.k_st, bhi + 1 - cs, krb, D * sizeof(T));
+    const rsrc_t vband = rows_rsrc(vbase + (int64_t)cs * p.v_st, bhi + 1 - cs, vrb, D * sizeof(T));
+    // band chunks are loaded in order: the per-thread offsets advance by one chunk per load
+    auto load_band = [&](int) {
+        kt.load_rows(kband, koff);
+        vt.load_rows(vband, voff);
+#pragma unroll
+        for (int n = 0; n < KT::NV; ++n) {
+            koff[n] += (uint32_t)BN * krb;
+            voff[n] += (uint32_t)BN * vrb;
         }
     };
-    load_chunk(0);
+    auto load_lmk = [&](int c) {  // landmark chunk c (slots c*BN ..)
+        auto pos = [&](int rr) -> int {
+            const int sl = c * BN + rr;
+            const int q = sl < bcm ? lpos[sl] : -1;
+            return q < len ? q : -1;
+        };
+        if (lmk32) {
+            uint32_t ko[KT::NV], vo[KT::NV];
+            KT::gather_offsets(tid, pos, krb, vrb, ko, vo);
+            kt.load_rows(krs, ko);
+            vt.load_rows(vrs, vo);
+        } else {
+            kt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr; },
+                    kbase);
+            vt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr; },
+                    vbase);
+        }
+    };
+    // landmark chunks first (their gathers only in the first loop), then the band
+    const int nlmk = nchunks - nband;
+    if (nlmk > 0) load_lmk(0);
+    else load_band(0);
     kt.store(Ks[0], tid);
     vt.store(Vs[0], tid);
     __syncthreads();
@@ -251,11 +263,20 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     for (int dt = 0; dt < D / 16; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     const float NEG = -INFINITY;
     const int lane_off = 4 * g;
-    for (int c = 0; c < nchunks; ++c) {
-        const int buf = c & 1;
-        if (c + 1 < nchunks) load_chunk(c + 1);
-        const bool band = c < nband;
-        const int base = band ? cs + c * BN : (c - nband) * BN;
+    // one chunk; `band` is a compile-time tag, so the band and landmark loops below are
+    // separate straight-line code
+    // chunk n of the sweep: landmark chunk n (n < nlmk), else band chunk n - nlmk
+    auto process = [&](int n, auto band_tag) {
+        constexpr bool band = decltype(band_tag)::value;
+        const int buf = n & 1;
+        const int c = band ? n - nlmk : n;
+        if (!band) {
+            if (n + 1 < nlmk) load_lmk(n + 1);
+            else if (nband > 0) load_band(0);
+        } else if (c + 1 < nband) {
+            load_band(c + 1);
+        }
+        const int base = band ? cs + c * BN : c * BN;
         floatx4 dS[NST];
         bool act[NST];
 #pragma unroll
@@ -328,12 +349,14 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
             for (int stt = 0; stt < NST; ++stt)
                 if (act[stt]) acc_rm32<D>((const float*)Ks[buf], KT::RS, stt * 16, lane, dS[stt], acc);
         }
-        if (c + 1 < nchunks) {
+        if (n + 1 < nchunks) {
             kt.store(Ks[buf ^ 1], tid);
             vt.store(Vs[buf ^ 1], tid);
         }
         __syncthreads();
-    }
+    };
+    for (int n = 0; n < nlmk; ++n) process(n, std::false_type{});
+    for (int n = nlmk; n < nchunks; ++n) process(n, std::true_type{});
     if (TR) {
         const float dw = sum_g4(dwacc);
         if (valid && g == 0) p.dw_h[(int64_t)(st + i) * p.n_heads + h] = dw;
@@ -383,17 +406,25 @@ struct QLoader {
             doff[n] = QT::row_offset(tid, n, drb);
         }
     }
-    // rows i0 .. min(i0 + BQ, iend) - 1; later rows read as zero
-    __device__ __forceinline__ void load(const AttnParams& p, const T* qb, const T* db, int i0, int iend, int) {
-        const int rows = min(BQ, iend - i0);
-        tq.load_rows(rows_rsrc(qb + (int64_t)i0 * p.q_st, rows, qrb, D * sizeof(T)), qoff);
-        tdo.load_rows(rows_rsrc(db + (int64_t)i0 * p.do_st, rows, drb, D * sizeof(T)), doff);
+    // resources over rows [i0, iend) of q and dO (later rows read as zero)
+    __device__ __forceinline__ void span(const AttnParams& p, const T* qb, const T* db, int i0, int iend, rsrc_t& rq,
+                                         rsrc_t& rd) const {
+        rq = rows_rsrc(qb + (int64_t)i0 * p.q_st, iend - i0, qrb, D * sizeof(T));
+        rd = rows_rsrc(db + (int64_t)i0 * p.do_st, iend - i0, drb, D * sizeof(T));
     }
-    // rows base + list[idx0 + rr] for idx0 + rr < n (list in LDS, offsets < nrows); later rows zero
-    __device__ __forceinline__ void gather(const AttnParams& p, const T* qb, const T* db, int base, int nrows,
-                                           const short* list, int idx0, int n, int tid) {
-        const rsrc_t rq = rows_rsrc(qb + (int64_t)base * p.q_st, nrows, qrb, D * sizeof(T));
-        const rsrc_t rd = rows_rsrc(db + (int64_t)base * p.do_st, nrows, drb, D * sizeof(T));
+    // rows c*BQ .. c*BQ + BQ - 1 of a span
+    __device__ __forceinline__ void load(rsrc_t rq, rsrc_t rd, int c) {
+        uint32_t q2[QT::NV], d2[QT::NV];
+#pragma unroll
+        for (int v = 0; v < QT::NV; ++v) {
+            q2[v] = qoff[v] + (uint32_t)(c * BQ) * qrb;
+            d2[v] = doff[v] + (uint32_t)(c * BQ) * drb;
+        }
+        tq.load_rows(rq, q2);
+        tdo.load_rows(rd, d2);
+    }
+    // rows list[idx0 + rr] of a span for idx0 + rr < n (list in LDS); later rows zero
+    __device__ __forceinline__ void gather(rsrc_t rq, rsrc_t rd, const short* list, int idx0, int n, int tid) {
 #pragma unroll
         for (int v = 0; v < QT::NV; ++v) {
             const int vi = tid + 256 * v, idx = idx0 + vi / QT::CPR;
@@ -578,13 +609,15 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (GQA ? 3 : 4) : 
 
     // ---- diagonal rows j0 .. j0+63 (contiguous), double-buffered
     const int ndiag = uniform(min(NDIAG, ceil_div(iend - j0, BQ)));
-    ld.load(p, qb, db, j0, iend, tid);
+    rsrc_t rq, rd;
+    ld.span(p, qb, db, j0, min(iend, j0 + 64), rq, rd);
+    ld.load(rq, rd, 0);
     ld.store(sq[0], tid);
     if (tid < BQ) stage_row(sq[0], tid, j0 + tid, j0 + tid < iend);
     __syncthreads();
     for (int c = 0; c < ndiag; ++c) {
         const int buf = c & 1;
-        if (c + 1 < ndiag) ld.load(p, qb, db, j0 + (c + 1) * BQ, iend, tid);
+        if (c + 1 < ndiag) ld.load(rq, rd, c + 1);
         compute(sq[buf], 0, j0 + c * BQ);
         if (c + 1 < ndiag) {
             ld.store(sq[buf ^ 1], tid);
@@ -649,9 +682,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (GQA ? 3 : 4) : 
         }
         __syncthreads();
         const int nfc = ceil_div(nf, BQ), nc = nfc + ceil_div(np, BQ);
+        ld.span(p, qb, db, seg, seg + nrows, rq, rd);
         auto gather_chunk = [&](int c) {
-            if (c < nfc) ld.gather(p, qb, db, seg, nrows, lst[0], c * BQ, nf, tid);
-            else ld.gather(p, qb, db, seg, nrows, lst[1], (c - nfc) * BQ, np, tid);
+            if (c < nfc) ld.gather(rq, rd, lst[0], c * BQ, nf, tid);
+            else ld.gather(rq, rd, lst[1], (c - nfc) * BQ, np, tid);
         };
         auto stage_chunk = [&](int c, QS& q) {
             ld.store(q, tid);
@@ -797,7 +831,11 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     // rows staged in LDS; visible landmark counts come from the dQ pass
     for (int t = t0; any_slot && t < ntile; t += p.n_chunks) {
         const int i0 = t * BQ;
-        ld.load(p, qb, db, i0, len, tid);
+        {
+            rsrc_t rq, rd;
+            ld.span(p, qb, db, i0, min(len, i0 + BQ), rq, rd);
+            ld.load(rq, rd, 0);
+        }
         // per-row data loaded with the tile (one memory latency per tile)
         int c = 0;
         float rl = 0.f, rd = 0.f;

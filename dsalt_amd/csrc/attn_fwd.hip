@@ -15,6 +15,8 @@
 // than 2^8); P is rounded to the input dtype before P V as in the reference
 // (:115,:147), V^T comes from the row-major tile through the transpose read,
 // and the row sums come from the same packed P through a ones operand.
+#include <type_traits>
+
 #include "attn.h"
 #include "tiles.h"
 #include "timing.h"
@@ -300,33 +302,43 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     const bool lmk32 = (D == 64 || sizeof(T) == 2) && kext != 0u && vext != 0u;
     const rsrc_t krs = make_rsrc(kbase, kext), vrs = make_rsrc(vbase, vext);
     KT kt, vt;
-    auto load_chunk = [&](int c) {
-        if (c < nband) {
-            const int j0 = cs + c * BN;
-            const int rows = min(BN, bhi + 1 - j0);
-            kt.load_rows(rows_rsrc(kbase + (int64_t)j0 * p.k_st, rows, krb, D * sizeof(T)), koff);
-            vt.load_rows(rows_rsrc(vbase + (int64_t)j0 * p.v_st, rows, vrb, D * sizeof(T)), voff);
-        } else {
-            auto pos = [&](int rr) -> int {
-                const int sl = (c - nband) * BN + rr;
-                const int q = sl < bcm ? lpos[sl] : -1;
-                return q < len ? q : -1;
-            };
-            if (lmk32) {
-                uint32_t ko[KT::NV], vo[KT::NV];
-                KT::gather_offsets(tid, pos, krb, vrb, ko, vo);
-                kt.load_rows(krs, ko);
-                vt.load_rows(vrs, vo);
-            } else {
-                kt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr; },
-                        kbase);
-                vt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr; },
-                        vbase);
-            }
+    // band rows [cs, bhi]: one resource per tensor over the whole band (rows past bhi read
+    // zero); band chunks are loaded in order, the per-thread offsets advancing one chunk per load
+    const int brows = nband > 0 ? bhi + 1 - cs : 0;
+    const rsrc_t kband = rows_rsrc(kbase + (int64_t)cs * p.k_st, brows, krb, D * sizeof(T));
+    const rsrc_t vband = rows_rsrc(vbase + (int64_t)cs * p.v_st, brows, vrb, D * sizeof(T));
+    auto load_band = [&]() {
+        kt.load_rows(kband, koff);
+        vt.load_rows(vband, voff);
+#pragma unroll
+        for (int n = 0; n < KT::NV; ++n) {
+            koff[n] += (uint32_t)BN * krb;
+            voff[n] += (uint32_t)BN * vrb;
         }
     };
+    auto load_lmk = [&](int c) {  // landmark chunk c (slots c*BN ..)
+        auto pos = [&](int rr) -> int {
+            const int sl = c * BN + rr;
+            const int q = sl < bcm ? lpos[sl] : -1;
+            return q < len ? q : -1;
+        };
+        if (lmk32) {
+            uint32_t ko[KT::NV], vo[KT::NV];
+            KT::gather_offsets(tid, pos, krb, vrb, ko, vo);
+            kt.load_rows(krs, ko);
+            vt.load_rows(vrs, vo);
+        } else {
+            kt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? kbase + (int64_t)j * p.k_st : (const T*)nullptr; },
+                    kbase);
+            vt.load(tid, [&](int rr) { int j = pos(rr); return j >= 0 ? vbase + (int64_t)j * p.v_st : (const T*)nullptr; },
+                    vbase);
+        }
+    };
+    // landmark chunks first (their gathers only in the first loop), then the band
+    const int nlmk = nchunks - nband;
     if (nchunks > 0) {
-        load_chunk(0);
+        if (nlmk > 0) load_lmk(0);
+        else load_band();
         kt.store(Ks[0], tid);
         vt.store(Vs[0], tid);
     }
@@ -348,11 +360,19 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     const float NEG = -INFINITY;
     const int lane_off = 4 * g;
 
-    for (int c = 0; c < nchunks; ++c) {
-        const int buf = c & 1;
-        if (c + 1 < nchunks) load_chunk(c + 1);
-        const bool band = c < nband;
-        const int base = band ? cs + c * BN : (c - nband) * BN;
+    // chunk n of the sweep: landmark chunk n (n < nlmk), else band chunk n - nlmk; `band` is a
+    // compile-time tag, so the two loops below are separate straight-line code
+    auto process = [&](int n, auto band_tag) {
+        constexpr bool band = decltype(band_tag)::value;
+        const int buf = n & 1;
+        const int c = band ? n - nlmk : n;
+        if (!band) {
+            if (n + 1 < nlmk) load_lmk(n + 1);
+            else if (nband > 0) load_band();
+        } else if (c + 1 < nband) {
+            load_band();
+        }
+        const int base = band ? cs + c * BN : c * BN;
         const T* kl = Ks[buf];
         floatx4 S[RG][NST];
         bool act[RG][NST];
@@ -512,12 +532,14 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
                     }
             }
         }
-        if (c + 1 < nchunks) {
+        if (n + 1 < nchunks) {
             kt.store(Ks[buf ^ 1], tid);
             vt.store(Vs[buf ^ 1], tid);
         }
         __syncthreads();
-    }
+    };
+    for (int n = 0; n < nlmk; ++n) process(n, std::false_type{});
+    for (int n = nlmk; n < nchunks; ++n) process(n, std::true_type{});
 
 #pragma unroll
     for (int u = 0; u < RG; ++u) {
