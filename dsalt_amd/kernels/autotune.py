@@ -1,39 +1,78 @@
 """Tile policy of the HIP kernels, with the reference's autotune entry points.
 
-The reference sweeps Triton tile sizes once per ``(head_dim, compute capability)``
-(``dsalt/kernels/autotune.py:192-278``).  The gfx950 kernels fix their tiles at compile
-time per (dtype, head_dim): 64 query rows per 256-thread block (4 waves x 16 rows, one
-query row per lane), key chunks of BLOCK_N rows staged in LDS, 16x16x32 MFMA tiles.
-``get_tuned_config`` reports that policy; ``autotune_blocks`` keeps the reference's
-contract (time each candidate's fwd+bwd runner with GPU events, cache the fastest) over the
-candidates the library offers.
+The reference sweeps Triton tile sizes once per ``(head_dim, compute capability)``, timing
+one fwd+bwd step per candidate with GPU events and caching the fastest
+(``dsalt/kernels/autotune.py:55-122,176-238,276-278``); its kernels then read the cached
+choice (``dsalt_triton_bwd.py:276-277``).  The gfx950 kernels are compiled in a few tilings
+per (dtype, head_dim) -- 64 query rows per 256-thread block (4 waves x 16 rows, one query
+row per lane), key chunks of BLOCK_N rows staged in LDS, 16x16x32 MFMA tiles -- selected at
+run time by the ``variant`` bits of the C ABI (``DSALT_VARIANT_*``):
+
+  * FWD_BN32  forward key chunks of 32 instead of 64 rows (16-bit, head_dim 64);
+  * FWD_RG2   forward blocks of 128 rows, two 16-row groups per wave (16-bit, head_dim 64);
+  * DQ_BN64   backward dQ key chunks of 64 instead of 32 rows (16-bit, head_dim 64);
+  * LMK_SHORT landmark-backward row chunks of 512 instead of 1024 rows (more blocks).
+
+``_candidate_configs`` lists the tilings a shape can use, ``autotune_blocks`` times each
+candidate's fwd+bwd runner and caches the winner per (head_dim, dtype, device), and
+``get_tuned_config`` returns it; ``dsalt_attention`` passes the cached variant to the
+kernels.  Every variant computes the same operator (the GPU tests check each against the
+oracle); only the speed differs.
 """
 from __future__ import annotations
 
 import torch
 
+from .._lib import VARIANT_DQ_BN64, VARIANT_FWD_BN32, VARIANT_FWD_RG2, VARIANT_LMK_SHORT
+
 _TUNED_CONFIG: dict = {}
 
-# compiled tile table: (head_dim, element bytes) -> forward key chunk, backward query chunk
-_TILES = {(64, 2): (64, 32), (128, 2): (32, 32), (64, 4): (32, 16), (128, 4): (16, 16)}
+# default compiled tiles: (head_dim, element bytes) -> forward key chunk, dQ key chunk,
+# dK/dV query chunk
+_TILES = {(64, 2): (64, 32, 32), (128, 2): (32, 32, 32), (64, 4): (32, 32, 32), (128, 4): (16, 16, 16)}
 
 
-def _device_key(head_dim: int, device) -> tuple:
+def _elem_bytes(dtype) -> int:
+    return 4 if dtype in (torch.float32, None) else 2
+
+
+def _device_key(head_dim: int, device, dtype=torch.bfloat16) -> tuple:
     name = torch.cuda.get_device_properties(device).gcnArchName if torch.cuda.is_available() else "cpu"
-    return (int(head_dim), str(name))
+    return (int(head_dim), _elem_bytes(dtype), str(name))
+
+
+def _config_of(head_dim: int, elem_bytes: int, variant: int) -> dict:
+    hd = 64 if head_dim <= 64 else 128
+    bn, bnq, bq = _TILES[(hd, 4 if elem_bytes == 4 else 2)]
+    tunable = hd == 64 and elem_bytes == 2
+    bm = 64
+    if tunable and variant & VARIANT_FWD_BN32:
+        bn = 32
+    if tunable and variant & VARIANT_FWD_RG2:
+        bm = 128
+    if tunable and variant & VARIANT_DQ_BN64:
+        bnq = 64
+    return {"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_N_BWD": bnq, "BLOCK_Q_BWD": bq, "num_warps": 4 * bm // 64,
+            "num_stages": 2, "LMK_ROWS": 512 if variant & VARIANT_LMK_SHORT else 1024, "variant": int(variant)}
 
 
 def _heuristic_config(head_dim: int, device=None, elem_bytes: int = 2) -> dict:
-    hd = 64 if head_dim <= 64 else 128
-    bn, bq = _TILES[(hd, 4 if elem_bytes == 4 else 2)]
-    return {"BLOCK_M": 64, "BLOCK_N": bn, "BLOCK_N_BWD": bq, "num_warps": 4, "num_stages": 2}
+    """The library's default tiling for the shape (variant 0)."""
+    return _config_of(head_dim, elem_bytes, 0)
 
 
-def _candidate_configs(head_dim: int, device=None) -> list[dict]:
-    return [_heuristic_config(head_dim, device)]
+def _candidate_configs(head_dim: int, device=None, elem_bytes: int = 2) -> list[dict]:
+    """Every tiling the compiled kernels offer for the shape (the heuristic first)."""
+    if head_dim == 64 and elem_bytes == 2:
+        variants = [0, VARIANT_FWD_BN32, VARIANT_FWD_RG2, VARIANT_DQ_BN64, VARIANT_LMK_SHORT,
+                    VARIANT_FWD_BN32 | VARIANT_LMK_SHORT, VARIANT_DQ_BN64 | VARIANT_LMK_SHORT]
+    else:
+        variants = [0, VARIANT_LMK_SHORT]
+    return [_config_of(head_dim, elem_bytes, v) for v in variants]
 
 
 def _bench_step(run_fwd_bwd, n_warmup: int = 3, n_iter: int = 10) -> float:
+    """Average time (ms) of one fwd+bwd step, timed with GPU events."""
     for _ in range(n_warmup):
         run_fwd_bwd()
     torch.cuda.synchronize()
@@ -46,28 +85,61 @@ def _bench_step(run_fwd_bwd, n_warmup: int = 3, n_iter: int = 10) -> float:
     return start.elapsed_time(end) / n_iter
 
 
-def autotune_blocks(head_dim: int, device, make_runner, verbose: bool = True) -> dict:
-    """Time ``make_runner(cfg)()`` for each candidate, cache and return the fastest config."""
-    key = _device_key(head_dim, device)
+def autotune_blocks(head_dim: int, device, make_runner, verbose: bool = True, dtype=torch.bfloat16) -> dict:
+    """Time ``make_runner(cfg)()`` (one fwd+bwd with the config's tiling; ``None`` when the
+    config cannot run) for each candidate; cache and return the fastest config."""
+    key = _device_key(head_dim, device, dtype)
     if key in _TUNED_CONFIG:
         return _TUNED_CONFIG[key]
     results = []
-    for cfg in _candidate_configs(head_dim, device):
+    for cfg in _candidate_configs(head_dim, device, _elem_bytes(dtype)):
         runner = make_runner(cfg)
         if runner is None:
+            results.append((cfg, None, "skip"))
             continue
         try:
-            results.append((cfg, _bench_step(runner)))
+            results.append((cfg, _bench_step(runner), None))
         except Exception as e:  # a candidate that cannot run is skipped
-            if verbose:
-                print(f"autotune: {cfg} failed: {type(e).__name__}")
-    best = min(results, key=lambda r: r[1])[0] if results else _heuristic_config(head_dim, device)
+            results.append((cfg, None, type(e).__name__))
+    valid = [(c, t) for c, t, _ in results if t is not None]
+    best = min(valid, key=lambda r: r[1])[0] if valid else _heuristic_config(head_dim, device, _elem_bytes(dtype))
     _TUNED_CONFIG[key] = best
-    if verbose and results:
-        for cfg, ms in results:
-            print(f"  dsalt tiles {cfg}: {ms:.4f} ms/step")
+    if verbose:
+        print(f"dsalt autotune head_dim={head_dim} ({key[2]}, {key[1]}-byte elements)")
+        for cfg, ms, err in results:
+            mark = "  <- best" if cfg is best else ""
+            t = f"{ms:.4f} ms/step" if ms is not None else err
+            print(f"  variant {cfg['variant']:2d}  BLOCK_M {cfg['BLOCK_M']:3d} BLOCK_N {cfg['BLOCK_N']:2d} "
+                  f"BLOCK_N_BWD {cfg['BLOCK_N_BWD']:2d} LMK_ROWS {cfg['LMK_ROWS']:4d}  {t}{mark}")
     return best
 
 
-def get_tuned_config(head_dim: int, device) -> dict | None:
-    return _TUNED_CONFIG.get(_device_key(head_dim, device))
+def get_tuned_config(head_dim: int, device, dtype=torch.bfloat16) -> dict | None:
+    """The cached config for ``(head_dim, dtype, device)``, or None before autotune_blocks."""
+    return _TUNED_CONFIG.get(_device_key(head_dim, device, dtype))
+
+
+def tuned_variant(head_dim: int, device, dtype) -> int:
+    """Variant bits the kernels should use: the cached winner's, else the default (0)."""
+    if not _TUNED_CONFIG:
+        return 0
+    cfg = get_tuned_config(head_dim, device, dtype)
+    return int(cfg["variant"]) if cfg else 0
+
+
+def operator_runner(q, k, v, w, cu_seqlens, lmk_idx, dout, *, max_seqlen=None):
+    """``make_runner`` for autotune_blocks over the operator's own fwd+bwd on the given
+    tensors (indices [H, S, 1, k] ascending, as ops.select_landmarks returns)."""
+    from .. import ops
+
+    def make_runner(cfg):
+        variant = cfg["variant"]
+
+        def run():
+            plan = ops.new_plan(q, k, cu_seqlens, lmk_idx, max_seqlen=max_seqlen)
+            out, lse = ops.attention_forward(q, k, v, w, cu_seqlens, lmk_idx, None, max_seqlen=max_seqlen, plan=plan,
+                                             variant=variant)
+            ops.attention_backward(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, None, max_seqlen=max_seqlen,
+                                   want_dbias=False, plan=plan, variant=variant)
+        return run
+    return make_runner

@@ -22,6 +22,7 @@ import math
 import torch
 
 from .. import ops
+from .autotune import tuned_variant
 
 
 def _mode_of(lmk_indices):
@@ -43,12 +44,13 @@ class DSALTAttentionFunction(torch.autograd.Function):
         cu_i = cu_seqlens.detach().to(torch.int32)
         scale = 1.0 / math.sqrt(q.shape[-1])
         plan = ops.new_plan(q, k, cu_i, idx_s, max_seqlen=max_seqlen, select_mode=mode, block_size=block_size)
+        variant = tuned_variant(q.shape[-1], q.device, q.dtype)  # autotune_blocks' choice, if made
         out, lse = ops.attention_forward(q, k, v, w_i, cu_i, idx_s, bias_s, scale=scale, max_seqlen=max_seqlen,
-                                         select_mode=mode, block_size=block_size, plan=plan)
+                                         select_mode=mode, block_size=block_size, plan=plan, variant=variant)
         ctx.save_for_backward(q, k, v, out, lse, idx_s, bias_s if bias_s is not None else torch.empty(0),
                               perm, w_i, cu_i, plan)
         ctx.has_bias = bias_s is not None
-        ctx.mode, ctx.max_seqlen, ctx.scale = mode, max_seqlen, scale
+        ctx.mode, ctx.max_seqlen, ctx.scale, ctx.variant = mode, max_seqlen, scale, variant
         ctx.bias_dtype = lmk_bias.dtype if lmk_bias is not None else None
         return out.float()
 
@@ -60,7 +62,7 @@ class DSALTAttentionFunction(torch.autograd.Function):
         dq, dk, dv, db = ops.attention_backward(grad_out.to(q.dtype), q, k, v, out, lse, w_i, cu_i, idx_s,
                                                 bias_s if ctx.has_bias else None, scale=ctx.scale,
                                                 max_seqlen=ctx.max_seqlen, want_dbias=ctx.needs_input_grad[4],
-                                                plan=plan)
+                                                plan=plan, variant=ctx.variant)
         d_bias = None
         if ctx.needs_input_grad[4] and db is not None:
             d_bias = torch.zeros_like(db).scatter_(-1, perm, db)[:, :, 0].to(ctx.bias_dtype)

@@ -30,6 +30,7 @@ import math
 import torch
 
 from .. import ops
+from .autotune import tuned_variant
 
 
 class DSALTTrainFunction(torch.autograd.Function):
@@ -44,10 +45,12 @@ class DSALTTrainFunction(torch.autograd.Function):
         w_c = w_cont.detach().to(torch.float32).contiguous()
         scale = 1.0 / math.sqrt(q.shape[-1])
         plan = ops.new_plan(q, k, cu_i, idx_s, max_seqlen=max_seqlen)
+        variant = tuned_variant(q.shape[-1], q.device, q.dtype)  # autotune_blocks' choice, if made
         out, lse = ops.train_forward(q, k, v, w_c, cu_i, idx_s, logw_s, tau_win=float(tau_win),
-                                     win_edge=float(win_edge), scale=scale, max_seqlen=max_seqlen, plan=plan)
+                                     win_edge=float(win_edge), scale=scale, max_seqlen=max_seqlen, plan=plan,
+                                     variant=variant)
         ctx.save_for_backward(q, k, v, out, lse, idx_s, logw_s, perm, w_c, cu_i, plan)
-        ctx.max_seqlen, ctx.scale = max_seqlen, scale
+        ctx.max_seqlen, ctx.scale, ctx.variant = max_seqlen, scale, variant
         ctx.tau_win, ctx.win_edge = float(tau_win), float(win_edge)
         ctx.logw_dtype, ctx.w_dtype = lmk_logw.dtype, w_cont.dtype
         return out.float()
@@ -58,7 +61,7 @@ class DSALTTrainFunction(torch.autograd.Function):
         dq, dk, dv, dlogw, d_w = ops.train_backward(
             grad_out.to(q.dtype), q, k, v, out, lse, w_c, cu_i, idx_s, logw_s, tau_win=ctx.tau_win,
             win_edge=ctx.win_edge, scale=ctx.scale, max_seqlen=ctx.max_seqlen,
-            want_dlogw=ctx.needs_input_grad[4], plan=plan)
+            want_dlogw=ctx.needs_input_grad[4], plan=plan, variant=ctx.variant)
         d_logw = None
         if ctx.needs_input_grad[4] and dlogw is not None:
             d_logw = torch.zeros_like(dlogw).scatter_(-1, perm, dlogw)[:, :, 0].to(ctx.logw_dtype)

@@ -77,3 +77,17 @@ def test_zscore_gradient_closed_form_matches_autograd():
     (vr.norm(dim=-1) * dn).sum().backward()
     got = _norm_grad(dn, vec, vec.norm(dim=-1))
     assert torch.allclose(got, vr.grad, atol=1e-12)
+
+
+def test_autotune_candidates_describe_the_compiled_tilings():
+    from dsalt_amd.kernels import autotune as AT
+    c64 = AT._candidate_configs(64, None, 2)
+    assert c64[0] == AT._heuristic_config(64, None, 2) and c64[0]["variant"] == 0
+    assert len({c["variant"] for c in c64}) == len(c64) >= 5
+    by = {c["variant"]: c for c in c64}
+    assert by[AT.VARIANT_FWD_BN32]["BLOCK_N"] == 32 and by[0]["BLOCK_N"] == 64
+    assert by[AT.VARIANT_FWD_RG2]["BLOCK_M"] == 128 and by[AT.VARIANT_DQ_BN64]["BLOCK_N_BWD"] == 64
+    assert by[AT.VARIANT_LMK_SHORT]["LMK_ROWS"] == 512
+    # shapes with one compiled tiling offer only the landmark-chunk choice
+    assert [c["variant"] for c in AT._candidate_configs(128, None, 2)] == [0, AT.VARIANT_LMK_SHORT]
+    assert AT.get_tuned_config.__name__ == "get_tuned_config"
