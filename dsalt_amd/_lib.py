@@ -18,6 +18,7 @@ SELECT_GLOBAL, SELECT_BLOCK = 0, 1
 STATS_PACKED, STATS_SEQUENCE = 0, 1
 ERR_NAMES = {1: "invalid argument", 2: "unsupported", 3: "workspace", 4: "HIP error"}
 ABI_VERSION = 2
+FWD_NOALLOC_MAX_PLAN_BYTES = 4 << 20  # DSALT_FWD_NOALLOC_MAX_PLAN_BYTES
 # tile variants of the attention kernels (DSALT_VARIANT_*)
 VARIANT_DEFAULT, VARIANT_FWD_BN32, VARIANT_FWD_RG2, VARIANT_DQ_BN64, VARIANT_LMK_SHORT = 0, 1, 2, 4, 8
 
@@ -125,6 +126,7 @@ SIGNATURES = {
     "dsalt_plan_bytes": ([ctypes.POINTER(Problem)], _sz),
     "dsalt_fwd_workspace_bytes": ([ctypes.POINTER(FwdArgs)], _sz),
     "dsalt_fwd": ([ctypes.POINTER(FwdArgs), _vp], ctypes.c_int),
+    "dsalt_fwd_noalloc": ([ctypes.POINTER(FwdArgs), _vp], ctypes.c_int),
     "dsalt_bwd_workspace_bytes": ([ctypes.POINTER(BwdArgs)], _sz),
     "dsalt_bwd": ([ctypes.POINTER(BwdArgs), _vp], ctypes.c_int),
     "dsalt_gather_landmarks": ([ctypes.POINTER(GatherArgs), _vp], ctypes.c_int),

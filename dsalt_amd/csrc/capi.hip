@@ -3,6 +3,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <map>
+#include <mutex>
 #include <string>
 
 #include "attn.h"
@@ -252,6 +254,70 @@ int dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream) {
     if (!a->workspace || a->workspace_bytes < need)
         return fail(DSALT_ERR_WORKSPACE, "forward needs %zu workspace bytes, got %zu", need, a->workspace_bytes);
     return hip_status(dsalt::fwd_launch(p, a->workspace, a->plan, (hipStream_t)stream), "dsalt_fwd");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------ forward without allocations
+// The row plan of dsalt_fwd_noalloc lives in this file-scope device array (one copy per
+// GPU, held until the process ends).  In host code `scratch` names a host-side stand-in,
+// not a device address: the address is looked up once per device with
+// hipGetSymbolAddress (with that device current) and only that address is used.
+namespace {
+
+constexpr size_t kScratchBytes = DSALT_FWD_NOALLOC_MAX_PLAN_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+std::map<int, void*> g_scratch_ptr;  // device -> address of its copy of `scratch`
+
+// address of `scratch` on device `dev` (looked up on the first call for that device)
+hipError_t scratch_on(int dev, void** out) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch_ptr.find(dev);
+    if (it != g_scratch_ptr.end()) {
+        *out = it->second;
+        return hipSuccess;
+    }
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+        const hipError_t e2 = hipSetDevice(cur);
+        if (e == hipSuccess) e = e2;
+    }
+    if (e != hipSuccess) return e;
+    if (ptr == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = ptr;
+    *out = ptr;
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsalt_fwd_noalloc(const dsalt_fwd_args* a, dsalt_stream_t stream) {
+    dsalt::AttnParams p;
+    int rc = fwd_params(a, true, &p);
+    if (rc) return rc;
+    const size_t need = dsalt::plan_bytes(p);
+    if (!a->plan && need > kScratchBytes)
+        return fail(DSALT_ERR_WORKSPACE,
+                    "dsalt_fwd_noalloc: the row plan needs %zu bytes, more than its %zu-byte device scratch "
+                    "(use dsalt_fwd with a workspace)", need, kScratchBytes);
+    void* ws = nullptr;
+    if (!a->plan) {
+        int dev = -1;
+        hipError_t e = stream ? hipStreamGetDevice((hipStream_t)stream, &dev) : hipGetDevice(&dev);
+        if (e == hipSuccess) e = scratch_on(dev, &ws);
+        if (e != hipSuccess) return hip_status(e, "dsalt_fwd_noalloc scratch");
+    }
+    // every kernel writes each plan entry it later reads: nothing needs clearing
+    return hip_status(dsalt::fwd_launch(p, ws, a->plan, (hipStream_t)stream), "dsalt_fwd_noalloc");
 }
 
 size_t dsalt_train_fwd_workspace_bytes(const dsalt_train_fwd_args* a) {

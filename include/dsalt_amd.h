@@ -321,6 +321,18 @@ int    dsalt_select(const dsalt_select_args* a, dsalt_stream_t stream);
 size_t dsalt_fwd_workspace_bytes(const dsalt_fwd_args* a);
 int    dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream);
 
+/* dsalt_fwd without allocations or a workspace argument.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The row plan
+ * goes to a file-scope device array of DSALT_FWD_NOALLOC_MAX_PLAN_BYTES per GPU (held
+ * until the process ends) unless a->plan is given; a->workspace is not read.  Larger
+ * problems (dsalt_plan_bytes(&a->p) above the maximum, i.e. more than 31,775 64-row
+ * tiles over all sequences) are rejected with DSALT_ERR_WORKSPACE.  Every call on one
+ * GPU shares that array: calls that overlap on one GPU (several streams or host
+ * threads) race and must be ordered by the caller.  Outputs are those of dsalt_fwd. */
+#define DSALT_FWD_NOALLOC_MAX_PLAN_BYTES ((size_t)4 << 20)
+int    dsalt_fwd_noalloc(const dsalt_fwd_args* a, dsalt_stream_t stream);
+
 size_t dsalt_bwd_workspace_bytes(const dsalt_bwd_args* a);
 int    dsalt_bwd(const dsalt_bwd_args* a, dsalt_stream_t stream);
 
