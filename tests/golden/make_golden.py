@@ -1,7 +1,7 @@
 """Writes the golden vectors under tests/golden/ from the reference library's CPU code.
 
 Run in the build container only (it reads /root/reference, which is not available where
-the tests run):  python tests/golden/make_golden.py
+the tests run):  python tests/golden/make_golden.py [--only-bf16]
 
 Only functions whose behaviour is a convention rather than mathematics are vectored here:
 the exclusion rule, -1 padding and the uniform/ragged branches of
@@ -13,8 +13,9 @@ builders (dsalt/kernels/window_utils.py:19-70), the packed block map
 (dsalt/kernels/selectors.py:37-67), the landmark gather (selectors.py:137-159), and the
 block-causal selection and exact kernel-semantics attention of
 results/causal_landmark_check.py:68-147, and the training log-bias of
-dsalt/modules/dsalt_attention.py:520-563 with its SDPA gradients.  Inputs are small and
-seeded (float32; the training case float64).
+dsalt/modules/dsalt_attention.py:520-563 with its SDPA gradients, and the bf16 selection
+(the reference's own bf16 norms, float32 statistics and topk at workload-like shapes).
+Inputs are small and seeded (float32, the training case float64, the bf16 selection bf16).
 """
 from __future__ import annotations
 
@@ -76,6 +77,29 @@ def selection_cases(LT, SEL):
                            w=w.numpy(), cu=cu.numpy(), k=np.int64(k), scores=scores.numpy(),
                            z_x=z_x.numpy(), z_v=z_v.numpy(), idx=_sort_sets(idx))
     return cases
+
+
+def bf16_selection_cases(SEL):
+    """bf16 selection at shapes like the benchmark workloads, shortened: the reference's own
+    bf16 arithmetic (norms in bf16, z-statistics in float32 over the packed batch, torch.topk)
+    on chosen value vectors: x = [v | h] and W_V = [I | 0], so x @ W_V^T reproduces v exactly
+    in bf16.  Stored: the windows, the reference's float32 scores and sets, and the SHA-256 of
+    the input bits (x is regenerated from its recipe, tests/helpers.py BF16_SELECT_SPECS)."""
+    sys.path.insert(0, os.path.dirname(os.path.dirname(OUT)))
+    from tests.helpers import BF16_SELECT_SPECS, bf16_select_inputs, sha256_of
+    out = {}
+    for name, (seed, lens, H, dh, extra, k, wmax, heavy) in BF16_SELECT_SPECS.items():
+        x, alpha, w, cu = bf16_select_inputs(name)
+        T = x.shape[0]
+        W_V = torch.cat([torch.eye(H * dh), torch.zeros(H * dh, extra)], 1).to(torch.bfloat16)
+        assert torch.equal((x @ W_V.T), x[:, :H * dh])  # the value vectors, exactly
+        SEL._SEQ_META_CACHE.clear()
+        idx, z_x, z_v = SEL._compute_landmark_indices(x, W_V, alpha, w, cu, k, 1, T,
+                                                      [int(c) for c in cu], head_dim=dh)
+        scores = alpha * z_v + (1.0 - alpha) * z_x.unsqueeze(1)
+        out[name] = dict(x_sha256=np.array(sha256_of(x)), w=w.numpy(), scores=scores.float().numpy(),
+                         idx=_sort_sets(idx))
+    return out
 
 
 def literal_case(LT, SEL, SA, DA):
@@ -217,6 +241,10 @@ def train_case(DA, seed: int = 600):
 
 def main():
     LT, SEL, SA, WU, DA, CLC = _import_reference()
+    for name, c in bf16_selection_cases(SEL).items():
+        np.savez_compressed(os.path.join(OUT, f"select_bf16_{name}.npz"), **c)
+    if "--only-bf16" in sys.argv:
+        return
     np.savez_compressed(os.path.join(OUT, "train_dense.npz"), **train_case(DA))
     for name, c in selection_cases(LT, SEL).items():
         np.savez_compressed(os.path.join(OUT, f"select_{name}.npz"), **c)

@@ -91,3 +91,65 @@ def oracle_bwd_heads(q, k, v, w, cu, idx, scale, dout, heads):
                                 idx[hh:hh + 1], scale, f64(dout[:, hh:hh + 1]))
 
     return _pool_map(one, heads)
+
+
+# bf16 selection fixtures: inputs regenerated from their recipe (torch's CPU generator),
+# checked against the stored SHA-256 of their bits before use
+BF16_SELECT_SPECS = {
+    # name: (seed, lens, H, dh, extra hidden columns, k, w_max, heavy tails)
+    "b4_h8": (700, [1024, 1024, 1024, 1024], 8, 64, 256, 64, 256, False),
+    "h16": (701, [4096], 16, 64, 256, 128, 512, True),
+}
+
+
+def bf16_select_inputs(name: str):
+    """(x [T, H*dh + extra] bf16, alpha [H], w [T] float, cu [S+1] int32) of a bf16 selection
+    fixture: x = [v | h] with the value vectors v [T, H, dh] first, so x @ [I | 0]^T = v."""
+    seed, lens, H, dh, extra, k, wmax, heavy = BF16_SELECT_SPECS[name]
+    g = torch.Generator().manual_seed(seed)
+    T = sum(lens)
+    v = torch.randn(T, H, dh, generator=g)
+    hx = torch.randn(T, extra, generator=g)
+    if heavy:  # heavy tails from powers of two (exact on every CPU, unlike exp)
+        v = v * torch.exp2(torch.round(torch.randn(T, H, 1, generator=g) * 1.4427))
+        hx = hx * torch.exp2(torch.round(0.5 * torch.randn(T, 1, generator=g) * 1.4427))
+    x = torch.cat([v.reshape(T, H * dh), hx], 1).to(torch.bfloat16)
+    alpha = torch.full((H,), 0.5)
+    w = torch.round(torch.sigmoid(torch.randn(T, generator=g)) * wmax).clamp(16, wmax)
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    return x, alpha, w, cu
+
+
+def sha256_of(t: torch.Tensor) -> str:
+    import hashlib
+    return hashlib.sha256(t.contiguous().view(torch.int16).numpy().tobytes()).hexdigest()
+
+
+def topk_violations(idx, scores, w, cu, k):
+    """Checks that each set of ``idx`` [H, S, k] (ascending, -1 padded) is a top-k of
+    ``scores`` [T, H] over the set's candidates (tokens j with j - start >= w_j): returns
+    (number of sets with a violation, largest score gap max(unselected) - min(selected))."""
+    idx = np.asarray(idx)
+    scores = np.asarray(scores, np.float64)
+    w = np.asarray(w).astype(np.int64)
+    cu = np.asarray(cu).astype(np.int64)
+    bad, gap = 0, -np.inf
+    for h in range(idx.shape[0]):
+        for s in range(len(cu) - 1):
+            st, en = int(cu[s]), int(cu[s + 1])
+            rel = np.arange(en - st)
+            cand = rel[rel >= w[st:en]]
+            sel = idx[h, s][idx[h, s] >= 0]
+            if len(cand) <= k:
+                if not np.array_equal(np.sort(sel), cand):
+                    bad += 1
+                continue
+            if len(sel) != k or not np.isin(sel, cand).all():
+                bad += 1
+                continue
+            rest = np.setdiff1d(cand, sel)
+            g = scores[st + rest, h].max() - scores[st + sel, h].min()
+            gap = max(gap, g)
+            if g > 0:
+                bad += 1
+    return bad, gap

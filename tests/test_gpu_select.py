@@ -179,3 +179,21 @@ def test_block_pruned_block_sizes(block):
     idx, ridx = _run(h, v, alpha, w, cu, 32, ops.SELECT_BLOCK, block, ops.STATS_SEQUENCE, want=False,
                      border_cap=ops.SELECT_FORCE_PRUNE)
     np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
+@pytest.mark.parametrize("name", ["b4_h8", "h16"])
+def test_bf16_selection_against_the_reference_scores(name):
+    """The GPU's bf16 selection on the fixtures of the reference's own bf16 arithmetic:
+    bit-exact to the C oracle, and a top-k of the reference's scores in every set."""
+    from tests.helpers import BF16_SELECT_SPECS, bf16_select_inputs, load_golden, sha256_of, topk_violations
+    z = load_golden(f"select_bf16_{name}")
+    x, alpha, _, cu = bf16_select_inputs(name)
+    assert sha256_of(x) == str(z["x_sha256"])
+    w = torch.from_numpy(z["w"])
+    _, lens, H, dh, _, k, _, _ = BF16_SELECT_SPECS[name]
+    T = x.shape[0]
+    v = x[:, :H * dh].reshape(T, H, dh)
+    idx, ridx = _run(x, v, alpha, w.int(), cu, k, ops.SELECT_GLOBAL, 512, ops.STATS_PACKED, want=False)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    bad, _ = topk_violations(idx.cpu().numpy()[:, :, 0], z["scores"], w, cu, k)
+    assert bad == 0

@@ -38,7 +38,7 @@ from oracle import select as OS
 from oracle import cross_entropy as OCE
 from oracle import rope as OR
 from oracle import train as OT
-from tests.helpers import load_golden, rel_err
+from tests.helpers import bits, load_golden, rel_err
 
 
 # ----------------------------------------------------------------- golden vectors
@@ -506,3 +506,35 @@ def test_ce_rows_match_torch(cw, ls, red, softcap, zs, scaling):
     keep = t != -100
     xs = softcap * np.tanh(x / softcap) if softcap else x
     assert np.all(am[keep] == xs[keep].argmax(1)) and np.all(am[~keep] == -1)
+
+
+# ---------------------------------------------------------------- bf16 selection pin
+# The reference's own bf16 path (bf16 norms, float32 statistics over the packed batch,
+# torch.topk) on workload-like shapes (tests/golden/select_bf16_*.npz): the oracle's canonical
+# arithmetic must choose a top-k of the reference's scores in every set.  Where the sets
+# differ, the differing tokens tie with the k-th score (bf16 norms collide often; torch.topk
+# breaks ties in its own order, the library by the lower index).
+@pytest.mark.parametrize("name", ["b4_h8", "h16"])
+def test_oracle_bf16_selection_is_a_top_k_of_the_reference_scores(name):
+    from tests.helpers import BF16_SELECT_SPECS, bf16_select_inputs, sha256_of, topk_violations
+    z = load_golden(f"select_bf16_{name}")
+    x, alpha, _, cu = bf16_select_inputs(name)
+    assert sha256_of(x) == str(z["x_sha256"]), "input recipe no longer reproduces the fixture's bits"
+    w = torch.from_numpy(z["w"])
+    _, _, H, dh, _, k, _, _ = BF16_SELECT_SPECS[name]
+    T = x.shape[0]
+    v = x[:, :H * dh].reshape(T, H, dh)
+    ridx = OS.select(bits(x), bits(v), alpha.numpy(), w.int().numpy(), cu.numpy(), k, OS.DTYPE_BF16,
+                     stats_scope=OS.STATS_PACKED)[:, :, 0]
+    bad, _ = topk_violations(ridx, z["scores"], w, cu, k)
+    assert bad == 0
+    sc = z["scores"]
+    cun = cu.numpy()
+    for hh in range(H):
+        for s in range(len(cun) - 1):
+            a, b = set(ridx[hh, s][ridx[hh, s] >= 0]), set(z["idx"][hh, s][z["idx"][hh, s] >= 0])
+            if a == b:
+                continue
+            st = int(cun[s])
+            kth = min(sc[st + j, hh] for j in b)
+            assert all(sc[st + j, hh] == kth for j in a ^ b), (hh, s)
