@@ -455,13 +455,13 @@ struct QLoader {
 // rows with lo_i > j0 + 63 are skipped.  List order is row order, so the sum
 // order is fixed and results are deterministic.
 // four waves per SIMD for 16-bit head_dim 64 (32-row stages keep it free of spills; three with
-// grouped heads, whose head loop needs more registers), two otherwise.
+// grouped heads or the training variant, which need more registers), two otherwise.
 // TR: training variant -- fully visible rows must also see every key of the block
 // past their edge_keys edge-bias keys; other rows add the soft edge bias.
 // GQA: the key/value head has several query heads (swept in order); without it the
 // sweep is straight-line code for one head.
 template <typename T, int D, bool TR, bool GQA>
-__global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (GQA ? 3 : 4) : 2) void bwd_dkdv_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3 : 4) : 2) void bwd_dkdv_kernel(AttnParams p) {
     constexpr int BQ = BwdShape<T, D>::BQ;
     constexpr int NQS = BQ / 16;
     constexpr int NDIAG = 64 / BQ;
@@ -471,6 +471,12 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (GQA ? 3 : 4) : 
     __shared__ __attribute__((aligned(16))) QS sq[2];
     __shared__ short lst[2][kSeg];
     __shared__ int wcnt[4][8];
+    // per-row data (window start, LSE in base 2, delta[, continuous window]) of the rows the
+    // current sweep stage covers (the diagonal rows, then one segment), filled once per stage
+    // so the chunk staging reads LDS instead of issuing dependent global loads
+    __shared__ int rt_lo[kSeg];
+    __shared__ float rt_l[kSeg], rt_d[kSeg];
+    __shared__ float rt_wt[TR ? kSeg : 1];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
     const int total = p.n_kv_heads * p.num_seqs * p.n_tiles;
@@ -514,15 +520,22 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (GQA ? 3 : 4) : 
     const T* db = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
     const float* lrow = p.lse2t + (int64_t)h * p.total_len + st;
     const float* drow = p.delta + (int64_t)h * p.total_len + st;
-    // per-row data of staged row i (or of no row when !ok)
-    auto stage_row = [&](QS& q, int r, int i, bool ok) {
+    // per-row table entry rr of rows base + rr (filled by the stage before its barrier)
+    auto fill_row = [&](int rr, int i) {
+        const int wi = max(wrow[i], 1);
+        rt_lo[rr] = max(i - wi + 1, 0);
+        rt_l[rr] = lrow[i];
+        rt_d[rr] = drow[i];
+        if (TR) rt_wt[rr] = p.w_cont[st + i];
+    };
+    // per-row data of staged row i = base + rr (or of no row when !ok), from the row table
+    auto stage_row = [&](QS& q, int r, int rr, int i, bool ok) {
         if (ok) {
-            const int wi = max(wrow[i], 1);
-            q.key[r] = max(i - wi + 1, 0);
-            q.lse2[r] = lrow[i];
-            q.dlt[r] = drow[i];
+            q.key[r] = rt_lo[rr];
+            q.lse2[r] = rt_l[rr];
+            q.dlt[r] = rt_d[rr];
             if (TR) {
-                q.wt[r] = p.w_cont[st + i];
+                q.wt[r] = rt_wt[rr];
                 q.ri[r] = i;
             }
         } else {
@@ -612,8 +625,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (GQA ? 3 : 4) : 
     rsrc_t rq, rd;
     ld.span(p, qb, db, j0, min(iend, j0 + 64), rq, rd);
     ld.load(rq, rd, 0);
+    if (tid < 64 && j0 + tid < iend) fill_row(tid, j0 + tid);
+    __syncthreads();
     ld.store(sq[0], tid);
-    if (tid < BQ) stage_row(sq[0], tid, j0 + tid, j0 + tid < iend);
+    if (tid < BQ) stage_row(sq[0], tid, tid, j0 + tid, j0 + tid < iend);
     __syncthreads();
     for (int c = 0; c < ndiag; ++c) {
         const int buf = c & 1;
@@ -621,8 +636,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (GQA ? 3 : 4) : 
         compute(sq[buf], 0, j0 + c * BQ);
         if (c + 1 < ndiag) {
             ld.store(sq[buf ^ 1], tid);
-            const int i = j0 + (c + 1) * BQ + tid;
-            if (tid < BQ) stage_row(sq[buf ^ 1], tid, i, i < iend);
+            const int rr = (c + 1) * BQ + tid;
+            if (tid < BQ) stage_row(sq[buf ^ 1], tid, rr, j0 + rr, j0 + rr < iend);
         }
         __syncthreads();
     }
@@ -637,7 +652,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (GQA ? 3 : 4) : 
             bool f = false, pp = false;
             if (r < nrows) {
                 const int i = seg + r;
-                const int lo = max(i - max(wrow[i], 1) + 1, 0);
+                fill_row(r, i);
+                const int lo = rt_lo[r];
                 f = lo <= j0 - (TR ? p.edge_keys : 0);
                 pp = !f && lo <= j0 + 63;
             }
@@ -694,7 +710,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (GQA ? 3 : 4) : 
                 const int idx = (full ? c : c - nfc) * BQ + tid;
                 const int n = full ? nf : np;
                 const bool ok = idx < n;
-                stage_row(q, tid, seg + (ok ? (int)lst[full ? 0 : 1][idx] : 0), ok);
+                const int rr = ok ? (int)lst[full ? 0 : 1][idx] : 0;
+                stage_row(q, tid, rr, seg + rr, ok);
             }
         };
         if (nc > 0) {
