@@ -61,10 +61,10 @@ __device__ __forceinline__ int lower_bound_i(const int* a, int n, int x) {
 
 // loads a landmark set into LDS; returns the number of valid (non -1) slots
 __device__ __forceinline__ int load_set(const AttnParams& p, int64_t set_off, int* lpos, int* nvalid_s, int tid,
-                                        float* lbs = nullptr) {
+                                        float* lbs = nullptr, int nthreads = 256) {
     if (tid == 0) *nvalid_s = 0;
     __syncthreads();
-    for (int i = tid; i < p.k_lmk; i += 256) {
+    for (int i = tid; i < p.k_lmk; i += nthreads) {
         int v = p.lmk[set_off + i];
         lpos[i] = v;
         if (v >= 0 && (i + 1 == p.k_lmk || p.lmk[set_off + i + 1] < 0)) *nvalid_s = i + 1;
@@ -379,9 +379,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
 // (base 2), delta, and a per-row key: the window start in the dK/dV sweep, the
 // visible landmark count in the landmark sweep (0 past the end).  Rows past
 // the end are zero with LSE 0 and delta 0, so they contribute exactly zero.
-template <typename T, int D, int BQ, bool TR = false>
+template <typename T, int D, int BQ, bool TR = false, int NT = 256>
 struct QStage {
-    typedef Tile<T, D, BQ> QT;
+    typedef Tile<T, D, BQ, NT> QT;
     T q[QT::ELEMS];
     T d[QT::ELEMS];
     float lse2[BQ];
@@ -391,9 +391,9 @@ struct QStage {
     int ri[TR ? BQ : 4];    // training variant: row index
 };
 
-template <typename T, int D, int BQ>
+template <typename T, int D, int BQ, int NT = 256>
 struct QLoader {
-    typedef Tile<T, D, BQ> QT;
+    typedef Tile<T, D, BQ, NT> QT;
     QT tq, tdo;
     uint32_t qoff[QT::NV], doff[QT::NV];
     uint32_t qrb, drb;
@@ -767,20 +767,23 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
 }
 
 // -------------------------------------------------------- landmark dK/dV
-// Block = (head, sequence, chunk c, group of 64*kLmkSub slots); wave w owns slots
-// grp*64*kLmkSub + 16*kLmkSub*w .. as kLmkSub 16-slot subtiles.  Chunk c takes the
-// BQ-row tiles c, c + n_chunks, c + 2 n_chunks, ... of the sequence: a row sees more
-// landmarks the later it is, so strided tiles give every block the same work (the
-// kernel lasts as long as its longest block).
-constexpr int kLmkSub = 1;
-constexpr int kLmkGroup = 64 * kLmkSub;
-
+// Block = (head, sequence, chunk c, group of 16*NW slots) with NW waves; wave w owns slots
+// grp*16*NW + 16*w .. +15.  Chunk c takes the BQ-row tiles c, c + n_chunks, c + 2 n_chunks,
+// ... of the sequence: a row sees more landmarks the later it is, so strided tiles give
+// every block the same work (the kernel lasts as long as its longest block).  Each row tile
+// is read from memory once per slot group: eight waves (128 slots) where a set has more
+// than 64 slots and the registers allow four waves per SIMD (16-bit, head_dim 64), else four.
 template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
+constexpr int lmk_waves(int k_lmk) { return (sizeof(T) == 2 && D == 64 && k_lmk > 64) ? 8 : 4; }
+
+template <typename T, int D, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void bwd_lmk_kernel(AttnParams p) {
+    constexpr int NT = 64 * NW;
+    constexpr int kLmkGroup = 16 * NW;
     constexpr int BQ = BwdShape<T, D>::BL;
     constexpr int NQS = BQ / 16;
     constexpr bool kHalf = sizeof(T) == 2;
-    typedef QStage<T, D, BQ> QS;
+    typedef QStage<T, D, BQ, false, NT> QS;
     typedef typename QS::QT QT;
     __shared__ __attribute__((aligned(16))) QS q;
     __shared__ int lpos[kMaxLandmarks];
@@ -803,10 +806,11 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     const int64_t set_off = (((int64_t)h * p.num_seqs + s) * p.n_sets) * K;
     const float c2 = p.c2;
     const float inv_scale = p.inv_scale;
-    const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid);
+    const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid, nullptr, NT);
 
-    // slots of this lane (kLmkSub subtiles)
-    const int sl0 = uniform(grp * kLmkGroup + wave * 16 * kLmkSub);
+    // slots of this lane
+    constexpr int kLmkSub = 1;
+    const int sl0 = uniform(grp * kLmkGroup + wave * 16);
     RowReg<T, D> kr[kLmkSub], vr[kLmkSub];
     int slot[kLmkSub];
     float bsl[kLmkSub];
@@ -844,14 +848,14 @@ __global__ __launch_bounds__(256, 2) void bwd_lmk_kernel(AttnParams p) {
     // the loop bound is uniform over the block (every wave reaches each barrier);
     // waves whose slots are all empty skip their products through act[] below
     const bool any_slot = grp * kLmkGroup < nvalid;
-    QLoader<T, D, BQ> ld(p, tid);
+    QLoader<T, D, BQ, NT> ld(p, tid);
     // rows staged in LDS; visible landmark counts come from the dQ pass
     for (int t = t0; any_slot && t < ntile; t += p.n_chunks) {
         const int i0 = t * BQ;
         {
-            rsrc_t rq, rd;
-            ld.span(p, qb, db, i0, min(len, i0 + BQ), rq, rd);
-            ld.load(rq, rd, 0);
+            rsrc_t rq, rdo;
+            ld.span(p, qb, db, i0, min(len, i0 + BQ), rq, rdo);
+            ld.load(rq, rdo, 0);
         }
         // per-row data loaded with the tile (one memory latency per tile)
         int c = 0;
@@ -1046,12 +1050,13 @@ hipError_t train_dw_launch(const AttnParams& p, hipStream_t stream) {
 
 // ---------------------------------------------------------------- launch
 // blocks of the landmark backward per (head, sequence, slot group): at most kRowChunk rows
-// each, and more (down to one 64-row tile each) until the launch has about four blocks per
-// CU, since a block's rows are one dependent chain of staged tiles
+// each, and more (down to one 64-row tile each) until the launch has about sixteen waves
+// per CU, since a block's rows are one dependent chain of staged tiles
 static int lmk_chunks(const AttnParams& p) {
-    const int ngrp = ceil_div(p.k_lmk, kLmkGroup);
+    const int nw = p.dtype != DSALT_DTYPE_F32 && p.head_dim == 64 && p.k_lmk > 64 ? 8 : 4;  // as lmk_waves
+    const int ngrp = ceil_div(p.k_lmk, 16 * nw);
     const int sets = max(1, p.n_heads * p.num_seqs * ngrp);
-    const int fill = ceil_div(1024, sets);
+    const int fill = ceil_div(4096 / nw, sets);
     const int rows = (p.variant & DSALT_VARIANT_LMK_SHORT) ? kRowChunk / 2 : kRowChunk;
     return max(ceil_div(p.max_seqlen, rows), min(fill, ceil_div(p.max_seqlen, 64)));
 }
@@ -1096,9 +1101,15 @@ static hipError_t bwd_run(const AttnParams& p, bool plan_given, hipStream_t stre
         else DSALT_LAUNCH("bwd_dkdv", (bwd_dkdv_kernel<T, D, false, false>), dim3(total_kv), dim3(256), 0, stream, p);
     }
     if (p.k_lmk > 0) {
-        const int ngrp = ceil_div(p.k_lmk, kLmkGroup);
-        DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D>), dim3(p.n_heads * p.num_seqs * p.n_chunks * ngrp), dim3(256),
-                     0, stream, p);
+        if (lmk_waves<T, D>(p.k_lmk) == 8) {
+            const int ngrp = ceil_div(p.k_lmk, 128);
+            DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D, 8>), dim3(p.n_heads * p.num_seqs * p.n_chunks * ngrp),
+                         dim3(512), 0, stream, p);
+        } else {
+            const int ngrp = ceil_div(p.k_lmk, 64);
+            DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D, 4>), dim3(p.n_heads * p.num_seqs * p.n_chunks * ngrp),
+                         dim3(256), 0, stream, p);
+        }
         const int64_t n = (int64_t)p.n_heads * p.num_seqs * p.k_lmk * D;
         DSALT_LAUNCH("bwd_lmk_sum", (bwd_lmk_sum_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                      stream, p);

@@ -53,12 +53,12 @@ __device__ __forceinline__ uint32_t gather_extent(int rows, uint32_t row_bytes, 
     return n <= 0x7fffffff ? (uint32_t)n : 0u;
 }
 
-template <typename T, int D, int ROWS>
+template <typename T, int D, int ROWS, int NT = 256>
 struct Tile {
     static constexpr int VW = 16 / (int)sizeof(T);  // elements per 16-byte vector
     static constexpr int CPR = D / VW;               // vectors per row
-    static constexpr int NV = ROWS * CPR / 256;      // vectors per thread (256 threads)
-    static_assert(ROWS * CPR % 256 == 0, "tile must split evenly over 256 threads");
+    static constexpr int NV = ROWS * CPR / NT;       // vectors per thread (NT threads)
+    static_assert(ROWS * CPR % NT == 0, "tile must split evenly over the block's threads");
     static constexpr int RS = D + Pad<T>::R;         // LDS row stride (elements)
     static constexpr int ELEMS = ROWS * RS;
     u4v r[NV];
@@ -68,7 +68,7 @@ struct Tile {
     __device__ __forceinline__ void load(int tid, RowFn row, const T* any_valid) {
 #pragma unroll
         for (int n = 0; n < NV; ++n) {
-            const int vi = tid + 256 * n, rr = vi / CPR, c = vi % CPR;
+            const int vi = tid + NT * n, rr = vi / CPR, c = vi % CPR;
             const T* src = row(rr);
             const bool ok = src != nullptr;
             u4v v = *(const u4v*)((ok ? src : any_valid) + c * VW);
@@ -77,7 +77,7 @@ struct Tile {
     }
     // byte offsets of this thread's vectors in a tile of consecutive rows
     __device__ __forceinline__ static uint32_t row_offset(int tid, int n, uint32_t row_bytes) {
-        const int vi = tid + 256 * n;
+        const int vi = tid + NT * n;
         return (uint32_t)(vi / CPR) * row_bytes + (uint32_t)(vi % CPR) * 16u;
     }
     // byte offsets of this thread's vectors for gathered rows of two tensors (row
@@ -88,7 +88,7 @@ struct Tile {
                                                           uint32_t (&o0)[NV], uint32_t (&o1)[NV]) {
 #pragma unroll
         for (int n = 0; n < NV; ++n) {
-            const int vi = tid + 256 * n, rr = vi / CPR, c = vi % CPR;
+            const int vi = tid + NT * n, rr = vi / CPR, c = vi % CPR;
             const int j = row(rr);
             o0[n] = j >= 0 ? (uint32_t)j * rb0 + (uint32_t)c * 16u : kNoRow;
             o1[n] = j >= 0 ? (uint32_t)j * rb1 + (uint32_t)c * 16u : kNoRow;
@@ -102,7 +102,7 @@ struct Tile {
     __device__ __forceinline__ void store(T* lds, int tid) const {
 #pragma unroll
         for (int n = 0; n < NV; ++n) {
-            const int vi = tid + 256 * n, rr = vi / CPR, c = vi % CPR;
+            const int vi = tid + NT * n, rr = vi / CPR, c = vi % CPR;
             *(u4v*)(lds + rr * RS + c * VW) = r[n];
         }
     }
