@@ -777,7 +777,7 @@ template <typename T, int D>
 constexpr int lmk_waves(int k_lmk) { return (sizeof(T) == 2 && D == 64 && k_lmk > 64) ? 8 : 4; }
 
 template <typename T, int D, int NW>
-__global__ __launch_bounds__(64 * NW, 2) void bwd_lmk_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * NW, (NW == 8 && sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_lmk_kernel(AttnParams p) {
     constexpr int NT = 64 * NW;
     constexpr int kLmkGroup = 16 * NW;
     constexpr int BQ = BwdShape<T, D>::BL;
@@ -849,23 +849,27 @@ __global__ __launch_bounds__(64 * NW, 2) void bwd_lmk_kernel(AttnParams p) {
     // waves whose slots are all empty skip their products through act[] below
     const bool any_slot = grp * kLmkGroup < nvalid;
     QLoader<T, D, BQ, NT> ld(p, tid);
-    // rows staged in LDS; visible landmark counts come from the dQ pass
-    for (int t = t0; any_slot && t < ntile; t += p.n_chunks) {
+    // row tile t (q, dO and per-row data) fetched into registers one tile ahead: its memory
+    // latency overlaps the products of the tile before
+    int c = 0;
+    float rl = 0.f, rd = 0.f;
+    auto fetch = [&](int t) {
         const int i0 = t * BQ;
-        {
-            rsrc_t rq, rdo;
-            ld.span(p, qb, db, i0, min(len, i0 + BQ), rq, rdo);
-            ld.load(rq, rdo, 0);
-        }
-        // per-row data loaded with the tile (one memory latency per tile)
-        int c = 0;
-        float rl = 0.f, rd = 0.f;
+        rsrc_t rq, rdo;
+        ld.span(p, qb, db, i0, min(len, i0 + BQ), rq, rdo);
+        ld.load(rq, rdo, 0);
+        c = 0;
+        rl = rd = 0.f;
         if (tid < BQ && i0 + tid < len) {
             const int64_t hr = (int64_t)h * p.total_len + st + i0 + tid;
             c = p.cnt[hr];
             rl = p.lse2t[hr];
             rd = p.delta[hr];
         }
+    };
+    if (any_slot && t0 < ntile) fetch(t0);
+    // rows staged in LDS; visible landmark counts come from the dQ pass
+    for (int t = t0; any_slot && t < ntile; t += p.n_chunks) {
         __syncthreads();
         ld.store(q, tid);
         if (tid < BQ) {
@@ -879,6 +883,7 @@ __global__ __launch_bounds__(64 * NW, 2) void bwd_lmk_kernel(AttnParams p) {
             }
         }
         __syncthreads();
+        if (t + p.n_chunks < ntile) fetch(t + p.n_chunks);
 #pragma unroll
         for (int u = 0; u < kLmkSub; ++u) {
             const int a = sl0 + u * 16;

@@ -516,10 +516,10 @@ struct KeyFn {
         if (block && pk) return packed(j, pk[(int64_t)rep_g * total_len + st + j]);
         if (j < w[st + j]) return 0ull;
         float zxj, zvj;
-        if (!block) {
+        if (zx) {
             zxj = zx[st + j];
             zvj = zv[(int64_t)rep_g * total_len + st + j];
-        } else {
+        } else {  // from the norms: zscore_rcp gives zscore's bits
             zxj = zscore_rcp(nx[st + j], mx, sx, rsx);
             zvj = zscore_rcp(nv[(int64_t)rep_g * total_len + st + j], mv, sv, rsv);
         }
@@ -734,7 +734,10 @@ __global__ __launch_bounds__(256) void sel_prune_list_kernel(SelectParams p, con
 constexpr int kPartMax = 2048;   // candidates per part (keys in LDS)
 constexpr int kMergeMax = 4096;  // keys per merge block
 
-__device__ __forceinline__ KeyFn global_key(const SelectParams& p, const float* zx, const float* zv, int st, int h) {
+// key of set (h, sequence s starting at st): z-scores from the norms and the range's
+// statistics (the same values sel_z stores)
+__device__ __forceinline__ KeyFn global_key(const SelectParams& p, const float* nx, const float* nv,
+                                            const double* stats, int s, int st, int h) {
     KeyFn key;
     key.w = p.w;
     key.total_len = p.total_len;
@@ -743,12 +746,21 @@ __device__ __forceinline__ KeyFn global_key(const SelectParams& p, const float* 
     key.rep_g = h / (p.n_heads / p.n_kv_heads);
     key.alpha = p.alpha[h];
     key.block = false;
-    key.zx = zx;
-    key.zv = zv;
-    key.nx = nullptr;
-    key.nv = nullptr;
+    key.zx = nullptr;
+    key.zv = nullptr;
+    key.nx = nx;
+    key.nv = nv;
     key.pk = nullptr;
-    key.mx = key.sx = key.mv = key.sv = 0.0;
+    const int nsig = 1 + p.n_kv_heads;
+    const int r = p.stats_scope == DSALT_STATS_PACKED ? 0 : s;
+    const double* sx = stats + (int64_t)r * nsig * 2;
+    const double* sv = stats + ((int64_t)r * nsig + 1 + key.rep_g) * 2;
+    key.mx = sx[0];
+    key.sx = sx[1];
+    key.mv = sv[0];
+    key.sv = sv[1];
+    key.rsx = __ddiv_rn(1.0, key.sx);
+    key.rsv = __ddiv_rn(1.0, key.sv);
     return key;
 }
 
@@ -774,8 +786,8 @@ __device__ void keep_largest(KthShared& sh, const unsigned long long* a, int n, 
 // (zero keys where it has fewer)
 constexpr int kSortThreads = kSelThreads;
 
-__global__ __launch_bounds__(kSortThreads) void sel_part_kernel(SelectParams p, const float* zx, const float* zv,
-                                                                int psize, int nparts, int kpad,
+__global__ __launch_bounds__(kSortThreads) void sel_part_kernel(SelectParams p, const float* nx, const float* nv,
+                                                                const double* stats, int psize, int nparts, int kpad,
                                                                 unsigned long long* out) {
     __shared__ KthShared sh;
     __shared__ unsigned long long keys[kPartMax];
@@ -784,7 +796,7 @@ __global__ __launch_bounds__(kSortThreads) void sel_part_kernel(SelectParams p, 
     const int s = sidx % p.num_seqs, h = sidx / p.num_seqs;
     int st, len;
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
-    const KeyFn key = global_key(p, zx, zv, st, h);
+    const KeyFn key = global_key(p, nx, nv, stats, s, st, h);
     const int j0 = part * psize;
     const int n = max(0, min(psize, len - j0));
     for (int i = tid; i < n; i += kSortThreads) keys[i] = key(j0 + i);
@@ -1243,8 +1255,10 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
         DSALT_LAUNCH("sel_sums", sel_sums_kernel, dim3(nranges, nsig), dim3(256), 0, stream, p, nx, nv, sums,
                      global ? stats : nullptr);
         if (global) {
-            DSALT_LAUNCH("sel_z", sel_z_kernel, dim3(ceil_div(p.max_seqlen, 256), p.num_seqs, nsig), dim3(256), 0,
-                         stream, p, nx, nv, stats, zx, zv);
+            // z-scores are stored only for the caller (the selection recomputes them from the norms)
+            if (p.z_x || p.z_v)
+                DSALT_LAUNCH("sel_z", sel_z_kernel, dim3(ceil_div(p.max_seqlen, 256), p.num_seqs, nsig), dim3(256), 0,
+                             stream, p, nx, nv, stats, zx, zv);
             if (p.scores)
                 DSALT_LAUNCH("sel_scores", sel_scores_kernel, dim3(ceil_div(p.max_seqlen, 256), p.num_seqs),
                              dim3(256), 0, stream, p, nx, nv, stats);
@@ -1284,8 +1298,8 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
     const size_t kb = align256(sizeof(unsigned long long) * (size_t)nsets_total * t.nparts * t.kpad);
     unsigned long long* ka = (unsigned long long*)w;
     unsigned long long* kb2 = (unsigned long long*)(w + kb);
-    DSALT_LAUNCH("sel_part", sel_part_kernel, dim3(nsets_total * t.nparts), dim3(kSortThreads), 0, stream, p, zx, zv,
-                 t.psize, t.nparts, t.kpad, ka);
+    DSALT_LAUNCH("sel_part", sel_part_kernel, dim3(nsets_total * t.nparts), dim3(kSortThreads), 0, stream, p, nx, nv,
+                 stats, t.psize, t.nparts, t.kpad, ka);
     // keys per merge block <= kMergeMax
     auto merge = [&](int nin, unsigned long long* out, int nout) {
         DSALT_LAUNCH("sel_merge", sel_merge_kernel, dim3(nsets_total * nout), dim3(kSortThreads), 0, stream, p, ka,
