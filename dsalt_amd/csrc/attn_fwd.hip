@@ -151,9 +151,10 @@ __device__ __forceinline__ int group_of(int w, int u) {
     return RG == 1 ? w : 4 * u + (u & 1 ? 3 - w : w);
 }
 
-// Fills the lane's row of block group G (0 .. 4*RG-1) from the row plan.
+// Fills the lane's row of block group G (0 .. 4*RG-1) from the row plan (everything but
+// the visible landmark counts, which need the block's landmark set in LDS).
 __device__ __forceinline__ void plan_group(const AttnParams& p, int64_t tile0, int ntl, int G, int r0, int st,
-                                           int len, const int* lpos, int nvalid, int lane, RowGroup& rg) {
+                                           int len, int lane, RowGroup& rg) {
     rg.i = -1;
     rg.lo = 0x7fffffff;
     rg.hi = -1;
@@ -177,12 +178,16 @@ __device__ __forceinline__ void plan_group(const AttnParams& p, int64_t tile0, i
             const int wi = max(p.w[st + rg.i], 1);
             rg.lo = max(rg.i - wi + 1, 0);
             rg.hi = rg.i;
-            rg.cnt = lower_bound_lds(lpos, nvalid, rg.lo);
             if (p.w_cont) rg.wt = p.w_cont[st + rg.i];
             rg.lou = rg.i - (wi - 1);
         }
     }
     if (p.w_cont) edge_table(p, rg.wt, rg.eb, nullptr);
+}
+
+// The group's visible landmark counts (the set's positions in LDS).
+__device__ __forceinline__ void plan_counts(const int* lpos, int nvalid, RowGroup& rg) {
+    rg.cnt = rg.valid ? lower_bound_lds(lpos, nvalid, rg.lo) : 0;
     rg.wcmax = uniform(row_max16(rg.cnt));
     rg.wcmin = uniform(row_min16(rg.valid ? rg.cnt : 0));
 }
@@ -222,7 +227,6 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     // block scalars live in the second K buffer until the first chunk is staged there
     // (keeps the block at 40 KB of LDS: four blocks per CU)
     int* red = (int*)Ks[1];
-    int& nvalid_s = red[4];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
     const int nblk = ceil_div(p.n_tiles, RG);
@@ -243,16 +247,18 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     const float inv_scale = p.inv_scale;
     const bool has_bias = p.lbias != nullptr;
 
-    if (tid == 0) nvalid_s = 0;
-    __syncthreads();
+    // Prologue: the loads that depend on no other load -- the landmark set, the row plan and,
+    // through it, the block's query rows and windows -- are all issued before the first
+    // barrier, and the first landmark chunk right after it, so a block waits for about two
+    // memory latencies before its first products.
+    int nv_loc = 0;  // one past the last valid slot (sets are ascending, -1 after the valid slots)
     for (int i = tid; i < K; i += 256) {
-        int v = p.lmk[set_off + i];
+        const int v = p.lmk[set_off + i];
+        const int vn = i + 1 < K ? p.lmk[set_off + i + 1] : -1;
         lpos[i] = v;
-        if (v >= 0 && (i + 1 == K || p.lmk[set_off + i + 1] < 0)) nvalid_s = i + 1;
+        if (v >= 0 && vn < 0) nv_loc = i + 1;
         if (has_bias) lbs[i] = p.lbias[set_off + i] * inv_scale;  // raw-score units
     }
-    __syncthreads();
-    const int nvalid = nvalid_s;
 
     // row groups of this wave and block-wide key range, from the row plan
     const int uw = uniform(wave);
@@ -266,23 +272,17 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     blo = uniform(blo);
     bhi = uniform(bhi);
     RowGroup rg[RG];
-    int wcm = 0;
 #pragma unroll
-    for (int u = 0; u < RG; ++u) {
-        plan_group(p, tile0, ntl, group_of<RG>(uw, u), r0, st, len, lpos, nvalid, lane, rg[u]);
-        wcm = max(wcm, rg[u].wcmax);
-    }
-    if (lane == 0) red[uw] = wcm;
-    __syncthreads();
-    const int bcm = uniform(max(max(red[0], red[1]), max(red[2], red[3])));
-    const int cs = (blo / BN) * BN;
-    const int nband = bhi >= blo ? (bhi - cs) / BN + 1 : 0;
-    const int nchunks = nband + ceil_div(bcm, BN);
-
+    for (int u = 0; u < RG; ++u) plan_group(p, tile0, ntl, group_of<RG>(uw, u), r0, st, len, lane, rg[u]);
     const T* qhead = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
     RowReg<T, D> qr[RG];
 #pragma unroll
     for (int u = 0; u < RG; ++u) qr[u].load(rg[u].valid ? qhead + (int64_t)rg[u].i * p.q_st : nullptr, qhead, g);
+
+    nv_loc = wave_max(nv_loc);
+    if (lane == 0) red[4 + uw] = nv_loc;
+    __syncthreads();
+    const int nvalid = uniform(max(max(red[4], red[5]), max(red[6], red[7])));
 
     const T* kbase = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)kvh * p.k_sh;
     const T* vbase = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)kvh * p.v_sh;
@@ -302,24 +302,13 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
     const bool lmk32 = (D == 64 || sizeof(T) == 2) && kext != 0u && vext != 0u;
     const rsrc_t krs = make_rsrc(kbase, kext), vrs = make_rsrc(vbase, vext);
     KT kt, vt;
-    // band rows [cs, bhi]: one resource per tensor over the whole band (rows past bhi read
-    // zero); band chunks are loaded in order, the per-thread offsets advancing one chunk per load
-    const int brows = nband > 0 ? bhi + 1 - cs : 0;
-    const rsrc_t kband = rows_rsrc(kbase + (int64_t)cs * p.k_st, brows, krb, D * sizeof(T));
-    const rsrc_t vband = rows_rsrc(vbase + (int64_t)cs * p.v_st, brows, vrb, D * sizeof(T));
-    auto load_band = [&]() {
-        kt.load_rows(kband, koff);
-        vt.load_rows(vband, voff);
-#pragma unroll
-        for (int n = 0; n < KT::NV; ++n) {
-            koff[n] += (uint32_t)BN * krb;
-            voff[n] += (uint32_t)BN * vrb;
-        }
-    };
-    auto load_lmk = [&](int c) {  // landmark chunk c (slots c*BN ..)
+    // landmark chunk c: slots c*BN .. below `lim` (slots past the block's largest count are
+    // masked out of every product, so the first chunk, fetched before that count is known,
+    // may take them from the set unmasked)
+    auto load_lmk_lim = [&](int c, int lim) {
         auto pos = [&](int rr) -> int {
             const int sl = c * BN + rr;
-            const int q = sl < bcm ? lpos[sl] : -1;
+            const int q = sl < lim ? lpos[sl] : -1;
             return q < len ? q : -1;
         };
         if (lmk32) {
@@ -334,11 +323,40 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
                     vbase);
         }
     };
+    if (nvalid > 0) load_lmk_lim(0, nvalid);
+
+    int wcm = 0;
+#pragma unroll
+    for (int u = 0; u < RG; ++u) {
+        plan_counts(lpos, nvalid, rg[u]);
+        wcm = max(wcm, rg[u].wcmax);
+    }
+    if (lane == 0) red[uw] = wcm;
+    __syncthreads();
+    const int bcm = uniform(max(max(red[0], red[1]), max(red[2], red[3])));
+    const int cs = (blo / BN) * BN;
+    const int nband = bhi >= blo ? (bhi - cs) / BN + 1 : 0;
+    const int nchunks = nband + ceil_div(bcm, BN);
+
+    // band rows [cs, bhi]: one resource per tensor over the whole band (rows past bhi read
+    // zero); band chunks are loaded in order, the per-thread offsets advancing one chunk per load
+    const int brows = nband > 0 ? bhi + 1 - cs : 0;
+    const rsrc_t kband = rows_rsrc(kbase + (int64_t)cs * p.k_st, brows, krb, D * sizeof(T));
+    const rsrc_t vband = rows_rsrc(vbase + (int64_t)cs * p.v_st, brows, vrb, D * sizeof(T));
+    auto load_band = [&]() {
+        kt.load_rows(kband, koff);
+        vt.load_rows(vband, voff);
+#pragma unroll
+        for (int n = 0; n < KT::NV; ++n) {
+            koff[n] += (uint32_t)BN * krb;
+            voff[n] += (uint32_t)BN * vrb;
+        }
+    };
+    auto load_lmk = [&](int c) { load_lmk_lim(c, bcm); };
     // landmark chunks first (their gathers only in the first loop), then the band
     const int nlmk = nchunks - nband;
     if (nchunks > 0) {
-        if (nlmk > 0) load_lmk(0);
-        else load_band();
+        if (nlmk == 0) load_band();  // else the first landmark chunk is in flight
         kt.store(Ks[0], tid);
         vt.store(Vs[0], tid);
     }

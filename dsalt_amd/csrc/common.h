@@ -67,6 +67,13 @@ __device__ __forceinline__ int row_max16(int v) {
     return max(v, dpp_ror(v, 8));
 }
 
+// maximum over the wave (every lane gets it)
+__device__ __forceinline__ int wave_max(int v) {
+    const int m = row_max16(v);
+    return max(max(__builtin_amdgcn_readlane(m, 0), __builtin_amdgcn_readlane(m, 16)),
+               max(__builtin_amdgcn_readlane(m, 32), __builtin_amdgcn_readlane(m, 48)));
+}
+
 // reductions over the 4 lanes l, l^16, l^32, l^48, with gfx950's lane-swap
 // instructions (VALU, no LDS round trip): permlane32_swap(x, x) yields the lower
 // and the upper 32 lanes each broadcast to both halves; permlane16_swap(y, y)
