@@ -71,7 +71,7 @@ def _candidate_configs(head_dim: int, device=None, elem_bytes: int = 2) -> list[
     return [_config_of(head_dim, elem_bytes, v) for v in variants]
 
 
-def _bench_step(run_fwd_bwd, n_warmup: int = 3, n_iter: int = 10) -> float:
+def _bench_step(run_fwd_bwd, n_warmup: int = 3, n_iter: int = 20) -> float:
     """Average time (ms) of one fwd+bwd step, timed with GPU events."""
     for _ in range(n_warmup):
         run_fwd_bwd()
@@ -85,30 +85,60 @@ def _bench_step(run_fwd_bwd, n_warmup: int = 3, n_iter: int = 10) -> float:
     return start.elapsed_time(end) / n_iter
 
 
-def autotune_blocks(head_dim: int, device, make_runner, verbose: bool = True, dtype=torch.bfloat16) -> dict:
+# a candidate replaces an earlier one (the heuristic first) only when it is faster by more
+# than this fraction: tilings that run the same kernels for a shape (e.g. the landmark-backward
+# chunking in a forward-only run) time alike, and the tie goes to the default
+_MARGIN = 0.015
+
+
+def autotune_blocks(head_dim: int, device, make_runner, verbose: bool = True, dtype=torch.bfloat16,
+                    rounds: int = 2) -> dict:
     """Time ``make_runner(cfg)()`` (one fwd+bwd with the config's tiling; ``None`` when the
-    config cannot run) for each candidate; cache and return the fastest config."""
+    config cannot run) for each candidate; cache and return the fastest config.  The GPU is
+    warmed up on the first candidate before any timing, and the candidates are timed
+    ``rounds`` times in rotated order, each keeping its best time."""
     key = _device_key(head_dim, device, dtype)
     if key in _TUNED_CONFIG:
         return _TUNED_CONFIG[key]
-    results = []
-    for cfg in _candidate_configs(head_dim, device, _elem_bytes(dtype)):
+    cands = _candidate_configs(head_dim, device, _elem_bytes(dtype))
+    runners, errors = [], {}
+    for cfg in cands:
         runner = make_runner(cfg)
+        runners.append(runner)
         if runner is None:
-            results.append((cfg, None, "skip"))
-            continue
-        try:
-            results.append((cfg, _bench_step(runner), None))
-        except Exception as e:  # a candidate that cannot run is skipped
-            results.append((cfg, None, type(e).__name__))
-    valid = [(c, t) for c, t, _ in results if t is not None]
-    best = min(valid, key=lambda r: r[1])[0] if valid else _heuristic_config(head_dim, device, _elem_bytes(dtype))
+            errors[cfg["variant"]] = "skip"
+    best_ms = {}
+    warm = False
+    for r in range(max(1, rounds)):
+        order = list(range(len(cands)))
+        order = order[r % len(order):] + order[:r % len(order)]
+        for i in order:
+            cfg, runner = cands[i], runners[i]
+            if runner is None or cfg["variant"] in errors:
+                continue
+            try:
+                if not warm:  # clocks up before the first timed candidate
+                    _bench_step(runner, n_warmup=10, n_iter=1)
+                    warm = True
+                ms = _bench_step(runner)
+            except Exception as e:  # a candidate that cannot run is skipped
+                errors[cfg["variant"]] = type(e).__name__
+                continue
+            best_ms[cfg["variant"]] = min(ms, best_ms.get(cfg["variant"], float("inf")))
+    best = None
+    for cfg in cands:  # candidate order: the heuristic first
+        ms = best_ms.get(cfg["variant"])
+        if ms is not None and (best is None or ms < best_ms[best["variant"]] * (1.0 - _MARGIN)):
+            best = cfg
+    if best is None:
+        best = _heuristic_config(head_dim, device, _elem_bytes(dtype))
     _TUNED_CONFIG[key] = best
     if verbose:
         print(f"dsalt autotune head_dim={head_dim} ({key[2]}, {key[1]}-byte elements)")
-        for cfg, ms, err in results:
+        for cfg in cands:
             mark = "  <- best" if cfg is best else ""
-            t = f"{ms:.4f} ms/step" if ms is not None else err
+            ms = best_ms.get(cfg["variant"])
+            t = f"{ms:.4f} ms/step" if ms is not None else errors.get(cfg["variant"], "skip")
             print(f"  variant {cfg['variant']:2d}  BLOCK_M {cfg['BLOCK_M']:3d} BLOCK_N {cfg['BLOCK_N']:2d} "
                   f"BLOCK_N_BWD {cfg['BLOCK_N_BWD']:2d} LMK_ROWS {cfg['LMK_ROWS']:4d}  {t}{mark}")
     return best
@@ -127,19 +157,24 @@ def tuned_variant(head_dim: int, device, dtype) -> int:
     return int(cfg["variant"]) if cfg else 0
 
 
-def operator_runner(q, k, v, w, cu_seqlens, lmk_idx, dout, *, max_seqlen=None):
+def operator_runner(q, k, v, w, cu_seqlens, lmk_idx, dout, *, max_seqlen=None, select_mode=None, block_size=None):
     """``make_runner`` for autotune_blocks over the operator's own fwd+bwd on the given
-    tensors (indices [H, S, 1, k] ascending, as ops.select_landmarks returns)."""
+    tensors (indices [H, S, n_sets, k] ascending, as ops.select_landmarks returns); with
+    ``dout=None`` the forward alone (inference configurations, block-causal sets)."""
     from .. import ops
+
+    mode = ops.SELECT_GLOBAL if select_mode is None else select_mode
+    bs = block_size or 512
 
     def make_runner(cfg):
         variant = cfg["variant"]
 
         def run():
-            plan = ops.new_plan(q, k, cu_seqlens, lmk_idx, max_seqlen=max_seqlen)
-            out, lse = ops.attention_forward(q, k, v, w, cu_seqlens, lmk_idx, None, max_seqlen=max_seqlen, plan=plan,
-                                             variant=variant)
-            ops.attention_backward(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, None, max_seqlen=max_seqlen,
-                                   want_dbias=False, plan=plan, variant=variant)
+            plan = ops.new_plan(q, k, cu_seqlens, lmk_idx, max_seqlen=max_seqlen, select_mode=mode, block_size=bs)
+            out, lse = ops.attention_forward(q, k, v, w, cu_seqlens, lmk_idx, None, max_seqlen=max_seqlen,
+                                             select_mode=mode, block_size=bs, plan=plan, variant=variant)
+            if dout is not None:
+                ops.attention_backward(dout, q, k, v, out, lse, w, cu_seqlens, lmk_idx, None, max_seqlen=max_seqlen,
+                                       want_dbias=False, plan=plan, variant=variant)
         return run
     return make_runner
