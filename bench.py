@@ -61,7 +61,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="fwdbwd_bf16_h16_l32768")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--variant", type=int, default=0, help="tile variant bits (DSALT_VARIANT_*) of the attention kernels")
+    ap.add_argument("--variant", default="auto",
+                    help="tile variant bits (DSALT_VARIANT_*) of the attention kernels, or 'auto': the autotune's "
+                         "winner for the workload's shape (timed before the warmup, outside the timed region)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy (negate) a MIB-MiB device buffer five times (HBM counter calibration) and exit")
     ap.add_argument("--traffic-from", metavar="DIR",
@@ -474,6 +476,20 @@ def main():
             return idx
     else:
         plan = None
+        variant = 0 if args.variant == "auto" else int(args.variant)
+        if args.variant == "auto":
+            # the reference's flow: tile sizes autotuned once per shape, then used by every call
+            import contextlib
+
+            from dsalt_amd.kernels import autotune as AT
+            idx0 = ops.select_landmarks(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, max_seqlen=maxlen,
+                                        select_mode=mode, block_size=wl.block_size, stats_scope=scope)
+            runner = AT.operator_runner(x["q"], x["k"], x["v"], x["w"], x["cu"], idx0,
+                                        x["dout"] if wl.backward else None, max_seqlen=maxlen, select_mode=mode,
+                                        block_size=wl.block_size)
+            with contextlib.redirect_stdout(sys.stderr):
+                variant = AT.autotune_blocks(D, dev, runner, verbose=True, dtype=x["q"].dtype)["variant"]
+            del idx0
 
         def step():
             nonlocal plan
@@ -483,10 +499,10 @@ def main():
                 plan = ops.new_plan(x["q"], x["k"], x["cu"], idx, max_seqlen=maxlen)
             out, lse = ops.attention_forward(x["q"], x["k"], x["v"], x["w"], x["cu"], idx, None, max_seqlen=maxlen,
                                              select_mode=mode, block_size=wl.block_size, plan=plan,
-                                             variant=args.variant)
+                                             variant=variant)
             if wl.backward:
                 ops.attention_backward(x["dout"], x["q"], x["k"], x["v"], out, lse, x["w"], x["cu"], idx, None,
-                                       max_seqlen=maxlen, want_dbias=False, plan=plan, variant=args.variant)
+                                       max_seqlen=maxlen, want_dbias=False, plan=plan, variant=variant)
             return idx
 
     idx = step()
@@ -601,7 +617,7 @@ def main():
                    "hidden": wl.hidden, "w_max": wl.w_max, "k_lmk": wl.k_lmk, "select": wl.select_mode,
                    "backward": wl.backward, "pairs": pairs,
                    **({"variant": "train", "tau_win": wl.tau_win, "win_edge": wl.win_edge, "tau_lmk": wl.tau_lmk}
-                      if wl.train else {})},
+                      if wl.train else {"tiling_variant": variant})},
         "roofline": roof,
         "step_roofline": {"bound": "hbm" if step_bytes / HBM_PEAK_GBS >= step_flops / (MFMA_PEAK_TFLOPS[dtn] * 1e3)
                           else "mfma", "t_roof_ms": round(t_roof * 1e3, 4),

@@ -208,6 +208,8 @@ __device__ __forceinline__ void band_edge(const AttnParams& p, const RowGroup& R
 }
 
 // One 256-thread block (4 waves) owns 64*RG query rows of one (head, sequence),
+// (two 16-row groups with 32-key chunks, 16-bit head_dim 64: held at four waves per SIMD, 128
+// VGPRs; the K and V^T operands of a chunk serve both groups of a wave)
 // taken in the row plan's order; wave w owns the 16-row groups RG*w .. RG*w+RG-1
 // (each lane one query row per group).  The K and V^T operands fetched from
 // LDS for a subtile serve all of a wave's groups.
@@ -216,7 +218,7 @@ __device__ __forceinline__ void band_edge(const AttnParams& p, const RowGroup& R
 // edge bias (edge_bias), so chunks classed "every row sees every key" must also
 // lie past every row's first edge_keys band keys.
 template <typename T, int D, int BN, int RG, bool TR>
-__global__ __launch_bounds__(256, 2) void fwd_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN == 32) ? 4 : 2) void fwd_kernel(AttnParams p) {
     constexpr int NST = BN / 16;
     constexpr bool kHalf = sizeof(T) == 2;
     typedef Tile<T, D, BN> KT;

@@ -67,10 +67,16 @@ def test_autotune_caches_and_the_operator_uses_the_winner():
             return base(cfg)
 
         best = AT.autotune_blocks(64, DEV, make_runner, verbose=False, dtype=torch.bfloat16)
-        assert sorted(calls) == sorted(c["variant"] for c in AT._candidate_configs(64, DEV, 2))
-        assert best in AT._candidate_configs(64, DEV, 2)
+        cands = AT._candidate_configs(64, DEV, 2)
+        assert sorted(calls) == sorted(c["variant"] for c in cands)
+        # forward and backward tilings are chosen separately: the winner takes its forward bits
+        # from one candidate and its backward bits from another
+        fwd_bits = {c["variant"] & AT._FWD_BITS for c in cands}
+        bwd_bits = {c["variant"] & AT._BWD_BITS for c in cands}
+        assert best["variant"] & AT._FWD_BITS in fwd_bits and best["variant"] & AT._BWD_BITS in bwd_bits
+        assert best == AT._config_of(64, 2, best["variant"])
         again = AT.autotune_blocks(64, DEV, make_runner, verbose=False, dtype=torch.bfloat16)
-        assert again is best and len(calls) == len(AT._candidate_configs(64, DEV, 2))  # cache hit
+        assert again is best and len(calls) == len(cands)  # cache hit
         assert AT.get_tuned_config(64, DEV, torch.bfloat16) is best
         assert AT.tuned_variant(64, DEV, torch.bfloat16) == best["variant"]
         # the autograd operator runs with the cached variant and still computes the operator
@@ -85,6 +91,25 @@ def test_autotune_caches_and_the_operator_uses_the_winner():
         assert rel_err(f64(out), ro) < 2e-2
         for a, b in zip((qq.grad, kk.grad, vv.grad), rg[:3]):
             assert rel_err(f64(a), b) < 2e-2
+    finally:
+        AT._TUNED_CONFIG.clear()
+        AT._TUNED_CONFIG.update(saved)
+
+
+def test_autotune_with_a_plain_runner_times_whole_steps():
+    q, k, v, w, cu, idx, maxlen, do = _case(torch.bfloat16, 64, seed=62)
+    dev = [t.to(DEV) for t in (q, k, v, w, cu, idx, do)]
+    saved = dict(AT._TUNED_CONFIG)
+    AT._TUNED_CONFIG.clear()
+    try:
+        base = AT.operator_runner(*dev[:6], dev[6], max_seqlen=maxlen)
+
+        def make_runner(cfg):
+            r = base(cfg)
+            return lambda: r()  # no .forward / .backward
+
+        best = AT.autotune_blocks(64, DEV, make_runner, verbose=False, dtype=torch.bfloat16)
+        assert best in AT._candidate_configs(64, DEV, 2)
     finally:
         AT._TUNED_CONFIG.clear()
         AT._TUNED_CONFIG.update(saved)
