@@ -8,7 +8,7 @@
 
 namespace dsalt {
 
-constexpr int kNoOwner = 0x7fffffff;  // lmk_owner of a row that is no landmark
+constexpr int kNoOwner = 0x7fffffff;  // owner of a key that is no landmark row
 
 struct AttnParams {
     int total_len, num_seqs, max_seqlen, n_heads, n_kv_heads, head_dim, k_lmk;
@@ -56,13 +56,11 @@ struct AttnParams {
     float* delta;            // [H, T] rowsum(O * dO), head-major (written by the dQ pass)
     int* cnt;                // [H, T] landmarks visible to each row (written by the dQ pass)
     float* lse2t;            // [H, T] LSE * log2(e), head-major (written by the dQ pass)
-    int* seq_wmax;           // [S] max clamped window per sequence
     float* part_k;           // [n_chunks, H, S, K, D] landmark dK partials
     float* part_v;           // [n_chunks, H, S, K, D]
     float* part_b;           // [n_chunks, H, S, K]
-    float* lmk_stage;        // [2, H, S, K, D] fp32 band dK / dV of landmark rows (dK/dV pass)
-    int* lmk_owner;          // [n_kv, T] h * K + slot of the first (head, slot) of the key/value
-                             // head's group holding the row as a landmark, kNoOwner elsewhere
+    float* lmk_stage;        // [2, H, S, K, D] fp32 band dK / dV of landmark rows (dK/dV pass), at
+                             // the row's owner: the first (head, slot) of its group holding it
     int n_chunks;            // row chunks of the landmark backward
 };
 

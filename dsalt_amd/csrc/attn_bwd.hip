@@ -3,16 +3,17 @@
 // Replaces _dsalt_bwd_preprocess and _dsalt_bwd_kernel
 // (dsalt/kernels/dsalt_triton_bwd.py:17-216), which accumulate dK/dV with
 // atomic_add.  Here every output element has exactly one writer:
-//   bwd_prep     clears the landmark-row owners and sets each sequence's
-//                largest window (from the forward's row plan when reused).
 //   bwd_dq       query-parallel, like the forward (64 rows per block, one row
 //                per lane): delta = rowsum(O dO) from the stored O (:44),
 //                dQ = scale * dS K over the band and the landmark slots
-//                (:148,:196); also records each 16-row tile's window-start
-//                range and the sequence's largest window for the sweep below.
+//                (:148,:196); also records each row's LSE, delta and visible
+//                landmark count for the passes below.
 //   bwd_dkdv     key-parallel over the band: 16 keys per wave, the query rows
 //                that can see them staged row-major in LDS (double-buffered);
-//                dV = P^T dO, dK = scale * dS^T Q (:198-199).
+//                dV = P^T dO, dK = scale * dS^T Q (:198-199); the rows to sweep end
+//                at the sequence's largest window (from the row plan's tile maxima),
+//                and a key that is a landmark row leaves its sums in fp32 for the
+//                landmark pass (its owner: the first (head, slot) of the group holding it).
 //   bwd_lmk      landmark slots x 1024-row chunks: partial dK/dV/d_bias of each
 //                (head, sequence, slot) (:150-155).
 //   bwd_lmk_sum  per landmark row: the band sums the dK/dV pass left in fp32
@@ -74,29 +75,6 @@ __device__ __forceinline__ int load_set(const AttnParams& p, int64_t set_off, in
     return *nvalid_s;
 }
 
-// Clears the landmark-row owners; per sequence, the largest window: from the forward's
-// row plan when it is reused (plan_given), else a start value that row_plan raises.
-__global__ __launch_bounds__(256) void bwd_prep_kernel(AttnParams p, int plan_given) {
-    if (p.lmk_owner) {
-        const int64_t n = (int64_t)p.n_kv_heads * p.total_len;
-        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
-            p.lmk_owner[i] = kNoOwner;
-    }
-    if ((int)blockIdx.x >= p.num_seqs) return;
-    const int s = blockIdx.x;
-    if (!plan_given) {
-        if (threadIdx.x == 0) p.seq_wmax[s] = 1;
-        return;
-    }
-    __shared__ int red[4];
-    int m = 1;
-    for (int t = threadIdx.x; t < p.n_tiles; t += 256) m = max(m, p.tile_wmax[(int64_t)s * p.n_tiles + t]);
-    for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) p.seq_wmax[s] = max(max(red[0], red[1]), max(red[2], red[3]));
-}
-
 // -------------------------------------------------------------------- dQ
 // TR: training variant -- band keys near the window start carry the soft edge bias,
 // and the lane also sums dS * d(bias)/d(w~) of its row into dw_h.
@@ -130,13 +108,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     const float inv_scale = p.inv_scale;
     const bool has_bias = p.lbias != nullptr;
     const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid, has_bias ? lbs : nullptr);
-    // landmark rows of this tile: the first (head, slot) of the group holding a row owns it
-    // (integer minimum: the same owner whatever the order of the updates)
-    if (p.lmk_owner)
-        for (int sl = tid; sl < nvalid; sl += 256) {
-            const int q = lpos[sl];
-            if (q >= r0 && q < min(r0 + 64, len)) atomicMin(p.lmk_owner + (int64_t)kvh * p.total_len + st + q, h * K + sl);
-        }
 
     // this wave's rows (ordered by window start) and their bounds, from the row plan
     const int uw = uniform(wave);
@@ -477,6 +448,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
     __shared__ int rt_lo[kSeg];
     __shared__ float rt_l[kSeg], rt_d[kSeg];
     __shared__ float rt_wt[TR ? kSeg : 1];
+    __shared__ int own_s[64];  // per key of the block: h * K + slot of its owner, or kNoOwner
+    __shared__ int wmax_s[4];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
     const int total = p.n_kv_heads * p.num_seqs * p.n_tiles;
@@ -501,7 +474,25 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
     kr.load(jvalid ? khead + (int64_t)j * p.k_st : nullptr, khead, g);
     vr.load(jvalid ? vhead + (int64_t)j * p.v_st : nullptr, vhead, g);
 
-    const int iend = uniform(min(len, j0 + 63 + p.seq_wmax[s]));
+    // The sequence's largest window, from the row plan's tile maxima, bounds the rows to
+    // sweep (known after the first barrier; the diagonal rows end at dend <= iend).  Keys of
+    // the block that are landmark rows get their owner: the first (head, slot) of the group
+    // holding the row (first copy of a repeated position, heads in order; an integer
+    // minimum over LDS atomics, so the same whatever their order), found while the first
+    // segment's rows load (or after the sweep when there is none).
+    const int dend = min(len, j0 + 64);
+    int iend = dend;
+    bool owners = p.k_lmk == 0;
+    auto find_owners = [&]() {
+        const int K = p.k_lmk;
+        for (int e = tid; e < rep * K; e += 256) {
+            const int hs = e / K, sl = e % K;
+            const int32_t* set = p.lmk + (((int64_t)(kvh * rep + hs) * p.num_seqs + s) * p.n_sets) * K;
+            const int v = set[sl];
+            if (v >= j0 && v < dend && (sl == 0 || set[sl - 1] != v)) atomicMin(own_s + (v - j0), (kvh * rep + hs) * K + sl);
+        }
+        owners = true;
+    };
     const int* wrow = p.w + st;
     QLoader<T, D, BQ> ld(p, tid);
     floatx4 adk[D / 16], adv[D / 16];
@@ -621,14 +612,22 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
     };
 
     // ---- diagonal rows j0 .. j0+63 (contiguous), double-buffered
-    const int ndiag = uniform(min(NDIAG, ceil_div(iend - j0, BQ)));
+    const int ndiag = uniform(min(NDIAG, ceil_div(dend - j0, BQ)));
     rsrc_t rq, rd;
-    ld.span(p, qb, db, j0, min(iend, j0 + 64), rq, rd);
+    ld.span(p, qb, db, j0, dend, rq, rd);
     ld.load(rq, rd, 0);
-    if (tid < 64 && j0 + tid < iend) fill_row(tid, j0 + tid);
+    if (tid < 64 && j0 + tid < dend) fill_row(tid, j0 + tid);
+    if (hh == 0) {  // loads in flight together with the diagonal rows'
+        if (tid < 64) own_s[tid] = kNoOwner;
+        int wm = 1;
+        for (int u = tid; u < p.n_tiles; u += 256) wm = max(wm, p.tile_wmax[(int64_t)s * p.n_tiles + u]);
+        wm = wave_max(wm);
+        if (lane == 0) wmax_s[wave] = wm;
+    }
     __syncthreads();
+    iend = uniform(min(len, j0 + 63 + max(max(wmax_s[0], wmax_s[1]), max(wmax_s[2], wmax_s[3]))));
     ld.store(sq[0], tid);
-    if (tid < BQ) stage_row(sq[0], tid, tid, j0 + tid, j0 + tid < iend);
+    if (tid < BQ) stage_row(sq[0], tid, tid, j0 + tid, j0 + tid < dend);
     __syncthreads();
     for (int c = 0; c < ndiag; ++c) {
         const int buf = c & 1;
@@ -637,7 +636,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
         if (c + 1 < ndiag) {
             ld.store(sq[buf ^ 1], tid);
             const int rr = (c + 1) * BQ + tid;
-            if (tid < BQ) stage_row(sq[buf ^ 1], tid, rr, j0 + rr, j0 + rr < iend);
+            if (tid < BQ) stage_row(sq[buf ^ 1], tid, rr, j0 + rr, j0 + rr < dend);
         }
         __syncthreads();
     }
@@ -667,6 +666,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
                 wcnt[wave][4 + u] = __popcll(bp[u]);
             }
         }
+        if (!owners) find_owners();
         __syncthreads();
         // list order: (u, wave, lane) = row order
         int nf = 0, np = 0, basef[kSeg / 256], basep[kSeg / 256];
@@ -728,11 +728,15 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
         }
     }
     }  // query heads of the group
+    if (!owners) {  // no row past the diagonal: the owners now
+        find_owners();
+        __syncthreads();
+    }
 
-    if (jvalid && p.lmk_owner) {
+    if (jvalid && p.k_lmk > 0) {
         // a landmark row: its band sums go to the landmark pass's final sum in fp32, which
         // rounds the total once (and writes the row)
-        const int own = p.lmk_owner[(int64_t)kvh * p.total_len + st + j];
+        const int own = own_s[j - j0];
         if (own != kNoOwner) {
             const int64_t so = (((int64_t)(own / p.k_lmk) * p.num_seqs + s) * p.k_lmk + own % p.k_lmk) * D;
             const int64_t half = (int64_t)p.n_heads * p.num_seqs * p.k_lmk * D;
@@ -1003,7 +1007,11 @@ __global__ __launch_bounds__(256) void bwd_lmk_sum_kernel(AttnParams p) {
         p.d_bias[(((int64_t)h * p.num_seqs + s) * p.n_sets) * K + sl] = sb;
     }
     if (pos < 0 || pos >= len) return;
-    if (p.lmk_owner[(int64_t)kvh * p.total_len + st + pos] != h * K + sl) return;
+    // only the owner of the row goes on: the first copy of the position in this set, and no
+    // earlier head of the group holding it
+    if (sl > 0 && set[sl - 1] == pos) return;
+    for (int hh = kvh * rep; hh < h; ++hh)
+        if (find_slot(p.lmk + (((int64_t)hh * p.num_seqs + s) * p.n_sets) * K, K, pos) >= 0) return;
     const int64_t half = (int64_t)p.n_heads * p.num_seqs * K * D;
     const int64_t so = prow(h, sl) * D + d;
     float sk = p.lmk_stage[so], sv = p.lmk_stage[half + so];
@@ -1073,11 +1081,9 @@ size_t bwd_workspace(const AttnParams& p) {
     b += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
     b += al(sizeof(int) * (size_t)p.total_len * p.n_heads);
     b += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
-    b += al(sizeof(int) * (size_t)p.num_seqs);
     b += 2 * al(sizeof(float) * (size_t)nch * p.n_heads * p.num_seqs * p.k_lmk * p.head_dim);
     b += al(sizeof(float) * (size_t)nch * p.n_heads * p.num_seqs * p.k_lmk);
     b += al(sizeof(float) * 2 * (size_t)p.n_heads * p.num_seqs * p.k_lmk * p.head_dim);
-    b += al(sizeof(int) * (size_t)p.n_kv_heads * p.total_len);
     return b;
 }
 
@@ -1085,9 +1091,6 @@ template <typename T, int D>
 static hipError_t bwd_run(const AttnParams& p, bool plan_given, hipStream_t stream) {
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
     const int total_kv = p.n_kv_heads * p.num_seqs * p.n_tiles;
-    const int64_t nown = p.lmk_owner ? (int64_t)p.n_kv_heads * p.total_len : 0;
-    const int nprep = max(p.num_seqs, (int)(nown < 262144 ? (nown + 255) / 256 : 1024));
-    DSALT_LAUNCH("bwd_prep", bwd_prep_kernel, dim3(nprep), dim3(256), 0, stream, p, plan_given ? 1 : 0);
     if (!plan_given) plan_launch(p, stream);
     constexpr int BN = BwdShape<T, D>::BN;
     const bool bn64 = sizeof(T) == 2 && D == 64 && (p.variant & DSALT_VARIANT_DQ_BN64);
@@ -1127,7 +1130,7 @@ hipError_t bwd_launch(AttnParams p, void* ws, const void* plan, hipStream_t stre
     p.n_chunks = lmk_chunks(p);
     char* w = (char*)ws;
     if (plan) {
-        char* pw = (char*)const_cast<void*>(plan);  // read only: bwd_prep and the kernels never write it
+        char* pw = (char*)const_cast<void*>(plan);  // read only: the kernels never write it
         plan_carve(p, pw);
         w += plan_bytes(p);
     } else {
@@ -1139,8 +1142,6 @@ hipError_t bwd_launch(AttnParams p, void* ws, const void* plan, hipStream_t stre
     w += al(sizeof(int) * (size_t)p.total_len * p.n_heads);
     p.lse2t = (float*)w;
     w += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
-    p.seq_wmax = (int*)w;
-    w += al(sizeof(int) * (size_t)p.num_seqs);
     const size_t npart = (size_t)p.n_chunks * p.n_heads * p.num_seqs * p.k_lmk;
     p.part_k = (float*)w;
     w += al(sizeof(float) * npart * p.head_dim);
@@ -1150,7 +1151,6 @@ hipError_t bwd_launch(AttnParams p, void* ws, const void* plan, hipStream_t stre
     w += al(sizeof(float) * npart);
     p.lmk_stage = (float*)w;
     w += al(sizeof(float) * 2 * (size_t)p.n_heads * p.num_seqs * p.k_lmk * p.head_dim);
-    p.lmk_owner = p.k_lmk > 0 ? (int*)w : nullptr;
     if (p.total_len == 0 || p.num_seqs == 0) return hipSuccess;
     const bool pg = plan != nullptr;
     if (p.dtype == DSALT_DTYPE_BF16) return p.head_dim == 64 ? bwd_run<bf16, 64>(p, pg, stream) : bwd_run<bf16, 128>(p, pg, stream);

@@ -49,9 +49,8 @@ __device__ __forceinline__ int lower_bound_lds(const int* a, int n, int x) {
 // rows past the end last), so the 16 rows a wave takes have close window
 // starts: the wave's key range [min lo, max i] and its count of masked
 // subtiles shrink.  Each 16-row group's {min lo, max lo, max i, min i} is
-// recorded, with the tile's largest clamped window, and, when seq_wmax is set,
-// the largest clamped window of each sequence (bounding the key-parallel
-// backward sweep).
+// recorded, with the tile's largest clamped window (whose maximum over a sequence
+// bounds the key-parallel backward sweep).
 __global__ __launch_bounds__(64) void row_plan_kernel(AttnParams p) {
     __shared__ int sp[64], slo[64];
     const int l = threadIdx.x;
@@ -104,7 +103,6 @@ __global__ __launch_bounds__(64) void row_plan_kernel(AttnParams p) {
     const int tm = max(max(__builtin_amdgcn_readlane(m, 0), __builtin_amdgcn_readlane(m, 16)),
                        max(__builtin_amdgcn_readlane(m, 32), __builtin_amdgcn_readlane(m, 48)));
     if (l == 0) p.tile_wmax[tile] = tm;
-    if (p.seq_wmax && l == 0 && tm > 0) atomicMax(p.seq_wmax + s, tm);
 }
 
 size_t plan_bytes(const AttnParams& p) {
@@ -641,7 +639,6 @@ hipError_t train_windows_launch(const AttnParams& p, int* w_int, hipStream_t str
 hipError_t fwd_launch(AttnParams p, void* ws, void* plan, hipStream_t stream) {
     char* w = (char*)(plan ? plan : ws);
     plan_carve(p, w);
-    p.seq_wmax = nullptr;
     if (p.dtype == DSALT_DTYPE_BF16) return fwd_dispatch<bf16>(p, stream);
     if (p.dtype == DSALT_DTYPE_F16) return fwd_dispatch<f16>(p, stream);
     return fwd_dispatch<float>(p, stream);
