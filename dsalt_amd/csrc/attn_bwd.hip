@@ -267,9 +267,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
                 } else {
                     // below every row's diagonal only the window start masks; the soft
                     // edge only reaches subtiles before lo_edge (wave-uniform tests)
+                    // key a + lane_off + r in [lo, hi] (hi ignored below every row's diagonal): one
+                    // unsigned compare of r - tl (a row past the end has lo > hi and fails it)
                     const bool upper = a + 15 > wHmin;
+                    const int x0 = a + lane_off - lo;
+                    const unsigned wd = upper ? (unsigned)hi - (unsigned)lo : 0x7fffffffu;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ci[r] = (r < tl || (upper && r > th)) ? NEG : 0.f;
+                    for (int r = 0; r < 4; ++r) ci[r] = (unsigned)(x0 + r) <= wd ? 0.f : NEG;
                     if (TR && a < lo_edge) {
                         if (p.edge_keys <= kEdgeTab) {
                             const int k0 = a + lane_off - lou;

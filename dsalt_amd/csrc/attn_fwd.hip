@@ -451,10 +451,14 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
 #pragma unroll
                 for (int stt = 0; stt < NST; ++stt) {
                     const int a = base + stt * 16;
-                    const int tl = R.lo - a - lane_off, th = R.hi - a - lane_off;
+                    const int tl = R.lo - a - lane_off;
+                    // key a + lane_off + r in [lo, hi]: one unsigned compare of r - tl against
+                    // hi - lo (a row past the end has lo > hi and fails it)
+                    const int x0 = a + lane_off - R.lo;
+                    const unsigned wd = (unsigned)R.hi - (unsigned)R.lo;
                     floatx4 ci;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ci[r] = (r < tl || r > th) ? NEG : 0.f;
+                    for (int r = 0; r < 4; ++r) ci[r] = (unsigned)(x0 + r) <= wd ? 0.f : NEG;
                     if (TR && a < R.wLmax + p.edge_keys) band_edge(p, R, a, lane_off, tl, true, ci);
                     KOp<T, D> ko;
                     ko.load(kl, KT::RS, stt * 16, lane);
@@ -471,9 +475,11 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
                     }
                     floatx4 ci;
                     if (band) {
-                        const int tl = R.lo - a - lane_off, th = R.hi - a - lane_off;
+                        const int tl = R.lo - a - lane_off;
+                        const int x0 = a + lane_off - R.lo;
+                        const unsigned wd = (unsigned)R.hi - (unsigned)R.lo;
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) ci[r] = (r < tl || r > th) ? NEG : 0.f;
+                        for (int r = 0; r < 4; ++r) ci[r] = (unsigned)(x0 + r) <= wd ? 0.f : NEG;
                         if (TR && a < R.wLmax + p.edge_keys) band_edge(p, R, a, lane_off, tl, true, ci);
                     } else {
                         // slots past the valid count are masked below (a + 15 < 512)
