@@ -219,7 +219,7 @@ template <typename T, int D, int BN, int RG, bool TR>
 __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN == 32) ? 4 : 2) void fwd_kernel(AttnParams p) {
     constexpr int NST = BN / 16;
     constexpr bool kHalf = sizeof(T) == 2;
-    typedef Tile<T, D, BN> KT;
+    typedef Tile<T, D, BN, 256, (BN == 64 ? 8 : Pad<T, D>::R)> KT;
     __shared__ __attribute__((aligned(16))) T Ks[2][KT::ELEMS];
     __shared__ __attribute__((aligned(16))) T Vs[2][KT::ELEMS];
     __shared__ int lpos[kMaxLandmarks];

@@ -24,10 +24,14 @@
 
 namespace dsalt {
 
-template <typename T> struct Pad;
-template <> struct Pad<bf16> { static constexpr int R = 8; };
-template <> struct Pad<f16> { static constexpr int R = 8; };
-template <> struct Pad<float> { static constexpr int R = 4; };
+// Row padding (elements) of an LDS tile.  16-bit head_dim 64 rows take 16 (160-byte rows:
+// both the row-operand and the transposed reads free of bank conflicts); head_dim 128 rows
+// and the forward's 64-key chunks take 8 (the 16-element padding would cost those blocks
+// a block per CU of LDS).
+template <typename T, int D> struct Pad { static constexpr int R = 8; };
+template <> struct Pad<bf16, 64> { static constexpr int R = 16; };
+template <> struct Pad<f16, 64> { static constexpr int R = 16; };
+template <int D> struct Pad<float, D> { static constexpr int R = 4; };
 
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
@@ -53,13 +57,13 @@ __device__ __forceinline__ uint32_t gather_extent(int rows, uint32_t row_bytes, 
     return n <= 0x7fffffff ? (uint32_t)n : 0u;
 }
 
-template <typename T, int D, int ROWS, int NT = 256>
+template <typename T, int D, int ROWS, int NT = 256, int PAD = Pad<T, D>::R>
 struct Tile {
     static constexpr int VW = 16 / (int)sizeof(T);  // elements per 16-byte vector
     static constexpr int CPR = D / VW;               // vectors per row
     static constexpr int NV = ROWS * CPR / NT;       // vectors per thread (NT threads)
     static_assert(ROWS * CPR % NT == 0, "tile must split evenly over the block's threads");
-    static constexpr int RS = D + Pad<T>::R;         // LDS row stride (elements)
+    static constexpr int RS = D + PAD;                // LDS row stride (elements)
     static constexpr int ELEMS = ROWS * RS;
     u4v r[NV];
 
