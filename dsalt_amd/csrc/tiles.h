@@ -24,13 +24,10 @@
 
 namespace dsalt {
 
-// Row padding (elements) of an LDS tile.  16-bit head_dim 64 rows take 16 (160-byte rows:
-// both the row-operand and the transposed reads free of bank conflicts); head_dim 128 rows
-// and the forward's 64-key chunks take 8 (the 16-element padding would cost those blocks
-// a block per CU of LDS).
-template <typename T, int D> struct Pad { static constexpr int R = 8; };
-template <> struct Pad<bf16, 64> { static constexpr int R = 16; };
-template <> struct Pad<f16, 64> { static constexpr int R = 16; };
+// Row padding (elements) of an LDS tile.  16-bit rows take 16 (160- / 288-byte rows: both
+// the row-operand and the transposed reads free of bank conflicts); the forward's and dQ's
+// 64-key chunks take 8 (the 16-element padding would cost those blocks a block per CU of LDS).
+template <typename T, int D> struct Pad { static constexpr int R = 16; };
 template <int D> struct Pad<float, D> { static constexpr int R = 4; };
 
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
