@@ -452,6 +452,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
     __shared__ int rt_lo[kSeg];
     __shared__ float rt_l[kSeg], rt_d[kSeg];
     __shared__ float rt_wt[TR ? kSeg : 1];
+    __shared__ int dt_lo[64];  // the same for the 64 diagonal rows
+    __shared__ float dt_l[64], dt_d[64];
+    __shared__ float dt_wt[TR ? 64 : 1];
     __shared__ int own_s[64];  // per key of the block: h * K + slot of its owner, or kNoOwner
     __shared__ int wmax_s[4];
 
@@ -482,21 +485,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
     // sweep (known after the first barrier; the diagonal rows end at dend <= iend).  Keys of
     // the block that are landmark rows get their owner: the first (head, slot) of the group
     // holding the row (first copy of a repeated position, heads in order; an integer
-    // minimum over LDS atomics, so the same whatever their order), found while the first
-    // segment's rows load (or after the sweep when there is none).
+    // minimum over LDS atomics, so the same whatever their order).
     const int dend = min(len, j0 + 64);
     int iend = dend;
-    bool owners = p.k_lmk == 0;
-    auto find_owners = [&]() {
-        const int K = p.k_lmk;
-        for (int e = tid; e < rep * K; e += 256) {
-            const int hs = e / K, sl = e % K;
-            const int32_t* set = p.lmk + (((int64_t)(kvh * rep + hs) * p.num_seqs + s) * p.n_sets) * K;
-            const int v = set[sl];
-            if (v >= j0 && v < dend && (sl == 0 || set[sl - 1] != v)) atomicMin(own_s + (v - j0), (kvh * rep + hs) * K + sl);
-        }
-        owners = true;
-    };
     const int* wrow = p.w + st;
     QLoader<T, D, BQ> ld(p, tid);
     floatx4 adk[D / 16], adv[D / 16];
@@ -507,6 +498,11 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
     }
     const float NEG = -INFINITY;
     const int lane_off = 4 * g;
+    const int seg0 = j0 + 64;  // first row after the diagonal
+    // one query head per key/value head: the first segment is prepared in the prologue and its
+    // first chunk fetched under the last diagonal stage; grouped heads (more registers live
+    // across the head loop) take every segment in the sweep after the diagonal
+    constexpr bool kPre = !GQA;
     // the query heads of this key/value head are swept one after the other (head order),
     // all adding into the same dK/dV registers
     for (int hh = 0; hh < rep; ++hh) {
@@ -515,22 +511,27 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
     const T* db = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
     const float* lrow = p.lse2t + (int64_t)h * p.total_len + st;
     const float* drow = p.delta + (int64_t)h * p.total_len + st;
-    // per-row table entry rr of rows base + rr (filled by the stage before its barrier)
-    auto fill_row = [&](int rr, int i) {
+    // row table entry rr of row i: window start, LSE, delta[, continuous window] (the
+    // diagonal rows have a table of their own, so the first segment's can be filled with it)
+    auto fill_row = [&](auto diag_tag, int rr, int i) -> int {
+        constexpr bool dg = decltype(diag_tag)::value;
         const int wi = max(wrow[i], 1);
-        rt_lo[rr] = max(i - wi + 1, 0);
-        rt_l[rr] = lrow[i];
-        rt_d[rr] = drow[i];
-        if (TR) rt_wt[rr] = p.w_cont[st + i];
+        const int lo = max(i - wi + 1, 0);
+        (dg ? dt_lo : rt_lo)[rr] = lo;
+        (dg ? dt_l : rt_l)[rr] = lrow[i];
+        (dg ? dt_d : rt_d)[rr] = drow[i];
+        if (TR) (dg ? dt_wt : rt_wt)[rr] = p.w_cont[st + i];
+        return lo;
     };
-    // per-row data of staged row i = base + rr (or of no row when !ok), from the row table
-    auto stage_row = [&](QS& q, int r, int rr, int i, bool ok) {
+    // per-row data of staged row i (table entry rr), or of no row when !ok
+    auto stage_row = [&](auto diag_tag, QS& q, int r, int rr, int i, bool ok) {
+        constexpr bool dg = decltype(diag_tag)::value;
         if (ok) {
-            q.key[r] = rt_lo[rr];
-            q.lse2[r] = rt_l[rr];
-            q.dlt[r] = rt_d[rr];
+            q.key[r] = (dg ? dt_lo : rt_lo)[rr];
+            q.lse2[r] = (dg ? dt_l : rt_l)[rr];
+            q.dlt[r] = (dg ? dt_d : rt_d)[rr];
             if (TR) {
-                q.wt[r] = rt_wt[rr];
+                q.wt[r] = (dg ? dt_wt : rt_wt)[rr];
                 q.ri[r] = i;
             }
         } else {
@@ -615,54 +616,14 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
         }
     };
 
-    // ---- diagonal rows j0 .. j0+63 (contiguous), double-buffered
-    const int ndiag = uniform(min(NDIAG, ceil_div(dend - j0, BQ)));
-    rsrc_t rq, rd;
-    ld.span(p, qb, db, j0, dend, rq, rd);
-    ld.load(rq, rd, 0);
-    if (tid < 64 && j0 + tid < dend) fill_row(tid, j0 + tid);
-    if (hh == 0) {  // loads in flight together with the diagonal rows'
-        if (tid < 64) own_s[tid] = kNoOwner;
-        int wm = 1;
-        for (int u = tid; u < p.n_tiles; u += 256) wm = max(wm, p.tile_wmax[(int64_t)s * p.n_tiles + u]);
-        wm = wave_max(wm);
-        if (lane == 0) wmax_s[wave] = wm;
-    }
-    __syncthreads();
-    iend = uniform(min(len, j0 + 63 + max(max(wmax_s[0], wmax_s[1]), max(wmax_s[2], wmax_s[3]))));
-    ld.store(sq[0], tid);
-    if (tid < BQ) stage_row(sq[0], tid, tid, j0 + tid, j0 + tid < dend);
-    __syncthreads();
-    for (int c = 0; c < ndiag; ++c) {
-        const int buf = c & 1;
-        if (c + 1 < ndiag) ld.load(rq, rd, c + 1);
-        compute(sq[buf], 0, j0 + c * BQ);
-        if (c + 1 < ndiag) {
-            ld.store(sq[buf ^ 1], tid);
-            const int rr = (c + 1) * BQ + tid;
-            if (tid < BQ) stage_row(sq[buf ^ 1], tid, rr, j0 + rr, j0 + rr < dend);
-        }
-        __syncthreads();
-    }
-
-    // ---- rows after the diagonal, segment by segment
-    for (int seg = j0 + 64; seg < iend; seg += kSeg) {
-        const int nrows = uniform(min(kSeg, iend - seg));
-        uint64_t bf[kSeg / 256], bp[kSeg / 256];
-#pragma unroll
-        for (int u = 0; u < kSeg / 256; ++u) {
-            const int r = u * 256 + tid;
-            bool f = false, pp = false;
-            if (r < nrows) {
-                const int i = seg + r;
-                fill_row(r, i);
-                const int lo = rt_lo[r];
-                f = lo <= j0 - (TR ? p.edge_keys : 0);
-                pp = !f && lo <= j0 + 63;
-            }
-            bf[u] = __ballot(f);
-            bp[u] = __ballot(pp);
-        }
+    // A segment's rows in two lists (row order within each): full rows lo <= j0 (no mask)
+    // and partial rows j0 < lo <= j0 + 63; rows with lo > j0 + 63 are skipped.  The per-wave
+    // counts of flags bf / bp go to wcnt; list_rows writes the lists once they are visible.
+    auto flag_rows = [&](int r, int lo, bool ok, bool& f, bool& pp) {
+        f = ok && lo <= j0 - (TR ? p.edge_keys : 0);
+        pp = ok && !f && lo <= j0 + 63;
+    };
+    auto count_rows = [&](const uint64_t* bf, const uint64_t* bp) {
         if (lane == 0) {
 #pragma unroll
             for (int u = 0; u < kSeg / 256; ++u) {
@@ -670,10 +631,12 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
                 wcnt[wave][4 + u] = __popcll(bp[u]);
             }
         }
-        if (!owners) find_owners();
-        __syncthreads();
-        // list order: (u, wave, lane) = row order
-        int nf = 0, np = 0, basef[kSeg / 256], basep[kSeg / 256];
+    };
+    int nf = 0, np = 0;
+    auto list_rows = [&](const uint64_t* bf, const uint64_t* bp) {
+        int basef[kSeg / 256], basep[kSeg / 256];
+        nf = 0;
+        np = 0;
 #pragma unroll
         for (int u = 0; u < kSeg / 256; ++u) {
             basef[u] = nf;
@@ -700,24 +663,129 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
             if (bf[u] & me) lst[0][basef[u] + rf] = (short)(u * 256 + tid);
             if (bp[u] & me) lst[1][basep[u] + rp] = (short)(u * 256 + tid);
         }
-        __syncthreads();
-        const int nfc = ceil_div(nf, BQ), nc = nfc + ceil_div(np, BQ);
-        ld.span(p, qb, db, seg, seg + nrows, rq, rd);
-        auto gather_chunk = [&](int c) {
-            if (c < nfc) ld.gather(rq, rd, lst[0], c * BQ, nf, tid);
-            else ld.gather(rq, rd, lst[1], (c - nfc) * BQ, np, tid);
-        };
-        auto stage_chunk = [&](int c, QS& q) {
-            ld.store(q, tid);
-            if (tid < BQ) {
-                const bool full = c < nfc;
-                const int idx = (full ? c : c - nfc) * BQ + tid;
-                const int n = full ? nf : np;
-                const bool ok = idx < n;
-                const int rr = ok ? (int)lst[full ? 0 : 1][idx] : 0;
-                stage_row(q, tid, rr, seg + rr, ok);
+    };
+    int seg = seg0, nfc = 0;
+    rsrc_t rqs, rds;  // rows of the current segment
+    auto gather_chunk = [&](int c) {
+        if (c < nfc) ld.gather(rqs, rds, lst[0], c * BQ, nf, tid);
+        else ld.gather(rqs, rds, lst[1], (c - nfc) * BQ, np, tid);
+    };
+    auto stage_chunk = [&](int c, QS& q) {
+        ld.store(q, tid);
+        if (tid < BQ) {
+            const bool full = c < nfc;
+            const int idx = (full ? c : c - nfc) * BQ + tid;
+            const int n = full ? nf : np;
+            const bool ok = idx < n;
+            const int rr = ok ? (int)lst[full ? 0 : 1][idx] : 0;
+            stage_row(std::false_type{}, q, tid, rr, seg + rr, ok);
+        }
+    };
+
+    // ---- prologue: the diagonal rows' first tile and data, the first segment's row data and
+    // flags (rows seg0 .. seg0 + kSeg - 1 below the sequence end; rows past the largest
+    // window reach are never flagged), the window bound and the landmark owners' positions:
+    // every load here depends on no other, and all are waited for at one barrier
+    const int ndiag = uniform(min(NDIAG, ceil_div(dend - j0, BQ)));
+    rsrc_t rq, rd;
+    ld.span(p, qb, db, j0, dend, rq, rd);
+    ld.load(rq, rd, 0);
+    if (tid < 64 && j0 + tid < dend) fill_row(std::true_type{}, tid, j0 + tid);
+    uint64_t bf[kSeg / 256], bp[kSeg / 256];
+#pragma unroll
+    for (int u = 0; u < kSeg / 256; ++u) {
+        const int r = u * 256 + tid;
+        const bool ok = kPre && seg0 + r < len;
+        const int lo = ok ? fill_row(std::false_type{}, r, seg0 + r) : 0;
+        bool f, pp;
+        flag_rows(r, lo, ok, f, pp);
+        bf[u] = __ballot(f);
+        bp[u] = __ballot(pp);
+    }
+    if (kPre) count_rows(bf, bp);
+    int own_at = -1, own_id = 0;  // this thread's landmark slot among the first 256 of the group
+    if (hh == 0) {
+        if (tid < 64) own_s[tid] = kNoOwner;
+        int wm = 1;
+        for (int u = tid; u < p.n_tiles; u += 256) wm = max(wm, p.tile_wmax[(int64_t)s * p.n_tiles + u]);
+        wm = wave_max(wm);
+        if (lane == 0) wmax_s[wave] = wm;
+        const int K = p.k_lmk;
+        if (tid < rep * K) {
+            const int hs = tid / K, sl = tid % K;
+            const int32_t* set = p.lmk + (((int64_t)(kvh * rep + hs) * p.num_seqs + s) * p.n_sets) * K;
+            const int v = set[sl];
+            if (v >= j0 && v < dend && (sl == 0 || set[sl - 1] != v)) {
+                own_at = v - j0;
+                own_id = (kvh * rep + hs) * K + sl;
             }
-        };
+        }
+    }
+    __syncthreads();
+    iend = uniform(min(len, j0 + 63 + max(max(wmax_s[0], wmax_s[1]), max(wmax_s[2], wmax_s[3]))));
+    if (hh == 0) {
+        if (own_at >= 0) atomicMin(own_s + own_at, own_id);
+        const int K = p.k_lmk;
+        for (int e = tid + 256; e < rep * K; e += 256) {  // groups of more than 256 slots
+            const int hs = e / K, sl = e % K;
+            const int32_t* set = p.lmk + (((int64_t)(kvh * rep + hs) * p.num_seqs + s) * p.n_sets) * K;
+            const int v = set[sl];
+            if (v >= j0 && v < dend && (sl == 0 || set[sl - 1] != v)) atomicMin(own_s + (v - j0), (kvh * rep + hs) * K + sl);
+        }
+    }
+    if (kPre) list_rows(bf, bp);
+    nfc = ceil_div(nf, BQ);
+    int nc = nfc + ceil_div(np, BQ);
+    ld.span(p, qb, db, seg0, min(len, seg0 + kSeg), rqs, rds);
+    ld.store(sq[0], tid);
+    if (tid < BQ) stage_row(std::true_type{}, sq[0], tid, tid, j0 + tid, j0 + tid < dend);
+    __syncthreads();
+
+    // ---- diagonal rows j0 .. j0+63, then the first segment's chunks: one double-buffered
+    // sweep (the last diagonal stage fetches the segment's first chunk)
+    for (int c = 0; c < ndiag; ++c) {
+        const int buf = c & 1;
+        const bool last = c + 1 == ndiag;
+        if (!last) ld.load(rq, rd, c + 1);
+        else if (nc > 0) gather_chunk(0);
+        compute(sq[buf], 0, j0 + c * BQ);
+        if (!last) {
+            ld.store(sq[buf ^ 1], tid);
+            const int rr = (c + 1) * BQ + tid;
+            if (tid < BQ) stage_row(std::true_type{}, sq[buf ^ 1], tid, rr, j0 + rr, j0 + rr < dend);
+        } else if (nc > 0) {
+            stage_chunk(0, sq[buf ^ 1]);
+        }
+        __syncthreads();
+    }
+    for (int c = 0; c < nc; ++c) {
+        const int buf = (ndiag + c) & 1;
+        if (c + 1 < nc) gather_chunk(c + 1);
+        compute(sq[buf], c < nfc ? 1 : 2, 0);
+        if (c + 1 < nc) stage_chunk(c + 1, sq[buf ^ 1]);
+        __syncthreads();
+    }
+
+    // ---- later segments (windows longer than kSeg - 63 rows), one at a time
+    for (seg = kPre ? seg0 + kSeg : seg0; seg < iend; seg += kSeg) {
+        const int nrows = uniform(min(kSeg, iend - seg));
+#pragma unroll
+        for (int u = 0; u < kSeg / 256; ++u) {
+            const int r = u * 256 + tid;
+            const bool ok = r < nrows;
+            const int lo = ok ? fill_row(std::false_type{}, r, seg + r) : 0;
+            bool f, pp;
+            flag_rows(r, lo, ok, f, pp);
+            bf[u] = __ballot(f);
+            bp[u] = __ballot(pp);
+        }
+        count_rows(bf, bp);
+        __syncthreads();
+        list_rows(bf, bp);
+        __syncthreads();
+        nfc = ceil_div(nf, BQ);
+        nc = nfc + ceil_div(np, BQ);
+        ld.span(p, qb, db, seg, seg + nrows, rqs, rds);
         if (nc > 0) {
             gather_chunk(0);
             stage_chunk(0, sq[0]);
@@ -732,10 +800,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
         }
     }
     }  // query heads of the group
-    if (!owners) {  // no row past the diagonal: the owners now
-        find_owners();
-        __syncthreads();
-    }
 
     if (jvalid && p.k_lmk > 0) {
         // a landmark row: its band sums go to the landmark pass's final sum in fp32, which
