@@ -53,7 +53,8 @@ struct AttnParams {
     int* tile_wmax;          // [S * n_tiles] largest clamped window of the tile's rows
     int variant;             // DSALT_VARIANT_* bits
     // backward workspace
-    float* delta;            // [H, T] rowsum(O * dO), head-major (written by the dQ pass)
+    float* delta;            // [H, T] -rowsum(O * dO), head-major (written by the dQ pass; the
+                             // key-parallel passes start their dP products from it)
     int* cnt;                // [H, T] landmarks visible to each row (written by the dQ pass)
     float* lse2t;            // [H, T] LSE * log2(e), head-major (written by the dQ pass)
     float* part_k;           // [n_chunks, H, S, K, D] landmark dK partials

@@ -167,7 +167,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     if (valid) {
         lse2 = p.lse[(int64_t)(st + i) * p.n_heads + h] * kLog2eB;
         if (g == 0) {
-            p.delta[hrow] = dlt;
+            p.delta[hrow] = -dlt;
             p.lse2t[hrow] = lse2;
         }
     }
@@ -360,7 +360,7 @@ struct QStage {
     T q[QT::ELEMS];
     T d[QT::ELEMS];
     float lse2[BQ];
-    float dlt[BQ];
+    float dlt[BQ];  // -delta
     int key[BQ];
     float wt[TR ? BQ : 4];  // training variant: continuous window of the row
     int ri[TR ? BQ : 4];    // training variant: row index
@@ -594,15 +594,15 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
                         ci[3] = (jj >= lo4.w && qd + 3 >= 0) ? eb[3] : NEG;
                     }
                 }
+                const floatx4 nd4 = *(const floatx4*)(q.dlt + qs * 16 + lane_off);  // -delta
                 const floatx4 sc = dot_rows<T, D>(q.q, QT::RS, qs * 16, lane, kr, ci);
-                const floatx4 dp = dot_rows<T, D>(q.d, QT::RS, qs * 16, lane, vr, floatx4{0.f, 0.f, 0.f, 0.f});
+                const floatx4 dp = dot_rows<T, D>(q.d, QT::RS, qs * 16, lane, vr, nd4);  // dP - delta
                 const floatx4 l4 = *(const floatx4*)(q.lse2 + qs * 16 + lane_off);
-                const floatx4 d4 = *(const floatx4*)(q.dlt + qs * 16 + lane_off);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float pr = __builtin_amdgcn_exp2f(sc[r] * c2 - l4[r]);
                     P[u][r] = pr;
-                    dS[u][r] = pr * (dp[r] - d4[r]);
+                    dS[u][r] = pr * dp[r];
                 }
             }
             if (!any) continue;
@@ -982,11 +982,11 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && sizeof(T) == 2 && D == 64) ? 4
                 const floatx4 sc = dot_rows<T, D>(q.q, QT::RS, qs * 16, lane, kr[u], ci);
                 const floatx4 dp = dot_rows<T, D>(q.d, QT::RS, qs * 16, lane, vr[u], floatx4{0.f, 0.f, 0.f, 0.f});
                 const floatx4 l4 = *(const floatx4*)(q.lse2 + qs * 16 + lane_off);
-                const floatx4 d4 = *(const floatx4*)(q.dlt + qs * 16 + lane_off);
+                const floatx4 nd4 = *(const floatx4*)(q.dlt + qs * 16 + lane_off);  // -delta
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float pr = __builtin_amdgcn_exp2f(sc[r] * c2 - l4[r]);
-                    const float dd = pr * (dp[r] - d4[r]);
+                    const float dd = pr * (dp[r] + nd4[r]);
                     P[qs][r] = pr;
                     dS[qs][r] = dd;
                     dbias[u] += dd;
