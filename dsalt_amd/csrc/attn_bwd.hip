@@ -398,16 +398,15 @@ struct QLoader {
         tq.load_rows(rq, q2);
         tdo.load_rows(rd, d2);
     }
-    // rows list[idx0 + rr] of a span for idx0 + rr < n (list in LDS); later rows zero
-    __device__ __forceinline__ void gather(rsrc_t rq, rsrc_t rd, const short* list, int idx0, int n, int tid) {
+    // rows list[rr] (rr < BQ) of a span, a negative entry reading zero
+    __device__ __forceinline__ void gather_list(rsrc_t rq, rsrc_t rd, const short* list, int tid) {
 #pragma unroll
         for (int v = 0; v < QT::NV; ++v) {
-            const int vi = tid + 256 * v, idx = idx0 + vi / QT::CPR;
+            const int vi = tid + 256 * v;
             const uint32_t cb = (uint32_t)(vi % QT::CPR) * 16u;
-            const bool ok = idx < n;
-            const uint32_t row = (uint32_t)list[min(idx, kSeg - 1)];
-            tq.r[v] = __builtin_amdgcn_raw_buffer_load_b128(rq, ok ? row * qrb + cb : 0x80000000u, 0, 0);
-            tdo.r[v] = __builtin_amdgcn_raw_buffer_load_b128(rd, ok ? row * drb + cb : 0x80000000u, 0, 0);
+            const int row = list[vi / QT::CPR];
+            tq.r[v] = __builtin_amdgcn_raw_buffer_load_b128(rq, row >= 0 ? (uint32_t)row * qrb + cb : 0x80000000u, 0, 0);
+            tdo.r[v] = __builtin_amdgcn_raw_buffer_load_b128(rd, row >= 0 ? (uint32_t)row * drb + cb : 0x80000000u, 0, 0);
         }
     }
     template <class QS>
@@ -435,26 +434,38 @@ struct QLoader {
 // past their edge_keys edge-bias keys; other rows add the soft edge bias.
 // GQA: the key/value head has several query heads (swept in order); without it the
 // sweep is straight-line code for one head.
+template <typename T, int D, int BQ, int NT = 256>
+struct QTiles {  // one staged chunk of the dK/dV sweep: BQ rows of Q and of dO
+    typedef Tile<T, D, BQ, NT> QT;
+    T q[QT::ELEMS];
+    T d[QT::ELEMS];
+};
+
 template <typename T, int D, bool TR, bool GQA>
 __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3 : 4) : 2) void bwd_dkdv_kernel(AttnParams p) {
     constexpr int BQ = BwdShape<T, D>::BQ;
     constexpr int NQS = BQ / 16;
     constexpr int NDIAG = 64 / BQ;
     constexpr bool kHalf = sizeof(T) == 2;
-    typedef QStage<T, D, BQ, TR> QS;
+    // list positions of a segment: full rows from 0, partial rows from the next chunk
+    // boundary, each list padded to whole chunks
+    constexpr int kLst = kSeg + 2 * BQ;
+    typedef QTiles<T, D, BQ> QS;
     typedef typename QS::QT QT;
     __shared__ __attribute__((aligned(16))) QS sq[2];
-    __shared__ short lst[2][kSeg];
     __shared__ int wcnt[4][8];
-    // per-row data (window start, LSE in base 2, delta[, continuous window]) of the rows the
-    // current sweep stage covers (the diagonal rows, then one segment), filled once per stage
-    // so the chunk staging reads LDS instead of issuing dependent global loads
-    __shared__ int rt_lo[kSeg];
-    __shared__ float rt_l[kSeg], rt_d[kSeg];
-    __shared__ float rt_wt[TR ? kSeg : 1];
-    __shared__ int dt_lo[64];  // the same for the 64 diagonal rows
-    __shared__ float dt_l[64], dt_d[64];
-    __shared__ float dt_wt[TR ? 64 : 1];
+    // per-row data of the rows a chunk covers, in chunk order, read by the products straight
+    // from these tables: window start (0x7fffffff for no row), LSE in base 2, -delta (0 for
+    // no row)[, continuous window, row index]; a segment's rows in list order with their row
+    // offsets (-1 for padding) for the gathers, the 64 diagonal rows in row order
+    __shared__ short lrw[kLst];
+    __shared__ __attribute__((aligned(16))) int lt_lo[kLst];
+    __shared__ __attribute__((aligned(16))) float lt_l[kLst], lt_d[kLst];
+    __shared__ __attribute__((aligned(16))) float lt_wt[TR ? kLst : 4];
+    __shared__ __attribute__((aligned(16))) int lt_ri[TR ? kLst : 4];
+    __shared__ __attribute__((aligned(16))) int dt_lo[64];
+    __shared__ __attribute__((aligned(16))) float dt_l[64], dt_d[64];
+    __shared__ __attribute__((aligned(16))) float dt_wt[TR ? 64 : 4];
     __shared__ int own_s[64];  // per key of the block: h * K + slot of its owner, or kNoOwner
     __shared__ int wmax_s[4];
 
@@ -511,45 +522,28 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
     const T* db = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
     const float* lrow = p.lse2t + (int64_t)h * p.total_len + st;
     const float* drow = p.delta + (int64_t)h * p.total_len + st;
-    // row table entry rr of row i: window start, LSE, delta[, continuous window] (the
-    // diagonal rows have a table of their own, so the first segment's can be filled with it)
-    auto fill_row = [&](auto diag_tag, int rr, int i) -> int {
-        constexpr bool dg = decltype(diag_tag)::value;
-        const int wi = max(wrow[i], 1);
-        const int lo = max(i - wi + 1, 0);
-        (dg ? dt_lo : rt_lo)[rr] = lo;
-        (dg ? dt_l : rt_l)[rr] = lrow[i];
-        (dg ? dt_d : rt_d)[rr] = drow[i];
-        if (TR) (dg ? dt_wt : rt_wt)[rr] = p.w_cont[st + i];
-        return lo;
+    // a row's data: window start, LSE, -delta[, continuous window]
+    struct RowData {
+        int lo;
+        float l, d, wt;
     };
-    // per-row data of staged row i (table entry rr), or of no row when !ok
-    auto stage_row = [&](auto diag_tag, QS& q, int r, int rr, int i, bool ok) {
-        constexpr bool dg = decltype(diag_tag)::value;
-        if (ok) {
-            q.key[r] = (dg ? dt_lo : rt_lo)[rr];
-            q.lse2[r] = (dg ? dt_l : rt_l)[rr];
-            q.dlt[r] = (dg ? dt_d : rt_d)[rr];
-            if (TR) {
-                q.wt[r] = (dg ? dt_wt : rt_wt)[rr];
-                q.ri[r] = i;
-            }
-        } else {
-            q.key[r] = 0x7fffffff;
-            q.lse2[r] = 0.f;
-            q.dlt[r] = 0.f;
-            if (TR) {
-                q.wt[r] = 0.f;
-                q.ri[r] = 0;
-            }
-        }
+    auto load_row = [&](int i) {
+        RowData r;
+        const int wi = max(wrow[i], 1);
+        r.lo = max(i - wi + 1, 0);
+        r.l = lrow[i];
+        r.d = drow[i];
+        r.wt = TR ? p.w_cont[st + i] : 0.f;
+        return r;
     };
 
-    // one staged chunk; kind 0: diagonal rows from i0, 1: full rows, 2: partial rows.
+    // one staged chunk; kind 0: diagonal rows from i0, 1: full rows, 2: partial rows; its
+    // per-row data at position `pos` of the diagonal table (dg) or the segment's list table.
     // Query subtiles are taken in the groups one accumulation consumes (two 16-row
     // subtiles for 16-bit types), so only one group's P and dS are live at a time.
     constexpr int GQ = kHalf ? 2 : 1;
-    auto compute = [&](const QS& q, int kind, int i0) {
+    auto compute = [&](auto diag_tag, const QS& q, int kind, int i0, int pos) {
+        constexpr bool dg = decltype(diag_tag)::value;
 #pragma unroll
         for (int hp = 0; hp < NQS / GQ; ++hp) {
             floatx4 P[GQ], dS[GQ];
@@ -559,6 +553,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
             for (int u = 0; u < GQ; ++u) {
                 const int qs = hp * GQ + u;
                 const int qa = i0 + qs * 16;
+                const int e = pos + qs * 16 + lane_off;  // table entry of the lane's first row
                 act[u] = kind != 0 || qa + 15 >= wj0;
                 any |= act[u];
                 if (!act[u]) {
@@ -568,14 +563,15 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
                 }
                 floatx4 ci = floatx4{0.f, 0.f, 0.f, 0.f};
                 if (kind != 1) {
-                    const int4 lo4 = *(const int4*)(q.key + qs * 16 + lane_off);
+                    const int4 lo4 = *(const int4*)((dg ? dt_lo : lt_lo) + e);
                     floatx4 eb = floatx4{0.f, 0.f, 0.f, 0.f};
                     // the soft edge reaches this key only for rows with jj < lo + edge_keys:
                     // skipped unless some lane of the wave has such a row
                     if (TR && __builtin_amdgcn_ballot_w64(jj < lo4.x + p.edge_keys || jj < lo4.y + p.edge_keys ||
                                                           jj < lo4.z + p.edge_keys || jj < lo4.w + p.edge_keys)) {
-                        const floatx4 w4 = *(const floatx4*)(q.wt + qs * 16 + lane_off);
-                        const int4 i4 = *(const int4*)(q.ri + qs * 16 + lane_off);
+                        const floatx4 w4 = *(const floatx4*)((dg ? dt_wt : lt_wt) + e);
+                        const int4 i4 = dg ? int4{qa + lane_off, qa + lane_off + 1, qa + lane_off + 2, qa + lane_off + 3}
+                                           : *(const int4*)(lt_ri + e);
                         eb[0] = edge_bias(p, w4[0], i4.x - jj);
                         eb[1] = edge_bias(p, w4[1], i4.y - jj);
                         eb[2] = edge_bias(p, w4[2], i4.z - jj);
@@ -594,10 +590,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
                         ci[3] = (jj >= lo4.w && qd + 3 >= 0) ? eb[3] : NEG;
                     }
                 }
-                const floatx4 nd4 = *(const floatx4*)(q.dlt + qs * 16 + lane_off);  // -delta
+                const floatx4 nd4 = *(const floatx4*)((dg ? dt_d : lt_d) + e);  // -delta
                 const floatx4 sc = dot_rows<T, D>(q.q, QT::RS, qs * 16, lane, kr, ci);
                 const floatx4 dp = dot_rows<T, D>(q.d, QT::RS, qs * 16, lane, vr, nd4);  // dP - delta
-                const floatx4 l4 = *(const floatx4*)(q.lse2 + qs * 16 + lane_off);
+                const floatx4 l4 = *(const floatx4*)((dg ? dt_l : lt_l) + e);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float pr = __builtin_amdgcn_exp2f(sc[r] * c2 - l4[r]);
@@ -618,8 +614,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
 
     // A segment's rows in two lists (row order within each): full rows lo <= j0 (no mask)
     // and partial rows j0 < lo <= j0 + 63; rows with lo > j0 + 63 are skipped.  The per-wave
-    // counts of flags bf / bp go to wcnt; list_rows writes the lists once they are visible.
-    auto flag_rows = [&](int r, int lo, bool ok, bool& f, bool& pp) {
+    // counts of flags bf / bp go to wcnt; list_rows writes the lists' row offsets and row data
+    // once the counts are visible, and pads each list to whole chunks.
+    auto flag_rows = [&](int lo, bool ok, bool& f, bool& pp) {
         f = ok && lo <= j0 - (TR ? p.edge_keys : 0);
         pp = ok && !f && lo <= j0 + 63;
     };
@@ -632,11 +629,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
             }
         }
     };
-    int nf = 0, np = 0;
-    auto list_rows = [&](const uint64_t* bf, const uint64_t* bp) {
+    int nfc = 0, nc = 0;
+    auto list_rows = [&](const uint64_t* bf, const uint64_t* bp, auto row_data, int seg) {
         int basef[kSeg / 256], basep[kSeg / 256];
-        nf = 0;
-        np = 0;
+        int nf = 0, np = 0;
 #pragma unroll
         for (int u = 0; u < kSeg / 256; ++u) {
             basef[u] = nf;
@@ -653,6 +649,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
         }
         nf = uniform(nf);
         np = uniform(np);
+        nfc = ceil_div(nf, BQ);
+        nc = nfc + ceil_div(np, BQ);
+        const int pbase = nfc * BQ;
 #pragma unroll
         for (int u = 0; u < kSeg / 256; ++u) {
             const uint32_t flo = (uint32_t)bf[u], fhi = (uint32_t)(bf[u] >> 32);
@@ -660,27 +659,40 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
             const int rf = __builtin_amdgcn_mbcnt_hi(fhi, __builtin_amdgcn_mbcnt_lo(flo, 0));
             const int rp = __builtin_amdgcn_mbcnt_hi(phi, __builtin_amdgcn_mbcnt_lo(plo, 0));
             const uint64_t me = 1ull << lane;
-            if (bf[u] & me) lst[0][basef[u] + rf] = (short)(u * 256 + tid);
-            if (bp[u] & me) lst[1][basep[u] + rp] = (short)(u * 256 + tid);
+            const bool inf = (bf[u] & me) != 0, inp = (bp[u] & me) != 0;
+            if (inf || inp) {
+                const int at = inf ? basef[u] + rf : pbase + basep[u] + rp;
+                const int r = u * 256 + tid;
+                const RowData x = row_data(u);
+                lrw[at] = (short)r;
+                lt_lo[at] = x.lo;
+                lt_l[at] = x.l;
+                lt_d[at] = x.d;
+                if (TR) {
+                    lt_wt[at] = x.wt;
+                    lt_ri[at] = seg + r;
+                }
+            }
+        }
+        // padding: rows of no list (zero Q and dO rows, LSE and -delta 0, no key visible)
+        if (tid < 2 * BQ) {
+            const int at = tid < BQ ? nf + tid : pbase + np + (tid - BQ);
+            const int lim = tid < BQ ? pbase : nc * BQ;
+            if (at < lim) {
+                lrw[at] = -1;
+                lt_lo[at] = 0x7fffffff;
+                lt_l[at] = 0.f;
+                lt_d[at] = 0.f;
+                if (TR) {
+                    lt_wt[at] = 0.f;
+                    lt_ri[at] = 0;
+                }
+            }
         }
     };
-    int seg = seg0, nfc = 0;
+    int seg = seg0;
     rsrc_t rqs, rds;  // rows of the current segment
-    auto gather_chunk = [&](int c) {
-        if (c < nfc) ld.gather(rqs, rds, lst[0], c * BQ, nf, tid);
-        else ld.gather(rqs, rds, lst[1], (c - nfc) * BQ, np, tid);
-    };
-    auto stage_chunk = [&](int c, QS& q) {
-        ld.store(q, tid);
-        if (tid < BQ) {
-            const bool full = c < nfc;
-            const int idx = (full ? c : c - nfc) * BQ + tid;
-            const int n = full ? nf : np;
-            const bool ok = idx < n;
-            const int rr = ok ? (int)lst[full ? 0 : 1][idx] : 0;
-            stage_row(std::false_type{}, q, tid, rr, seg + rr, ok);
-        }
-    };
+    auto gather_chunk = [&](int c) { ld.gather_list(rqs, rds, lrw + c * BQ, tid); };
 
     // ---- prologue: the diagonal rows' first tile and data, the first segment's row data and
     // flags (rows seg0 .. seg0 + kSeg - 1 below the sequence end; rows past the largest
@@ -690,15 +702,23 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
     rsrc_t rq, rd;
     ld.span(p, qb, db, j0, dend, rq, rd);
     ld.load(rq, rd, 0);
-    if (tid < 64 && j0 + tid < dend) fill_row(std::true_type{}, tid, j0 + tid);
+    if (tid < 64) {
+        const bool ok = j0 + tid < dend;
+        RowData r = ok ? load_row(j0 + tid) : RowData{0x7fffffff, 0.f, 0.f, 0.f};
+        dt_lo[tid] = r.lo;
+        dt_l[tid] = r.l;
+        dt_d[tid] = r.d;
+        if (TR) dt_wt[tid] = r.wt;
+    }
     uint64_t bf[kSeg / 256], bp[kSeg / 256];
+    RowData rdat[kSeg / 256];
 #pragma unroll
     for (int u = 0; u < kSeg / 256; ++u) {
         const int r = u * 256 + tid;
         const bool ok = kPre && seg0 + r < len;
-        const int lo = ok ? fill_row(std::false_type{}, r, seg0 + r) : 0;
+        rdat[u] = ok ? load_row(seg0 + r) : RowData{0x7fffffff, 0.f, 0.f, 0.f};
         bool f, pp;
-        flag_rows(r, lo, ok, f, pp);
+        flag_rows(rdat[u].lo, ok, f, pp);
         bf[u] = __ballot(f);
         bp[u] = __ballot(pp);
     }
@@ -733,12 +753,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
             if (v >= j0 && v < dend && (sl == 0 || set[sl - 1] != v)) atomicMin(own_s + (v - j0), (kvh * rep + hs) * K + sl);
         }
     }
-    if (kPre) list_rows(bf, bp);
-    nfc = ceil_div(nf, BQ);
-    int nc = nfc + ceil_div(np, BQ);
+    if (kPre) list_rows(bf, bp, [&](int u) { return rdat[u]; }, seg0);
     ld.span(p, qb, db, seg0, min(len, seg0 + kSeg), rqs, rds);
     ld.store(sq[0], tid);
-    if (tid < BQ) stage_row(std::true_type{}, sq[0], tid, tid, j0 + tid, j0 + tid < dend);
     __syncthreads();
 
     // ---- diagonal rows j0 .. j0+63, then the first segment's chunks: one double-buffered
@@ -748,54 +765,57 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
         const bool last = c + 1 == ndiag;
         if (!last) ld.load(rq, rd, c + 1);
         else if (nc > 0) gather_chunk(0);
-        compute(sq[buf], 0, j0 + c * BQ);
-        if (!last) {
-            ld.store(sq[buf ^ 1], tid);
-            const int rr = (c + 1) * BQ + tid;
-            if (tid < BQ) stage_row(std::true_type{}, sq[buf ^ 1], tid, rr, j0 + rr, j0 + rr < dend);
-        } else if (nc > 0) {
-            stage_chunk(0, sq[buf ^ 1]);
-        }
+        compute(std::true_type{}, sq[buf], 0, j0 + c * BQ, c * BQ);
+        if (!last || nc > 0) ld.store(sq[buf ^ 1], tid);
         __syncthreads();
     }
     for (int c = 0; c < nc; ++c) {
         const int buf = (ndiag + c) & 1;
         if (c + 1 < nc) gather_chunk(c + 1);
-        compute(sq[buf], c < nfc ? 1 : 2, 0);
-        if (c + 1 < nc) stage_chunk(c + 1, sq[buf ^ 1]);
+        compute(std::false_type{}, sq[buf], c < nfc ? 1 : 2, 0, c * BQ);
+        if (c + 1 < nc) ld.store(sq[buf ^ 1], tid);
         __syncthreads();
     }
 
-    // ---- later segments (windows longer than kSeg - 63 rows), one at a time
+    // ---- later segments (windows longer than kSeg - 63 rows), one at a time; their rows'
+    // data wait for the list positions in the second tile buffer (free until the segment's
+    // second chunk), not in registers
+    static_assert(sizeof(QS) >= sizeof(float) * (TR ? 4 : 3) * kSeg, "row scratch does not fit a tile buffer");
+    float* scr = (float*)&sq[1];
     for (seg = kPre ? seg0 + kSeg : seg0; seg < iend; seg += kSeg) {
         const int nrows = uniform(min(kSeg, iend - seg));
 #pragma unroll
         for (int u = 0; u < kSeg / 256; ++u) {
             const int r = u * 256 + tid;
             const bool ok = r < nrows;
-            const int lo = ok ? fill_row(std::false_type{}, r, seg + r) : 0;
+            const RowData x = ok ? load_row(seg + r) : RowData{0x7fffffff, 0.f, 0.f, 0.f};
+            scr[r] = __int_as_float(x.lo);
+            scr[kSeg + r] = x.l;
+            scr[2 * kSeg + r] = x.d;
+            if (TR) scr[3 * kSeg + r] = x.wt;
             bool f, pp;
-            flag_rows(r, lo, ok, f, pp);
+            flag_rows(x.lo, ok, f, pp);
             bf[u] = __ballot(f);
             bp[u] = __ballot(pp);
         }
         count_rows(bf, bp);
         __syncthreads();
-        list_rows(bf, bp);
+        list_rows(bf, bp, [&](int u) {
+            const int r = u * 256 + tid;
+            return RowData{__float_as_int(scr[r]), scr[kSeg + r], scr[2 * kSeg + r], TR ? scr[3 * kSeg + r] : 0.f};
+        }, seg);
         __syncthreads();
-        nfc = ceil_div(nf, BQ);
-        nc = nfc + ceil_div(np, BQ);
         ld.span(p, qb, db, seg, seg + nrows, rqs, rds);
         if (nc > 0) {
             gather_chunk(0);
-            stage_chunk(0, sq[0]);
+            ld.store(sq[0], tid);
         }
         __syncthreads();
         for (int c = 0; c < nc; ++c) {
             const int buf = c & 1;
             if (c + 1 < nc) gather_chunk(c + 1);
-            compute(sq[buf], c < nfc ? 1 : 2, 0);
-            if (c + 1 < nc) stage_chunk(c + 1, sq[buf ^ 1]);
+            compute(std::false_type{}, sq[buf], c < nfc ? 1 : 2, 0, c * BQ);
+            if (c + 1 < nc) ld.store(sq[buf ^ 1], tid);
             __syncthreads();
         }
     }
