@@ -149,36 +149,45 @@ __device__ __forceinline__ int group_of(int w, int u) {
     return RG == 1 ? w : 4 * u + (u & 1 ? 3 - w : w);
 }
 
-// Fills the lane's row of block group G (0 .. 4*RG-1) from the row plan (everything but
-// the visible landmark counts, which need the block's landmark set in LDS).
-__device__ __forceinline__ void plan_group(const AttnParams& p, int64_t tile0, int ntl, int G, int r0, int st,
-                                           int len, int lane, RowGroup& rg) {
-    rg.i = -1;
+// Fills the lane's row of block group G (0 .. 4*RG-1) from the row plan: plan_rows the row
+// and the group bounds, plan_window (after the rows of every group are requested) the
+// window; the visible landmark counts need the block's landmark set in LDS (plan_counts).
+struct PlanLoad {  // a group's plan entries as loaded
+    int b0, b1, b2, b3, pm;
+};
+// loads from valid addresses whether or not the group exists (G past the block's tiles reads
+// group 0), results selected in plan_rows: no load waits on a branch
+__device__ __forceinline__ PlanLoad plan_load(const AttnParams& p, int64_t tile0, int ntl, int G, int lane) {
+    const int Gc = G < 4 * ntl ? G : 0;
+    const int* bnd = p.plan_bounds + (tile0 + Gc / 4) * 16 + (Gc % 4) * 4;
+    return PlanLoad{bnd[0], bnd[1], bnd[2], bnd[3], (int)p.plan_perm[(tile0 + Gc / 4) * 64 + (Gc % 4) * 16 + (lane & 15)]};
+}
+__device__ __forceinline__ void plan_rows(const PlanLoad& l, int ntl, int G, int r0, int len, RowGroup& rg) {
+    const bool has = G < 4 * ntl;
+    const int Gc = has ? G : 0;
+    rg.wlo = has ? l.b0 : 0x7fffffff;
+    rg.wLmax = has ? l.b1 : (int)0x80000000;
+    rg.whi = has ? l.b2 : -1;
+    rg.wHmin = has ? l.b3 : 0x7fffffff;
+    rg.i = has ? r0 + (Gc / 4) * 64 + l.pm : -1;
+    rg.valid = has && rg.i < len;
     rg.lo = 0x7fffffff;
     rg.hi = -1;
     rg.cnt = 0;
-    rg.valid = false;
     rg.wt = 0.f;
     rg.lou = 0x7fffffff;
-    rg.wlo = 0x7fffffff;
-    rg.wLmax = (int)0x80000000;
-    rg.whi = -1;
-    rg.wHmin = 0x7fffffff;
-    if (G < 4 * ntl) {
-        const int* bnd = p.plan_bounds + (tile0 + G / 4) * 16 + (G % 4) * 4;
-        rg.wlo = bnd[0];
-        rg.wLmax = bnd[1];
-        rg.whi = bnd[2];
-        rg.wHmin = bnd[3];
-        rg.i = r0 + (G / 4) * 64 + p.plan_perm[(tile0 + G / 4) * 64 + (G % 4) * 16 + (lane & 15)];
-        rg.valid = rg.i < len;
-        if (rg.valid) {
-            const int wi = max(p.w[st + rg.i], 1);
-            rg.lo = max(rg.i - wi + 1, 0);
-            rg.hi = rg.i;
-            if (p.w_cont) rg.wt = p.w_cont[st + rg.i];
-            rg.lou = rg.i - (wi - 1);
-        }
+}
+
+__device__ __forceinline__ void plan_window(const AttnParams& p, int st, RowGroup& rg) {
+    // loads issued by every lane (a row past the end reads the sequence's first row)
+    const int at = st + (rg.valid ? rg.i : 0);
+    const int wi = max(p.w[at], 1);
+    const float wt = p.w_cont ? p.w_cont[at] : 0.f;
+    if (rg.valid) {
+        rg.lo = max(rg.i - wi + 1, 0);
+        rg.hi = rg.i;
+        rg.wt = wt;
+        rg.lou = rg.i - (wi - 1);
     }
     if (p.w_cont) edge_table(p, rg.wt, rg.eb, nullptr);
 }
@@ -247,38 +256,62 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     const float inv_scale = p.inv_scale;
     const bool has_bias = p.lbias != nullptr;
 
-    // Prologue: the loads that depend on no other load -- the landmark set, the row plan and,
-    // through it, the block's query rows and windows -- are all issued before the first
-    // barrier, and the first landmark chunk right after it, so a block waits for about two
-    // memory latencies before its first products.
-    int nv_loc = 0;  // one past the last valid slot (sets are ascending, -1 after the valid slots)
-    for (int i = tid; i < K; i += 256) {
-        const int v = p.lmk[set_off + i];
-        const int vn = i + 1 < K ? p.lmk[set_off + i + 1] : -1;
-        lpos[i] = v;
-        if (v >= 0 && vn < 0) nv_loc = i + 1;
-        if (has_bias) lbs[i] = p.lbias[set_off + i] * inv_scale;  // raw-score units
+    // Prologue: the loads that depend on no other load -- the landmark set, the row plan's
+    // group bounds and rows -- are issued together, then the rows' windows and query rows;
+    // the block's largest visible landmark count follows from the largest window start of
+    // its groups, so one barrier (the set in LDS) precedes the first landmark chunk's fetch.
+    int lv[kMaxLandmarks / 256], ln[kMaxLandmarks / 256];
+    float lb[kMaxLandmarks / 256];
+#pragma unroll
+    for (int u = 0; u < kMaxLandmarks / 256; ++u) {
+        lv[u] = -1;
+        ln[u] = -1;
+        lb[u] = 0.f;
+        if (u * 256 < K) {  // every lane loads (clamped slots), so no load waits on a branch
+            lv[u] = p.lmk[set_off + min(u * 256 + tid, K - 1)];
+            ln[u] = p.lmk[set_off + min(u * 256 + tid + 1, K - 1)];
+            if (has_bias) lb[u] = p.lbias[set_off + min(u * 256 + tid, K - 1)];
+        }
     }
 
-    // row groups of this wave and block-wide key range, from the row plan
+    // row groups of this wave, block-wide key range and largest window start, from the row plan
     const int uw = uniform(wave);
     const int64_t tile0 = (int64_t)s * p.n_tiles + (int64_t)b * RG;
     const int ntl = min(RG, p.n_tiles - b * RG);
-    int blo = 0x7fffffff, bhi = -1;
-    for (int G = 0; G < 4 * ntl; ++G) {
-        blo = min(blo, p.plan_bounds[tile0 * 16 + G * 4]);
-        bhi = max(bhi, p.plan_bounds[tile0 * 16 + G * 4 + 2]);
+    int blo = 0x7fffffff, bhi = -1, blmax = (int)0x80000000;
+    if (lane < 4 * ntl) {
+        const int* bnd = p.plan_bounds + tile0 * 16 + lane * 4;
+        blo = bnd[0];
+        blmax = bnd[1];
+        bhi = bnd[2];
     }
-    blo = uniform(blo);
-    bhi = uniform(bhi);
+    PlanLoad pl[RG];
+#pragma unroll
+    for (int u = 0; u < RG; ++u) pl[u] = plan_load(p, tile0, ntl, group_of<RG>(uw, u), lane);
+    __builtin_amdgcn_sched_barrier(0);  // every group's plan load issued before any is used
     RowGroup rg[RG];
 #pragma unroll
-    for (int u = 0; u < RG; ++u) plan_group(p, tile0, ntl, group_of<RG>(uw, u), r0, st, len, lane, rg[u]);
+    for (int u = 0; u < RG; ++u) plan_rows(pl[u], ntl, group_of<RG>(uw, u), r0, len, rg[u]);
+#pragma unroll
+    for (int u = 0; u < RG; ++u) plan_window(p, st, rg[u]);
     const T* qhead = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
     RowReg<T, D> qr[RG];
 #pragma unroll
     for (int u = 0; u < RG; ++u) qr[u].load(rg[u].valid ? qhead + (int64_t)rg[u].i * p.q_st : nullptr, qhead, g);
+    blo = uniform(-wave_max(-blo));
+    bhi = uniform(wave_max(bhi));
+    blmax = uniform(wave_max(blmax));
 
+    int nv_loc = 0;  // one past the last valid slot (sets are ascending, -1 after the valid slots)
+#pragma unroll
+    for (int u = 0; u < kMaxLandmarks / 256; ++u) {
+        const int i = u * 256 + tid;
+        if (i < K) {
+            lpos[i] = lv[u];
+            if (has_bias) lbs[i] = lb[u] * inv_scale;  // raw-score units
+            if (lv[u] >= 0 && (i + 1 == K || ln[u] < 0)) nv_loc = i + 1;
+        }
+    }
     nv_loc = wave_max(nv_loc);
     if (lane == 0) red[4 + uw] = nv_loc;
     __syncthreads();
@@ -325,15 +358,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     };
     if (nvalid > 0) load_lmk_lim(0, nvalid);
 
-    int wcm = 0;
 #pragma unroll
-    for (int u = 0; u < RG; ++u) {
-        plan_counts(lpos, nvalid, rg[u]);
-        wcm = max(wcm, rg[u].wcmax);
-    }
-    if (lane == 0) red[uw] = wcm;
-    __syncthreads();
-    const int bcm = uniform(max(max(red[0], red[1]), max(red[2], red[3])));
+    for (int u = 0; u < RG; ++u) plan_counts(lpos, nvalid, rg[u]);
+    // the block's largest visible count: that of its largest window start (counts grow with it)
+    const int bcm = uniform(lower_bound_lds(lpos, nvalid, blmax));
     const int cs = (blo / BN) * BN;
     const int nband = bhi >= blo ? (bhi - cs) / BN + 1 : 0;
     const int nchunks = nband + ceil_div(bcm, BN);
