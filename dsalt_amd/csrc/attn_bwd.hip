@@ -89,7 +89,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     __shared__ __attribute__((aligned(16))) float lbs[kMaxLandmarks];
     // block scalars live in the second K buffer until the first chunk is staged there
     int* red = (int*)Ks[1];
-    int& nvalid_s = red[4];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
@@ -107,26 +106,78 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     const float c2 = p.c2;
     const float inv_scale = p.inv_scale;
     const bool has_bias = p.lbias != nullptr;
-    const int nvalid = load_set(p, set_off, lpos, &nvalid_s, tid, has_bias ? lbs : nullptr);
 
+    // Prologue: the loads that depend on no other load -- the landmark set, the row plan's
+    // bounds and rows -- are issued together (every lane loads, from clamped addresses, so no
+    // load waits on a branch), then the rows' windows, LSE and row vectors; the block's
+    // largest visible landmark count follows from the tile's largest window start, so one
+    // barrier (the set in LDS) precedes the counts and the first chunk.
+    int lv[kMaxLandmarks / 256], ln[kMaxLandmarks / 256];
+    float lb[kMaxLandmarks / 256];
+#pragma unroll
+    for (int u = 0; u < kMaxLandmarks / 256; ++u) {
+        lv[u] = -1;
+        ln[u] = -1;
+        lb[u] = 0.f;
+        if (u * 256 < K) {
+            lv[u] = p.lmk[set_off + min(u * 256 + tid, K - 1)];
+            ln[u] = p.lmk[set_off + min(u * 256 + tid + 1, K - 1)];
+            if (has_bias) lb[u] = p.lbias[set_off + min(u * 256 + tid, K - 1)];
+        }
+    }
     // this wave's rows (ordered by window start) and their bounds, from the row plan
     const int uw = uniform(wave);
     const int64_t tile = (int64_t)s * p.n_tiles + t;
     const int* bnd = p.plan_bounds + tile * 16;
     const int wlo = bnd[uw * 4], wLmax = bnd[uw * 4 + 1], whi = bnd[uw * 4 + 2], wHmin = bnd[uw * 4 + 3];
-    const int blo = min(min(bnd[0], bnd[4]), min(bnd[8], bnd[12]));
-    const int bhi = max(max(bnd[2], bnd[6]), max(bnd[10], bnd[14]));
-    const int i = r0 + p.plan_perm[tile * 64 + uw * 16 + (lane & 15)];
+    int blo = 0x7fffffff, bhi = -1, blmax = (int)0x80000000;
+    if (lane < 4) {
+        blo = bnd[lane * 4];
+        blmax = bnd[lane * 4 + 1];
+        bhi = bnd[lane * 4 + 2];
+    }
+    const int pm = p.plan_perm[tile * 64 + uw * 16 + (lane & 15)];
+    __builtin_amdgcn_sched_barrier(0);  // the independent loads above issued before any is used
+    const int i = r0 + pm;
     const bool valid = i < len;
+    const int at = st + (valid ? i : 0);  // loads by every lane (a row past the end reads row 0)
+    const int wi = max(p.w[at], 1);
+    const float lse_raw = p.lse[(int64_t)at * p.n_heads + h];
+    const float wt_raw = TR ? p.w_cont[at] : 0.f;
+    const T* qhead = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
+    const T* dohead = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
+    const T* ohead = (const T*)p.o + (int64_t)st * p.o_st + (int64_t)h * p.o_sh;
+    RowReg<T, D> qr, dor, orr;
+    qr.load(valid ? qhead + (int64_t)i * p.q_st : nullptr, qhead, g);
+    dor.load(valid ? dohead + (int64_t)i * p.do_st : nullptr, dohead, g);
+    orr.load(valid ? ohead + (int64_t)i * p.o_st : nullptr, ohead, g);
+    blo = uniform(-wave_max(-blo));
+    bhi = uniform(wave_max(bhi));
+    blmax = uniform(wave_max(blmax));
+
+    int nv_loc = 0;  // one past the last valid slot (sets are ascending, -1 after the valid slots)
+#pragma unroll
+    for (int u = 0; u < kMaxLandmarks / 256; ++u) {
+        const int sl = u * 256 + tid;
+        if (sl < K) {
+            lpos[sl] = lv[u];
+            if (has_bias) lbs[sl] = lb[u] * inv_scale;  // landmark bias in raw-score units
+            if (lv[u] >= 0 && (sl + 1 == K || ln[u] < 0)) nv_loc = sl + 1;
+        }
+    }
+    nv_loc = wave_max(nv_loc);
+    if (lane == 0) red[4 + uw] = nv_loc;
+    __syncthreads();
+    const int nvalid = uniform(max(max(red[4], red[5]), max(red[6], red[7])));
+
     int lo = 0x7fffffff, hi = -1, cnt = 0, lou = 0x7fffffff;
     float wt = 0.f;
     if (valid) {
-        const int wi = max(p.w[st + i], 1);
         lo = max(i - wi + 1, 0);
         lou = i - (wi - 1);
         hi = i;
         cnt = lower_bound_i(lpos, nvalid, lo);
-        if (TR) wt = p.w_cont[st + i];
+        if (TR) wt = wt_raw;
     }
     // soft-edge bias and window gradient of keys lou .. lou+3 (training variant)
     float etb[TR ? kEdgeTab : 1], etg[TR ? kEdgeTab : 1];
@@ -137,20 +188,12 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     const int64_t hrow = (int64_t)h * p.total_len + st + i;
     if (valid && g == 0 && p.cnt) p.cnt[hrow] = cnt;
     const int wcmax = uniform(row_max16(cnt)), wcmin = uniform(row_min16(valid ? cnt : 0));
-    if (lane == 0) red[uw] = wcmax;
-    __syncthreads();
-    const int bcm = uniform(max(max(red[0], red[1]), max(red[2], red[3])));
+    // the block's largest visible count: that of its largest window start (counts grow with it)
+    const int bcm = uniform(lower_bound_i(lpos, nvalid, blmax));
     const int cs = (blo / BN) * BN;
     const int nband = (bhi - cs) / BN + 1;
     const int nchunks = nband + ceil_div(bcm, BN);
 
-    const T* qhead = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
-    const T* dohead = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
-    const T* ohead = (const T*)p.o + (int64_t)st * p.o_st + (int64_t)h * p.o_sh;
-    RowReg<T, D> qr, dor, orr;
-    qr.load(valid ? qhead + (int64_t)i * p.q_st : nullptr, qhead, g);
-    dor.load(valid ? dohead + (int64_t)i * p.do_st : nullptr, dohead, g);
-    orr.load(valid ? ohead + (int64_t)i * p.o_st : nullptr, ohead, g);
     // delta = rowsum(O * dO) over the stored (rounded) O
     float dpart = 0.f;
     if constexpr (kHalf) {
@@ -165,7 +208,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     const float dlt = sum_g4(dpart);
     float lse2 = 0.f;
     if (valid) {
-        lse2 = p.lse[(int64_t)(st + i) * p.n_heads + h] * kLog2eB;
+        lse2 = lse_raw * kLog2eB;
         if (g == 0) {
             p.delta[hrow] = -dlt;
             p.lse2t[hrow] = lse2;
