@@ -740,55 +740,71 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
     // ---- prologue: the diagonal rows' first tile and data, the first segment's row data and
     // flags (rows seg0 .. seg0 + kSeg - 1 below the sequence end; rows past the largest
     // window reach are never flagged), the window bound and the landmark owners' positions:
-    // every load here depends on no other, and all are waited for at one barrier
+    // every load here depends on no other; all are issued (by every lane, from clamped
+    // addresses, so no load waits on a branch) before any is used, and waited for at one
+    // barrier
     const int ndiag = uniform(min(NDIAG, ceil_div(dend - j0, BQ)));
     rsrc_t rq, rd;
     ld.span(p, qb, db, j0, dend, rq, rd);
     ld.load(rq, rd, 0);
-    if (tid < 64) {
-        const bool ok = j0 + tid < dend;
-        RowData r = ok ? load_row(j0 + tid) : RowData{0x7fffffff, 0.f, 0.f, 0.f};
-        dt_lo[tid] = r.lo;
-        dt_l[tid] = r.l;
-        dt_d[tid] = r.d;
-        if (TR) dt_wt[tid] = r.wt;
-    }
-    uint64_t bf[kSeg / 256], bp[kSeg / 256];
+    const RowData dgr = load_row(min(j0 + (tid & 63), len - 1));
     RowData rdat[kSeg / 256];
 #pragma unroll
+    for (int u = 0; u < kSeg / 256; ++u) rdat[u] = load_row(min(seg0 + u * 256 + tid, len - 1));
+    constexpr int kWm = 4;  // tile maxima read before the barrier by each thread (more: a loop)
+    int wmv[kWm];
+    int ov = -1, ovp = -1;  // this thread's landmark slot among the first 256 of the group, and the one before
+    const int K = p.k_lmk;
+    const int nown = rep * K;
+    const int32_t* oset = p.lmk + (((int64_t)(kvh * rep + min(tid, max(nown, 1) - 1) / max(K, 1)) * p.num_seqs + s) *
+                                   p.n_sets) * K;
+    const int osl = K > 0 ? min(tid, nown - 1) % K : 0;
+    if (hh == 0) {
+#pragma unroll
+        for (int k = 0; k < kWm; ++k) wmv[k] = p.tile_wmax[(int64_t)s * p.n_tiles + min(tid + 256 * k, p.n_tiles - 1)];
+        if (nown > 0) {
+            ov = oset[osl];
+            ovp = oset[max(osl - 1, 0)];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the loads above issued before any is used
+    if (tid < 64) {
+        const bool ok = j0 + tid < dend;
+        dt_lo[tid] = ok ? dgr.lo : 0x7fffffff;
+        dt_l[tid] = ok ? dgr.l : 0.f;
+        dt_d[tid] = ok ? dgr.d : 0.f;
+        if (TR) dt_wt[tid] = ok ? dgr.wt : 0.f;
+    }
+    uint64_t bf[kSeg / 256], bp[kSeg / 256];
+#pragma unroll
     for (int u = 0; u < kSeg / 256; ++u) {
-        const int r = u * 256 + tid;
-        const bool ok = kPre && seg0 + r < len;
-        rdat[u] = ok ? load_row(seg0 + r) : RowData{0x7fffffff, 0.f, 0.f, 0.f};
+        const bool ok = kPre && seg0 + u * 256 + tid < len;
         bool f, pp;
         flag_rows(rdat[u].lo, ok, f, pp);
         bf[u] = __ballot(f);
         bp[u] = __ballot(pp);
     }
     if (kPre) count_rows(bf, bp);
-    int own_at = -1, own_id = 0;  // this thread's landmark slot among the first 256 of the group
+    int own_at = -1, own_id = 0;
     if (hh == 0) {
         if (tid < 64) own_s[tid] = kNoOwner;
         int wm = 1;
-        for (int u = tid; u < p.n_tiles; u += 256) wm = max(wm, p.tile_wmax[(int64_t)s * p.n_tiles + u]);
+#pragma unroll
+        for (int k = 0; k < kWm; ++k) wm = max(wm, wmv[k]);
+        for (int u = tid + 256 * kWm; u < p.n_tiles; u += 256) wm = max(wm, p.tile_wmax[(int64_t)s * p.n_tiles + u]);
         wm = wave_max(wm);
         if (lane == 0) wmax_s[wave] = wm;
-        const int K = p.k_lmk;
-        if (tid < rep * K) {
-            const int hs = tid / K, sl = tid % K;
-            const int32_t* set = p.lmk + (((int64_t)(kvh * rep + hs) * p.num_seqs + s) * p.n_sets) * K;
-            const int v = set[sl];
-            if (v >= j0 && v < dend && (sl == 0 || set[sl - 1] != v)) {
-                own_at = v - j0;
-                own_id = (kvh * rep + hs) * K + sl;
-            }
+        // the slot values are first used here (not where they were loaded)
+        asm volatile("" : "+v"(ov), "+v"(ovp));
+        if (tid < nown && ov >= j0 && ov < dend && (osl == 0 || ovp != ov)) {
+            own_at = ov - j0;
+            own_id = (kvh * rep + tid / K) * K + osl;
         }
     }
     __syncthreads();
     iend = uniform(min(len, j0 + 63 + max(max(wmax_s[0], wmax_s[1]), max(wmax_s[2], wmax_s[3]))));
     if (hh == 0) {
         if (own_at >= 0) atomicMin(own_s + own_at, own_id);
-        const int K = p.k_lmk;
         for (int e = tid + 256; e < rep * K; e += 256) {  // groups of more than 256 slots
             const int hs = e / K, sl = e % K;
             const int32_t* set = p.lmk + (((int64_t)(kvh * rep + hs) * p.num_seqs + s) * p.n_sets) * K;
