@@ -526,14 +526,16 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
 #pragma unroll
         for (int u = 0; u < RG; ++u) {
             if (!gact[u]) continue;
+            // the lane's own maximum decides whether the row maximum can move the running one past
+            // the rescale threshold (the row maximum is the largest of its four lanes'), so the
+            // cross-lane reduction runs only when some lane exceeds it
             float mx = NEG;
 #pragma unroll
             for (int stt = 0; stt < NST; ++stt)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) mx = fmaxf(mx, S[u][stt][r]);
-            mx = max_g4(mx);
-            const float mnew = fmaxf(m_run[u], mx);
-            if (__any(mnew > m_run[u] + thr)) {
+            if (__any(mx > m_run[u] + thr)) {
+                const float mnew = fmaxf(m_run[u], max_g4(mx));
                 const float alpha = m_run[u] == NEG ? 0.f : __builtin_amdgcn_exp2f((m_run[u] - mnew) * c2);
 #pragma unroll
                 for (int dt = 0; dt < D / 16; ++dt) acc[u][dt] *= alpha;
