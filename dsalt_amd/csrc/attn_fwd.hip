@@ -400,7 +400,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
         for (int dt = 0; dt < D / 16; ++dt) acc[u][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
         lacc[u] = floatx4{0.f, 0.f, 0.f, 0.f};
         l_run[u] = 0.f;
-        m_run[u] = -INFINITY;
+        // a finite start below every score: the first rescale factor exp2((start - m) c2) is
+        // exactly 0 and masked scores exp2(-inf) stay 0, with no test for an unset maximum
+        m_run[u] = -1e30f;
     }
     const float thr = p.thr;
     const float NEG = -INFINITY;
@@ -536,14 +538,14 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
                 for (int r = 0; r < 4; ++r) mx = fmaxf(mx, S[u][stt][r]);
             if (__any(mx > m_run[u] + thr)) {
                 const float mnew = fmaxf(m_run[u], max_g4(mx));
-                const float alpha = m_run[u] == NEG ? 0.f : __builtin_amdgcn_exp2f((m_run[u] - mnew) * c2);
+                const float alpha = __builtin_amdgcn_exp2f((m_run[u] - mnew) * c2);
 #pragma unroll
                 for (int dt = 0; dt < D / 16; ++dt) acc[u][dt] *= alpha;
                 lacc[u] *= alpha;
                 l_run[u] *= alpha;
                 m_run[u] = mnew;
             }
-            const float msc = m_run[u] == NEG ? 0.f : m_run[u] * c2;
+            const float msc = m_run[u] * c2;
 #pragma unroll
             for (int stt = 0; stt < NST; ++stt)
 #pragma unroll
