@@ -93,7 +93,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
     const int L = xcd_swizzle(blockIdx.x, total);
-    const int t = L % p.n_tiles;
+    // each XCD sweeps whole heads, the last tiles of a sequence (most landmarks) first
+    const int t = p.n_tiles - 1 - L % p.n_tiles;
     const int s = (L / p.n_tiles) % p.num_seqs;
     const int h = L / (p.n_tiles * p.num_seqs);
     int st, len;

@@ -239,11 +239,15 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
     const int nblk = ceil_div(p.n_tiles, RG);
-    const int total = p.n_heads * p.num_seqs * nblk;
-    const int L = xcd_swizzle(blockIdx.x, total);
-    const int b = L % nblk;
-    const int s = (L / nblk) % p.num_seqs;
-    const int h = L / (nblk * p.num_seqs);
+    // tile-major order, the last tiles of every sequence first (their rows see the most
+    // landmarks: the longest blocks start first and short ones fill the end of the grid);
+    // blocks reach the XCDs round-robin, so where 8 divides heads x sequences each XCD keeps
+    // the same (head, sequence) pairs, and their K/V rows in its L2, throughout
+    const int nhs = p.n_heads * p.num_seqs;
+    const int hs = blockIdx.x % nhs;
+    const int b = nblk - 1 - (int)blockIdx.x / nhs;
+    const int h = hs % p.n_heads;
+    const int s = hs / p.n_heads;
     int st, len;
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
     const int r0 = b * 64 * RG;
