@@ -432,17 +432,16 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
 #pragma unroll
         for (int u = 0; u < RG; ++u) {
             const RowGroup& R = rg[u];
-            // chunk class for this group (wave-uniform): 0 no row sees it; 1 every
-            // row sees every key; 2 all subtiles in range, window starts only;
-            // 3 all in range, both window ends; 4 landmarks all visible, no bias;
-            // 5 anything else (subtile by subtile)
+            // chunk class for this group (wave-uniform): 0 no row sees it; 1 every row sees
+            // every key; 3 band keys under the two-sided window mask (subtiles wholly outside
+            // it included: their scores are -inf and their products add zeros, cheaper than
+            // the branches that would tell them apart); 4 landmarks all visible, no bias;
+            // 5 landmarks subtile by subtile
             int kind;
             if (band) {
                 const int last = base + BN - 1;
                 if (base > R.whi || last < R.wlo) kind = 0;
-                else if (base + 15 < R.wlo || last - 15 > R.whi) kind = 5;
                 else if (base >= R.wLmax + (TR ? p.edge_keys : 0) && last <= R.wHmin) kind = 1;
-                else if (last <= R.wHmin) kind = 2;
                 else kind = 3;
             } else {
                 if (base >= R.wcmax) kind = 0;
@@ -460,28 +459,14 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
                     ko.load(kl, KT::RS, stt * 16, lane);
                     S[u][stt] = ko.dot(qr[u], zero);
                 }
-            } else if (kind == 4) {  // every slot visible to every row, landmark bias only
+            } else if (!band && kind == 4) {  // every slot visible to every row, landmark bias only
 #pragma unroll
                 for (int stt = 0; stt < NST; ++stt) {
                     KOp<T, D> ko;
                     ko.load(kl, KT::RS, stt * 16, lane);
                     S[u][stt] = ko.dot(qr[u], *(const floatx4*)(lbs + base + stt * 16 + lane_off));
                 }
-            } else if (kind == 2) {
-#pragma unroll
-                for (int stt = 0; stt < NST; ++stt) {
-                    const int a = base + stt * 16;
-                    const int tl = R.lo - a - lane_off;
-                    floatx4 ci;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) ci[r] = r < tl ? NEG : 0.f;
-                    if (TR && a < R.wLmax + p.edge_keys)  // the soft edge reaches this subtile
-                        band_edge(p, R, a, lane_off, tl, false, ci);
-                    KOp<T, D> ko;
-                    ko.load(kl, KT::RS, stt * 16, lane);
-                    S[u][stt] = ko.dot(qr[u], ci);
-                }
-            } else if (kind == 3) {
+            } else if (band && kind == 3) {
 #pragma unroll
                 for (int stt = 0; stt < NST; ++stt) {
                     const int a = base + stt * 16;
@@ -498,30 +483,21 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
                     ko.load(kl, KT::RS, stt * 16, lane);
                     S[u][stt] = ko.dot(qr[u], ci);
                 }
-            } else if (kind == 5) {
+            } else if (!band && kind == 5) {
 #pragma unroll
                 for (int stt = 0; stt < NST; ++stt) {
                     const int a = base + stt * 16;
-                    act[u][stt] = band ? (a <= R.whi && a + 15 >= R.wlo) : (a < R.wcmax);
+                    act[u][stt] = a < R.wcmax;
                     if (!act[u][stt]) {
                         S[u][stt] = floatx4{NEG, NEG, NEG, NEG};
                         continue;
                     }
+                    // slots past the valid count are masked below (a + 15 < 512)
+                    const floatx4 bv = has_bias ? *(const floatx4*)(lbs + a + lane_off) : zero;
+                    const int tc = R.cnt - a - lane_off;
                     floatx4 ci;
-                    if (band) {
-                        const int tl = R.lo - a - lane_off;
-                        const int x0 = a + lane_off - R.lo;
-                        const unsigned wd = (unsigned)R.hi - (unsigned)R.lo;
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) ci[r] = (unsigned)(x0 + r) <= wd ? 0.f : NEG;
-                        if (TR && a < R.wLmax + p.edge_keys) band_edge(p, R, a, lane_off, tl, true, ci);
-                    } else {
-                        // slots past the valid count are masked below (a + 15 < 512)
-                        const floatx4 bv = has_bias ? *(const floatx4*)(lbs + a + lane_off) : zero;
-                        const int tc = R.cnt - a - lane_off;
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) ci[r] = r < tc ? bv[r] : NEG;
-                    }
+                    for (int r = 0; r < 4; ++r) ci[r] = r < tc ? bv[r] : NEG;
                     KOp<T, D> ko;
                     ko.load(kl, KT::RS, stt * 16, lane);
                     S[u][stt] = ko.dot(qr[u], ci);
