@@ -294,10 +294,14 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
         const int base = band ? cs + c * BN : c * BN;
         floatx4 dS[NST];
         bool act[NST];
+        // a band chunk some row sees is computed whole under the window mask (a subtile wholly
+        // outside every window scores -inf and adds zeros: cheaper than the branches that
+        // would skip it); landmark subtiles past the largest visible count are skipped
+        const bool cact = band ? (base <= whi && base + BN - 1 >= wlo) : true;
 #pragma unroll
         for (int stt = 0; stt < NST; ++stt) {
             const int a = base + stt * 16;
-            act[stt] = band ? (a <= whi && a + 15 >= wlo) : (a < wcmax);
+            act[stt] = band ? cact : (a < wcmax);
             if (!act[stt]) {
                 dS[stt] = floatx4{0.f, 0.f, 0.f, 0.f};
                 continue;
@@ -306,7 +310,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
             floatx4 eg = floatx4{0.f, 0.f, 0.f, 0.f};  // d(bias)/d(w~) per key (training variant)
             if (band) {
                 const int tl = lo - a - lane_off, th = hi - a - lane_off;
-                if (a >= lo_edge && a + 15 <= wHmin) {
+                if (TR && a >= lo_edge && a + 15 <= wHmin) {  // training: no edge bias, no mask
                     ci = floatx4{0.f, 0.f, 0.f, 0.f};
                 } else {
                     // below every row's diagonal only the window start masks; the soft
