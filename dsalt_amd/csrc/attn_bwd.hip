@@ -943,7 +943,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && sizeof(T) == 2 && D == 64) ? 4
     typedef typename QS::QT QT;
     __shared__ __attribute__((aligned(16))) QS q;
     __shared__ int lpos[kMaxLandmarks];
-    __shared__ int cmin_s[NQS], cmax_s[NQS];
+    __shared__ int cmax_s[NQS];
     __shared__ int nvalid_s;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
@@ -1032,11 +1032,8 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && sizeof(T) == 2 && D == 64) ? 4
             q.lse2[tid] = rl;
             q.dlt[tid] = rd;
             q.key[tid] = c;
-            const int mn = row_min16(c), mx = row_max16(c);
-            if ((tid & 15) == 0) {
-                cmin_s[tid >> 4] = mn;
-                cmax_s[tid >> 4] = mx;
-            }
+            const int mx = row_max16(c);
+            if ((tid & 15) == 0) cmax_s[tid >> 4] = mx;
         }
         __syncthreads();
         if (t + p.n_chunks < ntile) fetch(t + p.n_chunks);
@@ -1045,24 +1042,27 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && sizeof(T) == 2 && D == 64) ? 4
             const int a = sl0 + u * 16;
             floatx4 P[NQS], dS[NQS];
             bool act[NQS];
+            // a tile with some row seeing one of the wave's slots is computed whole under the
+            // count mask (subtiles whose rows see none of them add zeros: cheaper than the
+            // branches that would skip them or drop the mask)
+            int tmx = cmax_s[0];
+#pragma unroll
+            for (int qs = 1; qs < NQS; ++qs) tmx = max(tmx, cmax_s[qs]);
+            const bool tact = uniform(tmx) > a;
 #pragma unroll
             for (int qs = 0; qs < NQS; ++qs) {
-                act[qs] = uniform(cmax_s[qs]) > a;
+                act[qs] = tact;
                 if (!act[qs]) {
                     P[qs] = floatx4{0.f, 0.f, 0.f, 0.f};
                     dS[qs] = P[qs];
                     continue;
                 }
                 floatx4 ci;
-                if (uniform(cmin_s[qs]) > a + 15) {
-                    ci = floatx4{bsl[u], bsl[u], bsl[u], bsl[u]};
-                } else {
-                    const int4 c4 = *(const int4*)(q.key + qs * 16 + lane_off);
-                    ci[0] = slot[u] < c4.x ? bsl[u] : NEG;
-                    ci[1] = slot[u] < c4.y ? bsl[u] : NEG;
-                    ci[2] = slot[u] < c4.z ? bsl[u] : NEG;
-                    ci[3] = slot[u] < c4.w ? bsl[u] : NEG;
-                }
+                const int4 c4 = *(const int4*)(q.key + qs * 16 + lane_off);
+                ci[0] = slot[u] < c4.x ? bsl[u] : NEG;
+                ci[1] = slot[u] < c4.y ? bsl[u] : NEG;
+                ci[2] = slot[u] < c4.z ? bsl[u] : NEG;
+                ci[3] = slot[u] < c4.w ? bsl[u] : NEG;
                 const floatx4 sc = dot_rows<T, D>(q.q, QT::RS, qs * 16, lane, kr[u], ci);
                 const floatx4 dp = dot_rows<T, D>(q.d, QT::RS, qs * 16, lane, vr[u], floatx4{0.f, 0.f, 0.f, 0.f});
                 const floatx4 l4 = *(const floatx4*)(q.lse2 + qs * 16 + lane_off);
