@@ -296,12 +296,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
         bool act[NST];
         // a band chunk some row sees is computed whole under the window mask (a subtile wholly
         // outside every window scores -inf and adds zeros: cheaper than the branches that
-        // would skip it); landmark subtiles past the largest visible count are skipped
+        // would skip it; the training variant, whose edge terms cost more, skips it);
+        // landmark subtiles past the largest visible count are skipped
         const bool cact = band ? (base <= whi && base + BN - 1 >= wlo) : true;
 #pragma unroll
         for (int stt = 0; stt < NST; ++stt) {
             const int a = base + stt * 16;
-            act[stt] = band ? cact : (a < wcmax);
+            act[stt] = band ? (TR ? (a <= whi && a + 15 >= wlo) : cact) : (a < wcmax);
             if (!act[stt]) {
                 dS[stt] = floatx4{0.f, 0.f, 0.f, 0.f};
                 continue;

@@ -433,15 +433,17 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
         for (int u = 0; u < RG; ++u) {
             const RowGroup& R = rg[u];
             // chunk class for this group (wave-uniform): 0 no row sees it; 1 every row sees
-            // every key; 3 band keys under the two-sided window mask (subtiles wholly outside
-            // it included: their scores are -inf and their products add zeros, cheaper than
-            // the branches that would tell them apart); 4 landmarks all visible, no bias;
-            // 5 landmarks subtile by subtile
+            // every key; 2 (64-key chunks) every key at or below every row, window starts only;
+            // 3 band keys under the two-sided window mask (subtiles wholly outside it included:
+            // their scores are -inf and their products add zeros, cheaper than the branches
+            // that would tell them apart); 4 landmarks all visible, no bias; 5 landmarks
+            // subtile by subtile
             int kind;
             if (band) {
                 const int last = base + BN - 1;
                 if (base > R.whi || last < R.wlo) kind = 0;
                 else if (base >= R.wLmax + (TR ? p.edge_keys : 0) && last <= R.wHmin) kind = 1;
+                else if (BN > 32 && last <= R.wHmin) kind = 2;
                 else kind = 3;
             } else {
                 if (base >= R.wcmax) kind = 0;
@@ -465,6 +467,20 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
                     KOp<T, D> ko;
                     ko.load(kl, KT::RS, stt * 16, lane);
                     S[u][stt] = ko.dot(qr[u], *(const floatx4*)(lbs + base + stt * 16 + lane_off));
+                }
+            } else if (band && BN > 32 && kind == 2) {
+#pragma unroll
+                for (int stt = 0; stt < NST; ++stt) {
+                    const int a = base + stt * 16;
+                    const int tl = R.lo - a - lane_off;
+                    floatx4 ci;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ci[r] = r < tl ? NEG : 0.f;
+                    if (TR && a < R.wLmax + p.edge_keys)  // the soft edge reaches this subtile
+                        band_edge(p, R, a, lane_off, tl, false, ci);
+                    KOp<T, D> ko;
+                    ko.load(kl, KT::RS, stt * 16, lane);
+                    S[u][stt] = ko.dot(qr[u], ci);
                 }
             } else if (band && kind == 3) {
 #pragma unroll
