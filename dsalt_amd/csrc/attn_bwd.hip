@@ -1244,12 +1244,17 @@ template <typename T, int D>
 static hipError_t bwd_run(const AttnParams& p, bool plan_given, hipStream_t stream) {
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
     const int total_kv = p.n_kv_heads * p.num_seqs * p.n_tiles;
-    if (!plan_given) plan_launch(p, stream);
+    if (!plan_given) {
+        const hipError_t e = plan_launch(p, stream);
+        if (e != hipSuccess) return e;
+    }
     constexpr int BN = BwdShape<T, D>::BN;
-    const bool bn64 = sizeof(T) == 2 && D == 64 && (p.variant & DSALT_VARIANT_DQ_BN64);
-    if (bn64) {
-        if (p.w_cont) DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, 64, true>), dim3(total), dim3(256), 0, stream, p);
-        else DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, 64, false>), dim3(total), dim3(256), 0, stream, p);
+    constexpr bool kBn64 = sizeof(T) == 2 && D == 64;  // the only shape with a 64-key dQ tiling
+    if (kBn64 && (p.variant & DSALT_VARIANT_DQ_BN64)) {
+        if constexpr (kBn64) {
+            if (p.w_cont) DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, 64, true>), dim3(total), dim3(256), 0, stream, p);
+            else DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, 64, false>), dim3(total), dim3(256), 0, stream, p);
+        }
     } else {
         if (p.w_cont) DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, BN, true>), dim3(total), dim3(256), 0, stream, p);
         else DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, BN, false>), dim3(total), dim3(256), 0, stream, p);

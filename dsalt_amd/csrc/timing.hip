@@ -48,7 +48,7 @@ void timing_begin(const char* name, hipStream_t stream) {
     p.a = take_event();
     p.b = take_event();
     if (!p.a || !p.b) return;
-    hipEventRecord(p.a, stream);
+    if (hipEventRecord(p.a, stream) != hipSuccess) return;  // this launch goes untimed
     g_pending.push_back(p);
     t_open = (int)g_pending.size() - 1;
 }
@@ -56,7 +56,8 @@ void timing_begin(const char* name, hipStream_t stream) {
 void timing_end(hipStream_t stream) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (t_open < 0 || t_open >= (int)g_pending.size()) return;
-    hipEventRecord(g_pending[t_open].b, stream);
+    if (hipEventRecord(g_pending[t_open].b, stream) != hipSuccess)
+        g_pending.erase(g_pending.begin() + t_open);  // no end mark: drop the launch from the report
     t_open = -1;
 }
 
