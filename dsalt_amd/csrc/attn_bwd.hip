@@ -304,7 +304,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
             const int a = base + stt * 16;
             act[stt] = band ? (TR ? (a <= whi && a + 15 >= wlo) : cact) : (a < wcmax);
             if (!act[stt]) {
-                dS[stt] = floatx4{0.f, 0.f, 0.f, 0.f};
+                // an inactive band chunk of the inference variant adds nothing (both subtiles
+                // share its activity, so its dS is never read); a skipped subtile beside an
+                // active one adds zeros
+                if (!band || TR) dS[stt] = floatx4{0.f, 0.f, 0.f, 0.f};
                 continue;
             }
             floatx4 ci;
