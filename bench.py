@@ -134,7 +134,15 @@ def traffic_from(root: str, wl_name: str, copy_mib: int = 1024) -> dict:
     w_fac = known / copy_reading("copy_write", "WRITE_SIZE")
     fetch = read_pmc(os.path.join(root, "fetch"))
     write = read_pmc(os.path.join(root, "write"))
-    res = {"_calibration": {"copy_bytes": known, "fetch_factor": f_fac, "write_factor": w_fac},
+    b = f"python -u bench.py --workload {wl_name} --steps 2 --warmup 1 --no-cpu-baseline"
+    res = {"_commands": [f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/fetch -o run -- {b}",
+                         f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/write -o run -- {b}",
+                         f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/copy_fetch -o run -- "
+                         f"python -u bench.py --copy-calibration {copy_mib}",
+                         f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/copy_write -o run -- "
+                         f"python -u bench.py --copy-calibration {copy_mib}",
+                         f"python bench.py --traffic-from <out> --workload {wl_name}"],
+           "_calibration": {"copy_bytes": known, "fetch_factor": f_fac, "write_factor": w_fac},
            "_sources": kernel_source_sha()}
     for k in sorted(set(fetch) & set(write) & set(LABELS)):
         fb = fetch[k]["FETCH_SIZE"] * 1024.0 * f_fac
