@@ -113,7 +113,8 @@ hipError_t plan_launch(const AttnParams& p, hipStream_t stream);
 hipError_t fwd_launch(AttnParams p, void* ws, void* plan, hipStream_t stream);
 // training variant: integer windows floor(w~) + 1 written into `w_int` ([T] int32)
 hipError_t train_windows_launch(const AttnParams& p, int* w_int, hipStream_t stream);
-size_t bwd_workspace(const AttnParams& p);
+// plan_given: the caller supplies the row plan (no room for it in the workspace)
+size_t bwd_workspace(const AttnParams& p, bool plan_given);
 // plan: the row plan the forward wrote for the same rows, or null (computed here)
 hipError_t bwd_launch(AttnParams p, void* ws, const void* plan, hipStream_t stream);
 // training variant: d_w[t] = sum over heads of dw_h[t, h], in head order

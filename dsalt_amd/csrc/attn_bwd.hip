@@ -1230,10 +1230,10 @@ static int lmk_chunks(const AttnParams& p) {
     return max(ceil_div(p.max_seqlen, rows), min(fill, ceil_div(p.max_seqlen, 64)));
 }
 
-size_t bwd_workspace(const AttnParams& p) {
+size_t bwd_workspace(const AttnParams& p, bool plan_given) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const int nch = lmk_chunks(p);
-    size_t b = plan_bytes(p);
+    size_t b = plan_given ? 0 : plan_bytes(p);
     b += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
     b += al(sizeof(int) * (size_t)p.total_len * p.n_heads);
     b += al(sizeof(float) * (size_t)p.total_len * p.n_heads);
@@ -1293,9 +1293,8 @@ hipError_t bwd_launch(AttnParams p, void* ws, const void* plan, hipStream_t stre
     if (plan) {
         char* pw = (char*)const_cast<void*>(plan);  // read only: the kernels never write it
         plan_carve(p, pw);
-        w += plan_bytes(p);
     } else {
-        plan_carve(p, w);
+        plan_carve(p, w);  // advances w past the plan
     }
     p.delta = (float*)w;
     w += al(sizeof(float) * (size_t)p.total_len * p.n_heads);

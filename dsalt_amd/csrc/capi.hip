@@ -241,17 +241,18 @@ size_t dsalt_plan_bytes(const dsalt_problem* p) {
     return dsalt::plan_bytes(attn_common(*p, 1.0f));
 }
 
+// the forward's only workspace is the row plan, which a caller-given plan buffer replaces
 size_t dsalt_fwd_workspace_bytes(const dsalt_fwd_args* a) {
     if (!a || check_problem(a->p, true)) return 0;
-    return dsalt::plan_bytes(attn_common(a->p, 1.0f));
+    return a->plan ? 0 : dsalt::plan_bytes(attn_common(a->p, 1.0f));
 }
 
 int dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream) {
     dsalt::AttnParams p;
     int rc = fwd_params(a, true, &p);
     if (rc) return rc;
-    const size_t need = dsalt::plan_bytes(p);
-    if (!a->workspace || a->workspace_bytes < need)
+    const size_t need = a->plan ? 0 : dsalt::plan_bytes(p);
+    if (need && (!a->workspace || a->workspace_bytes < need))
         return fail(DSALT_ERR_WORKSPACE, "forward needs %zu workspace bytes, got %zu", need, a->workspace_bytes);
     return hip_status(dsalt::fwd_launch(p, a->workspace, a->plan, (hipStream_t)stream), "dsalt_fwd");
 }
@@ -323,7 +324,7 @@ int dsalt_fwd_noalloc(const dsalt_fwd_args* a, dsalt_stream_t stream) {
 size_t dsalt_train_fwd_workspace_bytes(const dsalt_train_fwd_args* a) {
     if (!a || check_problem(a->base.p, true)) return 0;
     const dsalt::AttnParams p = attn_common(a->base.p, 1.0f);
-    return wint_bytes(p) + dsalt::plan_bytes(p);
+    return wint_bytes(p) + (a->base.plan ? 0 : dsalt::plan_bytes(p));
 }
 
 int dsalt_train_fwd(const dsalt_train_fwd_args* a, dsalt_stream_t stream) {
@@ -332,7 +333,7 @@ int dsalt_train_fwd(const dsalt_train_fwd_args* a, dsalt_stream_t stream) {
     int rc = fwd_params(&a->base, false, &p);
     if (rc) return rc;
     if ((rc = train_params(a->w_cont, a->tau_win, a->win_edge, &p))) return rc;
-    const size_t need = wint_bytes(p) + dsalt::plan_bytes(p);
+    const size_t need = wint_bytes(p) + (a->base.plan ? 0 : dsalt::plan_bytes(p));
     if (!a->base.workspace || a->base.workspace_bytes < need)
         return fail(DSALT_ERR_WORKSPACE, "training forward needs %zu workspace bytes, got %zu", need,
                     a->base.workspace_bytes);
@@ -395,14 +396,14 @@ static int bwd_params(const dsalt_bwd_args* a, dsalt::AttnParams* out, bool need
 size_t dsalt_bwd_workspace_bytes(const dsalt_bwd_args* a) {
     dsalt::AttnParams p;
     if (bwd_params(a, &p)) return 0;
-    return dsalt::bwd_workspace(p);
+    return dsalt::bwd_workspace(p, a->plan != nullptr);
 }
 
 int dsalt_bwd(const dsalt_bwd_args* a, dsalt_stream_t stream) {
     dsalt::AttnParams p;
     int rc = bwd_params(a, &p);
     if (rc) return rc;
-    size_t need = dsalt::bwd_workspace(p);
+    size_t need = dsalt::bwd_workspace(p, a->plan != nullptr);
     if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
         return fail(DSALT_ERR_WORKSPACE, "backward needs %zu workspace bytes, got %zu", need, a->workspace_bytes);
     return hip_status(dsalt::bwd_launch(p, a->workspace, a->plan, (hipStream_t)stream), "dsalt_bwd");
@@ -416,7 +417,7 @@ static size_t train_bwd_extra(const dsalt::AttnParams& p) {
 size_t dsalt_train_bwd_workspace_bytes(const dsalt_train_bwd_args* a) {
     dsalt::AttnParams p;
     if (!a || bwd_params(&a->base, &p, false)) return 0;
-    return train_bwd_extra(p) + dsalt::bwd_workspace(p);
+    return train_bwd_extra(p) + dsalt::bwd_workspace(p, a->base.plan != nullptr);
 }
 
 int dsalt_train_bwd(const dsalt_train_bwd_args* a, dsalt_stream_t stream) {
@@ -426,7 +427,7 @@ int dsalt_train_bwd(const dsalt_train_bwd_args* a, dsalt_stream_t stream) {
     if (rc) return rc;
     if ((rc = train_params(a->w_cont, a->tau_win, a->win_edge, &p))) return rc;
     if (!a->d_w) return fail(DSALT_ERR_INVALID, "d_w is required");
-    const size_t need = train_bwd_extra(p) + dsalt::bwd_workspace(p);
+    const size_t need = train_bwd_extra(p) + dsalt::bwd_workspace(p, a->base.plan != nullptr);
     if (!a->base.workspace || a->base.workspace_bytes < need || !aligned16(a->base.workspace))
         return fail(DSALT_ERR_WORKSPACE, "training backward needs %zu workspace bytes, got %zu", need,
                     a->base.workspace_bytes);

@@ -95,6 +95,17 @@ def _workspace(nbytes: int, dev) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
 
 
+def _set_workspace(args, nbytes: int, dev):
+    """A workspace of nbytes in args (none when nbytes is 0: a caller-given plan replaces the
+    forward's only workspace); returns the tensor to keep alive."""
+    if nbytes == 0:
+        args.workspace, args.workspace_bytes = None, 0
+        return None
+    ws = _workspace(nbytes, dev)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+    return ws
+
+
 # --------------------------------------------------------------------- selection
 def select_landmarks(h: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, w: torch.Tensor,
                      cu_seqlens: torch.Tensor, k_lmk: int, *, max_seqlen: int | None = None,
@@ -240,8 +251,7 @@ def attention_forward(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias=None, *, scale=N
         return out, lse
     dev = out.device
     L = _lib.load()
-    ws = _workspace(L.dsalt_fwd_workspace_bytes(ctypes.byref(a)), dev)
-    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    ws = _set_workspace(a, L.dsalt_fwd_workspace_bytes(ctypes.byref(a)), dev)  # noqa: F841 (kept alive)
     _lib.check("dsalt_fwd", L.dsalt_fwd(ctypes.byref(a), _stream(dev)))
     return out, lse
 

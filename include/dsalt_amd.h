@@ -318,21 +318,28 @@ size_t dsalt_plan_bytes(const dsalt_problem* p);
 size_t dsalt_select_workspace_bytes(const dsalt_select_args* a);
 int    dsalt_select(const dsalt_select_args* a, dsalt_stream_t stream);
 
+/* Workspace of dsalt_fwd: the row plan, or 0 when a->plan supplies it. */
 size_t dsalt_fwd_workspace_bytes(const dsalt_fwd_args* a);
 int    dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream);
 
 /* dsalt_fwd without allocations or a workspace argument.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under HIP
- * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The row plan
- * goes to a file-scope device array of DSALT_FWD_NOALLOC_MAX_PLAN_BYTES per GPU (held
- * until the process ends) unless a->plan is given; a->workspace is not read.  Larger
- * problems (dsalt_plan_bytes(&a->p) above the maximum, i.e. more than 31,775 64-row
- * tiles over all sequences) are rejected with DSALT_ERR_WORKSPACE.  Every call on one
- * GPU shares that array: calls that overlap on one GPU (several streams or host
- * threads) race and must be ordered by the caller.  Outputs are those of dsalt_fwd. */
+ * graph capture, serving loops on one stream, harnesses that forbid hipMalloc).  The
+ * row plan goes to a file-scope device array of DSALT_FWD_NOALLOC_MAX_PLAN_BYTES per
+ * GPU (held until the process ends) unless a->plan is given; a->workspace is not read.
+ * Problems whose plan does not fit (dsalt_plan_bytes(&a->p) >
+ * DSALT_FWD_NOALLOC_MAX_PLAN_BYTES: with its three 256-byte-aligned sections, more than
+ * 31,772 tiles, where the tiles are num_seqs * ceil(max_seqlen / 64)) are rejected with
+ * DSALT_ERR_WORKSPACE.
+ * Single-stream contract: every call on one GPU shares that array, so calls without
+ * a->plan must be ordered on one stream (or ordered by the caller across streams and
+ * host threads).  Overlapping calls race on the array without any error being
+ * reported.  Outputs are those of dsalt_fwd. */
 #define DSALT_FWD_NOALLOC_MAX_PLAN_BYTES ((size_t)4 << 20)
 int    dsalt_fwd_noalloc(const dsalt_fwd_args* a, dsalt_stream_t stream);
 
+/* Workspace of dsalt_bwd (per-row data and landmark partials; the row plan too unless
+ * a->plan supplies it). */
 size_t dsalt_bwd_workspace_bytes(const dsalt_bwd_args* a);
 int    dsalt_bwd(const dsalt_bwd_args* a, dsalt_stream_t stream);
 

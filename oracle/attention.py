@@ -143,11 +143,15 @@ def attention_probs(q, k, w, cu, lmk_idx, scale, seq=0, lmk_bias=None, block_siz
     return P
 
 
-def attention_bwd(q, k, v, w, cu, lmk_idx, scale, dout, lmk_bias=None, block_size=None, out=None):
+def attention_bwd(q, k, v, w, cu, lmk_idx, scale, dout, lmk_bias=None, block_size=None, out=None,
+                  operand_round=None):
     """(dq, dk, dv, d_bias) in float64 for the kernel semantics.
 
     ``out`` is the forward output used for ``delta``; when None the exact fp64
-    forward is used.
+    forward is used.  ``operand_round`` (tests of the gradient checker only) is applied
+    to P and dS before the products that consume them, as 16-bit kernels round those
+    operands to the input dtype (the reference casts P to the input dtype before its
+    products, ``dsalt_triton_bwd.py:148,196-199``); None keeps everything in fp64.
     """
     q = np.asarray(q, np.float64)
     k = np.asarray(k, np.float64)
@@ -181,6 +185,9 @@ def attention_bwd(q, k, v, w, cu, lmk_idx, scale, dout, lmk_bias=None, block_siz
                 vl = vh[st + np.maximum(pos, 0)]
                 dsb = pb * (doh[st + i0:st + i1] @ vb.T - dl)
                 dsl = pl * (doh[st + i0:st + i1] @ vl.T - dl)
+                db_row = dsl.sum(0)
+                if operand_round is not None:
+                    pb, pl, dsb, dsl = (operand_round(a) for a in (pb, pl, dsb, dsl))
                 kb = kh[st + kr0:st + i1]
                 kl = kh[st + np.maximum(pos, 0)]
                 dq[st + i0:st + i1, h] += scale * (dsb @ kb + dsl @ kl)
@@ -189,7 +196,7 @@ def attention_bwd(q, k, v, w, cu, lmk_idx, scale, dout, lmk_bias=None, block_siz
                 ok = pos >= 0
                 np.add.at(dk[:, h], st + pos[ok], scale * (dsl.T @ qh[st + i0:st + i1])[ok])
                 np.add.at(dv[:, h], st + pos[ok], (pl.T @ doh[st + i0:st + i1])[ok])
-                dbias[h, s, b] += dsl.sum(0)
+                dbias[h, s, b] += db_row
     if rep > 1:
         dk = dk.reshape(T, H // rep, rep, D).sum(2)
         dv = dv.reshape(T, H // rep, rep, D).sum(2)

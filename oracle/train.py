@@ -98,3 +98,77 @@ def train_bwd(q, k, v, w_cont, cu, lmk_pos, lmk_logw, scale, tau_win, win_edge, 
                 rows = (pos <= np.arange(L)) & (pos < np.arange(L) - wv)
                 dlogw[h, s, slot] = ds[rows, pos].sum()
     return dq, dk, dv, dw, dlogw
+
+
+def _banded(q, k, w_cont, cu, lmk_pos, lmk_logw, scale, tau_win, win_edge, rb):
+    """Row blocks of at most ``rb`` rows with the logits over their band keys [kr0, i1) and
+    over the landmark slots (the same semantics as ``train_bias``, with each slot a key of
+    its own; the sets of the workloads hold distinct positions, where the two agree)."""
+    T, H, D = q.shape
+    for h in range(H):
+        for s in range(len(cu) - 1):
+            st, en = int(cu[s]), int(cu[s + 1])
+            L = en - st
+            wv = np.asarray(w_cont[st:en], np.float64)
+            pos = np.asarray(lmk_pos[h, s]).astype(np.int64)
+            lw = np.asarray(lmk_logw[h, s], np.float64)
+            okp = (pos >= 0) & (pos < L)
+            pz = np.where(okp, pos, 0)
+            for i0 in range(0, L, rb):
+                i1 = min(L, i0 + rb)
+                rows = np.arange(i0, i1)
+                wr = wv[i0:i1]
+                kr0 = int(max(0, np.floor((rows - np.maximum(wr, 0.0)).min())))
+                d = (rows[:, None] - np.arange(kr0, i1)[None, :]).astype(np.float64)
+                z = (wr[:, None] - d) / tau_win
+                in_band = (d >= 0) & (d <= wr[:, None])
+                core = d <= wr[:, None] - win_edge
+                sig = _sigmoid(z)
+                win = np.where(core, 0.0, np.log(np.maximum(sig, 1e-20)))
+                sb = (q[st + i0:st + i1, h] @ k[st + kr0:st + i1, h].T) * scale + np.where(in_band, win, -np.inf)
+                dbw = np.where(in_band & ~core, (1.0 - sig) / tau_win, 0.0)
+                vis = okp[None, :] & (pos[None, :] <= rows[:, None]) & (pos[None, :] < rows[:, None] - wr[:, None])
+                sl = (q[st + i0:st + i1, h] @ k[st + pz, h].T) * scale + np.where(vis, lw[None, :], -np.inf)
+                yield h, s, st, i0, i1, kr0, pz, okp, sb, sl, dbw
+
+
+def train_fwd_banded(q, k, v, w_cont, cu, lmk_pos, lmk_logw, scale, tau_win, win_edge, rb=512):
+    """``train_fwd`` over banded row blocks: the same values for full-length sequences."""
+    q, k, v = (np.asarray(t, np.float64) for t in (q, k, v))
+    out = np.zeros_like(q)
+    lse = np.full(q.shape[:2], -np.inf)
+    for h, s, st, i0, i1, kr0, pz, okp, sb, sl, _ in _banded(q, k, w_cont, cu, lmk_pos, lmk_logw, scale, tau_win,
+                                                              win_edge, rb):
+        m = np.maximum(sb.max(1), sl.max(1) if sl.shape[1] else -np.inf)[:, None]
+        pb, pl = np.exp(sb - m), np.exp(sl - m)
+        l = pb.sum(1, keepdims=True) + pl.sum(1, keepdims=True)
+        out[st + i0:st + i1, h] = (pb @ v[st + kr0:st + i1, h] + pl @ v[st + pz, h]) / l
+        lse[st + i0:st + i1, h] = (m + np.log(l))[:, 0]
+    return out, lse
+
+
+def train_bwd_banded(q, k, v, w_cont, cu, lmk_pos, lmk_logw, scale, tau_win, win_edge, dout, out=None, rb=512):
+    """``train_bwd`` over banded row blocks (dq, dk, dv, d_w, d_logw)."""
+    q, k, v, dout = (np.asarray(t, np.float64) for t in (q, k, v, dout))
+    o_ref, lse = train_fwd_banded(q, k, v, w_cont, cu, lmk_pos, lmk_logw, scale, tau_win, win_edge, rb)
+    o = o_ref if out is None else np.asarray(out, np.float64)
+    delta = (o * dout).sum(-1)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    dw = np.zeros(q.shape[0])
+    dlogw = np.zeros(np.asarray(lmk_logw).shape)
+    for h, s, st, i0, i1, kr0, pz, okp, sb, sl, dbw in _banded(q, k, w_cont, cu, lmk_pos, lmk_logw, scale, tau_win,
+                                                                win_edge, rb):
+        r = slice(st + i0, st + i1)
+        ls = lse[r, h][:, None]
+        pb, pl = np.exp(sb - ls), np.exp(sl - ls)
+        dl = delta[r, h][:, None]
+        dsb = pb * (dout[r, h] @ v[st + kr0:st + i1, h].T - dl)
+        dsl = pl * (dout[r, h] @ v[st + pz, h].T - dl)
+        dq[r, h] += scale * (dsb @ k[st + kr0:st + i1, h] + dsl @ k[st + pz, h])
+        dk[st + kr0:st + i1, h] += scale * (dsb.T @ q[r, h])
+        dv[st + kr0:st + i1, h] += pb.T @ dout[r, h]
+        np.add.at(dk[:, h], st + pz[okp], scale * (dsl.T @ q[r, h])[okp])
+        np.add.at(dv[:, h], st + pz[okp], (pl.T @ dout[r, h])[okp])
+        dw[r] += (dsb * dbw).sum(1)
+        dlogw[h, s] += dsl.sum(0)
+    return dq, dk, dv, dw, dlogw

@@ -80,15 +80,17 @@ def oracle_fwd_heads(q, k, v, w, cu, idx, scale, heads, block_size=None):
     return _pool_map(one, heads)
 
 
-def oracle_bwd_heads(q, k, v, w, cu, idx, scale, dout, heads):
+def oracle_bwd_heads(q, k, v, w, cu, idx, scale, dout, heads, out=None):
     """float64 oracle (dq, dk, dv, d_bias) of the listed heads (one key/value head per query
-    head), one head per thread."""
+    head), one head per thread; ``out`` [T, H, D] (the stored forward output) feeds delta."""
     from oracle import attention as OA
     wn, cun = w.numpy(), cu.numpy()
+    o = None if out is None else f64(out)
 
     def one(hh):
         return OA.attention_bwd(f64(q[:, hh:hh + 1]), f64(k[:, hh:hh + 1]), f64(v[:, hh:hh + 1]), wn, cun,
-                                idx[hh:hh + 1], scale, f64(dout[:, hh:hh + 1]))
+                                idx[hh:hh + 1], scale, f64(dout[:, hh:hh + 1]),
+                                out=None if o is None else o[:, hh:hh + 1])
 
     return _pool_map(one, heads)
 
@@ -153,3 +155,92 @@ def topk_violations(idx, scores, w, cu, k):
             if g > 0:
                 bad += 1
     return bad, gap
+
+
+# ---------------------------------------------------------------- gradient checker
+# A gradient is compared per head in two ways, so that a large landmark row cannot hide the
+# error of the ordinary rows (a landmark row sums contributions of up to every query of its
+# sequence, so its entries can be tens of times larger than any other row's):
+#   * class bound: rows are split into landmark rows (a position that some set of the head
+#     holds) and all others; in each class max |a - b| / max |b| < tol;
+#   * row bound: every row whose norm is at least ROW_FLOOR times the median row norm of its
+#     class satisfies ||a_i - b_i|| / ||b_i|| < tol.
+# Rows below the floor (gradients that cancel to almost nothing, such as the first row's dq)
+# are held by the class bound only.
+ROW_FLOOR = 0.25
+
+
+def landmark_rows(idx, cu, T: int) -> np.ndarray:
+    """bool [T, H]: row t holds a position of one of head h's landmark sets.
+
+    idx [H, S, n_sets, k] (or [H, S, k]) sequence-relative positions, -1 for empty slots."""
+    idx = np.asarray(idx)
+    if idx.ndim == 3:
+        idx = idx[:, :, None, :]
+    cu = np.asarray(cu).astype(np.int64)
+    H, S = idx.shape[:2]
+    m = np.zeros((T, H), bool)
+    for h in range(H):
+        for s in range(S):
+            st, L = int(cu[s]), int(cu[s + 1] - cu[s])
+            p = idx[h, s].reshape(-1).astype(np.int64)
+            p = p[(p >= 0) & (p < L)]
+            m[st + p, h] = True
+    return m
+
+
+def grad_errors(a, b, lmk=None, floor: float = ROW_FLOOR) -> dict:
+    """Class and row errors of one head's gradient a against b ([T, D]); lmk [T] bool marks
+    the landmark rows (None: one class)."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    T = b.shape[0]
+    lmk = np.zeros(T, bool) if lmk is None else np.asarray(lmk, bool)
+    rn = np.linalg.norm(b, axis=1)
+    en = np.linalg.norm(a - b, axis=1)
+    out = {}
+    for cls, m in (("landmark", lmk), ("other", ~lmk)):
+        if not m.any():
+            continue
+        den = np.abs(b[m]).max()
+        out[f"{cls}_class"] = float(np.abs(a[m] - b[m]).max() / (den if den > 0 else 1.0))
+        sel = m & (rn >= floor * np.median(rn[m])) & (rn > 0)
+        if sel.any():
+            r = en[sel] / rn[sel]
+            j = int(np.argmax(r))
+            out[f"{cls}_row"] = float(r[j])
+            out[f"{cls}_row_at"] = int(np.nonzero(sel)[0][j])
+            out[f"{cls}_rows_checked"] = int(sel.sum())
+    return out
+
+
+def assert_grad_close(what, a, b, tol: float, lmk=None, floor: float = ROW_FLOOR) -> dict:
+    """Raises AssertionError (with every figure) unless both bounds above hold."""
+    e = grad_errors(a, b, lmk, floor)
+    bad = {k: v for k, v in e.items() if (k.endswith("_class") or k.endswith("_row")) and not v < tol}
+    assert not bad, (what, tol, e)
+    return e
+
+
+def check_grads(what, got, ref, idx, cu, tol: float) -> None:
+    """dq [T, H, D] per query head and dk, dv [T, G, D] per key/value head (each group's
+    landmark rows: the union of its query heads' sets) through ``assert_grad_close``.
+    The reference's backward takes delta = rowsum(O dO) from the stored output
+    (dsalt/kernels/dsalt_triton_bwd.py:17-49), so ``ref`` is the oracle fed the output the
+    kernels stored: rows whose dP - delta nearly cancels then compare like for like.
+
+    got: tensors or arrays (dq, dk, dv); ref: float64 arrays of the same shapes."""
+    got = [f64(t) if isinstance(t, torch.Tensor) else np.asarray(t, np.float64) for t in got]
+    ref = [np.asarray(t, np.float64) for t in ref]
+    idx = idx.cpu().numpy() if isinstance(idx, torch.Tensor) else np.asarray(idx)
+    cu = cu.cpu().numpy() if isinstance(cu, torch.Tensor) else np.asarray(cu)
+    T, H = got[0].shape[:2]
+    G = got[1].shape[1]
+    rep = H // G
+    lm = landmark_rows(idx, cu, T)
+    for h in range(H):
+        assert_grad_close((what, "dq", h), got[0][:, h], ref[0][:, h], tol)
+    for g in range(G):
+        lg = lm[:, g * rep:(g + 1) * rep].any(1)
+        for name, a, b in (("dk", got[1], ref[1]), ("dv", got[2], ref[2])):
+            assert_grad_close((what, name, g), a[:, g], b[:, g], tol, lg)

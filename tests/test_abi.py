@@ -134,6 +134,29 @@ def test_unknown_variant_bits_and_plan_size():
     assert lib.dsalt_plan_bytes(ctypes.byref(p)) == 0
 
 
+def test_workspaces_drop_the_plan_when_a_plan_is_given():
+    """The row plan is the forward's only workspace: with a caller-given plan buffer dsalt_fwd
+    needs none, and the backward's workspace shrinks by the plan's bytes."""
+    lib = _lib.load()
+    a = _valid_fwd()
+    a.plan = None
+    plan_b = lib.dsalt_plan_bytes(ctypes.byref(a.p))
+    assert plan_b > 0 and lib.dsalt_fwd_workspace_bytes(ctypes.byref(a)) == plan_b
+    a.plan = 1 << 20  # any non-null address: only the query runs
+    assert lib.dsalt_fwd_workspace_bytes(ctypes.byref(a)) == 0
+    b = _lib.BwdArgs()
+    b.p = _lib.Problem(256, 1, 256, 4, 4, 64, 8, 0, 0, _lib.DTYPE_BF16)
+    fake = 1 << 20
+    b.q = b.k = b.v = b.out = b.dout = b.dq = b.dk = b.dv = b.w = b.cu_seqlens = b.lse = b.lmk_idx = fake
+    b.q_stride_t = b.k_stride_t = b.v_stride_t = b.o_stride_t = b.do_stride_t = 4 * 64
+    b.q_stride_h = b.k_stride_h = b.v_stride_h = b.o_stride_h = b.do_stride_h = 64
+    b.scale = 0.125
+    full = lib.dsalt_bwd_workspace_bytes(ctypes.byref(b))
+    assert full > 0
+    b.plan = fake
+    assert lib.dsalt_bwd_workspace_bytes(ctypes.byref(b)) == full - lib.dsalt_plan_bytes(ctypes.byref(b.p))
+
+
 def test_workspace_sizes_and_small_workspace():
     lib = _lib.load()
     s = _lib.SelectArgs()

@@ -1,6 +1,9 @@
 """Attention forward/backward on the GPU against the float64 oracle.
 
-Tolerances (relative, max|a-b| / max|b|): 1e-5 for fp32, 2e-2 for bf16 and fp16.
+Tolerances (relative, max|a-b| / max|b|): 1e-5 for fp32, 2e-2 for bf16 and fp16.  Gradients
+of q, k and v are held to them per head by ``tests.helpers.check_grads``: landmark rows and
+the other rows each against their own largest entry, and every row above a quarter of its
+class's median norm against its own norm.
 """
 from __future__ import annotations
 
@@ -12,7 +15,7 @@ import torch
 
 from dsalt_amd import ops
 from oracle import attention as OA
-from tests.helpers import f64, rel_err
+from tests.helpers import check_grads, f64, rel_err
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -108,10 +111,10 @@ def _bwd_check(dt, lens, H, D, K, wmax, seed, bias=False):
                                             lbd, scale=scale, max_seqlen=maxlen)
     torch.cuda.synchronize()
     rdq, rdk, rdv, rdb = OA.attention_bwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale,
-                                          f64(do), lmk_bias=None if lb is None else lb.double().numpy())
-    for name, a, b in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv), ("dbias", db, rdb)):
-        e = rel_err(f64(a), b)
-        assert e < TOL[dt], (name, e)
+                                          f64(do), lmk_bias=None if lb is None else lb.double().numpy(),
+                                          out=f64(out))
+    check_grads("bwd", (dq, dk, dv), (rdq, rdk, rdv), idx, cu, TOL[dt])
+    assert rel_err(f64(db), rdb) < TOL[dt]
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32, torch.float16])
@@ -206,10 +209,9 @@ def test_bwd_grouped_heads_native(H, G, D, dt):
     torch.cuda.synchronize()
     assert res[1].shape == (q.shape[0], G, D) and res[2].shape == (q.shape[0], G, D)
     ref = OA.attention_bwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale, f64(do),
-                           lmk_bias=lb.double().numpy())
-    for name, a, b in zip(("dq", "dk", "dv", "dbias"), res, ref):
-        e = rel_err(f64(a), b)
-        assert e < TOL[dt], (name, e)
+                           lmk_bias=lb.double().numpy(), out=f64(out))
+    check_grads("gqa", res[:3], ref[:3], idx, cu, TOL[dt])
+    assert rel_err(f64(res[3]), ref[3]) < TOL[dt]
     res2 = ops.attention_backward(dev[7], dev[0], dev[1], dev[2], out, lse, dev[3], dev[4], dev[5], dev[6],
                                   scale=scale, max_seqlen=maxlen)
     for a, b in zip(res, res2):
@@ -228,9 +230,9 @@ def test_bwd_grouped_heads_shared_landmarks():
                                  scale=scale, max_seqlen=maxlen)
     torch.cuda.synchronize()
     ref = OA.attention_bwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale, f64(do),
-                           lmk_bias=lb.double().numpy())
-    for name, a, b in zip(("dq", "dk", "dv", "dbias"), res, ref):
-        assert rel_err(f64(a), b) < 2e-2, name
+                           lmk_bias=lb.double().numpy(), out=f64(out))
+    check_grads("shared", res[:3], ref[:3], idx, cu, 2e-2)
+    assert rel_err(f64(res[3]), ref[3]) < 2e-2
 
 
 def test_repeated_landmark_positions_count_each_copy():
@@ -254,9 +256,9 @@ def test_repeated_landmark_positions_count_each_copy():
                              lmk_bias=lb.double().numpy())
     assert rel_err(f64(out), ro) < 1e-5
     ref = OA.attention_bwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale, f64(do),
-                           lmk_bias=lb.double().numpy())
-    for name, a, b in zip(("dq", "dk", "dv", "dbias"), res, ref):
-        assert rel_err(f64(a), b) < 1e-5, name
+                           lmk_bias=lb.double().numpy(), out=f64(out))
+    check_grads("repeated", res[:3], ref[:3], idx, cu, 1e-5)
+    assert rel_err(f64(res[3]), ref[3]) < 1e-5
 
 
 @pytest.mark.parametrize("G", [4, 2])

@@ -15,7 +15,7 @@ import torch
 from dsalt_amd import ops
 from dsalt_amd.kernels import autotune as AT
 from oracle import attention as OA
-from tests.helpers import f64, rel_err
+from tests.helpers import check_grads, f64, rel_err
 from tests.test_gpu_attention import _inputs
 
 pytestmark = pytest.mark.gpu
@@ -35,7 +35,6 @@ def test_every_candidate_matches_the_oracle(dt, D):
     q, k, v, w, cu, idx, maxlen, do = _case(dt, D)
     scale = 1.0 / math.sqrt(D)
     ro, _ = OA.attention_fwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale)
-    rg = OA.attention_bwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale, f64(do))
     dev = [t.to(DEV) for t in (q, k, v, w, cu, idx, do)]
     cands = AT._candidate_configs(D, DEV, 4 if dt == torch.float32 else 2)
     assert cands[0]["variant"] == 0 and len({c["variant"] for c in cands}) == len(cands)
@@ -48,8 +47,25 @@ def test_every_candidate_matches_the_oracle(dt, D):
                                                variant=cfg["variant"])
         torch.cuda.synchronize()
         assert rel_err(f64(out), ro) < TOL[dt], cfg
-        for name, a, b in zip(("dq", "dk", "dv"), (dq, dk, dv), rg[:3]):
-            assert rel_err(f64(a), b) < TOL[dt], (cfg, name)
+        rg = OA.attention_bwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale, f64(do),
+                              out=f64(out))
+        check_grads(("variant", cfg["variant"]), (dq, dk, dv), rg[:3], idx, cu, TOL[dt])
+
+
+@pytest.mark.parametrize("variant", [c["variant"] for c in AT._candidate_configs(64, None, 2)])
+def test_every_candidate_block_causal_forward(variant):
+    """The block-causal operator with every 16-bit head_dim-64 tiling (the autograd operator
+    passes the tuned variant in block-causal mode too): 128-query blocks, GQA, ragged."""
+    dt = torch.bfloat16
+    q, k, v, w, cu, idx, lb, maxlen = _inputs([900, 400], 4, 2, 64, 40, 300, dt, 63, mode=ops.SELECT_BLOCK,
+                                              block=128)
+    dev = [t.to(DEV) for t in (q, k, v, w, cu, idx)]
+    out, lse = ops.attention_forward(*dev, None, scale=0.125, max_seqlen=maxlen, select_mode=ops.SELECT_BLOCK,
+                                     block_size=128, variant=variant)
+    torch.cuda.synchronize()
+    ro, rl = OA.attention_fwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), 0.125, block_size=128)
+    assert rel_err(f64(out), ro) < TOL[dt]
+    assert rel_err(f64(lse), rl) < 2e-3
 
 
 def test_autotune_caches_and_the_operator_uses_the_winner():

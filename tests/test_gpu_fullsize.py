@@ -10,9 +10,17 @@ landmark variant as the benchmark runs them):
     2048, block-causal k=128, w_max 512, L32768;
   * the 36-layer Qwen2.5-3B-shaped prefill at L32768 through properties (finite logits, a
     bit-identical rerun) and its first layer's selection and attention against the oracle.
-Landmark indices must equal the C oracle's bit for bit; outputs and gradients must be within
-1e-5 (fp32) or 2e-2 (bf16) relative error (max |a - b| / max |b|, per head) of the float64
-oracle, and the LSE within 1e-6 (fp32) or 2e-3 (bf16).  The oracle runs one head per thread.
+  * forward + backward bf16 of the training variant (the headline tensors with continuous
+    windows, soft edge 4, landmark log-weights) on all 16 heads against the banded fp64
+    training oracle.
+Landmark indices must equal the C oracle's bit for bit; outputs must be within 1e-5 (fp32) or
+2e-2 (bf16) relative error (max |a - b| / max |b|, per head) of the float64 oracle, and the
+LSE within 1e-6 (fp32) or 2e-3 (bf16).  Gradients are held to the same tolerance per head by
+``tests.helpers.assert_grad_close``: landmark rows and the other rows each against their own
+largest entry, and every row above a quarter of its class's median norm against its own norm
+(a landmark row of the headline shape is tens of times larger than an ordinary row, so one
+bound over all rows would not see errors on the ordinary rows).  The oracle runs one head
+per thread.
 """
 from __future__ import annotations
 
@@ -24,7 +32,8 @@ import torch
 
 from dsalt_amd import ops
 from dsalt_amd.workloads import WORKLOADS, generate
-from tests.helpers import f64, oracle_bwd_heads, oracle_fwd_heads, oracle_select_by_group, rel_err
+from tests.helpers import (_pool_map, check_grads, f64, oracle_bwd_heads, oracle_fwd_heads,
+                           oracle_select_by_group, rel_err)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -75,13 +84,10 @@ def _run(name, fwd_heads=None, bwd=False):
     dq, dk, dv, _ = ops.attention_backward(dev["dout"], dev["q"], dev["k"], dev["v"], out, lse, dev["w"],
                                            dev["cu"], idx, None, max_seqlen=wl.seqlen, want_dbias=False)
     torch.cuda.synchronize()
-    g = [f64(t) for t in (dq, dk, dv)]
     refs = oracle_bwd_heads(x["q"], x["k"], x["v"], x["w"], x["cu"], idx.cpu().numpy(),
-                            1.0 / math.sqrt(wl.head_dim), x["dout"], list(range(wl.heads)))
-    for hh, r in enumerate(refs):
-        for name_g, a, b in zip(("dq", "dk", "dv"), g, r[:3]):
-            e = rel_err(a[:, hh], b[:, 0])
-            assert e < TOL[wl.dtype], (name, hh, name_g, e)
+                            1.0 / math.sqrt(wl.head_dim), x["dout"], list(range(wl.heads)), out=out)
+    ref = [np.concatenate([r[j] for r in refs], axis=1) for j in range(3)]
+    check_grads(name, (dq, dk, dv), ref, idx, x["cu"], TOL[wl.dtype])
     # the backward is deterministic: a second call gives the same bits
     r2 = ops.attention_backward(dev["dout"], dev["q"], dev["k"], dev["v"], out, lse, dev["w"], dev["cu"], idx,
                                 None, max_seqlen=wl.seqlen, want_dbias=False)
@@ -102,8 +108,59 @@ def test_fwdbwd_bf16_h16_l32768_full():
 
 
 def test_fwd_bf16_h16_l131072_block_full():
-    # selection bit-exact on all 16 heads, the forward compared on four of them
-    _run("fwd_bf16_h16_l131072_block", fwd_heads=[0, 5, 10, 15])
+    # selection bit-exact and the forward compared on all 16 heads
+    _run("fwd_bf16_h16_l131072_block")
+
+
+def test_train_bf16_h16_l32768_full():
+    """The training variant at the benchmark's shape: the layer's hard selection from floor(w~),
+    landmark log-weights log sigmoid(s / tau_lmk), soft edge 4; output, LSE and every gradient
+    of all 16 heads against the banded float64 training oracle."""
+    from oracle import train as OT
+    wl = WORKLOADS["train_bf16_h16_l32768"]
+    x = generate(wl)
+    dev = {k: v.to(DEV) for k, v in x.items()}
+    maxlen = wl.seqlen
+    idx, _, _, sc = ops.select_landmarks(dev["h"], dev["v"], dev["alpha"], dev["w"], dev["cu"], wl.k_lmk,
+                                         max_seqlen=maxlen, stats_scope=ops.STATS_SEQUENCE, want_scores=True)
+    pos = idx[:, :, 0].long()
+    H = pos.shape[0]
+    s_sel = sc[dev["cu"][:-1].long()[None, :, None] + pos.clamp(min=0), torch.arange(H, device=DEV)[:, None, None]]
+    logw = torch.log(torch.sigmoid(s_sel / wl.tau_lmk).clamp(min=1e-20))
+    logw = torch.where(pos >= 0, logw, torch.full_like(logw, float("-inf")))
+    print("workload train_bf16_h16_l32768: forward + backward", flush=True)
+    out, lse = ops.train_forward(dev["q"], dev["k"], dev["v"], dev["w_cont"], dev["cu"], idx, logw.unsqueeze(2),
+                                 tau_win=wl.tau_win, win_edge=wl.win_edge, max_seqlen=maxlen)
+    dq, dk, dv, dlw, dw = ops.train_backward(dev["dout"], dev["q"], dev["k"], dev["v"], out, lse, dev["w_cont"],
+                                             dev["cu"], idx, logw.unsqueeze(2), tau_win=wl.tau_win,
+                                             win_edge=wl.win_edge, max_seqlen=maxlen)
+    torch.cuda.synchronize()
+    print("workload train_bf16_h16_l32768: banded oracle on all heads", flush=True)
+    pos_c, logw_c, wc, cu = idx[:, :, 0].cpu().numpy(), logw.double().cpu().numpy(), x["w_cont"].double().numpy(), \
+        x["cu"].numpy()
+    args = [f64(x[n]) for n in ("q", "k", "v", "dout")]
+    o_st = f64(out)  # delta from the stored output, as the reference's backward
+
+    def one(hh):
+        q1, k1, v1, d1 = (a[:, hh:hh + 1] for a in args)
+        o1, l1 = OT.train_fwd_banded(q1, k1, v1, wc, cu, pos_c[hh:hh + 1], logw_c[hh:hh + 1], 1.0 / 8.0,
+                                     wl.tau_win, wl.win_edge)
+        g1 = OT.train_bwd_banded(q1, k1, v1, wc, cu, pos_c[hh:hh + 1], logw_c[hh:hh + 1], 1.0 / 8.0, wl.tau_win,
+                                 wl.win_edge, d1, out=o_st[:, hh:hh + 1])
+        return o1, l1, g1
+
+    refs = _pool_map(one, range(H))
+    o, l = f64(out), f64(lse)
+    for hh, (ro, rl, _) in enumerate(refs):
+        assert rel_err(o[:, hh], ro[:, 0]) < 2e-2, hh
+        assert rel_err(l[:, hh], rl[:, 0]) < 2e-3, hh
+    ref = [np.concatenate([r[2][j] for r in refs], axis=1) for j in range(3)]
+    check_grads("train", (dq, dk, dv), ref, idx, x["cu"], 2e-2)
+    # window gradient: the sum over heads; log-weight gradient per (head, slot)
+    rdw = sum(r[2][3] for r in refs)
+    assert rel_err(f64(dw), rdw) < 2e-2
+    rdlw = np.concatenate([r[2][4] for r in refs], axis=0)
+    assert rel_err(f64(dlw[:, :, 0]), rdlw) < 2e-2
 
 
 def test_fwd_bf16_h16kv2_l32768_block_full():

@@ -1,7 +1,9 @@
 """Training variant (soft-edge band, weighted landmarks) on the GPU against the float64 oracle.
 
 Tolerances (relative, max|a-b| / max|b|): 1e-5 for fp32, 2e-2 for bf16 and fp16, for the
-output and every gradient (q, k, v, landmark log-weights, continuous windows).
+output and every gradient (q, k, v, landmark log-weights, continuous windows); the gradients of
+q, k and v per head through ``tests.helpers.check_grads`` (landmark rows and the other rows
+each against their own largest entry, and a per-row bound).
 """
 from __future__ import annotations
 
@@ -14,7 +16,7 @@ import torch
 from dsalt_amd import ops
 from dsalt_amd.kernels import dsalt_triton_train_attention
 from oracle import train as OT
-from tests.helpers import f64, rel_err
+from tests.helpers import check_grads, f64, rel_err
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -42,30 +44,31 @@ def _inputs(lens, H, D, K, wlo, whi, dt, seed, integer_every=0):
     return q, k, v, w, cu, pos, logw, do, max(lens)
 
 
-def _oracle(q, k, v, w, cu, pos, logw, do, scale, tau, edge):
+def _oracle(q, k, v, w, cu, pos, logw, do, scale, tau, edge, out=None):
+    """(forward, backward) of the oracle; ``out``: the stored output that feeds delta."""
     return (OT.train_fwd(f64(q), f64(k), f64(v), w.double().numpy(), cu.numpy(), pos.numpy(), logw.double().numpy(),
                          scale, tau, edge),
             OT.train_bwd(f64(q), f64(k), f64(v), w.double().numpy(), cu.numpy(), pos.numpy(), logw.double().numpy(),
-                         scale, tau, edge, f64(do)))
+                         scale, tau, edge, f64(do), out=None if out is None else f64(out)))
 
 
-def _check(lens, H, D, K, wlo, whi, dt, seed, tau=1.0, edge=4.0, integer_every=0):
+def _check(lens, H, D, K, wlo, whi, dt, seed, tau=1.0, edge=4.0, integer_every=0, variant=0):
     q, k, v, w, cu, pos, logw, do, maxlen = _inputs(lens, H, D, K, wlo, whi, dt, seed, integer_every)
     scale = 1.0 / math.sqrt(D)
     qd, kd, vd, wd, cud = (t.to(DEV) for t in (q, k, v, w, cu))
     idx = pos.unsqueeze(2).to(DEV)
     lw = logw.unsqueeze(2).to(DEV)
     out, lse = ops.train_forward(qd, kd, vd, wd, cud, idx, lw, tau_win=tau, win_edge=edge, scale=scale,
-                                 max_seqlen=maxlen)
+                                 max_seqlen=maxlen, variant=variant)
     dq, dk, dv, dlw, dw = ops.train_backward(do.to(DEV), qd, kd, vd, out, lse, wd, cud, idx, lw, tau_win=tau,
-                                             win_edge=edge, scale=scale, max_seqlen=maxlen)
+                                             win_edge=edge, scale=scale, max_seqlen=maxlen, variant=variant)
     torch.cuda.synchronize()
-    (ro, rl), (rdq, rdk, rdv, rdw, rdlw) = _oracle(q, k, v, w, cu, pos, logw, do, scale, tau, edge)
+    (ro, rl), (rdq, rdk, rdv, rdw, rdlw) = _oracle(q, k, v, w, cu, pos, logw, do, scale, tau, edge, out=out)
     tol = TOL[dt]
     assert rel_err(f64(out), ro) < tol
     assert rel_err(f64(lse), rl) < (1e-6 if dt == torch.float32 else 2e-3)
-    for name, a, b in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv), ("d_w", dw, rdw),
-                       ("d_logw", dlw[:, :, 0], rdlw)):
+    check_grads("train", (dq, dk, dv), (rdq, rdk, rdv), pos, cu, tol)
+    for name, a, b in (("d_w", dw, rdw), ("d_logw", dlw[:, :, 0], rdlw)):
         e = rel_err(f64(a), b)
         assert e < tol, (name, e)
     fin = torch.isfinite(logw)
@@ -76,6 +79,18 @@ def _check(lens, H, D, K, wlo, whi, dt, seed, tau=1.0, edge=4.0, integer_every=0
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32, torch.float16])
 def test_train_d64(dt):
     _check([300, 181, 64], 4, 64, 24, 0.5, 90.0, dt, seed=41, integer_every=5)
+
+
+def _train_variants():
+    from dsalt_amd.kernels import autotune as AT
+    return [c["variant"] for c in AT._candidate_configs(64, None, 2)]
+
+
+@pytest.mark.parametrize("variant", _train_variants())
+def test_train_d64_every_tiling(variant):
+    """Every tiling the autotune may choose for 16-bit head_dim 64: the training operator runs the
+    tuned variant's instantiations of the soft-edge kernels."""
+    _check([700, 181], 4, 64, 24, 0.5, 300.0, torch.bfloat16, seed=51, integer_every=5, variant=variant)
 
 
 def test_train_d128_bf16():
@@ -160,12 +175,12 @@ def test_autograd_function_gqa_unsorted_slots():
                          scale, 1.3, 5.0)
     rdq, rdk, rdv, rdw, rdlw = OT.train_bwd(f64(q), kr, vr, w.double().numpy(), cu.numpy(), pos.numpy(),
                                             logw.double().numpy(), scale, 1.3, 5.0,
-                                            do.to(dt).double().numpy())
+                                            do.to(dt).double().numpy(), out=f64(out.detach()))
     rdk = rdk.reshape(T, G, H // G, D).sum(2)
     rdv = rdv.reshape(T, G, H // G, D).sum(2)
     assert rel_err(f64(out), ro) < 2e-2
-    for name, a, b in (("dq", qd.grad, rdq), ("dk", kd.grad, rdk), ("dv", vd.grad, rdv), ("d_w", wd.grad, rdw),
-                       ("d_logw", lwd.grad, rdlw)):
+    check_grads("train_autograd", (qd.grad, kd.grad, vd.grad), (rdq, rdk, rdv), pos, cu, 2e-2)
+    for name, a, b in (("d_w", wd.grad, rdw), ("d_logw", lwd.grad, rdlw)):
         e = rel_err(f64(a), b)
         assert e < 2e-2, (name, e)
     assert lwd.grad.dtype == torch.float32 and wd.grad.dtype == torch.float32
@@ -321,9 +336,9 @@ def test_train_workload_shortened_against_oracle():
     c = {k: v.cpu() for k, v in x.items()}
     pos = idx[:, :, 0].cpu()
     (ro, _), (rdq, rdk, rdv, rdw, rdlw) = _oracle(c["q"], c["k"], c["v"], c["w_cont"], c["cu"], pos, logw.cpu(),
-                                                  c["dout"], 1.0 / 8.0, wl.tau_win, wl.win_edge)
-    for name, a, b in (("out", out, ro), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv), ("d_w", dw, rdw),
-                       ("d_logw", dlw[:, :, 0], rdlw)):
+                                                  c["dout"], 1.0 / 8.0, wl.tau_win, wl.win_edge, out=out)
+    check_grads("train_workload", (dq, dk, dv), (rdq, rdk, rdv), pos, c["cu"], 2e-2)
+    for name, a, b in (("out", out, ro), ("d_w", dw, rdw), ("d_logw", dlw[:, :, 0], rdlw)):
         e = rel_err(f64(a), b)
         assert e < 2e-2, (name, e)
 

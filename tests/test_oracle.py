@@ -24,6 +24,8 @@ Parity status of each oracle function (how it is pinned):
                                  + rotation of 2-vectors preserves norms (fp32)
   train.train_bwd                golden (float64 autograd of the reference dense form)
                                  + central finite differences in w~ and lmk_logw
+  train.train_fwd_banded /       train_fwd / train_bwd (dense, pinned above) on ragged sequences
+  train.train_bwd_banded         with several row blocks, edges wider than windows, empty slots
 """
 from __future__ import annotations
 
@@ -538,3 +540,29 @@ def test_oracle_bf16_selection_is_a_top_k_of_the_reference_scores(name):
             st = int(cun[s])
             kth = min(sc[st + j, hh] for j in b)
             assert all(sc[st + j, hh] == kth for j in a ^ b), (hh, s)
+
+
+@pytest.mark.parametrize("rb", [64, 512])
+def test_train_banded_matches_dense(rb):
+    """The banded training oracle (full-length workloads) against the dense one."""
+    g = np.random.default_rng(91)
+    lens = [300, 181, 64]
+    T, H, D, K = sum(lens), 3, 16, 12
+    q, k, v, do = (g.standard_normal((T, H, D)) for _ in range(4))
+    w_cont = g.uniform(0.0, 90.0, T)
+    w_cont[::7] = np.floor(w_cont[::7])  # integer windows: the band end and the landmark cut at d = w~
+    cu = np.array([0] + list(np.cumsum(lens)), np.int64)
+    pos = np.full((H, len(lens), K), -1, np.int64)
+    for h in range(H):
+        for s, L in enumerate(lens):
+            n = min(K - (h % 2), L)
+            pos[h, s, :n] = np.sort(g.permutation(L)[:n])
+    logw = np.where(pos >= 0, np.log(1.0 / (1.0 + np.exp(-g.standard_normal(pos.shape)))), -np.inf)
+    for tau, edge in ((1.0, 4.0), (2.0, 120.0)):
+        a = (q, k, v, w_cont, cu, pos, logw, 0.25, tau, edge)
+        o1, l1 = OT.train_fwd(*a)
+        o2, l2 = OT.train_fwd_banded(*a, rb=rb)
+        np.testing.assert_allclose(o2, o1, rtol=0, atol=1e-12)
+        np.testing.assert_allclose(l2, l1, rtol=0, atol=1e-12)
+        for x, y in zip(OT.train_bwd_banded(*a, do, rb=rb), OT.train_bwd(*a, do)):
+            np.testing.assert_allclose(x, y, rtol=0, atol=1e-11)
