@@ -483,7 +483,6 @@ def main():
                                tau_win=tau_win, win_edge=win_edge, max_seqlen=maxlen)
             return idx
     else:
-        plan = None
         variant = 0 if args.variant == "auto" else int(args.variant)
         if args.variant == "auto":
             # the reference's flow: tile sizes autotuned once per shape, then used by every call
@@ -499,15 +498,18 @@ def main():
                 variant = AT.autotune_blocks(D, dev, runner, verbose=True, dtype=x["q"].dtype)["variant"]
             del idx0
 
+        # the forward's row plan: written by the selection's norms launch and read by the forward
+        # (plan_ready) and the backward
+        plan = ops.new_plan(x["q"], x["k"], x["cu"], torch.empty(H, x["cu"].numel() - 1, 1, wl.k_lmk,
+                                                                 dtype=torch.int32, device=dev),
+                            max_seqlen=maxlen, select_mode=mode, block_size=wl.block_size)
+
         def step():
-            nonlocal plan
             idx = ops.select_landmarks(x["h"], x["v"], x["alpha"], x["w"], x["cu"], wl.k_lmk, max_seqlen=maxlen,
-                                       select_mode=mode, block_size=wl.block_size, stats_scope=scope)
-            if plan is None and wl.backward:  # the forward's row plan, reused by the backward
-                plan = ops.new_plan(x["q"], x["k"], x["cu"], idx, max_seqlen=maxlen)
+                                       select_mode=mode, block_size=wl.block_size, stats_scope=scope, plan=plan)
             out, lse = ops.attention_forward(x["q"], x["k"], x["v"], x["w"], x["cu"], idx, None, max_seqlen=maxlen,
                                              select_mode=mode, block_size=wl.block_size, plan=plan,
-                                             variant=variant)
+                                             plan_ready=True, variant=variant)
             if wl.backward:
                 ops.attention_backward(x["dout"], x["q"], x["k"], x["v"], out, lse, x["w"], x["cu"], idx, None,
                                        max_seqlen=maxlen, want_dbias=False, plan=plan, variant=variant)

@@ -17,10 +17,11 @@ DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 SELECT_GLOBAL, SELECT_BLOCK = 0, 1
 STATS_PACKED, STATS_SEQUENCE = 0, 1
 ERR_NAMES = {1: "invalid argument", 2: "unsupported", 3: "workspace", 4: "HIP error"}
-ABI_VERSION = 2
+ABI_VERSION = 3
 FWD_NOALLOC_MAX_PLAN_BYTES = 4 << 20  # DSALT_FWD_NOALLOC_MAX_PLAN_BYTES
 # tile variants of the attention kernels (DSALT_VARIANT_*)
 VARIANT_DEFAULT, VARIANT_FWD_BN32, VARIANT_FWD_RG2, VARIANT_DQ_BN64, VARIANT_LMK_SHORT = 0, 1, 2, 4, 8
+VARIANT_FWD_BN64 = 16
 
 _i32, _i64, _vp, _sz, _f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float
 
@@ -45,7 +46,7 @@ class SelectArgs(ctypes.Structure):
                 ("v", _vp), ("v_stride_t", _i64), ("v_stride_h", _i64),
                 ("alpha", _vp), ("w", _vp), ("cu_seqlens", _vp), ("lmk_idx", _vp),
                 ("z_x", _vp), ("z_v", _vp), ("scores", _vp),
-                ("workspace", _vp), ("workspace_bytes", _sz)]
+                ("workspace", _vp), ("workspace_bytes", _sz), ("plan", _vp)]
 
 
 class FwdArgs(ctypes.Structure):
@@ -56,7 +57,8 @@ class FwdArgs(ctypes.Structure):
                 ("w", _vp), ("cu_seqlens", _vp), ("lmk_idx", _vp), ("lmk_bias", _vp),
                 ("out", _vp), ("o_stride_t", _i64), ("o_stride_h", _i64),
                 ("lse", _vp), ("scale", _f32),
-                ("workspace", _vp), ("workspace_bytes", _sz), ("plan", _vp), ("variant", _i32)]
+                ("workspace", _vp), ("workspace_bytes", _sz), ("plan", _vp), ("variant", _i32),
+                ("plan_ready", _i32)]
 
 
 class BwdArgs(ctypes.Structure):

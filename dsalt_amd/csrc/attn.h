@@ -109,8 +109,9 @@ __device__ __forceinline__ float edge_lookup(const float* t, int k) {
 size_t plan_bytes(const AttnParams& p);
 void plan_carve(AttnParams& p, char*& ws);  // assigns plan_perm / plan_bounds / tile_wmax from a buffer
 hipError_t plan_launch(const AttnParams& p, hipStream_t stream);
-// plan: a caller buffer of plan_bytes() that receives the row plan, or null (workspace)
-hipError_t fwd_launch(AttnParams p, void* ws, void* plan, hipStream_t stream);
+// plan: a caller buffer of plan_bytes() that receives the row plan, or null (workspace);
+// plan_ready: the buffer already holds the plan of these rows (not recomputed)
+hipError_t fwd_launch(AttnParams p, void* ws, void* plan, bool plan_ready, hipStream_t stream);
 // training variant: integer windows floor(w~) + 1 written into `w_int` ([T] int32)
 hipError_t train_windows_launch(const AttnParams& p, int* w_int, hipStream_t stream);
 // plan_given: the caller supplies the row plan (no room for it in the workspace)

@@ -18,6 +18,7 @@
 #include <type_traits>
 
 #include "attn.h"
+#include "plan.h"
 #include "tiles.h"
 #include "timing.h"
 
@@ -44,65 +45,11 @@ __device__ __forceinline__ int lower_bound_lds(const int* a, int n, int x) {
 }
 
 // ------------------------------------------------------------- row plan
-// Head-independent preparation shared by the forward and dQ kernels.  Within
-// each 64-row tile the rows are ordered by window start lo_i (ties by row;
-// rows past the end last), so the 16 rows a wave takes have close window
-// starts: the wave's key range [min lo, max i] and its count of masked
-// subtiles shrink.  Each 16-row group's {min lo, max lo, max i, min i} is
-// recorded, with the tile's largest clamped window (whose maximum over a sequence
-// bounds the key-parallel backward sweep).
+// (plan.h): one wave per 64-row tile
 __global__ __launch_bounds__(64) void row_plan_kernel(AttnParams p) {
     __shared__ int sp[64], slo[64];
-    const int l = threadIdx.x;
-    const int tile = blockIdx.x;  // s * n_tiles + t
-    const int s = tile / p.n_tiles, t = tile % p.n_tiles;
-    int st, len;
-    seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
-    const int r0 = t * 64;
-    const int i = r0 + l;
-    const bool valid = i < len;
-    int lo = 0x7fffffff, wcl = 0;
-    if (valid) {
-        const int wi = max(p.w[st + i], 1);
-        lo = max(i - wi + 1, 0);
-        wcl = min(wi, len);
-    }
-    const uint32_t khi = (uint32_t)lo >> 26, klo = ((uint32_t)lo << 6) | (uint32_t)l;  // key lo * 64 + l
-    int rank = 0;
-    for (int j = 0; j < 64; ++j) {
-        const uint32_t jhi = (uint32_t)__builtin_amdgcn_readlane((int)khi, j);
-        const uint32_t jlo = (uint32_t)__builtin_amdgcn_readlane((int)klo, j);
-        rank += (jhi < khi || (jhi == khi && jlo < klo)) ? 1 : 0;
-    }
-    sp[rank] = l;
-    slo[l] = lo;
-    __syncthreads();
-    const int pl = sp[l];  // row offset at sorted position l
-    p.plan_perm[(int64_t)tile * 64 + l] = (uint8_t)pl;
-    const int ri = r0 + pl;
-    const bool rv = ri < len;
-    int rlo = 0x7fffffff, rlmax = (int)0x80000000, rhi = -1, rhmin = 0x7fffffff;
-    if (rv) {
-        rlo = slo[pl];
-        rlmax = rlo;
-        rhi = ri;
-        rhmin = ri;
-    }
-    rlo = row_min16(rlo);
-    rlmax = row_max16(rlmax);
-    rhi = row_max16(rhi);
-    rhmin = row_min16(rhmin);
-    if ((l & 15) == 0) {
-        int* b = p.plan_bounds + ((int64_t)tile * 4 + (l >> 4)) * 4;
-        b[0] = rlo;
-        b[1] = rlmax;
-        b[2] = rhi;
-        b[3] = rhmin;
-    }
-    const int m = row_max16(wcl);
-    const int tm = max(max(__builtin_amdgcn_readlane(m, 0), __builtin_amdgcn_readlane(m, 16)),
-                       max(__builtin_amdgcn_readlane(m, 32), __builtin_amdgcn_readlane(m, 48)));
-    if (l == 0) p.tile_wmax[tile] = tm;
+    row_plan_tile(p.w, p.cu, p.total_len, p.max_seqlen, p.n_tiles, blockIdx.x, true, threadIdx.x, sp, slo,
+                  PlanOut{p.plan_perm, p.plan_bounds, p.tile_wmax});
 }
 
 size_t plan_bytes(const AttnParams& p) {
@@ -613,23 +560,38 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
 
 // Tilings (DSALT_VARIANT_* bits): for 16-bit head_dim 64, 32-key chunks instead of 64
 // (FWD_BN32) and two 16-row groups per wave (FWD_RG2, 128 rows per block: the block must
-// stay within one landmark set, block_size a multiple of 128); other shapes take their
-// single compiled tiling.
+// stay within one landmark set, block_size a multiple of 128); for 16-bit head_dim 128, two
+// row groups per wave (FWD_RG2, same condition) or 64-key chunks instead of 32 (FWD_BN64;
+// ignored with FWD_RG2);
+// fp32 takes its single compiled tiling.
 template <typename T, int D, bool TR>
 static void fwd_run(const AttnParams& p, hipStream_t stream) {
     constexpr int BN = FwdShape<T, D>::BN;
-    if constexpr (sizeof(T) == 2 && D == 64) {
-        const bool bn32 = (p.variant & DSALT_VARIANT_FWD_BN32) != 0;
+    if constexpr (sizeof(T) == 2) {
         const bool rg2 = (p.variant & DSALT_VARIANT_FWD_RG2) != 0 && (p.block_size == 0 || p.block_size % 128 == 0);
         const int total = p.n_heads * p.num_seqs * ceil_div(p.n_tiles, rg2 ? 2 : 1);
-        if (rg2) {
-            if (bn32) DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 32, 2, TR>), dim3(total), dim3(256), 0, stream, p);
-            else DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, BN, 2, TR>), dim3(total), dim3(256), 0, stream, p);
-            return;
-        }
-        if (bn32) {
-            DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 32, 1, TR>), dim3(total), dim3(256), 0, stream, p);
-            return;
+        if constexpr (D == 64) {
+            const bool bn32 = (p.variant & DSALT_VARIANT_FWD_BN32) != 0;
+            if (rg2) {
+                if (bn32) DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 32, 2, TR>), dim3(total), dim3(256), 0, stream, p);
+                else DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, BN, 2, TR>), dim3(total), dim3(256), 0, stream, p);
+                return;
+            }
+            if (bn32) {
+                DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 32, 1, TR>), dim3(total), dim3(256), 0, stream, p);
+                return;
+            }
+        } else if constexpr (!TR) {  // head_dim 128 (inference shapes)
+            // two row groups keep 32-key chunks (with 64-key chunks they would spill at 256 VGPRs)
+            const bool bn64 = (p.variant & DSALT_VARIANT_FWD_BN64) != 0;
+            if (rg2) {
+                DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, BN, 2, TR>), dim3(total), dim3(256), 0, stream, p);
+                return;
+            }
+            if (bn64) {
+                DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, 64, 1, TR>), dim3(total), dim3(256), 0, stream, p);
+                return;
+            }
         }
     }
     const int total = p.n_heads * p.num_seqs * p.n_tiles;
@@ -637,10 +599,12 @@ static void fwd_run(const AttnParams& p, hipStream_t stream) {
 }
 
 template <typename T>
-static hipError_t fwd_dispatch(const AttnParams& p, hipStream_t stream) {
+static hipError_t fwd_dispatch(const AttnParams& p, bool plan_ready, hipStream_t stream) {
     if (p.n_heads * p.num_seqs * p.n_tiles == 0) return hipSuccess;
-    const hipError_t e = plan_launch(p, stream);
-    if (e != hipSuccess) return e;
+    if (!plan_ready) {
+        const hipError_t e = plan_launch(p, stream);
+        if (e != hipSuccess) return e;
+    }
     const bool tr = p.w_cont != nullptr;
     if (p.head_dim == 64) {
         if (tr) fwd_run<T, 64, true>(p, stream);
@@ -670,12 +634,13 @@ hipError_t train_windows_launch(const AttnParams& p, int* w_int, hipStream_t str
     return hipGetLastError();
 }
 
-hipError_t fwd_launch(AttnParams p, void* ws, void* plan, hipStream_t stream) {
+hipError_t fwd_launch(AttnParams p, void* ws, void* plan, bool plan_ready, hipStream_t stream) {
     char* w = (char*)(plan ? plan : ws);
     plan_carve(p, w);
-    if (p.dtype == DSALT_DTYPE_BF16) return fwd_dispatch<bf16>(p, stream);
-    if (p.dtype == DSALT_DTYPE_F16) return fwd_dispatch<f16>(p, stream);
-    return fwd_dispatch<float>(p, stream);
+    const bool ready = plan_ready && plan != nullptr;
+    if (p.dtype == DSALT_DTYPE_BF16) return fwd_dispatch<bf16>(p, ready, stream);
+    if (p.dtype == DSALT_DTYPE_F16) return fwd_dispatch<f16>(p, ready, stream);
+    return fwd_dispatch<float>(p, ready, stream);
 }
 
 }  // namespace dsalt

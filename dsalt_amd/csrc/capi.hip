@@ -83,7 +83,7 @@ int check_rows(const void* ptr, int64_t st, int64_t sh, int dtype, const char* n
 }
 
 dsalt::SelectParams select_params(const dsalt_select_args* a) {
-    dsalt::SelectParams p;
+    dsalt::SelectParams p = {};
     const dsalt_problem& q = a->p;
     p.total_len = q.total_len;
     p.num_seqs = q.num_seqs;
@@ -110,6 +110,17 @@ dsalt::SelectParams select_params(const dsalt_select_args* a) {
     p.z_x = a->z_x;
     p.z_v = a->z_v;
     p.scores = a->scores;
+    p.n_tiles = (q.max_seqlen + 63) / 64;
+    if (a->plan) {  // the forward's row plan, carved as dsalt_fwd reads it
+        dsalt::AttnParams ap = {};
+        ap.num_seqs = q.num_seqs;
+        ap.n_tiles = p.n_tiles;
+        char* w = (char*)a->plan;
+        dsalt::plan_carve(ap, w);
+        p.plan_perm = ap.plan_perm;
+        p.plan_bounds = ap.plan_bounds;
+        p.tile_wmax = ap.tile_wmax;
+    }
     return p;
 }
 
@@ -254,7 +265,8 @@ int dsalt_fwd(const dsalt_fwd_args* a, dsalt_stream_t stream) {
     const size_t need = a->plan ? 0 : dsalt::plan_bytes(p);
     if (need && (!a->workspace || a->workspace_bytes < need))
         return fail(DSALT_ERR_WORKSPACE, "forward needs %zu workspace bytes, got %zu", need, a->workspace_bytes);
-    return hip_status(dsalt::fwd_launch(p, a->workspace, a->plan, (hipStream_t)stream), "dsalt_fwd");
+    return hip_status(dsalt::fwd_launch(p, a->workspace, a->plan, a->plan_ready != 0, (hipStream_t)stream),
+                      "dsalt_fwd");
 }
 
 }  // extern "C"
@@ -318,7 +330,8 @@ int dsalt_fwd_noalloc(const dsalt_fwd_args* a, dsalt_stream_t stream) {
         if (e != hipSuccess) return hip_status(e, "dsalt_fwd_noalloc scratch");
     }
     // every kernel writes each plan entry it later reads: nothing needs clearing
-    return hip_status(dsalt::fwd_launch(p, ws, a->plan, (hipStream_t)stream), "dsalt_fwd_noalloc");
+    return hip_status(dsalt::fwd_launch(p, ws, a->plan, a->plan_ready != 0, (hipStream_t)stream),
+                      "dsalt_fwd_noalloc");
 }
 
 size_t dsalt_train_fwd_workspace_bytes(const dsalt_train_fwd_args* a) {
@@ -341,7 +354,7 @@ int dsalt_train_fwd(const dsalt_train_fwd_args* a, dsalt_stream_t stream) {
     p.w = w_int;
     hipError_t e = dsalt::train_windows_launch(p, w_int, (hipStream_t)stream);
     if (e == hipSuccess)
-        e = dsalt::fwd_launch(p, (char*)a->base.workspace + wint_bytes(p), a->base.plan, (hipStream_t)stream);
+        e = dsalt::fwd_launch(p, (char*)a->base.workspace + wint_bytes(p), a->base.plan, false, (hipStream_t)stream);
     return hip_status(e, "dsalt_train_fwd");
 }
 

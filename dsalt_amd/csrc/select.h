@@ -22,6 +22,11 @@ struct SelectParams {
     float* z_x;
     float* z_v;
     float* scores;
+    // optional row plan of the forward (plan.h), written by extra blocks of the norms launch
+    uint8_t* plan_perm;      // null: no plan
+    int* plan_bounds;
+    int* tile_wmax;
+    int n_tiles;             // 64-row tiles per sequence, ceil(max_seqlen / 64)
 };
 
 struct GatherParams {

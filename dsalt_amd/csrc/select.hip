@@ -42,6 +42,7 @@
 // The arithmetic order above is the canonical one that the CPU oracle
 // restates; this file is compiled with -ffp-contract=off.
 #include "common.h"
+#include "plan.h"
 #include "select.h"
 #include "timing.h"
 
@@ -89,13 +90,22 @@ __device__ __forceinline__ int seq_of(const SelectParams& p, int t) {
     return lo;
 }
 
+// Blocks past the norms' `nblk` (when the caller asked for the forward's row plan) plan four
+// 64-row tiles each, one per wave: independent work that rides in the same launch.
 template <typename T>
-__global__ __launch_bounds__(256) void sel_norms_kernel(SelectParams p, float* nx, float* nv, uint32_t* pk) {
+__global__ __launch_bounds__(256) void sel_norms_kernel(SelectParams p, float* nx, float* nv, uint32_t* pk, int nblk) {
     constexpr int VW = 16 / (int)sizeof(T);
     typedef uint32_t u4 __attribute__((ext_vector_type(4)));
     extern __shared__ double ss[];  // [kNormTB][1 + n_kv] sums of squares
     const int nsig = 1 + p.n_kv_heads;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if ((int)blockIdx.x >= nblk) {
+        __shared__ int sp[4][64], slo[4][64];
+        const int tile = ((int)blockIdx.x - nblk) * 4 + wave;
+        row_plan_tile(p.w, p.cu, p.total_len, p.max_seqlen, p.n_tiles, tile, tile < p.num_seqs * p.n_tiles, lane,
+                      sp[wave], slo[wave], PlanOut{p.plan_perm, p.plan_bounds, p.tile_wmax});
+        return;
+    }
     const int t0 = blockIdx.x * kNormTB;
     const int hch = p.hidden / VW, gh = pow2ceil64(hch);
     const int vch = p.head_dim / VW, gv = pow2ceil64(vch);
@@ -189,40 +199,53 @@ __device__ __forceinline__ void mean_std(double s1, double s2, int n, double& me
     sd = s;
 }
 
+// The canonical sum of a range: kSumParts strided partials (partial t adds elements
+// r0 + t + kSumParts m in increasing m), then a halving tree.
+constexpr int kSumParts = 1024;
+
 __global__ __launch_bounds__(256) void sel_sums_kernel(SelectParams p, const float* nx, const float* nv,
                                                        double* sums, double* stats) {
-    // U loads in flight per thread (one memory round trip per 256*U values).  The
-    // summation order is the canonical one; reads past the range return zero, and
-    // adding +0 to these sums of non-negative norms changes no bit.
-    constexpr int U = 64;
-    __shared__ double a1[256], a2[256];
+    // thread t owns partials t + 256 q (q = 0..3), U chain steps of each in flight; reads past
+    // the range return zero, and adding +0 to these sums of non-negative norms changes no bit
+    constexpr int Q = kSumParts / 256, U = 8;
+    __shared__ double a1[kSumParts], a2[kSumParts];
     const int r = blockIdx.x, sig = blockIdx.y, t = threadIdx.x;
     const float* x = sig == 0 ? nx : nv + (int64_t)(sig - 1) * p.total_len;
     int r0, r1;
     range_of(p, r, r0, r1);
-    double s1 = 0.0, s2 = 0.0;
-    for (int j0 = r0; j0 < r1; j0 += 256 * U) {
-        const int n = min(256 * U, r1 - j0);
+    double s1[Q], s2[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) s1[q] = s2[q] = 0.0;
+    for (int j0 = r0; j0 < r1; j0 += kSumParts * U) {
+        const int n = min(kSumParts * U, r1 - j0);
         const __amdgpu_buffer_rsrc_t rs =
             __builtin_amdgcn_make_buffer_rsrc((void*)(x + j0), (short)0, (int)(n * sizeof(float)), 0x00020000);
-        float xv[U];
+        float xv[U][Q];
 #pragma unroll
-        for (int k = 0; k < U; ++k)
-            xv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)(t + 256 * k) * 4u, 0, 0));
+        for (int m = 0; m < U; ++m)
 #pragma unroll
-        for (int k = 0; k < U; ++k) {
-            double v = (double)xv[k];
-            s1 = __dadd_rn(s1, v);
-            s2 = __dadd_rn(s2, __dmul_rn(v, v));
-        }
+            for (int q = 0; q < Q; ++q)
+                xv[m][q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                          rs, (uint32_t)(t + 256 * q + kSumParts * m) * 4u, 0, 0));
+#pragma unroll
+        for (int m = 0; m < U; ++m)
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const double v = (double)xv[m][q];
+                s1[q] = __dadd_rn(s1[q], v);
+                s2[q] = __dadd_rn(s2[q], __dmul_rn(v, v));
+            }
     }
-    a1[t] = s1;
-    a2[t] = s2;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        a1[t + 256 * q] = s1[q];
+        a2[t + 256 * q] = s2[q];
+    }
     __syncthreads();
-    for (int off = 128; off >= 1; off >>= 1) {
-        if (t < off) {
-            a1[t] = __dadd_rn(a1[t], a1[t + off]);
-            a2[t] = __dadd_rn(a2[t], a2[t + off]);
+    for (int off = kSumParts / 2; off >= 1; off >>= 1) {
+        for (int i = t; i < off; i += 256) {
+            a1[i] = __dadd_rn(a1[i], a1[i + off]);
+            a2[i] = __dadd_rn(a2[i], a2[i + off]);
         }
         __syncthreads();
     }
@@ -735,9 +758,10 @@ constexpr int kPartMax = 2048;   // candidates per part (keys in LDS)
 constexpr int kMergeMax = 4096;  // keys per merge block
 
 // key of set (h, sequence s starting at st): z-scores from the norms and the range's
-// statistics (the same values sel_z stores)
-__device__ __forceinline__ KeyFn global_key(const SelectParams& p, const float* nx, const float* nv,
-                                            const double* stats, int s, int st, int h) {
+// statistics (mean, std of the hidden-state and value-vector norms; the same values sel_z
+// stores)
+__device__ __forceinline__ KeyFn global_key_of(const SelectParams& p, const float* nx, const float* nv, int st, int h,
+                                               double mx, double sx, double mv, double sv) {
     KeyFn key;
     key.w = p.w;
     key.total_len = p.total_len;
@@ -751,17 +775,76 @@ __device__ __forceinline__ KeyFn global_key(const SelectParams& p, const float* 
     key.nx = nx;
     key.nv = nv;
     key.pk = nullptr;
-    const int nsig = 1 + p.n_kv_heads;
-    const int r = p.stats_scope == DSALT_STATS_PACKED ? 0 : s;
-    const double* sx = stats + (int64_t)r * nsig * 2;
-    const double* sv = stats + ((int64_t)r * nsig + 1 + key.rep_g) * 2;
-    key.mx = sx[0];
-    key.sx = sx[1];
-    key.mv = sv[0];
-    key.sv = sv[1];
+    key.mx = mx;
+    key.sx = sx;
+    key.mv = mv;
+    key.sv = sv;
     key.rsx = __ddiv_rn(1.0, key.sx);
     key.rsv = __ddiv_rn(1.0, key.sv);
     return key;
+}
+
+__device__ __forceinline__ int global_range(const SelectParams& p, int s) {
+    return p.stats_scope == DSALT_STATS_PACKED ? 0 : s;
+}
+
+// Statistics of range r for the hidden-state norms (q = 0) and the norms of value head g
+// (q = 1), computed by one 1024-thread block in sel_sums' canonical order: thread t sums
+// partial t of both signals, then the halving tree, then mean_std.  The global top-k parts
+// use it when no caller asked for z or scores, so no sel_sums launch precedes them.
+__device__ void pair_stats(const SelectParams& p, const float* nx, const float* nv, int r, int g, double (&mean)[2],
+                           double (&sd)[2]) {
+    static_assert(kSelThreads == kSumParts, "one partial per thread");
+    constexpr int U = 16;
+    __shared__ double a1[2][kSumParts], a2[2][kSumParts];
+    const int t = threadIdx.x;
+    int r0, r1;
+    range_of(p, r, r0, r1);
+    const float* xs[2] = {nx, nv + (int64_t)g * p.total_len};
+    double s1[2] = {0.0, 0.0}, s2[2] = {0.0, 0.0};
+    for (int j0 = r0; j0 < r1; j0 += kSumParts * U) {
+        const int n = min(kSumParts * U, r1 - j0);
+        float xv[2][U];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc((void*)(xs[q] + j0), (short)0, (int)(n * sizeof(float)), 0x00020000);
+#pragma unroll
+            for (int m = 0; m < U; ++m)
+                xv[q][m] = __builtin_bit_cast(float,
+                                              __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)(t + kSumParts * m) * 4u, 0, 0));
+        }
+#pragma unroll
+        for (int m = 0; m < U; ++m)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const double v = (double)xv[q][m];
+                s1[q] = __dadd_rn(s1[q], v);
+                s2[q] = __dadd_rn(s2[q], __dmul_rn(v, v));
+            }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        a1[q][t] = s1[q];
+        a2[q][t] = s2[q];
+    }
+    __syncthreads();
+    for (int off = kSumParts / 2; off >= 1; off >>= 1) {
+        if (t < off) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                a1[q][t] = __dadd_rn(a1[q][t], a1[q][t + off]);
+                a2[q][t] = __dadd_rn(a2[q][t], a2[q][t + off]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        mean[u] = 0.0;
+        sd[u] = 1.0;
+        if (r1 > r0) mean_std(a1[u][0], a2[u][0], r1 - r0, mean[u], sd[u]);
+    }
 }
 
 // Writes the kpad largest of the n keys a[0..n) (LDS) to o, in no particular order: the keys
@@ -796,7 +879,20 @@ __global__ __launch_bounds__(kSortThreads) void sel_part_kernel(SelectParams p, 
     const int s = sidx % p.num_seqs, h = sidx / p.num_seqs;
     int st, len;
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
-    const KeyFn key = global_key(p, nx, nv, stats, s, st, h);
+    const int g = h / (p.n_heads / p.n_kv_heads), r = global_range(p, s);
+    double mean[2], sd[2];
+    if (stats) {  // written by sel_sums
+        const int nsig = 1 + p.n_kv_heads;
+        const double* sx = stats + (int64_t)r * nsig * 2;
+        const double* sv = stats + ((int64_t)r * nsig + 1 + g) * 2;
+        mean[0] = sx[0];
+        sd[0] = sx[1];
+        mean[1] = sv[0];
+        sd[1] = sv[1];
+    } else {
+        pair_stats(p, nx, nv, r, g, mean, sd);
+    }
+    const KeyFn key = global_key_of(p, nx, nv, st, h, mean[0], sd[0], mean[1], sd[1]);
     const int j0 = part * psize;
     const int n = max(0, min(psize, len - j0));
     for (int i = tid; i < n; i += kSortThreads) keys[i] = key(j0 + i);
@@ -1245,15 +1341,21 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
     }
     if (p.total_len > 0) {
         const int blocks = ceil_div(p.total_len, kNormTB);
+        const int plan_blocks = p.plan_perm ? ceil_div(p.num_seqs * p.n_tiles, 4) : 0;
+        const dim3 grid(blocks + plan_blocks);
         const size_t shm = sizeof(double) * kNormTB * nsig;
         if (p.dtype == DSALT_DTYPE_BF16)
-            DSALT_LAUNCH("sel_norms", sel_norms_kernel<bf16>, dim3(blocks), dim3(256), shm, stream, p, nx, nv, pk);
+            DSALT_LAUNCH("sel_norms", sel_norms_kernel<bf16>, grid, dim3(256), shm, stream, p, nx, nv, pk, blocks);
         else if (p.dtype == DSALT_DTYPE_F16)
-            DSALT_LAUNCH("sel_norms", sel_norms_kernel<f16>, dim3(blocks), dim3(256), shm, stream, p, nx, nv, nullptr);
+            DSALT_LAUNCH("sel_norms", sel_norms_kernel<f16>, grid, dim3(256), shm, stream, p, nx, nv, nullptr, blocks);
         else
-            DSALT_LAUNCH("sel_norms", sel_norms_kernel<float>, dim3(blocks), dim3(256), shm, stream, p, nx, nv, nullptr);
-        DSALT_LAUNCH("sel_sums", sel_sums_kernel, dim3(nranges, nsig), dim3(256), 0, stream, p, nx, nv, sums,
-                     global ? stats : nullptr);
+            DSALT_LAUNCH("sel_norms", sel_norms_kernel<float>, grid, dim3(256), shm, stream, p, nx, nv, nullptr, blocks);
+        // the global top-k parts compute the statistics they need themselves (the same order)
+        // unless z or scores are written for the caller
+        const bool global_parts_only = global && !p.z_x && !p.z_v && !p.scores;
+        if (!global_parts_only)
+            DSALT_LAUNCH("sel_sums", sel_sums_kernel, dim3(nranges, nsig), dim3(256), 0, stream, p, nx, nv, sums,
+                         global ? stats : nullptr);
         if (global) {
             // z-scores are stored only for the caller (the selection recomputes them from the norms)
             if (p.z_x || p.z_v)
@@ -1298,8 +1400,9 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
     const size_t kb = align256(sizeof(unsigned long long) * (size_t)nsets_total * t.nparts * t.kpad);
     unsigned long long* ka = (unsigned long long*)w;
     unsigned long long* kb2 = (unsigned long long*)(w + kb);
+    const bool stats_written = p.z_x || p.z_v || p.scores;
     DSALT_LAUNCH("sel_part", sel_part_kernel, dim3(nsets_total * t.nparts), dim3(kSortThreads), 0, stream, p, nx, nv,
-                 stats, t.psize, t.nparts, t.kpad, ka);
+                 stats_written ? stats : nullptr, t.psize, t.nparts, t.kpad, ka);
     // keys per merge block <= kMergeMax
     auto merge = [&](int nin, unsigned long long* out, int nout) {
         DSALT_LAUNCH("sel_merge", sel_merge_kernel, dim3(nsets_total * nout), dim3(kSortThreads), 0, stream, p, ka,

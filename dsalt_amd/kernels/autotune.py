@@ -9,8 +9,10 @@ row per lane), key chunks of BLOCK_N rows staged in LDS, 16x16x32 MFMA tiles -- 
 run time by the ``variant`` bits of the C ABI (``DSALT_VARIANT_*``):
 
   * FWD_BN32  forward key chunks of 32 instead of 64 rows (16-bit, head_dim 64);
-  * FWD_RG2   forward blocks of 128 rows, two 16-row groups per wave (16-bit, head_dim 64; with
-              FWD_BN32 the kernel is held at four waves per SIMD);
+  * FWD_RG2   forward blocks of 128 rows, two 16-row groups per wave (16-bit; for head_dim 64
+              with FWD_BN32 the kernel is held at four waves per SIMD);
+  * FWD_BN64  forward key chunks of 64 instead of 32 rows (16-bit, head_dim 128, inference;
+              ignored with FWD_RG2);
   * DQ_BN64   backward dQ key chunks of 64 instead of 32 rows (16-bit, head_dim 64);
   * LMK_SHORT landmark-backward row chunks of 512 instead of 1024 rows (more blocks).
 
@@ -24,7 +26,7 @@ from __future__ import annotations
 
 import torch
 
-from .._lib import VARIANT_DQ_BN64, VARIANT_FWD_BN32, VARIANT_FWD_RG2, VARIANT_LMK_SHORT
+from .._lib import VARIANT_DQ_BN64, VARIANT_FWD_BN32, VARIANT_FWD_BN64, VARIANT_FWD_RG2, VARIANT_LMK_SHORT
 
 _TUNED_CONFIG: dict = {}
 
@@ -45,11 +47,14 @@ def _device_key(head_dim: int, device, dtype=torch.bfloat16) -> tuple:
 def _config_of(head_dim: int, elem_bytes: int, variant: int) -> dict:
     hd = 64 if head_dim <= 64 else 128
     bn, bnq, bq = _TILES[(hd, 4 if elem_bytes == 4 else 2)]
-    tunable = hd == 64 and elem_bytes == 2
+    half = elem_bytes == 2
+    tunable = hd == 64 and half
     bm = 64
     if tunable and variant & VARIANT_FWD_BN32:
         bn = 32
-    if tunable and variant & VARIANT_FWD_RG2:
+    if half and hd == 128 and variant & VARIANT_FWD_BN64 and not variant & VARIANT_FWD_RG2:
+        bn = 64
+    if half and variant & VARIANT_FWD_RG2:
         bm = 128
     if tunable and variant & VARIANT_DQ_BN64:
         bnq = 64
@@ -68,13 +73,15 @@ def _candidate_configs(head_dim: int, device=None, elem_bytes: int = 2) -> list[
     if head_dim == 64 and elem_bytes == 2:
         variants = [0, VARIANT_FWD_BN32, VARIANT_FWD_RG2, VARIANT_FWD_RG2 | VARIANT_FWD_BN32,
                     VARIANT_DQ_BN64, VARIANT_LMK_SHORT, VARIANT_DQ_BN64 | VARIANT_LMK_SHORT]
+    elif head_dim == 128 and elem_bytes == 2:
+        variants = [0, VARIANT_FWD_RG2, VARIANT_FWD_BN64, VARIANT_LMK_SHORT]
     else:
         variants = [0, VARIANT_LMK_SHORT]
     return [_config_of(head_dim, elem_bytes, v) for v in variants]
 
 
 # variant bits of the forward kernels and of the backward kernels (independent choices)
-_FWD_BITS = VARIANT_FWD_BN32 | VARIANT_FWD_RG2
+_FWD_BITS = VARIANT_FWD_BN32 | VARIANT_FWD_RG2 | VARIANT_FWD_BN64
 _BWD_BITS = VARIANT_DQ_BN64 | VARIANT_LMK_SHORT
 
 

@@ -111,12 +111,14 @@ def select_landmarks(h: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, w: t
                      cu_seqlens: torch.Tensor, k_lmk: int, *, max_seqlen: int | None = None,
                      select_mode: int = SELECT_GLOBAL, block_size: int = 512,
                      stats_scope: int = STATS_PACKED, want_scores: bool = False,
-                     border_cap: int | None = None):
+                     border_cap: int | None = None, plan: torch.Tensor | None = None):
     """Landmark indices [H, S, n_sets, k] (int32, ascending, -1 padded).
 
     h [T, hidden], v [T, n_kv, D] (value vectors x W_V^T without bias), alpha [H] in (0,1),
     w [T] integer windows, cu_seqlens [S+1].  With ``want_scores`` (global variant) also
-    returns z_x [T], z_v [T, n_kv] and scores [T, H] in fp32.
+    returns z_x [T], z_v [T, n_kv] and scores [T, H] in fp32.  ``plan`` (ops.new_plan)
+    receives the forward's row plan of these windows, computed in the norms launch; pass it
+    to attention_forward with ``plan_ready=True``.
     """
     dev = _gpu(h, v, alpha, w, cu_seqlens)
     if h.dim() != 2 or h.stride(1) != 1:
@@ -154,6 +156,7 @@ def select_landmarks(h: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, w: t
     a.z_x = zx.data_ptr() if zx is not None else None
     a.z_v = zv.data_ptr() if zv is not None else None
     a.scores = sc.data_ptr() if sc is not None else None
+    a.plan = _check_plan(plan, a) or None
     L = _lib.load()
     if border_cap is None:
         need = L.dsalt_select_workspace_bytes(ctypes.byref(a))
@@ -238,15 +241,18 @@ def _check_plan(plan, a) -> int:
 
 def attention_forward(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias=None, *, scale=None,
                       max_seqlen=None, select_mode=SELECT_GLOBAL, block_size=512, plan=None,
-                      variant=VARIANT_DEFAULT):
+                      variant=VARIANT_DEFAULT, plan_ready=False):
     """(out [T,H,D] in q.dtype, lse [T,H] fp32).  lmk_idx [H,S,n_sets,K] int32 ascending with
     -1 padding at the end of each set (as select_landmarks returns; a position may repeat, each
     copy counts).  ``plan`` (ops.new_plan) receives the row plan for attention_backward of the
-    same rows; ``variant`` picks a tiling (VARIANT_* bits, kernels.autotune)."""
+    same rows; ``variant`` picks a tiling (VARIANT_* bits, kernels.autotune); ``plan_ready``:
+    ``plan`` already holds the row plan of these windows (select_landmarks(plan=...)), so the
+    forward reads it instead of recomputing it."""
     a, out, lse, keep = _fwd_args(q, k, v, w, cu_seqlens, lmk_idx, lmk_bias, scale, max_seqlen, select_mode,
                                   block_size)
     a.plan = _check_plan(plan, a) or None
     a.variant = int(variant)
+    a.plan_ready = 1 if (plan_ready and plan is not None) else 0
     if q.shape[0] == 0:
         return out, lse
     dev = out.device

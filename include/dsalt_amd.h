@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DSALT_ABI_VERSION 2
+#define DSALT_ABI_VERSION 3
 
 /* element types of token tensors */
 #define DSALT_DTYPE_F32  0
@@ -99,6 +99,11 @@ typedef struct dsalt_select_args {
     float* z_v;                /* optional out [T, n_kv] (global variant)           */
     float* scores;             /* optional out [T, H]    (global variant)           */
     void* workspace; size_t workspace_bytes;
+    /* Optional (NULL: none): a buffer of dsalt_plan_bytes(&p) bytes that receives the
+     * forward's row plan of these rows (from w and cu_seqlens), computed in the same
+     * launch as the norms.  dsalt_fwd with the same buffer, w, cu_seqlens and shape and
+     * plan_ready set then skips its own plan pass.  No counterpart in the reference. */
+    void* plan;
 } dsalt_select_args;
 
 /* Attention forward.  Replaces _dsalt_fwd_kernel and its launcher
@@ -127,6 +132,10 @@ typedef struct dsalt_fwd_args {
      * variants compute the same result with different tilings; which is fastest
      * depends on the shape (the autotune of dsalt/kernels/autotune.py:55-238). */
     int32_t variant;
+    /* Non-zero: `plan` already holds the row plan of this call's w, cu_seqlens and shape
+     * (written by dsalt_select or an earlier dsalt_fwd) and is read, not recomputed.
+     * Ignored without `plan`, and by dsalt_train_fwd (its windows are floor(w~) + 1). */
+    int32_t plan_ready;
 } dsalt_fwd_args;
 
 /* Attention backward.  Replaces _dsalt_bwd_preprocess + _dsalt_bwd_kernel and
@@ -307,10 +316,12 @@ int    dsalt_silu_mul(const dsalt_silu_mul_args* a, dsalt_stream_t stream);
  * Bits are independent; a bit a shape cannot use is ignored. */
 #define DSALT_VARIANT_DEFAULT    0
 #define DSALT_VARIANT_FWD_BN32   1  /* forward: 32-key chunks (16-bit types, head_dim 64)        */
-#define DSALT_VARIANT_FWD_RG2    2  /* forward: two 16-row groups per wave (16-bit, head_dim 64)  */
+#define DSALT_VARIANT_FWD_RG2    2  /* forward: two 16-row groups per wave (16-bit types)       */
 #define DSALT_VARIANT_DQ_BN64    4  /* backward dQ: 64-key chunks (16-bit types, head_dim 64)     */
 #define DSALT_VARIANT_LMK_SHORT  8  /* backward landmark pass: 512-row chunks                    */
-#define DSALT_VARIANT_MASK       15
+#define DSALT_VARIANT_FWD_BN64  16  /* forward: 64-key chunks (16-bit types, head_dim 128,
+                                       inference operator; ignored with FWD_RG2)                 */
+#define DSALT_VARIANT_MASK       31
 
 /* Bytes of the row-plan buffer of dsalt_fwd_args.plan / dsalt_bwd_args.plan. */
 size_t dsalt_plan_bytes(const dsalt_problem* p);

@@ -23,8 +23,9 @@
  *     (offsets G/2 .. 1); sqrt by canon_sqrt64 (Heron iteration, IEEE ops
  *     only); rounded to fp32, then to the input dtype (torch computes the norm
  *     of a bf16 tensor in bf16).
- *   - statistics: fp64 sums over a range by 256 strided partial sums followed
- *     by a halving tree; mean = S1/n, var = (S2 - (n*mean)*mean)/max(n-1,1)
+ *   - statistics: fp64 sums over a range by 1024 strided partial sums (partial
+ *     t adds elements r0 + t + 1024 m in increasing m) followed by a halving
+ *     tree (offsets 512 .. 1); mean = S1/n, var = (S2 - (n*mean)*mean)/max(n-1,1)
  *     clamped at 0, std = max(canon_sqrt64(var), 1e-6).  Block-causal prefix
  *     sums add whole-block sums in block order.
  *   - z = fp32((a - mean) / std) computed in fp64, for both variants.
@@ -151,11 +152,12 @@ void oracle_norms(const dsalt_select_args* a, float* nx, float* nv) {
 }
 
 /* -------------------------------------------------------------- statistics */
+#define SUM_PARTS 1024
 void oracle_range_sums(const float* x, int64_t r0, int64_t r1, double* s1_out, double* s2_out) {
-    double a1[256], a2[256];
-    for (int t = 0; t < 256; ++t) {
+    static _Thread_local double a1[SUM_PARTS], a2[SUM_PARTS];
+    for (int t = 0; t < SUM_PARTS; ++t) {
         double s1 = 0.0, s2 = 0.0;
-        for (int64_t j = r0 + t; j < r1; j += 256) {
+        for (int64_t j = r0 + t; j < r1; j += SUM_PARTS) {
             double v = (double)x[j];
             s1 = s1 + v;
             s2 = s2 + v * v;
@@ -163,7 +165,7 @@ void oracle_range_sums(const float* x, int64_t r0, int64_t r1, double* s1_out, d
         a1[t] = s1;
         a2[t] = s2;
     }
-    for (int off = 128; off >= 1; off >>= 1)
+    for (int off = SUM_PARTS / 2; off >= 1; off >>= 1)
         for (int t = 0; t < off; ++t) {
             a1[t] = a1[t] + a1[t + off];
             a2[t] = a2[t] + a2[t + off];

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_function():
     for n in names:
         assert hasattr(lib, n), n
     assert set(_lib.SIGNATURES) == names
-    assert lib.dsalt_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.dsalt_abi_version() == _lib.ABI_VERSION == 3
 
 
 STRUCTS = {

@@ -274,3 +274,45 @@ def test_backward_reusing_the_forward_plan_is_bit_identical(G):
     torch.cuda.synchronize()
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("lens,G,mode", [([700, 333, 64], 4, ops.SELECT_GLOBAL), ([4096], 2, ops.SELECT_GLOBAL),
+                                         ([900, 1], 4, ops.SELECT_BLOCK)])
+def test_plan_from_selection_is_the_forwards_plan(lens, G, mode):
+    """The row plan written by the selection's norms launch equals the one the forward computes,
+    byte for byte, and a forward that reads it (plan_ready) gives the same bits."""
+    H, D, K = 4, 64, 24
+    g = torch.Generator().manual_seed(70 + len(lens))
+    T = sum(lens)
+    q = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(T, G, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(T, G, D, generator=g).to(torch.bfloat16)
+    h = torch.randn(T, 128, generator=g).to(torch.bfloat16)
+    w = torch.randint(1, 300, (T,), generator=g, dtype=torch.int32)
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    dev = [t.to(DEV) for t in (q, k, v, h, w, cu)]
+    qd, kd, vd, hd, wd, cud = dev
+    maxlen = max(lens)
+    alpha = torch.full((H,), 0.5, device=DEV)
+    plan_sel = ops.new_plan(qd, kd, cud, torch.empty(H, len(lens), 1, K, dtype=torch.int32, device=DEV),
+                            max_seqlen=maxlen)
+    plan_sel.fill_(0xAB)
+    idx = ops.select_landmarks(hd, vd, alpha, wd, cud, K, max_seqlen=maxlen, select_mode=mode, block_size=128,
+                               plan=plan_sel)
+    idx2 = ops.select_landmarks(hd, vd, alpha, wd, cud, K, max_seqlen=maxlen, select_mode=mode, block_size=128)
+    plan_fwd = torch.zeros_like(plan_sel)
+    a = ops.attention_forward(qd, kd, vd, wd, cud, idx, None, max_seqlen=maxlen, select_mode=mode, block_size=128,
+                              plan=plan_fwd)
+    b = ops.attention_forward(qd, kd, vd, wd, cud, idx, None, max_seqlen=maxlen, select_mode=mode, block_size=128,
+                              plan=plan_sel, plan_ready=True)
+    torch.cuda.synchronize()
+    assert torch.equal(idx, idx2)
+    # every byte the forward reads: the three plan sections of the tiles in use
+    tiles = len(lens) * ((maxlen + 63) // 64)
+    al = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    t64 = al(tiles * 64)  # perm: 64 bytes a tile; bounds: 16 ints a tile; then the largest windows
+    sec = [(0, tiles * 64), (t64, t64 + tiles * 64), (2 * t64, 2 * t64 + 4 * tiles)]
+    for s0, s1 in sec:
+        assert torch.equal(plan_sel[s0:s1], plan_fwd[s0:s1])
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)

@@ -52,18 +52,21 @@ def test_every_candidate_matches_the_oracle(dt, D):
         check_grads(("variant", cfg["variant"]), (dq, dk, dv), rg[:3], idx, cu, TOL[dt])
 
 
-@pytest.mark.parametrize("variant", [c["variant"] for c in AT._candidate_configs(64, None, 2)])
-def test_every_candidate_block_causal_forward(variant):
-    """The block-causal operator with every 16-bit head_dim-64 tiling (the autograd operator
-    passes the tuned variant in block-causal mode too): 128-query blocks, GQA, ragged."""
+@pytest.mark.parametrize("D,variant", [(d, c["variant"]) for d in (64, 128)
+                                       for c in AT._candidate_configs(d, None, 2)])
+def test_every_candidate_block_causal_forward(D, variant):
+    """The block-causal operator with every 16-bit tiling (the autograd operator passes the
+    tuned variant in block-causal mode too; the head_dim-128 inference shapes are block-causal):
+    128-query blocks, GQA, ragged."""
     dt = torch.bfloat16
-    q, k, v, w, cu, idx, lb, maxlen = _inputs([900, 400], 4, 2, 64, 40, 300, dt, 63, mode=ops.SELECT_BLOCK,
+    q, k, v, w, cu, idx, lb, maxlen = _inputs([900, 400], 4, 2, D, 40, 300, dt, 63, mode=ops.SELECT_BLOCK,
                                               block=128)
     dev = [t.to(DEV) for t in (q, k, v, w, cu, idx)]
-    out, lse = ops.attention_forward(*dev, None, scale=0.125, max_seqlen=maxlen, select_mode=ops.SELECT_BLOCK,
+    scale = 1.0 / math.sqrt(D)
+    out, lse = ops.attention_forward(*dev, None, scale=scale, max_seqlen=maxlen, select_mode=ops.SELECT_BLOCK,
                                      block_size=128, variant=variant)
     torch.cuda.synchronize()
-    ro, rl = OA.attention_fwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), 0.125, block_size=128)
+    ro, rl = OA.attention_fwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale, block_size=128)
     assert rel_err(f64(out), ro) < TOL[dt]
     assert rel_err(f64(lse), rl) < 2e-3
 
