@@ -31,6 +31,7 @@ import torch
 
 from .. import ops
 from .autotune import tuned_variant
+from .dsalt_attn import pad_head_dim, padded_head_dim
 
 
 class DSALTTrainFunction(torch.autograd.Function):
@@ -43,9 +44,12 @@ class DSALTTrainFunction(torch.autograd.Function):
         max_seqlen = ops._max_seqlen(cu_seqlens, cu_list)
         cu_i = cu_seqlens.detach().to(torch.int32)
         w_c = w_cont.detach().to(torch.float32).contiguous()
-        scale = 1.0 / math.sqrt(q.shape[-1])
+        head_dim = q.shape[-1]
+        scale = 1.0 / math.sqrt(head_dim)
+        dp = padded_head_dim(head_dim)  # other head_dims run zero-padded (see dsalt_attn)
+        q, k, v = (pad_head_dim(t, dp) for t in (q, k, v))
         plan = ops.new_plan(q, k, cu_i, idx_s, max_seqlen=max_seqlen)
-        variant = tuned_variant(q.shape[-1], q.device, q.dtype)  # autotune_blocks' choice, if made
+        variant = tuned_variant(dp, q.device, q.dtype)  # autotune_blocks' choice, if made
         out, lse = ops.train_forward(q, k, v, w_c, cu_i, idx_s, logw_s, tau_win=float(tau_win),
                                      win_edge=float(win_edge), scale=scale, max_seqlen=max_seqlen, plan=plan,
                                      variant=variant)
@@ -53,19 +57,24 @@ class DSALTTrainFunction(torch.autograd.Function):
         ctx.max_seqlen, ctx.scale, ctx.variant = max_seqlen, scale, variant
         ctx.tau_win, ctx.win_edge = float(tau_win), float(win_edge)
         ctx.logw_dtype, ctx.w_dtype = lmk_logw.dtype, w_cont.dtype
-        return out.float()
+        ctx.head_dim = head_dim
+        return out[..., :head_dim].float().contiguous()
 
     @staticmethod
     def backward(ctx, grad_out):
         q, k, v, out, lse, idx_s, logw_s, perm, w_c, cu_i, plan = ctx.saved_tensors
         dq, dk, dv, dlogw, d_w = ops.train_backward(
-            grad_out.to(q.dtype), q, k, v, out, lse, w_c, cu_i, idx_s, logw_s, tau_win=ctx.tau_win,
+            pad_head_dim(grad_out.to(q.dtype), q.shape[-1]), q, k, v, out, lse, w_c, cu_i, idx_s, logw_s,
+            tau_win=ctx.tau_win,
             win_edge=ctx.win_edge, scale=ctx.scale, max_seqlen=ctx.max_seqlen,
             want_dlogw=ctx.needs_input_grad[4], plan=plan, variant=ctx.variant)
         d_logw = None
         if ctx.needs_input_grad[4] and dlogw is not None:
             d_logw = torch.zeros_like(dlogw).scatter_(-1, perm, dlogw)[:, :, 0].to(ctx.logw_dtype)
         d_wc = d_w.to(ctx.w_dtype) if ctx.needs_input_grad[5] else None
+        d = ctx.head_dim
+        if d != q.shape[-1]:
+            dq, dk, dv = (t[..., :d].contiguous() for t in (dq, dk, dv))
         return dq, dk, dv, None, d_logw, d_wc, None, None, None, None, None
 
 

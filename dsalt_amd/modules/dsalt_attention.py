@@ -38,7 +38,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .. import ops
-from ..kernels.dsalt_attn import dsalt_attention
+from ..kernels.dsalt_attn import dsalt_attention, pad_head_dim, padded_head_dim
 from ..kernels.dsalt_train import dsalt_train_attention
 from ..kernels.landmark_tokens_ker import hybrid_scores_per_head
 from ..kernels.selectors import _compute_landmark_indices
@@ -194,21 +194,28 @@ class DSALTAttention(nn.Module):
         idx = lmk.to(torch.int32) if lmk.dim() == 4 else lmk.to(torch.int32).unsqueeze(2)
         mode = ops.SELECT_BLOCK if self.select_mode == "block" else ops.SELECT_GLOBAL
         w32 = w.to(torch.int32)
-        out, lse = ops.attention_forward(q, k, v, w32, cu_seqlens, idx, None, max_seqlen=maxlen, select_mode=mode,
-                                         block_size=self.block_size)
+        # head_dims other than the compiled 64 / 128 run zero-padded, scaled by the true head_dim
+        dp = padded_head_dim(D)
+        if dp != D:
+            q, k, v = (pad_head_dim(t, dp) for t in (q, k, v))
+        scale = 1.0 / math.sqrt(D)
+        out, lse = ops.attention_forward(q, k, v, w32, cu_seqlens, idx, None, scale=scale, max_seqlen=maxlen,
+                                         select_mode=mode, block_size=self.block_size)
+        if dp != D:
+            out = out[..., :D].contiguous()
         self._last_P = self._last_P_sparse = None
         if self._collect_last_P:
-            self._export_last_P(q, k, w32, cu_seqlens, idx, lse, maxlen, mode, cu_list)
+            self._export_last_P(q, k, w32, cu_seqlens, idx, lse, maxlen, mode, cu_list, scale)
         return self._apply_out_proj(out.view(total_len, self.d_model)), self._aux_zero(x.device, x.dtype)
 
-    def _export_last_P(self, q, k, w32, cu_seqlens, idx, lse, maxlen, mode, cu_list):
+    def _export_last_P(self, q, k, w32, cu_seqlens, idx, lse, maxlen, mode, cu_list, scale):
         """Attention probabilities of the first sequence (sparse; dense when short)."""
         from ..kernels.attention_probs import SparseAttentionProbs
         cu_h = list(cu_list) if cu_list is not None else cu_seqlens.detach().to("cpu").tolist()
         n0 = cu_h[1] - cu_h[0]
         p_win, p_lmk = ops.export_probs(q, k, w32, cu_seqlens, idx, lse, seq=0, rows=n0, seq_len=n0,
-                                        w_cap=max(1, min(n0, self.n_max + 1)), max_seqlen=maxlen, select_mode=mode,
-                                        block_size=self.block_size)
+                                        w_cap=max(1, min(n0, self.n_max + 1)), scale=scale, max_seqlen=maxlen,
+                                        select_mode=mode, block_size=self.block_size)
         sp = SparseAttentionProbs(p_win, p_lmk, idx[:, 0].long(), self.block_size if mode == ops.SELECT_BLOCK else 0)
         self._last_P_sparse = sp
         if n0 <= self.last_P_dense_max:

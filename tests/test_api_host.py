@@ -96,3 +96,18 @@ def test_autotune_candidates_describe_the_compiled_tilings():
     # fp32 shapes have one compiled tiling: only the landmark-chunk choice
     assert [c["variant"] for c in AT._candidate_configs(128, None, 4)] == [0, AT.VARIANT_LMK_SHORT]
     assert AT.get_tuned_config.__name__ == "get_tuned_config"
+
+
+def test_head_dim_padding_helpers():
+    """head_dims up to 128 map to the compiled 64 / 128 and pad with zero columns."""
+    import pytest as _pt
+    import torch as _t
+    from dsalt_amd.kernels.dsalt_attn import pad_head_dim, padded_head_dim
+    assert [padded_head_dim(d) for d in (1, 32, 64, 65, 96, 128)] == [64, 64, 64, 128, 128, 128]
+    for bad in (0, 129, 256):
+        with _pt.raises(ValueError):
+            padded_head_dim(bad)
+    x = _t.randn(5, 3, 40)
+    y = pad_head_dim(x, 64)
+    assert y.shape == (5, 3, 64) and _t.equal(y[..., :40], x) and not y[..., 40:].any()
+    assert pad_head_dim(y, 64) is y

@@ -128,10 +128,13 @@ def test_standalone_backward_signature():
     assert rel_err(f64(db), rdb[:, :, 0]) < 2e-2
 
 
-@pytest.mark.parametrize("mode", ["global", "block"])
-def test_dsalt_attention_layer(mode):
+@pytest.mark.parametrize("mode,d", [("global", 256), ("block", 256), ("global", 320)])
+def test_dsalt_attention_layer(mode, d):
+    """The layer's inference branch (fused QKV, RoPE kernel, strided attention) against its
+    parts with the float64 oracle; d = 320 gives head_dim 80 (run zero-padded to 128)."""
     torch.manual_seed(0)
-    d, H, G, T = 256, 4, 2, 640
+    H, G, T = 4, 2, 640
+    D = d // H
     m = DSALTAttention(d, H, 32, 128, 16, 2048, n_kv_heads=G, qkv_bias=True, select_mode=mode,
                        block_size=128).to(DEV).eval()
     x = torch.randn(T, d, device=DEV)
@@ -140,20 +143,59 @@ def test_dsalt_attention_layer(mode):
     assert out.shape == (T, d) and float(aux) == 0.0
     # same computation from its parts, with the float64 oracle as the attention
     with torch.no_grad():
-        q = m.q_proj(x).view(T, H, 64)
-        k = m.k_proj(x).view(T, G, 64)
-        v = m.v_proj(x).view(T, G, 64)
+        q = m.q_proj(x).view(T, H, D)
+        k = m.k_proj(x).view(T, G, D)
+        v = m.v_proj(x).view(T, G, D)
         pos = torch.cat([torch.arange(400), torch.arange(T - 400)]).to(DEV)
         q, k = K.apply_rotary_emb(q, k, m.rope_cos[pos].unsqueeze(1), m.rope_sin[pos].unsqueeze(1))
         w = m._window_sizes(x, floor=True)
         lmk, _, _ = K._compute_landmark_indices(x, m.v_proj.weight, m._alpha(), w, cu, 16, 32, T, [0, 400, T],
-                                                head_dim=64, select_mode=mode, block_size=128)
+                                                head_dim=D, select_mode=mode, block_size=128)
     idx4 = lmk.cpu().numpy() if mode == "block" else lmk.cpu().numpy()[:, :, None]
-    ro, _ = OA.attention_fwd(f64(q), f64(k), f64(v), w.long().cpu().numpy(), cu.cpu().numpy(), idx4, 1 / 8.0,
-                             block_size=128 if mode == "block" else None)
+    ro, _ = OA.attention_fwd(f64(q), f64(k), f64(v), w.long().cpu().numpy(), cu.cpu().numpy(), idx4,
+                             1 / math.sqrt(D), block_size=128 if mode == "block" else None)
     ref = m.out_proj(torch.tensor(ro, dtype=torch.float32, device=DEV).view(T, d))
     assert rel_err(f64(out), f64(ref)) < 1e-5
     # batched input runs as packed sequences
     xb = x[:512].view(2, 256, d)
     ob, _ = m(xb)
     assert ob.shape == (2, 256, d)
+
+
+@pytest.mark.parametrize("D,dt", [(32, torch.bfloat16), (80, torch.bfloat16), (96, torch.float32), (48, torch.float16)])
+def test_autograd_operator_other_head_dims(D, dt):
+    """head_dims the kernels are not compiled for run zero-padded to 64 / 128 with the scale of
+    the true head_dim (the reference pads to the next power of two): output and gradients
+    against the oracle at the true head_dim."""
+    from tests.helpers import check_grads
+    q, k, v, w, cu, idx, bias = _op_case(dt, G=2, D=D, seed=D)
+    tol = 1e-5 if dt == torch.float32 else 2e-2
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    bd = bias.to(DEV).requires_grad_(True)
+    out = K.dsalt_triton_attention(qd, kd, vd, idx.to(DEV), bd, w.to(DEV), cu.to(DEV))
+    assert out.shape == q.shape
+    g = torch.Generator().manual_seed(6)
+    do = torch.randn(out.shape, generator=g)
+    out.backward(do.to(DEV))
+    assert qd.grad.shape == q.shape and kd.grad.shape == k.shape
+    scale = 1.0 / math.sqrt(D)
+    idx4 = idx.numpy()[:, :, None]
+    b4 = bias.double().numpy()[:, :, None]
+    wi = w.clamp(min=1).long().numpy()
+    ro, _ = OA.attention_fwd(f64(q), f64(k), f64(v), wi, cu.numpy(), idx4, scale, lmk_bias=b4)
+    assert rel_err(f64(out), ro) < tol
+    rg = OA.attention_bwd(f64(q), f64(k), f64(v), wi, cu.numpy(), idx4, scale, f64(do.to(dt)), lmk_bias=b4,
+                          out=f64(out.to(dt)))
+    check_grads(("head_dim", D), (qd.grad, kd.grad, vd.grad), rg[:3], idx, cu, tol)
+    assert rel_err(f64(bd.grad), rg[3][:, :, 0]) < tol
+    # the standalone backward pads the same way (forward outputs from the padded operator)
+    from dsalt_amd.kernels.dsalt_attn import pad_head_dim, padded_head_dim
+    dp = padded_head_dim(D)
+    idx_s, bias_s, _ = ops.sort_landmarks(idx.to(DEV).unsqueeze(2), bd.detach().unsqueeze(2))
+    o_p, lse = ops.attention_forward(*(pad_head_dim(t.detach(), dp) for t in (qd, kd, vd)),
+                                     w.to(DEV).clamp(min=1).int(), cu.to(DEV), idx_s, bias_s, scale=scale)
+    dq2, dk2, dv2, db2 = K.dsalt_triton_backward(do.to(DEV), qd.detach(), kd.detach(), vd.detach(),
+                                                 o_p[..., :D].contiguous(), lse, None, None, idx.to(DEV),
+                                                 bd.detach(), w.to(DEV), cu.to(DEV), scale)
+    assert dq2.shape == q.shape and dk2.shape == k.shape
+    check_grads(("standalone head_dim", D), (dq2, dk2, dv2), rg[:3], idx, cu, tol)
