@@ -152,8 +152,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     qr.load(valid ? qhead + (int64_t)i * p.q_st : nullptr, qhead, g);
     dor.load(valid ? dohead + (int64_t)i * p.do_st : nullptr, dohead, g);
     orr.load(valid ? ohead + (int64_t)i * p.o_st : nullptr, ohead, g);
-    blo = uniform(-wave_max(-blo));
-    bhi = uniform(wave_max(bhi));
+    // the band's key range, clamped to the sequence: a plan made for other windows or offsets
+    // gives wrong values, never reads outside the sequence's rows
+    blo = max(uniform(-wave_max(-blo)), 0);
+    bhi = min(uniform(wave_max(bhi)), len - 1);
     blmax = uniform(wave_max(blmax));
 
     int nv_loc = 0;  // one past the last valid slot (sets are ascending, -1 after the valid slots)

@@ -249,8 +249,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     RowReg<T, D> qr[RG];
 #pragma unroll
     for (int u = 0; u < RG; ++u) qr[u].load(rg[u].valid ? qhead + (int64_t)rg[u].i * p.q_st : nullptr, qhead, g);
-    blo = uniform(-wave_max(-blo));
-    bhi = uniform(wave_max(bhi));
+    // the band's key range, clamped to the sequence: a plan made for other windows or offsets
+    // gives wrong values, never reads outside the sequence's rows
+    blo = max(uniform(-wave_max(-blo)), 0);
+    bhi = min(uniform(wave_max(bhi)), len - 1);
     blmax = uniform(wave_max(blmax));
 
     int nv_loc = 0;  // one past the last valid slot (sets are ascending, -1 after the valid slots)
