@@ -38,16 +38,16 @@ class DSALTConfig:
 
     def __post_init__(self) -> None:
         if self.d_model % self.n_heads != 0:
-            raise ValueError(f"d_model ({self.d_model}) must be divisible by n_heads ({self.n_heads})")
+            raise ValueError(f"{self.n_heads} heads do not split a model width of {self.d_model} evenly")
         if not (0 <= self.n_min <= self.n_max):
-            raise ValueError(f"required 0 <= n_min <= n_max, got n_min={self.n_min} n_max={self.n_max}")
+            raise ValueError(f"window bounds out of order: n_min={self.n_min}, n_max={self.n_max} (need 0 <= n_min <= n_max)")
         if self.k_lmk < 0:
-            raise ValueError(f"k_lmk must be >= 0, got {self.k_lmk}")
+            raise ValueError(f"negative landmark count k_lmk={self.k_lmk}")
         if self.n_kv_heads is not None and (self.n_kv_heads <= 0 or self.n_heads % self.n_kv_heads != 0):
             raise ValueError(f"n_heads ({self.n_heads}) must be a positive multiple of n_kv_heads "
                              f"({self.n_kv_heads}) for grouped-query attention")
         if self.loss_fn not in ("auto", "chunked", "liger"):
-            raise ValueError(f"loss_fn must be 'auto', 'chunked' or 'liger', got {self.loss_fn!r}")
+            raise ValueError(f"unknown loss_fn {self.loss_fn!r} (one of 'auto', 'chunked', 'liger')")
         if self.select_mode not in ("global", "block"):
             raise ValueError(f"select_mode must be 'global' or 'block', got {self.select_mode!r}")
 

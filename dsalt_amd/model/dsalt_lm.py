@@ -43,7 +43,7 @@ class DSALTLMHeadModel(nn.Module):
                  select_mode: str = "global", block_size: int = 512, stats_scope: str = "packed"):
         super().__init__()
         if loss_fn not in ("auto", "chunked", "liger"):
-            raise ValueError(f"loss_fn must be 'auto', 'chunked' or 'liger', got {loss_fn!r}")
+            raise ValueError(f"unknown loss_fn {loss_fn!r} (one of 'auto', 'chunked', 'liger')")
         self.d_model, self.n_layers, self.vocab_size = d_model, n_layers, vocab_size
         self.lm_head_chunk_size, self.loss_fn, self.aux_loss_weight = lm_head_chunk_size, loss_fn, aux_loss_weight
         if d_ff is None:
