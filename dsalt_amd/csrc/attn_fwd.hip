@@ -86,6 +86,10 @@ struct RowGroup {
     int lou;   // unclamped window start i - floor(wt) (training variant)
     float eb[kEdgeTab];  // soft-edge bias of keys lou .. lou+3 (training variant, win_edge <= 4)
     int wlo, wLmax, whi, wHmin, wcmax, wcmin;
+    // several landmark sets per block (block-causal, block_size not a multiple of 64): the
+    // row's set starts at slot ls of the staged sets, its visible slots are ls .. ls+cnt-1;
+    // wcmax / wcmin then bound ls + cnt, wsmin / wsmax the set starts of the group's rows
+    int ls, wsmin, wsmax;
 };
 
 // Block group (plan tile u, group within it) taken by wave w: groups are ordered
@@ -146,6 +150,24 @@ __device__ __forceinline__ void plan_counts(const int* lpos, int nvalid, RowGrou
     rg.wcmin = uniform(row_min16(rg.valid ? rg.cnt : 0));
 }
 
+// The same with the block's sets staged side by side: set first + j at slots j*K .. j*K+K-1,
+// nvs[j] valid positions (row i belongs to set i / block_size).
+__device__ __forceinline__ void plan_counts_sets(const int* lpos, const int* nvs, int K, int block_size, int first,
+                                                 int nsets, RowGroup& rg) {
+    int ls = 0, cnt = 0;
+    if (rg.valid) {
+        const int j = min(max(rg.i / block_size - first, 0), nsets - 1);
+        ls = j * K;
+        cnt = lower_bound_lds(lpos + ls, nvs[j], rg.lo);
+    }
+    rg.ls = ls;
+    rg.cnt = cnt;
+    rg.wcmax = uniform(row_max16(ls + cnt));
+    rg.wcmin = uniform(row_min16(rg.valid ? ls + cnt : 0));
+    rg.wsmin = uniform(row_min16(rg.valid ? ls : 0x7fffffff));
+    rg.wsmax = uniform(row_max16(ls));
+}
+
 // Soft-edge bias of the lane's four keys a + lane_off + r of a band subtile (training
 // variant), masked keys (r < tl, and r past the diagonal when `upper`) left at -inf.
 __device__ __forceinline__ void band_edge(const AttnParams& p, const RowGroup& R, int a, int lane_off, int tl,
@@ -171,15 +193,22 @@ __device__ __forceinline__ void band_edge(const AttnParams& p, const RowGroup& R
 // TR: the training variant -- band keys near a row's window start carry the soft
 // edge bias (edge_bias), so chunks classed "every row sees every key" must also
 // lie past every row's first edge_keys band keys.
-template <typename T, int D, int BN, int RG, bool TR>
+//
+// MS: block-causal sets with block_size not a multiple of 64 (one row group per wave, inference
+// only): the block's rows may belong to several sets, all staged in LDS side by side; each row
+// sees the slots of its own set only (a two-sided slot mask, like the band's key mask).
+template <typename T, int D, int BN, int RG, bool TR, bool MS = false>
 __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN == 32) ? 4 : 2) void fwd_kernel(AttnParams p) {
+    static_assert(!MS || (RG == 1 && !TR), "several sets per block: one row group, inference");
     constexpr int NST = BN / 16;
     constexpr bool kHalf = sizeof(T) == 2;
+    constexpr int LCAP = MS ? kMultiSetSlots : kMaxLandmarks;
     typedef Tile<T, D, BN, 256, (BN == 64 ? 8 : Pad<T, D>::R)> KT;
     __shared__ __attribute__((aligned(16))) T Ks[2][KT::ELEMS];
     __shared__ __attribute__((aligned(16))) T Vs[2][KT::ELEMS];
-    __shared__ int lpos[kMaxLandmarks];
-    __shared__ __attribute__((aligned(16))) float lbs[kMaxLandmarks];
+    __shared__ int lpos[LCAP];
+    __shared__ __attribute__((aligned(16))) float lbs[LCAP];
+    static_assert(KT::ELEMS * sizeof(T) >= sizeof(int) * (8 + kMaxTileSets), "block scalars fit a K buffer");
     // block scalars live in the second K buffer until the first chunk is staged there
     // (keeps the block at 40 KB of LDS: four blocks per CU)
     int* red = (int*)Ks[1];
@@ -203,6 +232,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     const int set = p.block_size ? r0 / p.block_size : 0;
     const int K = p.k_lmk;
     const int64_t set_off = (((int64_t)h * p.num_seqs + s) * p.n_sets + set) * K;
+    // sets of the block's rows (MS): set .. set + nsets - 1, at most LCAP slots in all
+    int nsets = 1;
+    if (MS) {
+        const int last = min(r0 + 63, len - 1) / p.block_size;
+        nsets = min(min(last - set + 1, kMaxTileSets), LCAP / max(K, 1));
+    }
+    const int nslots = nsets * K;
     const float c2 = p.c2;
     const float inv_scale = p.inv_scale;
     const bool has_bias = p.lbias != nullptr;
@@ -211,17 +247,25 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     // group bounds and rows -- are issued together, then the rows' windows and query rows;
     // the block's largest visible landmark count follows from the largest window start of
     // its groups, so one barrier (the set in LDS) precedes the first landmark chunk's fetch.
-    int lv[kMaxLandmarks / 256], ln[kMaxLandmarks / 256];
-    float lb[kMaxLandmarks / 256];
+    int lv[LCAP / 256], ln[LCAP / 256];
+    float lb[LCAP / 256];
 #pragma unroll
-    for (int u = 0; u < kMaxLandmarks / 256; ++u) {
+    for (int u = 0; u < LCAP / 256; ++u) {
         lv[u] = -1;
         ln[u] = -1;
         lb[u] = 0.f;
-        if (u * 256 < K) {  // every lane loads (clamped slots), so no load waits on a branch
+        if (!MS && u * 256 < K) {  // every lane loads (clamped slots), so no load waits on a branch
             lv[u] = p.lmk[set_off + min(u * 256 + tid, K - 1)];
             ln[u] = p.lmk[set_off + min(u * 256 + tid + 1, K - 1)];
             if (has_bias) lb[u] = p.lbias[set_off + min(u * 256 + tid, K - 1)];
+        } else if (MS && u * 256 < nslots) {
+            // slot e: position sl of set set + j (the block's sets are consecutive, K slots each)
+            const int e = min(u * 256 + tid, nslots - 1);
+            const int j = e / K, sl = e - j * K;
+            const int64_t o = set_off + (int64_t)j * K;
+            lv[u] = p.lmk[o + sl];
+            ln[u] = p.lmk[o + min(sl + 1, K - 1)];
+            if (has_bias) lb[u] = p.lbias[o + sl];
         }
     }
 
@@ -255,20 +299,41 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     bhi = min(uniform(wave_max(bhi)), len - 1);
     blmax = uniform(wave_max(blmax));
 
-    int nv_loc = 0;  // one past the last valid slot (sets are ascending, -1 after the valid slots)
+    int nvalid;  // valid slots of the (first) set; MS: of any set, and nvs[j] per set
+    int* nvs = red + 8;
+    if constexpr (!MS) {
+        int nv_loc = 0;  // one past the last valid slot (sets are ascending, -1 after the valid slots)
 #pragma unroll
-    for (int u = 0; u < kMaxLandmarks / 256; ++u) {
-        const int i = u * 256 + tid;
-        if (i < K) {
-            lpos[i] = lv[u];
-            if (has_bias) lbs[i] = lb[u] * inv_scale;  // raw-score units
-            if (lv[u] >= 0 && (i + 1 == K || ln[u] < 0)) nv_loc = i + 1;
+        for (int u = 0; u < LCAP / 256; ++u) {
+            const int i = u * 256 + tid;
+            if (i < K) {
+                lpos[i] = lv[u];
+                if (has_bias) lbs[i] = lb[u] * inv_scale;  // raw-score units
+                if (lv[u] >= 0 && (i + 1 == K || ln[u] < 0)) nv_loc = i + 1;
+            }
         }
+        nv_loc = wave_max(nv_loc);
+        if (lane == 0) red[4 + uw] = nv_loc;
+        __syncthreads();
+        nvalid = uniform(max(max(red[4], red[5]), max(red[6], red[7])));
+    } else {
+        if (tid < kMaxTileSets) nvs[tid] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < LCAP / 256; ++u) {
+            const int e = u * 256 + tid;
+            if (e < nslots) {
+                const int j = e / K, sl = e - j * K;
+                lpos[e] = lv[u];
+                if (has_bias) lbs[e] = lb[u] * inv_scale;
+                if (lv[u] >= 0 && (sl + 1 == K || ln[u] < 0)) nvs[j] = sl + 1;  // one writer per set
+            }
+        }
+        __syncthreads();
+        int any = 0;
+        for (int j = 0; j < nsets; ++j) any |= nvs[j];
+        nvalid = uniform(any);
     }
-    nv_loc = wave_max(nv_loc);
-    if (lane == 0) red[4 + uw] = nv_loc;
-    __syncthreads();
-    const int nvalid = uniform(max(max(red[4], red[5]), max(red[6], red[7])));
 
     const T* kbase = (const T*)p.k + (int64_t)st * p.k_st + (int64_t)kvh * p.k_sh;
     const T* vbase = (const T*)p.v + (int64_t)st * p.v_st + (int64_t)kvh * p.v_sh;
@@ -309,12 +374,21 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
                     vbase);
         }
     };
-    if (nvalid > 0) load_lmk_lim(0, nvalid);
+    if (nvalid > 0) load_lmk_lim(0, MS ? nslots : nvalid);
 
+    int bcm;
+    if constexpr (!MS) {
 #pragma unroll
-    for (int u = 0; u < RG; ++u) plan_counts(lpos, nvalid, rg[u]);
-    // the block's largest visible count: that of its largest window start (counts grow with it)
-    const int bcm = uniform(lower_bound_lds(lpos, nvalid, blmax));
+        for (int u = 0; u < RG; ++u) plan_counts(lpos, nvalid, rg[u]);
+        // the block's largest visible count: that of its largest window start (counts grow with it)
+        bcm = uniform(lower_bound_lds(lpos, nvalid, blmax));
+    } else {
+#pragma unroll
+        for (int u = 0; u < RG; ++u) plan_counts_sets(lpos, nvs, K, p.block_size, set, nsets, rg[u]);
+        // the last set's rows end furthest: its count at the block's largest window start bounds them
+        const int lj = (nsets - 1) * K;
+        bcm = uniform(lj + lower_bound_lds(lpos + lj, nvs[nsets - 1], blmax));
+    }
     const int cs = (blo / BN) * BN;
     const int nband = bhi >= blo ? (bhi - cs) / BN + 1 : 0;
     const int nchunks = nband + ceil_div(bcm, BN);
@@ -394,9 +468,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
                 else if (base >= R.wLmax + (TR ? p.edge_keys : 0) && last <= R.wHmin) kind = 1;
                 else if (BN > 32 && last <= R.wHmin) kind = 2;
                 else kind = 3;
-            } else {
+            } else if (!MS) {
                 if (base >= R.wcmax) kind = 0;
                 else if (base + BN - 1 < R.wcmin) kind = 4;
+                else kind = 5;
+            } else {
+                if (base >= R.wcmax || base + BN - 1 < R.wsmin) kind = 0;
+                else if (base >= R.wsmax && base + BN - 1 < R.wcmin) kind = 4;
                 else kind = 5;
             }
             gact[u] = kind != 0;
@@ -452,17 +530,23 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
 #pragma unroll
                 for (int stt = 0; stt < NST; ++stt) {
                     const int a = base + stt * 16;
-                    act[u][stt] = a < R.wcmax;
+                    act[u][stt] = a < R.wcmax && (!MS || a + 15 >= R.wsmin);
                     if (!act[u][stt]) {
                         S[u][stt] = floatx4{NEG, NEG, NEG, NEG};
                         continue;
                     }
-                    // slots past the valid count are masked below (a + 15 < 512)
+                    // slots past the valid count are masked below (a + 15 < LCAP)
                     const floatx4 bv = has_bias ? *(const floatx4*)(lbs + a + lane_off) : zero;
-                    const int tc = R.cnt - a - lane_off;
                     floatx4 ci;
+                    if constexpr (!MS) {
+                        const int tc = R.cnt - a - lane_off;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ci[r] = r < tc ? bv[r] : NEG;
+                        for (int r = 0; r < 4; ++r) ci[r] = r < tc ? bv[r] : NEG;
+                    } else {  // slot in [ls, ls + cnt): one unsigned compare
+                        const int x0 = a + lane_off - R.ls;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) ci[r] = (unsigned)(x0 + r) < (unsigned)R.cnt ? bv[r] : NEG;
+                    }
                     KOp<T, D> ko;
                     ko.load(kl, KT::RS, stt * 16, lane);
                     S[u][stt] = ko.dot(qr[u], ci);
@@ -565,10 +649,18 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
 // stay within one landmark set, block_size a multiple of 128); for 16-bit head_dim 128, two
 // row groups per wave (FWD_RG2, same condition) or 64-key chunks instead of 32 (FWD_BN64;
 // ignored with FWD_RG2);
-// fp32 takes its single compiled tiling.
+// fp32 takes its single compiled tiling.  Block-causal sets of a block_size that is not a
+// multiple of 64 take the default tiling with several sets per block (variant bits ignored).
 template <typename T, int D, bool TR>
 static void fwd_run(const AttnParams& p, hipStream_t stream) {
     constexpr int BN = FwdShape<T, D>::BN;
+    if constexpr (!TR) {
+        if (p.block_size % 64) {
+            DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, BN, 1, false, true>), dim3(p.n_heads * p.num_seqs * p.n_tiles),
+                         dim3(256), 0, stream, p);
+            return;
+        }
+    }
     if constexpr (sizeof(T) == 2) {
         const bool rg2 = (p.variant & DSALT_VARIANT_FWD_RG2) != 0 && (p.block_size == 0 || p.block_size % 128 == 0);
         const int total = p.n_heads * p.num_seqs * ceil_div(p.n_tiles, rg2 ? 2 : 1);

@@ -61,8 +61,8 @@ int check_problem(const dsalt_problem& p, bool attention) {
         return fail(DSALT_ERR_INVALID, "k_lmk %d outside [0, %d]", p.k_lmk, dsalt::kMaxLandmarks);
     if (p.select_mode != DSALT_SELECT_GLOBAL && p.select_mode != DSALT_SELECT_BLOCK)
         return fail(DSALT_ERR_INVALID, "unknown select_mode %d", p.select_mode);
-    if (p.select_mode == DSALT_SELECT_BLOCK && (p.block_size < 64 || p.block_size % 64))
-        return fail(DSALT_ERR_INVALID, "block_size %d must be a positive multiple of 64", p.block_size);
+    if (p.select_mode == DSALT_SELECT_BLOCK && p.block_size < 1)
+        return fail(DSALT_ERR_INVALID, "block_size %d must be positive", p.block_size);
     if (p.dtype != DSALT_DTYPE_F32 && p.dtype != DSALT_DTYPE_BF16 && p.dtype != DSALT_DTYPE_F16)
         return fail(DSALT_ERR_INVALID, "unknown dtype %d", p.dtype);
     return DSALT_OK;
@@ -195,11 +195,29 @@ int dsalt_select(const dsalt_select_args* a, dsalt_stream_t stream) {
     return dsalt_select_with_border_cap(a, stream, 1 << 30);
 }
 
+// Most landmark sets the rows of one 64-row tile belong to (block-causal sets).
+static int max_sets_per_tile(const dsalt_problem& p) {
+    if (p.select_mode != DSALT_SELECT_BLOCK || p.block_size % 64 == 0) return 1;
+    int m = 1;
+    for (int r0 = 0; r0 < p.max_seqlen; r0 += 64) {
+        const int last = (r0 + 63 < p.max_seqlen ? r0 + 63 : p.max_seqlen - 1) / p.block_size;
+        const int n = last - r0 / p.block_size + 1;
+        if (n > m) m = n;
+    }
+    return m;
+}
+
 // forward parameters; `need_w` is false for the training variant (windows from w_cont)
 static int fwd_params(const dsalt_fwd_args* a, bool need_w, dsalt::AttnParams* out) {
     if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
     int rc = check_problem(a->p, true);
     if (rc) return rc;
+    // block sizes that are not multiples of 64: a tile's sets are staged in LDS together
+    const int tsets = max_sets_per_tile(a->p);
+    if (tsets > 1 && tsets * a->p.k_lmk > dsalt::kMultiSetSlots)
+        return fail(DSALT_ERR_UNSUPPORTED,
+                    "block_size %d: 64-row tiles span %d landmark sets; %d sets x k_lmk %d exceeds %d slots",
+                    a->p.block_size, tsets, tsets, a->p.k_lmk, dsalt::kMultiSetSlots);
     const int dt = a->p.dtype;
     if ((rc = check_rows(a->q, a->q_stride_t, a->q_stride_h, dt, "q"))) return rc;
     if ((rc = check_rows(a->k, a->k_stride_t, a->k_stride_h, dt, "k"))) return rc;

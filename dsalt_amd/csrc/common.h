@@ -21,6 +21,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 constexpr int kMaxLandmarks = 512;
+// Block-causal problems whose block_size is not a multiple of 64: a 64-row tile spans up to
+// kMaxTileSets landmark sets, staged side by side (sets x k_lmk at most kMultiSetSlots).
+constexpr int kMaxTileSets = 64;
+constexpr int kMultiSetSlots = 1024;
 
 __device__ __forceinline__ float to_float(float x) { return x; }
 __device__ __forceinline__ float to_float(bf16 x) { return (float)x; }

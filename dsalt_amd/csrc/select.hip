@@ -709,8 +709,8 @@ __global__ __launch_bounds__(256) void sel_prune_mark_kernel(SelectParams p, con
 }
 
 // per (super-block, sequence, kv head): the survivors' in-sequence indices, in token order,
-// at the super-block's offset of the (kv head, sequence) list, and at every 16th token of
-// the sequence the number of survivors below it
+// at the super-block's offset of the (kv head, sequence) list, and at every token of the
+// sequence the number of survivors below it (a block of any size starts at any token)
 __global__ __launch_bounds__(256) void sel_prune_list_kernel(SelectParams p, const uint8_t* keep, const int* cnt,
                                                              int32_t* list, int32_t* below) {
     __shared__ int wsum[4], woff[4];
@@ -747,10 +747,12 @@ __global__ __launch_bounds__(256) void sel_prune_list_kernel(SelectParams p, con
     int base = woff[0] + woff[1] + woff[2] + woff[3] + inc - c;
     for (int w2 = 0; w2 < wave; ++w2) base += wsum[w2];
     int32_t* lo = list + (int64_t)g * p.total_len + st;
-    if (a < len) below[(int64_t)g * p.total_len + st + a] = base;  // survivors below token a
+    int32_t* bl = below + (int64_t)g * p.total_len + st;
 #pragma unroll
-    for (int u = 0; u < PER; ++u)
+    for (int u = 0; u < PER; ++u) {
+        if (a + u < len) bl[a + u] = base;  // survivors below token a + u
         if (kb[u]) lo[base++] = a + u;
+    }
 }
 
 // ------------------------------------------- global variant: parts + merges
@@ -990,9 +992,8 @@ __global__ __launch_bounds__(NT) void sel_topk_kernel(SelectParams p, const floa
     // entries below b0 where it applies to this head (alpha in [0, 1]), else 0 .. b0-1
     const int32_t* cl = nullptr;
     if (block && plist && key.alpha >= 0.f && key.alpha <= 1.f) {
-        // b0 is a multiple of 16 (block_size is a multiple of 64, checked at the boundary)
         cl = plist + (int64_t)key.rep_g * p.total_len + st;
-        n = pbelow[(int64_t)key.rep_g * p.total_len + st + n];
+        n = pbelow[(int64_t)key.rep_g * p.total_len + st + n];  // survivors below b0
     }
     auto cand = [&](int e) { return cl ? cl[e] : e; };
     const int cap = min(border_cap, kBorderCap);

@@ -97,6 +97,24 @@ def test_fwd_validation(field, value, code):
     assert lib.dsalt_last_error()
 
 
+def test_block_sizes_and_the_sets_of_a_tile():
+    """Any block_size >= 1; when it is not a multiple of 64 the forward stages every set a
+    64-row tile's rows use: at most 1024 slots (sets x k_lmk)."""
+    lib = _lib.load()
+    a = _valid_fwd()
+    a.p.select_mode = _lib.SELECT_BLOCK
+    for bs in (100, 64, 7):
+        a.p.block_size = bs
+        assert lib.dsalt_fwd(ctypes.byref(a), None) == 3  # accepted up to the missing workspace
+    a.p.block_size, a.p.k_lmk = 16, 256  # tiles of 128 rows in 16-row blocks: 4 sets x 256
+    assert lib.dsalt_fwd(ctypes.byref(a), None) == 3
+    a.p.k_lmk = 257
+    assert lib.dsalt_fwd(ctypes.byref(a), None) == 2
+    assert b"sets" in lib.dsalt_last_error()
+    a.p.block_size = 0
+    assert lib.dsalt_fwd(ctypes.byref(a), None) == 1
+
+
 def test_misaligned_and_null_pointers_rejected():
     lib = _lib.load()
     a = _valid_fwd()

@@ -39,8 +39,11 @@ def test_compute_landmark_indices_matches_reference(name):
     np.testing.assert_allclose(sc.cpu().numpy(), z["scores"], atol=3e-6)
 
 
-def test_block_causal_selection_matches_reference():
-    z = load_golden("block_causal_b64")
+@pytest.mark.parametrize("name", ["b64", "mha", "gqa"])
+def test_block_causal_selection_matches_reference(name):
+    """The reference's block-causal selection and attention (blocks of 64, and of 32 rows at
+    head_dim 8: sets change inside a 64-row tile, q/k/v run zero-padded to head_dim 64)."""
+    z = load_golden(f"block_causal_{name}")
     T, B, k = z["x"].shape[0], int(z["block"]), int(z["k"])
     dh = z["v"].shape[2]
     cu = np.array([0, T], np.int32)
@@ -128,15 +131,17 @@ def test_standalone_backward_signature():
     assert rel_err(f64(db), rdb[:, :, 0]) < 2e-2
 
 
-@pytest.mark.parametrize("mode,d", [("global", 256), ("block", 256), ("global", 320)])
-def test_dsalt_attention_layer(mode, d):
+@pytest.mark.parametrize("mode,d,bs", [("global", 256, 128), ("block", 256, 128), ("global", 320, 128),
+                                       ("block", 256, 100)])
+def test_dsalt_attention_layer(mode, d, bs):
     """The layer's inference branch (fused QKV, RoPE kernel, strided attention) against its
-    parts with the float64 oracle; d = 320 gives head_dim 80 (run zero-padded to 128)."""
+    parts with the float64 oracle; d = 320 gives head_dim 80 (run zero-padded to 128); block
+    size 100 puts the rows of some 64-row tiles in two landmark sets."""
     torch.manual_seed(0)
     H, G, T = 4, 2, 640
     D = d // H
     m = DSALTAttention(d, H, 32, 128, 16, 2048, n_kv_heads=G, qkv_bias=True, select_mode=mode,
-                       block_size=128).to(DEV).eval()
+                       block_size=bs).to(DEV).eval()
     x = torch.randn(T, d, device=DEV)
     cu = torch.tensor([0, 400, T], dtype=torch.int32, device=DEV)
     out, aux = m(x, cu, cu_list=[0, 400, T])
@@ -150,10 +155,10 @@ def test_dsalt_attention_layer(mode, d):
         q, k = K.apply_rotary_emb(q, k, m.rope_cos[pos].unsqueeze(1), m.rope_sin[pos].unsqueeze(1))
         w = m._window_sizes(x, floor=True)
         lmk, _, _ = K._compute_landmark_indices(x, m.v_proj.weight, m._alpha(), w, cu, 16, 32, T, [0, 400, T],
-                                                head_dim=D, select_mode=mode, block_size=128)
+                                                head_dim=D, select_mode=mode, block_size=bs)
     idx4 = lmk.cpu().numpy() if mode == "block" else lmk.cpu().numpy()[:, :, None]
     ro, _ = OA.attention_fwd(f64(q), f64(k), f64(v), w.long().cpu().numpy(), cu.cpu().numpy(), idx4,
-                             1 / math.sqrt(D), block_size=128 if mode == "block" else None)
+                             1 / math.sqrt(D), block_size=bs if mode == "block" else None)
     ref = m.out_proj(torch.tensor(ro, dtype=torch.float32, device=DEV).view(T, d))
     assert rel_err(f64(out), f64(ref)) < 1e-5
     # batched input runs as packed sequences

@@ -83,6 +83,17 @@ def test_fwd_block_causal(dt):
     _fwd_check(q, k, v, w, cu, idx, lb, maxlen, mode=ops.SELECT_BLOCK, block=128)
 
 
+@pytest.mark.parametrize("dt,D,block,K", [(torch.bfloat16, 64, 100, 32), (torch.bfloat16, 128, 200, 48),
+                                          (torch.float32, 64, 48, 40), (torch.float16, 64, 30, 16),
+                                          (torch.float32, 128, 7, 24), (torch.bfloat16, 64, 1, 8)])
+def test_fwd_block_causal_any_block_size(dt, D, block, K):
+    """Block sizes that are not multiples of 64: the rows of a 64-row tile belong to up to
+    ceil(63 / block) + 1 sets, staged together (GQA, landmark bias, ragged sequences)."""
+    q, k, v, w, cu, idx, lb, maxlen = _inputs([520, 333], 4, 2, D, K, 150, dt, seed=block + D,
+                                              mode=ops.SELECT_BLOCK, block=block, bias=True)
+    _fwd_check(q, k, v, w, cu, idx, lb, maxlen, mode=ops.SELECT_BLOCK, block=block)
+
+
 def test_fwd_special_cases():
     T, H, D = 200, 2, 64
     g = torch.Generator().manual_seed(7)

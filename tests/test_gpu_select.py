@@ -172,9 +172,17 @@ def test_block_pruned_workload_shortened():
     np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
 
 
-@pytest.mark.parametrize("block", [64, 128])
+@pytest.mark.parametrize("block", [1, 37, 100, 200])
+def test_block_select_any_block_size(block):
+    # block sizes that are not multiples of 64 (sets start at any token), an empty sequence
+    h, v, alpha, w, cu = _case([700, 0, 413], 96, 2, 64, 4, torch.bfloat16, 120, seed=13)
+    idx, ridx = _run(h, v, alpha, w, cu, 16, ops.SELECT_BLOCK, block, ops.STATS_SEQUENCE, want=False)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
+@pytest.mark.parametrize("block", [64, 128, 37, 100])
 def test_block_pruned_block_sizes(block):
-    # the smallest block sizes (many sets, each reading its survivor count at its start)
+    # small block sizes (many sets, each reading its survivor count at its start, any token)
     h, v, alpha, w, cu = _case([9000, 6000], 128, 2, 64, 4, torch.bfloat16, 300, seed=11, scale_tails=True)
     idx, ridx = _run(h, v, alpha, w, cu, 32, ops.SELECT_BLOCK, block, ops.STATS_SEQUENCE, want=False,
                      border_cap=ops.SELECT_FORCE_PRUNE)
