@@ -78,15 +78,18 @@ __device__ __forceinline__ int load_set(const AttnParams& p, int64_t set_off, in
 // -------------------------------------------------------------------- dQ
 // TR: training variant -- band keys near the window start carry the soft edge bias,
 // and the lane also sums dS * d(bias)/d(w~) of its row into dw_h.
-template <typename T, int D, int BN, bool TR>
+// LK: sets of more than kSetSlots landmarks (inference operator), staged by a loop.
+template <typename T, int D, int BN, bool TR, bool LK = false>
 __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR ? 5 : 6) : 4) : 2) void bwd_dq_kernel(AttnParams p) {
+    static_assert(!(LK && TR), "large sets: inference operator");
     constexpr int NST = BN / 16;
     constexpr bool kHalf = sizeof(T) == 2;
+    constexpr int LCAP = LK ? kMaxLandmarks : kSetSlots;
     typedef Tile<T, D, BN, 256, (BN == 64 ? 8 : Pad<T, D>::R)> KT;
     __shared__ __attribute__((aligned(16))) T Ks[2][KT::ELEMS];
     __shared__ __attribute__((aligned(16))) T Vs[2][KT::ELEMS];
-    __shared__ int lpos[kMaxLandmarks];
-    __shared__ __attribute__((aligned(16))) float lbs[kMaxLandmarks];
+    __shared__ int lpos[LCAP];
+    __shared__ __attribute__((aligned(16))) float lbs[LCAP];
     // block scalars live in the second K buffer until the first chunk is staged there
     int* red = (int*)Ks[1];
 
@@ -113,14 +116,15 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     // load waits on a branch), then the rows' windows, LSE and row vectors; the block's
     // largest visible landmark count follows from the tile's largest window start, so one
     // barrier (the set in LDS) precedes the counts and the first chunk.
-    int lv[kMaxLandmarks / 256], ln[kMaxLandmarks / 256];
-    float lb[kMaxLandmarks / 256];
+    constexpr int NLV = LK ? 1 : kSetSlots / 256;  // LK: the set is staged by a loop below
+    int lv[NLV], ln[NLV];
+    float lb[NLV];
 #pragma unroll
-    for (int u = 0; u < kMaxLandmarks / 256; ++u) {
+    for (int u = 0; u < NLV; ++u) {
         lv[u] = -1;
         ln[u] = -1;
         lb[u] = 0.f;
-        if (u * 256 < K) {
+        if (!LK && u * 256 < K) {
             lv[u] = p.lmk[set_off + min(u * 256 + tid, K - 1)];
             ln[u] = p.lmk[set_off + min(u * 256 + tid + 1, K - 1)];
             if (has_bias) lb[u] = p.lbias[set_off + min(u * 256 + tid, K - 1)];
@@ -158,20 +162,25 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     bhi = min(uniform(wave_max(bhi)), len - 1);
     blmax = uniform(wave_max(blmax));
 
-    int nv_loc = 0;  // one past the last valid slot (sets are ascending, -1 after the valid slots)
+    int nvalid;
+    if constexpr (!LK) {
+        int nv_loc = 0;  // one past the last valid slot (sets are ascending, -1 after the valid slots)
 #pragma unroll
-    for (int u = 0; u < kMaxLandmarks / 256; ++u) {
-        const int sl = u * 256 + tid;
-        if (sl < K) {
-            lpos[sl] = lv[u];
-            if (has_bias) lbs[sl] = lb[u] * inv_scale;  // landmark bias in raw-score units
-            if (lv[u] >= 0 && (sl + 1 == K || ln[u] < 0)) nv_loc = sl + 1;
+        for (int u = 0; u < NLV; ++u) {
+            const int sl = u * 256 + tid;
+            if (sl < K) {
+                lpos[sl] = lv[u];
+                if (has_bias) lbs[sl] = lb[u] * inv_scale;  // landmark bias in raw-score units
+                if (lv[u] >= 0 && (sl + 1 == K || ln[u] < 0)) nv_loc = sl + 1;
+            }
         }
+        nv_loc = wave_max(nv_loc);
+        if (lane == 0) red[4 + uw] = nv_loc;
+        __syncthreads();
+        nvalid = uniform(max(max(red[4], red[5]), max(red[6], red[7])));
+    } else {
+        nvalid = uniform(load_set(p, set_off, lpos, red + 4, tid, has_bias ? lbs : nullptr));
     }
-    nv_loc = wave_max(nv_loc);
-    if (lane == 0) red[4 + uw] = nv_loc;
-    __syncthreads();
-    const int nvalid = uniform(max(max(red[4], red[5]), max(red[6], red[7])));
 
     int lo = 0x7fffffff, hi = -1, cnt = 0, lou = 0x7fffffff;
     float wt = 0.f;
@@ -938,7 +947,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
 template <typename T, int D>
 constexpr int lmk_waves(int k_lmk) { return (sizeof(T) == 2 && D == 64 && k_lmk > 64) ? 8 : 4; }
 
-template <typename T, int D, int NW>
+// LK: sets of more than kSetSlots landmarks (the set's positions in a larger LDS copy).
+template <typename T, int D, int NW, bool LK = false>
 __global__ __launch_bounds__(64 * NW, (NW == 8 && sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_lmk_kernel(AttnParams p) {
     constexpr int NT = 64 * NW;
     constexpr int kLmkGroup = 16 * NW;
@@ -948,7 +958,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && sizeof(T) == 2 && D == 64) ? 4
     typedef QStage<T, D, BQ, false, NT> QS;
     typedef typename QS::QT QT;
     __shared__ __attribute__((aligned(16))) QS q;
-    __shared__ int lpos[kMaxLandmarks];
+    __shared__ int lpos[LK ? kMaxLandmarks : kSetSlots];
     __shared__ int cmax_s[NQS];
     __shared__ int nvalid_s;
 
@@ -1255,7 +1265,10 @@ static hipError_t bwd_run(const AttnParams& p, bool plan_given, hipStream_t stre
     }
     constexpr int BN = BwdShape<T, D>::BN;
     constexpr bool kBn64 = sizeof(T) == 2 && D == 64;  // the only shape with a 64-key dQ tiling
-    if (kBn64 && (p.variant & DSALT_VARIANT_DQ_BN64)) {
+    const bool lk = p.k_lmk > kSetSlots;               // large sets (inference operator only)
+    if (lk) {
+        DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, BN, false, true>), dim3(total), dim3(256), 0, stream, p);
+    } else if (kBn64 && (p.variant & DSALT_VARIANT_DQ_BN64)) {
         if constexpr (kBn64) {
             if (p.w_cont) DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, 64, true>), dim3(total), dim3(256), 0, stream, p);
             else DSALT_LAUNCH("bwd_dq", (bwd_dq_kernel<T, D, 64, false>), dim3(total), dim3(256), 0, stream, p);
@@ -1273,13 +1286,13 @@ static hipError_t bwd_run(const AttnParams& p, bool plan_given, hipStream_t stre
     }
     if (p.k_lmk > 0) {
         if (lmk_waves<T, D>(p.k_lmk) == 8) {
-            const int ngrp = ceil_div(p.k_lmk, 128);
-            DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D, 8>), dim3(p.n_heads * p.num_seqs * p.n_chunks * ngrp),
-                         dim3(512), 0, stream, p);
+            const dim3 grid(p.n_heads * p.num_seqs * p.n_chunks * ceil_div(p.k_lmk, 128));
+            if (lk) DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D, 8, true>), grid, dim3(512), 0, stream, p);
+            else DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D, 8>), grid, dim3(512), 0, stream, p);
         } else {
-            const int ngrp = ceil_div(p.k_lmk, 64);
-            DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D, 4>), dim3(p.n_heads * p.num_seqs * p.n_chunks * ngrp),
-                         dim3(256), 0, stream, p);
+            const dim3 grid(p.n_heads * p.num_seqs * p.n_chunks * ceil_div(p.k_lmk, 64));
+            if (lk) DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D, 4, true>), grid, dim3(256), 0, stream, p);
+            else DSALT_LAUNCH("bwd_lmk", (bwd_lmk_kernel<T, D, 4>), grid, dim3(256), 0, stream, p);
         }
         const int64_t n = (int64_t)p.n_heads * p.num_seqs * p.k_lmk * D;
         DSALT_LAUNCH("bwd_lmk_sum", (bwd_lmk_sum_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0,

@@ -156,7 +156,7 @@ __device__ __forceinline__ void plan_counts_sets(const int* lpos, const int* nvs
                                                  int nsets, RowGroup& rg) {
     int ls = 0, cnt = 0;
     if (rg.valid) {
-        const int j = min(max(rg.i / block_size - first, 0), nsets - 1);
+        const int j = block_size ? min(max(rg.i / block_size - first, 0), nsets - 1) : 0;
         ls = j * K;
         cnt = lower_bound_lds(lpos + ls, nvs[j], rg.lo);
     }
@@ -194,15 +194,16 @@ __device__ __forceinline__ void band_edge(const AttnParams& p, const RowGroup& R
 // edge bias (edge_bias), so chunks classed "every row sees every key" must also
 // lie past every row's first edge_keys band keys.
 //
-// MS: block-causal sets with block_size not a multiple of 64 (one row group per wave, inference
-// only): the block's rows may belong to several sets, all staged in LDS side by side; each row
-// sees the slots of its own set only (a two-sided slot mask, like the band's key mask).
+// MS: sets of more than kSetSlots landmarks, or block-causal sets with block_size not a
+// multiple of 64 (one row group per wave, inference only): the block's rows may belong to
+// several sets, all staged in LDS side by side; each row sees the slots of its own set only
+// (a two-sided slot mask, like the band's key mask).
 template <typename T, int D, int BN, int RG, bool TR, bool MS = false>
 __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN == 32) ? 4 : 2) void fwd_kernel(AttnParams p) {
     static_assert(!MS || (RG == 1 && !TR), "several sets per block: one row group, inference");
     constexpr int NST = BN / 16;
     constexpr bool kHalf = sizeof(T) == 2;
-    constexpr int LCAP = MS ? kMultiSetSlots : kMaxLandmarks;
+    constexpr int LCAP = MS ? kMultiSetSlots : kSetSlots;
     typedef Tile<T, D, BN, 256, (BN == 64 ? 8 : Pad<T, D>::R)> KT;
     __shared__ __attribute__((aligned(16))) T Ks[2][KT::ELEMS];
     __shared__ __attribute__((aligned(16))) T Vs[2][KT::ELEMS];
@@ -234,7 +235,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     const int64_t set_off = (((int64_t)h * p.num_seqs + s) * p.n_sets + set) * K;
     // sets of the block's rows (MS): set .. set + nsets - 1, at most LCAP slots in all
     int nsets = 1;
-    if (MS) {
+    if (MS && p.block_size) {
         const int last = min(r0 + 63, len - 1) / p.block_size;
         nsets = min(min(last - set + 1, kMaxTileSets), LCAP / max(K, 1));
     }
@@ -247,10 +248,12 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     // group bounds and rows -- are issued together, then the rows' windows and query rows;
     // the block's largest visible landmark count follows from the largest window start of
     // its groups, so one barrier (the set in LDS) precedes the first landmark chunk's fetch.
-    int lv[LCAP / 256], ln[LCAP / 256];
-    float lb[LCAP / 256];
+    // (MS: the sets are staged by a loop after the plan's loads)
+    constexpr int NLV = MS ? 1 : kSetSlots / 256;
+    int lv[NLV], ln[NLV];
+    float lb[NLV];
 #pragma unroll
-    for (int u = 0; u < LCAP / 256; ++u) {
+    for (int u = 0; u < NLV; ++u) {
         lv[u] = -1;
         ln[u] = -1;
         lb[u] = 0.f;
@@ -258,14 +261,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
             lv[u] = p.lmk[set_off + min(u * 256 + tid, K - 1)];
             ln[u] = p.lmk[set_off + min(u * 256 + tid + 1, K - 1)];
             if (has_bias) lb[u] = p.lbias[set_off + min(u * 256 + tid, K - 1)];
-        } else if (MS && u * 256 < nslots) {
-            // slot e: position sl of set set + j (the block's sets are consecutive, K slots each)
-            const int e = min(u * 256 + tid, nslots - 1);
-            const int j = e / K, sl = e - j * K;
-            const int64_t o = set_off + (int64_t)j * K;
-            lv[u] = p.lmk[o + sl];
-            ln[u] = p.lmk[o + min(sl + 1, K - 1)];
-            if (has_bias) lb[u] = p.lbias[o + sl];
         }
     }
 
@@ -304,7 +299,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     if constexpr (!MS) {
         int nv_loc = 0;  // one past the last valid slot (sets are ascending, -1 after the valid slots)
 #pragma unroll
-        for (int u = 0; u < LCAP / 256; ++u) {
+        for (int u = 0; u < NLV; ++u) {
             const int i = u * 256 + tid;
             if (i < K) {
                 lpos[i] = lv[u];
@@ -319,15 +314,15 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     } else {
         if (tid < kMaxTileSets) nvs[tid] = 0;
         __syncthreads();
-#pragma unroll
-        for (int u = 0; u < LCAP / 256; ++u) {
-            const int e = u * 256 + tid;
-            if (e < nslots) {
-                const int j = e / K, sl = e - j * K;
-                lpos[e] = lv[u];
-                if (has_bias) lbs[e] = lb[u] * inv_scale;
-                if (lv[u] >= 0 && (sl + 1 == K || ln[u] < 0)) nvs[j] = sl + 1;  // one writer per set
-            }
+        // slot e: position sl of set set + j (the block's sets are consecutive, K slots each)
+        for (int e = tid; e < nslots; e += 256) {
+            const int j = e / K, sl = e - j * K;
+            const int64_t o = set_off + (int64_t)j * K;
+            const int v = p.lmk[o + sl];
+            const int vn = sl + 1 < K ? p.lmk[o + sl + 1] : -1;
+            lpos[e] = v;
+            if (has_bias) lbs[e] = p.lbias[o + sl] * inv_scale;
+            if (v >= 0 && (sl + 1 == K || vn < 0)) nvs[j] = sl + 1;  // one writer per set
         }
         __syncthreads();
         int any = 0;
@@ -649,13 +644,14 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
 // stay within one landmark set, block_size a multiple of 128); for 16-bit head_dim 128, two
 // row groups per wave (FWD_RG2, same condition) or 64-key chunks instead of 32 (FWD_BN64;
 // ignored with FWD_RG2);
-// fp32 takes its single compiled tiling.  Block-causal sets of a block_size that is not a
-// multiple of 64 take the default tiling with several sets per block (variant bits ignored).
+// fp32 takes its single compiled tiling.  Sets of more than kSetSlots landmarks, and
+// block-causal sets of a block_size that is not a multiple of 64, take the default tiling's
+// wide instantiation (variant bits ignored).
 template <typename T, int D, bool TR>
 static void fwd_run(const AttnParams& p, hipStream_t stream) {
     constexpr int BN = FwdShape<T, D>::BN;
     if constexpr (!TR) {
-        if (p.block_size % 64) {
+        if (p.block_size % 64 || p.k_lmk > kSetSlots) {
             DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, BN, 1, false, true>), dim3(p.n_heads * p.num_seqs * p.n_tiles),
                          dim3(256), 0, stream, p);
             return;

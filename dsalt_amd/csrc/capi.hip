@@ -212,6 +212,10 @@ static int fwd_params(const dsalt_fwd_args* a, bool need_w, dsalt::AttnParams* o
     if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
     int rc = check_problem(a->p, true);
     if (rc) return rc;
+    // sets of more than kSetSlots landmarks: the inference operator only
+    if (!need_w && a->p.k_lmk > dsalt::kSetSlots)
+        return fail(DSALT_ERR_UNSUPPORTED, "the training variant takes at most %d landmarks (k_lmk %d)", dsalt::kSetSlots,
+                    a->p.k_lmk);
     // block sizes that are not multiples of 64: a tile's sets are staged in LDS together
     const int tsets = max_sets_per_tile(a->p);
     if (tsets > 1 && tsets * a->p.k_lmk > dsalt::kMultiSetSlots)
@@ -380,6 +384,9 @@ static int bwd_params(const dsalt_bwd_args* a, dsalt::AttnParams* out, bool need
     if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
     int rc = check_problem(a->p, true);
     if (rc) return rc;
+    if (!need_w && a->p.k_lmk > dsalt::kSetSlots)
+        return fail(DSALT_ERR_UNSUPPORTED, "the training variant takes at most %d landmarks (k_lmk %d)", dsalt::kSetSlots,
+                    a->p.k_lmk);
     if (a->p.select_mode != DSALT_SELECT_GLOBAL)
         return fail(DSALT_ERR_UNSUPPORTED, "backward of the block-causal variant is not implemented");
     const int dt = a->p.dtype;

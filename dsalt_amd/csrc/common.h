@@ -20,11 +20,14 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
-constexpr int kMaxLandmarks = 512;
-// Block-causal problems whose block_size is not a multiple of 64: a 64-row tile spans up to
-// kMaxTileSets landmark sets, staged side by side (sets x k_lmk at most kMultiSetSlots).
+// Landmark slots per set: at most kMaxLandmarks.  The single-set attention kernels keep a set
+// of up to kSetSlots in LDS; larger sets, and the several sets a 64-row tile's rows use when
+// a block-causal block_size is not a multiple of 64 (at most kMaxTileSets, staged side by
+// side: sets x k_lmk at most kMultiSetSlots), take the wide instantiations.
+constexpr int kMaxLandmarks = 2048;
+constexpr int kSetSlots = 512;
 constexpr int kMaxTileSets = 64;
-constexpr int kMultiSetSlots = 1024;
+constexpr int kMultiSetSlots = 2048;
 
 __device__ __forceinline__ float to_float(float x) { return x; }
 __device__ __forceinline__ float to_float(bf16 x) { return (float)x; }

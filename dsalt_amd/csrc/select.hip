@@ -405,12 +405,13 @@ constexpr int kSampleList = 1024;  // sample of a pruned list (its candidates ar
 
 constexpr int kKthCand = 64;       // radix passes of kth_desc stop once the bin holds at most this many keys
 
-template <int NT_>
+// KCAP: the largest set size the block writes (kSetSlots, or kMaxLandmarks for large sets)
+template <int NT_, int KCAP>
 struct TopkShared {
     static constexpr int NT = NT_;
     uint32_t hist[NT_ / kWave][256];
     unsigned long long border[kBorderCap > kSample ? kBorderCap : kSample];
-    int sel[kMaxLandmarks];
+    int sel[KCAP];
     unsigned long long cand[kKthCand];
     unsigned long long kth;
     uint32_t total;
@@ -514,7 +515,7 @@ __device__ unsigned long long kth_desc(Sh& sh, const unsigned long long* a, int 
 }
 
 // out[0..m) = the m distinct values v[0..m) (LDS) in ascending order: each value's rank
-// is the number of smaller values (m <= kMaxLandmarks, one thread per value)
+// is the number of smaller values (m <= the set size, one thread per value)
 template <int NT>
 __device__ void rank_sort_asc(const int* v, int m, int32_t* out, int tid) {
     for (int t = tid; t < m; t += NT) {
@@ -904,12 +905,13 @@ __global__ __launch_bounds__(kSortThreads) void sel_part_kernel(SelectParams p, 
 
 // merge parts [op*G, op*G+G) of set sidx (G*kpad <= kMergeMax keys): with `out`, keep
 // the kpad best keys; without, write the set's landmark indices (ascending, -1 padded)
+template <int KCAP>
 __global__ __launch_bounds__(kSortThreads) void sel_merge_kernel(SelectParams p, const unsigned long long* in,
                                                                  int nin, int G, int kpad, unsigned long long* out,
                                                                  int nout) {
     __shared__ KthShared sh;
     __shared__ unsigned long long keys[kMergeMax];
-    __shared__ int sel[kMaxLandmarks];
+    __shared__ int sel[KCAP];
     const int tid = threadIdx.x;
     const int op = blockIdx.x % nout, sidx = blockIdx.x / nout;
     const int q0 = op * G, q1 = min(nin, q0 + G);
@@ -939,12 +941,12 @@ __global__ __launch_bounds__(kSortThreads) void sel_merge_kernel(SelectParams p,
     for (int i = nsel + tid; i < K; i += kSortThreads) o[i] = -1;
 }
 
-template <int NT>
+template <int NT, int KCAP>
 __global__ __launch_bounds__(NT) void sel_topk_kernel(SelectParams p, const float* zx, const float* zv,
                                                                const float* nx, const float* nv, const uint32_t* pk,
                                                                const double* stats, int border_cap,
                                                                const int32_t* plist, const int32_t* pbelow) {
-    __shared__ TopkShared<NT> sh;
+    __shared__ TopkShared<NT, KCAP> sh;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // blocks of one (head, sequence) are contiguous in the XCD-swizzled order, so each XCD's
     // L2 holds the norms of few heads; within them later sets, which scan longer prefixes,
@@ -1389,12 +1391,20 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
             DSALT_LAUNCH("sel_prune_list", sel_prune_list_kernel, pg, dim3(256), 0, stream, p, pkeep, pcnt, plist,
                          pbelow);
         }
-        if (prune)
-            DSALT_LAUNCH("sel_topk", sel_topk_kernel<kTopkThreadsPruned>, dim3(nsets_total), dim3(kTopkThreadsPruned), 0,
-                         stream, p, zx, zv, nx, nv, pk, stats, border_cap, plist, pbelow);
+        // sets of more than kSetSlots take instantiations with a larger output buffer in LDS
+        const bool lk = p.k_lmk > kSetSlots;
+        if (prune && lk)
+            DSALT_LAUNCH("sel_topk", (sel_topk_kernel<kTopkThreadsPruned, kMaxLandmarks>), dim3(nsets_total),
+                         dim3(kTopkThreadsPruned), 0, stream, p, zx, zv, nx, nv, pk, stats, border_cap, plist, pbelow);
+        else if (prune)
+            DSALT_LAUNCH("sel_topk", (sel_topk_kernel<kTopkThreadsPruned, kSetSlots>), dim3(nsets_total),
+                         dim3(kTopkThreadsPruned), 0, stream, p, zx, zv, nx, nv, pk, stats, border_cap, plist, pbelow);
+        else if (lk)
+            DSALT_LAUNCH("sel_topk", (sel_topk_kernel<kTopkThreads, kMaxLandmarks>), dim3(nsets_total),
+                         dim3(kTopkThreads), 0, stream, p, zx, zv, nx, nv, pk, stats, border_cap, nullptr, nullptr);
         else
-            DSALT_LAUNCH("sel_topk", sel_topk_kernel<kTopkThreads>, dim3(nsets_total), dim3(kTopkThreads), 0, stream, p,
-                         zx, zv, nx, nv, pk, stats, border_cap, nullptr, nullptr);
+            DSALT_LAUNCH("sel_topk", (sel_topk_kernel<kTopkThreads, kSetSlots>), dim3(nsets_total), dim3(kTopkThreads),
+                         0, stream, p, zx, zv, nx, nv, pk, stats, border_cap, nullptr, nullptr);
         return hipGetLastError();
     }
     const TopkPlan t = topk_plan(p, border_cap);
@@ -1406,8 +1416,12 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
                  stats_written ? stats : nullptr, t.psize, t.nparts, t.kpad, ka);
     // keys per merge block <= kMergeMax
     auto merge = [&](int nin, unsigned long long* out, int nout) {
-        DSALT_LAUNCH("sel_merge", sel_merge_kernel, dim3(nsets_total * nout), dim3(kSortThreads), 0, stream, p, ka,
-                     nin, t.G, t.kpad, out, nout);
+        if (p.k_lmk > kSetSlots)
+            DSALT_LAUNCH("sel_merge", sel_merge_kernel<kMaxLandmarks>, dim3(nsets_total * nout), dim3(kSortThreads), 0,
+                         stream, p, ka, nin, t.G, t.kpad, out, nout);
+        else
+            DSALT_LAUNCH("sel_merge", sel_merge_kernel<kSetSlots>, dim3(nsets_total * nout), dim3(kSortThreads), 0,
+                         stream, p, ka, nin, t.G, t.kpad, out, nout);
     };
     int nin = t.nparts;
     while (nin > t.G) {

@@ -20,7 +20,7 @@ from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, SELECT_BLOCK, SELECT_GLOBAL
                    TrainFwdArgs)
 
 _DT = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
-MAX_LANDMARKS = 512
+MAX_LANDMARKS = 2048  # landmarks per set (the training variant: at most 512)
 # select_landmarks(border_cap=...): full capacity with the block-causal candidate pruning
 # forced at any sequence length (it runs by itself from 65536 tokens on)
 SELECT_FORCE_PRUNE = 0x3FFFFFFF

@@ -67,11 +67,11 @@ typedef struct dsalt_problem {
     int32_t n_heads;     /* H query heads                                            */
     int32_t n_kv_heads;  /* key/value heads, divides H (GQA when < H)                */
     int32_t head_dim;    /* D: 64 or 128                                             */
-    int32_t k_lmk;       /* landmark slots per set, 0..512                           */
+    int32_t k_lmk;       /* landmark slots per set, 0..2048 (training variant: 0..512) */
     int32_t select_mode; /* DSALT_SELECT_*                                           */
     int32_t block_size;  /* query block of the block-causal variant (>= 1; when not a multiple
                             of 64 the forward stages every set a 64-row tile's rows use: at
-                            most 1024 slots, sets x k_lmk)                                     */
+                            most 2048 slots, sets x k_lmk)                                     */
     int32_t dtype;       /* DSALT_DTYPE_* of the token tensors                       */
 } dsalt_problem;
 

@@ -87,7 +87,7 @@ def _valid_fwd():
 
 
 @pytest.mark.parametrize("field,value,code", [
-    ("head_dim", 96, 2), ("k_lmk", 513, 1), ("n_kv_heads", 3, 1), ("dtype", 7, 1),
+    ("head_dim", 96, 2), ("k_lmk", 2049, 1), ("n_kv_heads", 3, 1), ("dtype", 7, 1),
     ("select_mode", 1, 1), ("max_seqlen", 0, 1)])
 def test_fwd_validation(field, value, code):
     lib = _lib.load()
@@ -99,16 +99,16 @@ def test_fwd_validation(field, value, code):
 
 def test_block_sizes_and_the_sets_of_a_tile():
     """Any block_size >= 1; when it is not a multiple of 64 the forward stages every set a
-    64-row tile's rows use: at most 1024 slots (sets x k_lmk)."""
+    64-row tile's rows use: at most 2048 slots (sets x k_lmk)."""
     lib = _lib.load()
     a = _valid_fwd()
     a.p.select_mode = _lib.SELECT_BLOCK
     for bs in (100, 64, 7):
         a.p.block_size = bs
         assert lib.dsalt_fwd(ctypes.byref(a), None) == 3  # accepted up to the missing workspace
-    a.p.block_size, a.p.k_lmk = 16, 256  # tiles of 128 rows in 16-row blocks: 4 sets x 256
+    a.p.block_size, a.p.k_lmk = 16, 512  # 64-row tiles in 16-row blocks: 4 sets x 512
     assert lib.dsalt_fwd(ctypes.byref(a), None) == 3
-    a.p.k_lmk = 257
+    a.p.k_lmk = 513
     assert lib.dsalt_fwd(ctypes.byref(a), None) == 2
     assert b"sets" in lib.dsalt_last_error()
     a.p.block_size = 0
@@ -236,6 +236,13 @@ def test_train_rejects_block_sets_and_small_workspace():
     assert need >= 128 * 4 + 128 * 2 * 4
     b.base.workspace, b.base.workspace_bytes = fake, need - 16
     assert lib.dsalt_train_bwd(ctypes.byref(b), None) == 3
+    # sets of more than 512 landmarks: the inference operator only
+    b.base.p.k_lmk = 513
+    assert lib.dsalt_train_bwd(ctypes.byref(b), None) == 2
+    t = _valid_train_fwd()
+    t.base.p.k_lmk = 513
+    assert lib.dsalt_train_fwd(ctypes.byref(t), None) == 2
+    assert b"512" in lib.dsalt_last_error()
 
 
 def _valid_rope():

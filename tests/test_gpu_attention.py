@@ -229,6 +229,40 @@ def test_bwd_grouped_heads_native(H, G, D, dt):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("H,G,D,dt,K", [(4, 2, 64, torch.bfloat16, 1000), (4, 2, 64, torch.bfloat16, 2048),
+                                        (4, 4, 128, torch.float32, 600), (4, 2, 128, torch.float16, 1500)])
+def test_large_landmark_sets(H, G, D, dt, K):
+    """Sets of more than 512 landmarks (up to 2048): the wide instantiations of the forward,
+    the dQ pass and the landmark backward; GQA, landmark bias, a sequence with fewer
+    candidates than slots (-1 padding).  Forward against the oracle, every gradient through
+    the class and row bounds, bit-identical rerun."""
+    q, k, v, w, cu, idx, lb, maxlen, do = _bwd_gqa_case(H, G, D, dt, seed=K + D, lens=(2600, 1300, 400), K=K,
+                                                        wmax=300)
+    scale = 1.0 / math.sqrt(D)
+    out, lse = _fwd_check(q, k, v, w, cu, idx, lb, maxlen)
+    dev = [t.to(DEV) for t in (q, k, v, w, cu, idx, lb, do)]
+    res = ops.attention_backward(dev[7], dev[0], dev[1], dev[2], out, lse, dev[3], dev[4], dev[5], dev[6],
+                                 scale=scale, max_seqlen=maxlen)
+    torch.cuda.synchronize()
+    ref = OA.attention_bwd(f64(q), f64(k), f64(v), w.numpy(), cu.numpy(), idx.numpy(), scale, f64(do),
+                           lmk_bias=lb.double().numpy(), out=f64(out))
+    check_grads(("large sets", K), res[:3], ref[:3], idx, cu, TOL[dt])
+    assert rel_err(f64(res[3]), ref[3]) < TOL[dt]
+    res2 = ops.attention_backward(dev[7], dev[0], dev[1], dev[2], out, lse, dev[3], dev[4], dev[5], dev[6],
+                                  scale=scale, max_seqlen=maxlen)
+    for a, b in zip(res, res2):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("block,K", [(512, 700), (100, 600), (1024, 2048)])
+def test_large_landmark_sets_block_causal(block, K):
+    """Block-causal sets of more than 512 landmarks, alone per tile (block 512, 1024) or
+    three per tile (block 100: 3 x 600 slots)."""
+    q, k, v, w, cu, idx, lb, maxlen = _inputs([3000, 1100], 4, 2, 64, K, 200, torch.bfloat16, seed=block + K,
+                                              mode=ops.SELECT_BLOCK, block=block, bias=True)
+    _fwd_check(q, k, v, w, cu, idx, lb, maxlen, mode=ops.SELECT_BLOCK, block=block)
+
+
 def test_bwd_grouped_heads_shared_landmarks():
     """Heads of one group selecting the same positions: each landmark row's gradient is the
     sum over the group's heads (one writer per row)."""

@@ -172,6 +172,26 @@ def test_block_pruned_workload_shortened():
     np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
 
 
+@pytest.mark.parametrize("K,scope", [(600, ops.STATS_SEQUENCE), (2048, ops.STATS_PACKED)])
+def test_global_select_large_sets(K, scope):
+    # more than 512 landmarks per set: per-part keys of up to 2048, merges of two parts, a
+    # sequence with fewer candidates than slots
+    h, v, alpha, w, cu = _case([6000, 1500, 900], 128, 2, 64, 4, torch.bfloat16, 300, seed=17)
+    (idx, zx, zv, sc), (ridx, rzx, rzv, rsc) = _run(h, v, alpha, w, cu, K, ops.SELECT_GLOBAL, 512, scope)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_array_equal(sc.cpu().numpy(), rsc)
+
+
+@pytest.mark.parametrize("K,block,cap", [(700, 1024, None), (1500, 2048, None), (700, 1024, "prune")])
+def test_block_select_large_sets(K, block, cap):
+    # block-causal sets of more than 512 landmarks: all-in-LDS, sampled-threshold and radix
+    # paths, and with forced pruning the survivor lists
+    h, v, alpha, w, cu = _case([12000, 3000], 128, 2, 64, 4, torch.bfloat16, 300, seed=19)
+    idx, ridx = _run(h, v, alpha, w, cu, K, ops.SELECT_BLOCK, block, ops.STATS_SEQUENCE, want=False,
+                     border_cap=ops.SELECT_FORCE_PRUNE if cap else None)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+
+
 @pytest.mark.parametrize("block", [1, 37, 100, 200])
 def test_block_select_any_block_size(block):
     # block sizes that are not multiples of 64 (sets start at any token), an empty sequence
