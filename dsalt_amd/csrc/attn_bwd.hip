@@ -399,8 +399,20 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
         const float dw = sum_g4(dwacc);
         if (valid && g == 0) p.dw_h[(int64_t)(st + i) * p.n_heads + h] = dw;
     }
-    if (valid) {
-        T* drow = (T*)p.dq + (int64_t)(st + i) * p.n_heads * D + (int64_t)h * D;
+    const int64_t rstride = (int64_t)p.n_heads * D;
+    T* dq0 = (T*)p.dq + (int64_t)st * rstride + (int64_t)h * D;
+    if constexpr (!TR) {
+        // dQ rows whole, staged in the idle K/V buffers (waves 0-1 in Ks, 2-3 in Vs)
+        typedef StoreRows<T, D> SR;
+        static_assert(KT::ELEMS >= SR::ELEMS, "row staging does not fit the chunk buffers");
+        T* stage = (wave < 2 ? &Ks[0][0] : &Vs[0][0]) + (wave & 1) * SR::ELEMS;
+        const int vi = valid ? i : -1;
+        SR::run(stage, acc, p.scale, lane, [&](int rr) {
+            const int ir = __shfl(vi, rr);
+            return ir >= 0 ? dq0 + ir * rstride : (T*)nullptr;
+        });
+    } else if (valid) {  // (the training variant's registers leave no room for the staging)
+        T* drow = dq0 + i * rstride;
 #pragma unroll
         for (int dt = 0; dt < D / 16; ++dt) {
             T ov[4];
@@ -900,11 +912,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
     }
     }  // query heads of the group
 
+    bool owner = false;
     if (jvalid && p.k_lmk > 0) {
         // a landmark row: its band sums go to the landmark pass's final sum in fp32, which
         // rounds the total once (and writes the row)
         const int own = own_s[j - j0];
         if (own != kNoOwner) {
+            owner = true;
             const int64_t so = (((int64_t)(own / p.k_lmk) * p.num_seqs + s) * p.k_lmk + own % p.k_lmk) * D;
             const int64_t half = (int64_t)p.n_heads * p.num_seqs * p.k_lmk * D;
 #pragma unroll
@@ -912,29 +926,19 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
                 *(floatx4*)(p.lmk_stage + so + dt * 16 + lane_off) = adk[dt] * p.scale;
                 *(floatx4*)(p.lmk_stage + half + so + dt * 16 + lane_off) = adv[dt];
             }
-            return;
         }
     }
-    if (jvalid) {
-        T* kd = (T*)p.dk + (int64_t)(st + j) * p.n_kv_heads * D + (int64_t)kvh * D;
-        T* vd = (T*)p.dv + (int64_t)(st + j) * p.n_kv_heads * D + (int64_t)kvh * D;
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) {
-            T ok[4], ov[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                ok[r] = from_float<T>(adk[dt][r] * p.scale);
-                ov[r] = from_float<T>(adv[dt][r]);
-            }
-            if constexpr (kHalf) {
-                *(uint2*)(kd + dt * 16 + lane_off) = *(const uint2*)ok;
-                *(uint2*)(vd + dt * 16 + lane_off) = *(const uint2*)ov;
-            } else {
-                *(floatx4*)(kd + dt * 16 + lane_off) = *(const floatx4*)ok;
-                *(floatx4*)(vd + dt * 16 + lane_off) = *(const floatx4*)ov;
-            }
-        }
-    }
+    // the other rows: dK, then dV, as whole rows staged in the wave's part of the query tile
+    // buffers (idle after the last barrier)
+    typedef StoreRows<T, D> SR;
+    static_assert(sizeof(sq) >= sizeof(T) * 4 * SR::ELEMS, "row staging does not fit the tile buffers");
+    T* stage = (T*)&sq[0] + wave * SR::ELEMS;
+    const int wr = jvalid && !owner;
+    const int64_t rstride = (int64_t)p.n_kv_heads * D;
+    T* kd0 = (T*)p.dk + (int64_t)(st + wj0) * rstride + (int64_t)kvh * D;
+    T* vd0 = (T*)p.dv + (int64_t)(st + wj0) * rstride + (int64_t)kvh * D;
+    SR::run(stage, adk, p.scale, lane, [&](int rr) { return __shfl(wr, rr) ? kd0 + rr * rstride : (T*)nullptr; });
+    SR::run(stage, adv, 1.0f, lane, [&](int rr) { return __shfl(wr, rr) ? vd0 + rr * rstride : (T*)nullptr; });
 }
 
 // -------------------------------------------------------- landmark dK/dV

@@ -621,21 +621,21 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     for (int n = 0; n < nlmk; ++n) process(n, std::false_type{});
     for (int n = nlmk; n < nchunks; ++n) process(n, std::true_type{});
 
+    // output rows whole, staged in the idle K/V buffers (waves 0-1 in Ks, 2-3 in Vs; the
+    // groups of a wave one after the other)
+    typedef StoreRows<T, D> SR;
+    static_assert(KT::ELEMS >= SR::ELEMS, "row staging does not fit the chunk buffers");
+    T* stage = (wave < 2 ? &Ks[0][0] : &Vs[0][0]) + (wave & 1) * SR::ELEMS;
+    T* o0 = (T*)p.o + (int64_t)st * p.o_st + (int64_t)h * p.o_sh;
 #pragma unroll
     for (int u = 0; u < RG; ++u) {
         const float l_tot = kHalf ? lacc[u][0] : sum_g4(l_run[u]);
-        if (!rg[u].valid) continue;
-        const float inv = 1.0f / l_tot;
-        T* orow = (T*)p.o + (int64_t)(st + rg[u].i) * p.o_st + (int64_t)h * p.o_sh;
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) {
-            T ov[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) ov[r] = from_float<T>(acc[u][dt][r] * inv);
-            if constexpr (kHalf) *(uint2*)(orow + dt * 16 + lane_off) = *(const uint2*)ov;
-            else *(floatx4*)(orow + dt * 16 + lane_off) = *(const floatx4*)ov;
-        }
-        if (g == 0) p.lse_out[(int64_t)(st + rg[u].i) * p.n_heads + h] = m_run[u] * p.scale + __logf(l_tot);
+        const int vi = rg[u].valid ? rg[u].i : -1;
+        SR::run(stage, acc[u], rg[u].valid ? 1.0f / l_tot : 0.f, lane, [&](int rr) {
+            const int ir = __shfl(vi, rr);
+            return ir >= 0 ? o0 + (int64_t)ir * p.o_st : (T*)nullptr;
+        });
+        if (rg[u].valid && g == 0) p.lse_out[(int64_t)(st + rg[u].i) * p.n_heads + h] = m_run[u] * p.scale + __logf(l_tot);
     }
 }
 

@@ -307,4 +307,44 @@ template <typename T> __device__ __forceinline__ typename Vec8<T>::type ones8() 
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// Whole-row output of a wave's 16 rows held in the accumulator layout (acc[dt][r]: column
+// 16 dt + 4 (lane >> 4) + r of the row of lane & 15), times `mul`: the values go through
+// `stage` (LDS private to the wave, StoreRows::ELEMS elements) and leave as 16-byte pieces,
+// D * sizeof(T) / 16 lanes per row, so each store instruction writes whole rows (stores of
+// 8-byte pieces, four instructions per row, cost the kernels up to a tenth of their time).
+// dst(rr) is row rr's destination (rr = 0..15, the row of accumulator lane rr), nullptr for
+// a row not written.  Every lane of the wave calls it.
+template <typename T, int D>
+struct StoreRows {
+    static constexpr int RS = D + 16 / (int)sizeof(T);  // row stride in LDS: 16 bytes of padding
+    static constexpr int ELEMS = 16 * RS;
+    template <typename Dst>
+    __device__ __forceinline__ static void run(T* stage, const floatx4 (&acc)[D / 16], float mul, int lane, Dst dst) {
+        const int j = lane & 15, g = lane >> 4;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) {
+            T v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = from_float<T>(acc[dt][r] * mul);
+            T* at = stage + j * RS + dt * 16 + 4 * g;
+            if constexpr (sizeof(T) == 2) *(uint2*)at = *(const uint2*)v;
+            else *(floatx4*)at = *(const floatx4*)v;
+        }
+        // the wave's LDS writes are seen by its reads below (no other wave touches `stage`)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        constexpr int VE = 16 / (int)sizeof(T);  // elements per 16 bytes
+        constexpr int LPR = D / VE;              // lanes per row
+        constexpr int RPI = 64 / LPR;            // rows per store instruction
+#pragma unroll
+        for (int u = 0; u < 16 / RPI; ++u) {
+            const int rr = u * RPI + lane / LPR, c = (lane % LPR) * VE;
+            const uint4 val = *(const uint4*)(stage + rr * RS + c);
+            T* d = dst(rr);
+            if (d) *(uint4*)(d + c) = val;
+        }
+    }
+};
+
 }  // namespace dsalt
