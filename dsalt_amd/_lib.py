@@ -22,6 +22,7 @@ FWD_NOALLOC_MAX_PLAN_BYTES = 4 << 20  # DSALT_FWD_NOALLOC_MAX_PLAN_BYTES
 # tile variants of the attention kernels (DSALT_VARIANT_*)
 VARIANT_DEFAULT, VARIANT_FWD_BN32, VARIANT_FWD_RG2, VARIANT_DQ_BN64, VARIANT_LMK_SHORT = 0, 1, 2, 4, 8
 VARIANT_FWD_BN64 = 16
+VARIANT_FWD_8W = 32
 
 _i32, _i64, _vp, _sz, _f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float
 

@@ -183,7 +183,7 @@ __device__ __forceinline__ void band_edge(const AttnParams& p, const RowGroup& R
     }
 }
 
-// One 256-thread block (4 waves) owns 64*RG query rows of one (head, sequence),
+// One 256-thread block (4 waves; NW = 8 below: 512 threads) owns 64*RG query rows of one (head, sequence),
 // (two 16-row groups with 32-key chunks, 16-bit head_dim 64: held at four waves per SIMD, 128
 // VGPRs; the K and V^T operands of a chunk serve both groups of a wave)
 // taken in the row plan's order; wave w owns the 16-row groups RG*w .. RG*w+RG-1
@@ -198,24 +198,30 @@ __device__ __forceinline__ void band_edge(const AttnParams& p, const RowGroup& R
 // multiple of 64 (one row group per wave, inference only): the block's rows may belong to
 // several sets, all staged in LDS side by side; each row sees the slots of its own set only
 // (a two-sided slot mask, like the band's key mask).
-template <typename T, int D, int BN, int RG, bool TR, bool MS = false>
-__global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN == 32) ? 4 : 2) void fwd_kernel(AttnParams p) {
+//
+// NW = 8: eight waves, one row group each, over two plan tiles (128 rows): every staged chunk
+// serves twice the rows (head_dim 128, where the chunks' staging is most of the time).
+template <typename T, int D, int BN, int RG, bool TR, bool MS = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW, (sizeof(T) == 2 && D == 64 && RG == 2 && BN == 32) ? 4 : 2) void fwd_kernel(AttnParams p) {
     static_assert(!MS || (RG == 1 && !TR), "several sets per block: one row group, inference");
+    static_assert(NW == 4 || (NW == 8 && RG == 1 && !MS), "eight waves: one row group each, one set per block");
+    constexpr int NT = 64 * NW;
+    constexpr int TPB = RG * NW / 4;  // plan tiles (64 rows) per block
     constexpr int NST = BN / 16;
     constexpr bool kHalf = sizeof(T) == 2;
     constexpr int LCAP = MS ? kMultiSetSlots : kSetSlots;
-    typedef Tile<T, D, BN, 256, (BN == 64 ? 8 : Pad<T, D>::R)> KT;
+    typedef Tile<T, D, BN, NT, (BN == 64 ? 8 : Pad<T, D>::R)> KT;
     __shared__ __attribute__((aligned(16))) T Ks[2][KT::ELEMS];
     __shared__ __attribute__((aligned(16))) T Vs[2][KT::ELEMS];
     __shared__ int lpos[LCAP];
     __shared__ __attribute__((aligned(16))) float lbs[LCAP];
-    static_assert(KT::ELEMS * sizeof(T) >= sizeof(int) * (8 + kMaxTileSets), "block scalars fit a K buffer");
+    static_assert(KT::ELEMS * sizeof(T) >= sizeof(int) * (16 + kMaxTileSets), "block scalars fit a K buffer");
     // block scalars live in the second K buffer until the first chunk is staged there
     // (keeps the block at 40 KB of LDS: four blocks per CU)
     int* red = (int*)Ks[1];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
-    const int nblk = ceil_div(p.n_tiles, RG);
+    const int nblk = ceil_div(p.n_tiles, TPB);
     // tile-major order, the last tiles of every sequence first (their rows see the most
     // landmarks: the longest blocks start first and short ones fill the end of the grid);
     // blocks reach the XCDs round-robin, so where 8 divides heads x sequences each XCD keeps
@@ -227,7 +233,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     const int s = hs / p.n_heads;
     int st, len;
     seq_bounds(p.cu, s, p.total_len, p.max_seqlen, st, len);
-    const int r0 = b * 64 * RG;
+    const int r0 = b * 64 * TPB;
     if (r0 >= len) return;
     const int kvh = h / (p.n_heads / p.n_kv_heads);
     const int set = p.block_size ? r0 / p.block_size : 0;
@@ -249,7 +255,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     // the block's largest visible landmark count follows from the largest window start of
     // its groups, so one barrier (the set in LDS) precedes the first landmark chunk's fetch.
     // (MS: the sets are staged by a loop after the plan's loads)
-    constexpr int NLV = MS ? 1 : kSetSlots / 256;
+    constexpr int NLV = MS ? 1 : kSetSlots / NT;
     int lv[NLV], ln[NLV];
     float lb[NLV];
 #pragma unroll
@@ -257,17 +263,17 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
         lv[u] = -1;
         ln[u] = -1;
         lb[u] = 0.f;
-        if (!MS && u * 256 < K) {  // every lane loads (clamped slots), so no load waits on a branch
-            lv[u] = p.lmk[set_off + min(u * 256 + tid, K - 1)];
-            ln[u] = p.lmk[set_off + min(u * 256 + tid + 1, K - 1)];
-            if (has_bias) lb[u] = p.lbias[set_off + min(u * 256 + tid, K - 1)];
+        if (!MS && u * NT < K) {  // every lane loads (clamped slots), so no load waits on a branch
+            lv[u] = p.lmk[set_off + min(u * NT + tid, K - 1)];
+            ln[u] = p.lmk[set_off + min(u * NT + tid + 1, K - 1)];
+            if (has_bias) lb[u] = p.lbias[set_off + min(u * NT + tid, K - 1)];
         }
     }
 
     // row groups of this wave, block-wide key range and largest window start, from the row plan
     const int uw = uniform(wave);
-    const int64_t tile0 = (int64_t)s * p.n_tiles + (int64_t)b * RG;
-    const int ntl = min(RG, p.n_tiles - b * RG);
+    const int64_t tile0 = (int64_t)s * p.n_tiles + (int64_t)b * TPB;
+    const int ntl = min(TPB, p.n_tiles - b * TPB);
     int blo = 0x7fffffff, bhi = -1, blmax = (int)0x80000000;
     if (lane < 4 * ntl) {
         const int* bnd = p.plan_bounds + tile0 * 16 + lane * 4;
@@ -295,12 +301,12 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     blmax = uniform(wave_max(blmax));
 
     int nvalid;  // valid slots of the (first) set; MS: of any set, and nvs[j] per set
-    int* nvs = red + 8;
+    int* nvs = red + 16;
     if constexpr (!MS) {
         int nv_loc = 0;  // one past the last valid slot (sets are ascending, -1 after the valid slots)
 #pragma unroll
         for (int u = 0; u < NLV; ++u) {
-            const int i = u * 256 + tid;
+            const int i = u * NT + tid;
             if (i < K) {
                 lpos[i] = lv[u];
                 if (has_bias) lbs[i] = lb[u] * inv_scale;  // raw-score units
@@ -310,12 +316,15 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
         nv_loc = wave_max(nv_loc);
         if (lane == 0) red[4 + uw] = nv_loc;
         __syncthreads();
-        nvalid = uniform(max(max(red[4], red[5]), max(red[6], red[7])));
+        int nvm = red[4];
+#pragma unroll
+        for (int w2 = 1; w2 < NW; ++w2) nvm = max(nvm, red[4 + w2]);
+        nvalid = uniform(nvm);
     } else {
         if (tid < kMaxTileSets) nvs[tid] = 0;
         __syncthreads();
         // slot e: position sl of set set + j (the block's sets are consecutive, K slots each)
-        for (int e = tid; e < nslots; e += 256) {
+        for (int e = tid; e < nslots; e += NT) {
             const int j = e / K, sl = e - j * K;
             const int64_t o = set_off + (int64_t)j * K;
             const int v = p.lmk[o + sl];
@@ -624,8 +633,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64 && RG == 2 && BN ==
     // output rows whole, staged in the idle K/V buffers (waves 0-1 in Ks, 2-3 in Vs; the
     // groups of a wave one after the other)
     typedef StoreRows<T, D> SR;
-    static_assert(KT::ELEMS >= SR::ELEMS, "row staging does not fit the chunk buffers");
-    T* stage = (wave < 2 ? &Ks[0][0] : &Vs[0][0]) + (wave & 1) * SR::ELEMS;
+    static_assert(2 * KT::ELEMS >= (NW / 2) * SR::ELEMS, "row staging does not fit the chunk buffers");
+    T* stage = (wave < NW / 2 ? &Ks[0][0] : &Vs[0][0]) + (wave % (NW / 2)) * SR::ELEMS;
     T* o0 = (T*)p.o + (int64_t)st * p.o_st + (int64_t)h * p.o_sh;
 #pragma unroll
     for (int u = 0; u < RG; ++u) {
@@ -674,6 +683,12 @@ static void fwd_run(const AttnParams& p, hipStream_t stream) {
         } else if constexpr (!TR) {  // head_dim 128 (inference shapes)
             // two row groups keep 32-key chunks (with 64-key chunks they would spill at 256 VGPRs)
             const bool bn64 = (p.variant & DSALT_VARIANT_FWD_BN64) != 0;
+            const bool w8 = (p.variant & DSALT_VARIANT_FWD_8W) != 0 && (p.block_size == 0 || p.block_size % 128 == 0);
+            if (w8) {
+                DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, BN, 1, TR, false, 8>),
+                             dim3(p.n_heads * p.num_seqs * ceil_div(p.n_tiles, 2)), dim3(512), 0, stream, p);
+                return;
+            }
             if (rg2) {
                 DSALT_LAUNCH("attn_fwd", (fwd_kernel<T, D, BN, 2, TR>), dim3(total), dim3(256), 0, stream, p);
                 return;

@@ -13,6 +13,9 @@ run time by the ``variant`` bits of the C ABI (``DSALT_VARIANT_*``):
               with FWD_BN32 the kernel is held at four waves per SIMD);
   * FWD_BN64  forward key chunks of 64 instead of 32 rows (16-bit, head_dim 128, inference;
               ignored with FWD_RG2);
+  * FWD_8W    forward blocks of 128 rows in eight waves, one row group each: every staged key
+              chunk serves twice the rows (16-bit, head_dim 128, inference; ignores FWD_RG2 and
+              FWD_BN64);
   * DQ_BN64   backward dQ key chunks of 64 instead of 32 rows (16-bit, head_dim 64);
   * LMK_SHORT landmark-backward row chunks of 512 instead of 1024 rows (more blocks).
 
@@ -26,7 +29,8 @@ from __future__ import annotations
 
 import torch
 
-from .._lib import VARIANT_DQ_BN64, VARIANT_FWD_BN32, VARIANT_FWD_BN64, VARIANT_FWD_RG2, VARIANT_LMK_SHORT
+from .._lib import (VARIANT_DQ_BN64, VARIANT_FWD_8W, VARIANT_FWD_BN32, VARIANT_FWD_BN64, VARIANT_FWD_RG2,
+                    VARIANT_LMK_SHORT)
 
 _TUNED_CONFIG: dict = {}
 
@@ -52,13 +56,14 @@ def _config_of(head_dim: int, elem_bytes: int, variant: int) -> dict:
     bm = 64
     if tunable and variant & VARIANT_FWD_BN32:
         bn = 32
-    if half and hd == 128 and variant & VARIANT_FWD_BN64 and not variant & VARIANT_FWD_RG2:
+    w8 = half and hd == 128 and bool(variant & VARIANT_FWD_8W)
+    if half and hd == 128 and variant & VARIANT_FWD_BN64 and not variant & VARIANT_FWD_RG2 and not w8:
         bn = 64
-    if half and variant & VARIANT_FWD_RG2:
+    if half and variant & VARIANT_FWD_RG2 or w8:
         bm = 128
     if tunable and variant & VARIANT_DQ_BN64:
         bnq = 64
-    return {"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_N_BWD": bnq, "BLOCK_Q_BWD": bq, "num_warps": 4 * bm // 64,
+    return {"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_N_BWD": bnq, "BLOCK_Q_BWD": bq, "num_warps": 8 if w8 else 4,
             "num_stages": 2, "LMK_ROWS": 512 if variant & VARIANT_LMK_SHORT else 1024, "variant": int(variant)}
 
 
@@ -74,14 +79,14 @@ def _candidate_configs(head_dim: int, device=None, elem_bytes: int = 2) -> list[
         variants = [0, VARIANT_FWD_BN32, VARIANT_FWD_RG2, VARIANT_FWD_RG2 | VARIANT_FWD_BN32,
                     VARIANT_DQ_BN64, VARIANT_LMK_SHORT, VARIANT_DQ_BN64 | VARIANT_LMK_SHORT]
     elif head_dim == 128 and elem_bytes == 2:
-        variants = [0, VARIANT_FWD_RG2, VARIANT_FWD_BN64, VARIANT_LMK_SHORT]
+        variants = [0, VARIANT_FWD_RG2, VARIANT_FWD_BN64, VARIANT_FWD_8W, VARIANT_LMK_SHORT]
     else:
         variants = [0, VARIANT_LMK_SHORT]
     return [_config_of(head_dim, elem_bytes, v) for v in variants]
 
 
 # variant bits of the forward kernels and of the backward kernels (independent choices)
-_FWD_BITS = VARIANT_FWD_BN32 | VARIANT_FWD_RG2 | VARIANT_FWD_BN64
+_FWD_BITS = VARIANT_FWD_BN32 | VARIANT_FWD_RG2 | VARIANT_FWD_BN64 | VARIANT_FWD_8W
 _BWD_BITS = VARIANT_DQ_BN64 | VARIANT_LMK_SHORT
 
 

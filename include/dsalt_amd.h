@@ -323,7 +323,10 @@ int    dsalt_silu_mul(const dsalt_silu_mul_args* a, dsalt_stream_t stream);
 #define DSALT_VARIANT_LMK_SHORT  8  /* backward landmark pass: 512-row chunks                    */
 #define DSALT_VARIANT_FWD_BN64  16  /* forward: 64-key chunks (16-bit types, head_dim 128,
                                        inference operator; ignored with FWD_RG2)                 */
-#define DSALT_VARIANT_MASK       31
+#define DSALT_VARIANT_FWD_8W    32  /* forward: blocks of 128 rows, eight waves of one row group
+                                       each (16-bit, head_dim 128, inference operator; ignores
+                                       FWD_RG2 and FWD_BN64)                                     */
+#define DSALT_VARIANT_MASK       63
 
 /* Bytes of the row-plan buffer of dsalt_fwd_args.plan / dsalt_bwd_args.plan. */
 size_t dsalt_plan_bytes(const dsalt_problem* p);

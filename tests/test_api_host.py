@@ -90,7 +90,8 @@ def test_autotune_candidates_describe_the_compiled_tilings():
     assert by[AT.VARIANT_LMK_SHORT]["LMK_ROWS"] == 512
     # 16-bit head_dim 128: two row groups per wave or 64-key chunks in the forward
     c128 = {c["variant"]: c for c in AT._candidate_configs(128, None, 2)}
-    assert list(c128) == [0, AT.VARIANT_FWD_RG2, AT.VARIANT_FWD_BN64, AT.VARIANT_LMK_SHORT]
+    assert list(c128) == [0, AT.VARIANT_FWD_RG2, AT.VARIANT_FWD_BN64, AT.VARIANT_FWD_8W, AT.VARIANT_LMK_SHORT]
+    assert c128[AT.VARIANT_FWD_8W]["BLOCK_M"] == 128 and c128[AT.VARIANT_FWD_8W]["BLOCK_N"] == 32
     assert c128[0]["BLOCK_N"] == 32 and c128[AT.VARIANT_FWD_BN64]["BLOCK_N"] == 64
     assert c128[AT.VARIANT_FWD_RG2]["BLOCK_M"] == 128 and c128[AT.VARIANT_FWD_RG2]["BLOCK_N"] == 32
     # fp32 shapes have one compiled tiling: only the landmark-chunk choice
