@@ -1,6 +1,7 @@
 """Edge cases of the operator on the GPU against the oracle: empty and one-token sequences in a
-packed batch, no landmarks, the largest landmark sets, every landmark slot empty, the GQA ratio
-of the 3B decoder, and windows covering whole sequences.  Indices bit-exact; outputs and
+packed batch (also with block-causal blocks that are not multiples of 64 rows), no landmarks,
+the largest landmark sets (512 slots and the wide kernels' 2048), every landmark slot empty,
+the GQA ratio of the 3B decoder, and windows covering whole sequences.  Indices bit-exact; outputs and
 gradients relative max|a-b| / max|b| within 1e-5 (fp32) or 2e-2 (bf16)."""
 from __future__ import annotations
 
@@ -74,12 +75,28 @@ def test_empty_sequences_block_causal():
          block=64, backward=False)
 
 
+def test_empty_sequences_block_causal_any_block_size():
+    # blocks of 50 rows: 64-row tiles over two sets, next to empty and one-token sequences
+    _run(_case([0, 300, 0, 1, 70], 2, 2, 64, 8, 40, torch.bfloat16, seed=207), 8, mode=ops.SELECT_BLOCK,
+         block=50, backward=False)
+
+
 def test_no_landmarks():
     _run(_case([257, 190], 4, 4, 64, 0, 90, torch.bfloat16, seed=202), 0)
 
 
+def test_no_landmarks_block_causal_any_block_size():
+    _run(_case([257, 190], 4, 4, 64, 0, 90, torch.bfloat16, seed=208), 0, mode=ops.SELECT_BLOCK, block=37,
+         backward=False)
+
+
 def test_largest_landmark_sets():
     _run(_case([1200, 700], 2, 2, 128, 512, 300, torch.bfloat16, seed=203), 512)
+
+
+def test_largest_landmark_sets_of_the_wide_kernels():
+    # 2048 slots: more than the sequences' candidates (every set ends in -1 padding)
+    _run(_case([2500, 700], 2, 2, 64, 2048, 300, torch.bfloat16, seed=209), 2048)
 
 
 def test_gqa_ratio_of_the_3b_decoder():
