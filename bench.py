@@ -120,7 +120,7 @@ def read_pmc(root: str) -> dict:
     return out
 
 
-def traffic_from(root: str, wl_name: str, copy_mib: int = 1024) -> dict:
+def traffic_from(root: str, wl_name: str, copy_mib: int = 1024, variant: str = "auto") -> dict:
     """HBM bytes per launch of each kernel: FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled by
     the ratio of a plain copy's known bytes to that counter's reading for the copy."""
     known = copy_mib * 2**20
@@ -135,13 +135,16 @@ def traffic_from(root: str, wl_name: str, copy_mib: int = 1024) -> dict:
     fetch = read_pmc(os.path.join(root, "fetch"))
     write = read_pmc(os.path.join(root, "write"))
     b = f"python -u bench.py --workload {wl_name} --steps 2 --warmup 1 --no-cpu-baseline"
+    if variant != "auto":  # the tiling the counted runs used
+        b += f" --variant {variant}"
     res = {"_commands": [f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/fetch -o run -- {b}",
                          f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/write -o run -- {b}",
                          f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/copy_fetch -o run -- "
                          f"python -u bench.py --copy-calibration {copy_mib}",
                          f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/copy_write -o run -- "
                          f"python -u bench.py --copy-calibration {copy_mib}",
-                         f"python bench.py --traffic-from <out> --workload {wl_name}"],
+                         f"python bench.py --traffic-from <out> --workload {wl_name}"
+                         + (f" --variant {variant}" if variant != "auto" else "")],
            "_calibration": {"copy_bytes": known, "fetch_factor": f_fac, "write_factor": w_fac},
            "_sources": kernel_source_sha()}
     for k in sorted(set(fetch) & set(write) & set(LABELS)):
@@ -406,7 +409,7 @@ def model_bench(args, wl):
 def main():
     args = parse()
     if args.traffic_from:
-        print(json.dumps(traffic_from(args.traffic_from, args.workload, args.copy_calibration or 1024), indent=1))
+        print(json.dumps(traffic_from(args.traffic_from, args.workload, args.copy_calibration or 1024, args.variant), indent=1))
         return
     if args.kernel_stats:
         import csv

@@ -68,3 +68,7 @@ def test_traffic_record_scales_by_the_copy(tmp_path, monkeypatch):
     assert any("--traffic-from" in c for c in rec["_commands"])
     with open(tmp_path / "profiles" / "traffic_unit_workload.json") as f:
         assert json.load(f)["bwd_dq"] == rec["bwd_dq"]
+    assert not any("--variant" in c for c in rec["_commands"])
+    # a counted run with a fixed tiling names it in the bench commands and the rewrite
+    rec = bench.traffic_from(str(out), "unit_workload", copy_mib=1, variant="3")
+    assert [c.endswith("--variant 3") for c in rec["_commands"]] == [True, True, False, False, True]
