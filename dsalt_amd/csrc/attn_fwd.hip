@@ -389,9 +389,10 @@ __global__ __launch_bounds__(64 * NW, (sizeof(T) == 2 && D == 64 && RG == 2 && B
     } else {
 #pragma unroll
         for (int u = 0; u < RG; ++u) plan_counts_sets(lpos, nvs, K, p.block_size, set, nsets, rg[u]);
-        // the last set's rows end furthest: its count at the block's largest window start bounds them
+        // the last set's rows end furthest: its count at the block's largest window start bounds
+        // them; with every set empty there is no landmark chunk (and the first was not fetched)
         const int lj = (nsets - 1) * K;
-        bcm = uniform(lj + lower_bound_lds(lpos + lj, nvs[nsets - 1], blmax));
+        bcm = nvalid > 0 ? uniform(lj + lower_bound_lds(lpos + lj, nvs[nsets - 1], blmax)) : 0;
     }
     const int cs = (blo / BN) * BN;
     const int nband = bhi >= blo ? (bhi - cs) / BN + 1 : 0;

@@ -81,6 +81,16 @@ def test_empty_sequences_block_causal_any_block_size():
          block=50, backward=False)
 
 
+@pytest.mark.parametrize("D,dt", [(128, torch.bfloat16), (64, torch.float32)])
+def test_block_causal_tiles_whose_sets_are_all_empty(D, dt):
+    # 17-row blocks: a 64-row tile spans four sets; the first 200 tokens' windows reach the
+    # sequence start, so they are never candidates and the first tiles' sets are all empty
+    # while later tiles hold landmarks (such tiles once staged a chunk that was never fetched)
+    x = _case([400, 60], 4, 2, D, 29, 600, dt, seed=210)
+    x["w"][:200] = 600
+    _run(x, 29, mode=ops.SELECT_BLOCK, block=17, backward=False)
+
+
 def test_no_landmarks():
     _run(_case([257, 190], 4, 4, 64, 0, 90, torch.bfloat16, seed=202), 0)
 

@@ -1,0 +1,115 @@
+"""A seeded sweep of random operator configurations on the GPU against the oracle.
+
+Each case draws a packed batch of ragged sequences (empty and one-token sequences included),
+grouped key/value heads read in place, head_dim 64 or 128, fp32 / bf16 / fp16, global or
+block-causal selection (block sizes that are and are not multiples of 64), landmark counts from
+none to more than the sequences hold, landmark biases, and a tiling variant (bits the shape does
+not compile are ignored by the library).  Landmark indices must be bit-exact; outputs relative
+max|a-b| / max|b| within 1e-5 (fp32) or 2e-2 (16-bit); log-sum-exps within 1e-4 / 2e-2; the
+gradients of global sets through the landmark-row / other-row class and per-row bounds of the
+other gradient tests.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from dsalt_amd import ops
+from oracle import attention as OA
+from oracle import select as OS
+from tests.helpers import bits, check_grads, f64, oracle_dtype, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+LSE_TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+N_CASES = 24
+SET_SLOTS = 2048  # landmark slots the forward stages for one 64-row tile, over all its sets
+
+
+def draw(seed: int) -> dict:
+    """Configuration of case `seed` (numpy's generator, so the draw is fixed across platforms)."""
+    r = np.random.default_rng(10_000 + seed)
+    S = int(r.integers(1, 5))
+    lens = []
+    for _ in range(S):
+        u = r.random()
+        lens.append(0 if u < 0.12 else 1 if u < 0.2 else int(r.integers(2, 700)))
+    if sum(lens) < 2:
+        lens[0] = int(r.integers(64, 400))
+    G = int(r.choice([1, 2, 4]))
+    H = G * int(r.choice([1, 2, 4]))
+    D = int(r.choice([64, 128]))
+    dt = [torch.float32, torch.bfloat16, torch.float16][int(r.choice(3, p=[0.3, 0.5, 0.2]))]
+    block = r.random() < 0.4
+    bs = int(r.choice([17, 50, 64, 100, 128, 256, 512])) if block else 64
+    u = r.random()
+    K = 0 if u < 0.1 else int(r.integers(1, 64)) if u < 0.45 else int(r.integers(64, 513)) if u < 0.9 \
+        else int(r.integers(513, 1200))
+    if block:  # a 64-row tile stages every set it spans
+        K = min(K, SET_SLOTS // (1 if bs % 64 == 0 else 63 // bs + 2))
+    wmax = int(r.integers(1, 700))
+    bias = bool(r.random() < 0.3)
+    if D == 64:
+        variant = int(r.choice([0, 1, 2, 3])) | int(r.choice([0, 4])) | int(r.choice([0, 8]))
+    else:
+        variant = int(r.choice([0, 2, 16, 32])) | int(r.choice([0, 8]))
+    backward = not block and bool(r.random() < 0.7)
+    return dict(lens=lens, H=H, G=G, D=D, dt=dt, mode=ops.SELECT_BLOCK if block else ops.SELECT_GLOBAL,
+                block=bs, K=K, wmax=wmax, bias=bias, variant=variant, backward=backward, seed=seed)
+
+
+def inputs(c: dict, hidden: int = 96) -> dict:
+    g = torch.Generator().manual_seed(20_000 + c["seed"])
+    T, H, G, D, dt = sum(c["lens"]), c["H"], c["G"], c["D"], c["dt"]
+    return {"q": torch.randn(T, H, D, generator=g).to(dt), "k": torch.randn(T, G, D, generator=g).to(dt),
+            "v": torch.randn(T, G, D, generator=g).to(dt), "h": torch.randn(T, hidden, generator=g).to(dt),
+            "w": torch.randint(1, c["wmax"] + 1, (T,), generator=g, dtype=torch.int32),
+            "do": torch.randn(T, H, D, generator=g).to(dt),
+            "cu": torch.tensor([0] + list(np.cumsum(c["lens"])), dtype=torch.int32),
+            "alpha": torch.rand(H, generator=g)}
+
+
+@pytest.mark.parametrize("seed", range(N_CASES))
+def test_random_configuration(seed):
+    c = draw(seed)
+    print("case", {k: (str(v) if k == "dt" else v) for k, v in c.items()}, flush=True)
+    x = inputs(c)
+    dt, K, mode, bs = c["dt"], c["K"], c["mode"], c["block"]
+    maxlen = max(1, max(c["lens"]))
+    d = {k: v.to(DEV) for k, v in x.items()}
+    idx = ops.select_landmarks(d["h"], d["v"], d["alpha"], d["w"], d["cu"], K, max_seqlen=maxlen, select_mode=mode,
+                               block_size=bs, stats_scope=ops.STATS_SEQUENCE)
+    ridx = OS.select(bits(x["h"]), bits(x["v"]), x["alpha"].numpy(), x["w"].numpy(), x["cu"].numpy(), K,
+                     oracle_dtype(dt), mode=mode, block_size=bs, stats_scope=OS.STATS_SEQUENCE)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    bias = None
+    if c["bias"] and K > 0:
+        bias = torch.randn(idx.shape, generator=torch.Generator().manual_seed(30_000 + seed)) * 0.5
+    scale = 1.0 / math.sqrt(c["D"])
+    out, lse = ops.attention_forward(d["q"], d["k"], d["v"], d["w"], d["cu"], idx,
+                                     None if bias is None else bias.to(DEV), scale=scale, max_seqlen=maxlen,
+                                     select_mode=mode, block_size=bs, variant=c["variant"])
+    torch.cuda.synchronize()
+    ro, rl = OA.attention_fwd(f64(x["q"]), f64(x["k"]), f64(x["v"]), x["w"].numpy(), x["cu"].numpy(), ridx, scale,
+                              lmk_bias=None if bias is None else bias.double().numpy(),
+                              block_size=bs if mode == ops.SELECT_BLOCK else None)
+    assert rel_err(f64(out), ro) < TOL[dt], "out"
+    fin = np.isfinite(rl)
+    assert np.all(np.isfinite(lse.cpu().numpy()[fin]))
+    assert np.abs(f64(lse)[fin] - rl[fin]).max(initial=0.0) < LSE_TOL[dt], "lse"
+    if not c["backward"]:
+        return
+    dq, dk, dv, db = ops.attention_backward(d["do"], d["q"], d["k"], d["v"], out, lse, d["w"], d["cu"], idx,
+                                            None if bias is None else bias.to(DEV), scale=scale, max_seqlen=maxlen,
+                                            want_dbias=bias is not None, variant=c["variant"])
+    torch.cuda.synchronize()
+    rdq, rdk, rdv, rdb = OA.attention_bwd(f64(x["q"]), f64(x["k"]), f64(x["v"]), x["w"].numpy(), x["cu"].numpy(),
+                                          ridx, scale, f64(x["do"]),
+                                          lmk_bias=None if bias is None else bias.double().numpy(), out=f64(out))
+    check_grads(("sweep", seed), (dq, dk, dv), (rdq, rdk, rdv), ridx, x["cu"], TOL[dt])
+    if bias is not None:
+        assert rel_err(db.cpu().double().numpy(), rdb) < TOL[dt], "d_bias"
