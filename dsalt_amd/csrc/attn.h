@@ -65,6 +65,14 @@ struct AttnParams {
     int n_chunks;            // row chunks of the landmark backward
 };
 
+// Training variant: a row's continuous window as the kernels take it, in [0, max_seqlen +
+// ceil(win_edge)].  Above that bound every band key of any row (d <= max_seqlen - 1) lies in
+// the core (wt - d > win_edge), no landmark is visible and d bias / d wt is 0, so the clamp
+// changes no value; floor and fraction are both taken from the clamped window.
+__device__ __forceinline__ float train_wt(const AttnParams& p, float w_cont) {
+    return fminf(fmaxf(w_cont, 0.f), (float)(p.max_seqlen + p.edge_keys));
+}
+
 // Training variant, band key at distance d = i - j of a row with continuous window wt:
 // logit bias log sigmoid((wt - d) / tau) outside the core d <= wt - edge, 0 inside,
 // returned in raw-score units (divided by the logit scale).

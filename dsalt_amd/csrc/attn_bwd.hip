@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? (BN == 32 ? (TR 
     const int at = st + (valid ? i : 0);  // loads by every lane (a row past the end reads row 0)
     const int wi = max(p.w[at], 1);
     const float lse_raw = p.lse[(int64_t)at * p.n_heads + h];
-    const float wt_raw = TR ? p.w_cont[at] : 0.f;
+    const float wt_raw = TR ? train_wt(p, p.w_cont[at]) : 0.f;
     const T* qhead = (const T*)p.q + (int64_t)st * p.q_st + (int64_t)h * p.q_sh;
     const T* dohead = (const T*)p.dout + (int64_t)st * p.do_st + (int64_t)h * p.do_sh;
     const T* ohead = (const T*)p.o + (int64_t)st * p.o_st + (int64_t)h * p.o_sh;
@@ -608,7 +608,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 2 && D == 64) ? ((GQA || TR) ? 3
         r.lo = max(i - wi + 1, 0);
         r.l = lrow[i];
         r.d = drow[i];
-        r.wt = TR ? p.w_cont[st + i] : 0.f;
+        r.wt = TR ? train_wt(p, p.w_cont[st + i]) : 0.f;
         return r;
     };
 

@@ -133,7 +133,7 @@ __device__ __forceinline__ void plan_window(const AttnParams& p, int st, RowGrou
     // loads issued by every lane (a row past the end reads the sequence's first row)
     const int at = st + (rg.valid ? rg.i : 0);
     const int wi = max(p.w[at], 1);
-    const float wt = p.w_cont ? p.w_cont[at] : 0.f;
+    const float wt = p.w_cont ? train_wt(p, p.w_cont[at]) : 0.f;
     if (rg.valid) {
         rg.lo = max(rg.i - wi + 1, 0);
         rg.hi = rg.i;
@@ -727,7 +727,7 @@ static hipError_t fwd_dispatch(const AttnParams& p, bool plan_ready, hipStream_t
 __global__ __launch_bounds__(256) void train_windows_kernel(AttnParams p, int* w_int) {
     const int t = blockIdx.x * 256 + threadIdx.x;
     if (t >= p.total_len) return;
-    const float wt = fminf(fmaxf(p.w_cont[t], 0.f), (float)p.max_seqlen);
+    const float wt = train_wt(p, p.w_cont[t]);
     w_int[t] = (int)floorf(wt) + 1;
     if (p.dw_h)  // backward: rows outside every sequence keep a zero gradient
         for (int h = 0; h < p.n_heads; ++h) p.dw_h[(int64_t)t * p.n_heads + h] = 0.f;

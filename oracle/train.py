@@ -56,6 +56,8 @@ def _blocks(q, k, v, w_cont, cu, lmk_pos, lmk_logw, scale, tau_win, win_edge):
     for h in range(H):
         for s in range(len(cu) - 1):
             st, en = int(cu[s]), int(cu[s + 1])
+            if en == st:  # an empty sequence has no rows
+                continue
             bias, dbw = train_bias(w_cont[st:en], lmk_pos[h, s], lmk_logw[h, s], tau_win, win_edge)
             logits = (q[st:en, h] @ k[st:en, h].T) * scale + bias
             yield h, s, st, en, logits, dbw

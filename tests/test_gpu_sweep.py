@@ -7,7 +7,9 @@ none to more than the sequences hold, landmark biases, and a tiling variant (bit
 not compile are ignored by the library).  Landmark indices must be bit-exact; outputs relative
 max|a-b| / max|b| within 1e-5 (fp32) or 2e-2 (16-bit); log-sum-exps within 1e-4 / 2e-2; the
 gradients of global sets through the landmark-row / other-row class and per-row bounds of the
-other gradient tests.
+other gradient tests.  A second sweep draws configurations of the training operator (soft window
+edge, landmark log-weights, continuous windows up to past the sequence ends) and checks them
+as tests/test_gpu_train.py does.
 """
 from __future__ import annotations
 
@@ -113,3 +115,31 @@ def test_random_configuration(seed):
     check_grads(("sweep", seed), (dq, dk, dv), (rdq, rdk, rdv), ridx, x["cu"], TOL[dt])
     if bias is not None:
         assert rel_err(db.cpu().double().numpy(), rdb) < TOL[dt], "d_bias"
+
+
+def draw_train(seed: int) -> dict:
+    """Training-operator configuration of case `seed` (global sets, one sequence of at least 16
+    tokens, so no head's gradients are all the exact zeros of one-token sequences)."""
+    r = np.random.default_rng(50_000 + seed)
+    S = int(r.integers(1, 4))
+    lens = [0 if r.random() < 0.1 else 1 if r.random() < 0.1 else int(r.integers(2, 600)) for _ in range(S)]
+    lens[0] = max(lens[0], 16)
+    D = int(r.choice([64, 128]))
+    dt = [torch.float32, torch.bfloat16, torch.float16][int(r.choice(3, p=[0.3, 0.5, 0.2]))]
+    wlo = float(r.uniform(0.3, 50))
+    cfg = dict(lens=lens, H=int(r.integers(1, 7)), D=D, dt=dt, K=0 if r.random() < 0.08 else int(r.integers(1, 513)),
+               wlo=wlo, whi=float(wlo + r.uniform(0.5, 650)), tau=float(r.uniform(0.3, 2.0)),
+               edge=float(r.choice([0.5, 1.0, 4.0, 6.0, 10.0])), integer_every=int(r.choice([0, 3, 5])))
+    cfg["variant"] = (int(r.choice([0, 1, 2, 3])) | int(r.choice([0, 4])) | int(r.choice([0, 8]))) if D == 64 else 0
+    return cfg
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_training_configuration(seed):
+    """The training operator (soft window edge, landmark log-weights, continuous windows that
+    may pass the sequence ends) against the float64 oracle, as in tests/test_gpu_train.py."""
+    from tests import test_gpu_train as TT
+    c = draw_train(seed)
+    print("case", {k: (str(v) if k == "dt" else v) for k, v in c.items()}, flush=True)
+    TT._check(c["lens"], c["H"], c["D"], c["K"], c["wlo"], c["whi"], c["dt"], seed=60_000 + seed, tau=c["tau"],
+              edge=c["edge"], integer_every=c["integer_every"], variant=c["variant"])

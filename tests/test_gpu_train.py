@@ -36,7 +36,7 @@ def _inputs(lens, H, D, K, wlo, whi, dt, seed, integer_every=0):
     pos = torch.full((H, len(lens), K), -1, dtype=torch.int32)
     for hh in range(H):
         for s, L in enumerate(lens):
-            n = min(K - (hh % 2), L)  # leave a -1 slot in every other head
+            n = max(0, min(K - (hh % 2), L))  # leave a -1 slot in every other head
             pos[hh, s, :n] = torch.randperm(L, generator=g)[:n].sort().values.to(torch.int32)
     logw = torch.nn.functional.logsigmoid(torch.randn(pos.shape, generator=g))
     logw = torch.where(pos >= 0, logw, torch.full_like(logw, float("-inf")))
@@ -101,6 +101,14 @@ def test_train_d128_bf16():
 def test_train_edge_wider_than_windows(dt):
     # win_edge above every window: the whole band carries the soft-edge bias (no core)
     _check([257, 99], 2, 64, 16, 0.0, 7.5, dt, seed=43, tau=2.0, edge=9.0, integer_every=3)
+
+
+@pytest.mark.parametrize("dt,edge", [(torch.float32, 4.0), (torch.float32, 10.0), (torch.bfloat16, 4.0)])
+def test_train_windows_longer_than_sequences(dt, edge):
+    # w~ up to 3x the longest sequence (integer and fractional): every band key of such a row
+    # lies in the core; the kernels clamp w~ keeping floor and fraction of one value (clamping
+    # the floor alone once moved the edge onto core keys of the rows near the sequence ends)
+    _check([150, 64, 1], 3, 64, 20, 5.0, 450.0, dt, seed=45, edge=edge, integer_every=3)
 
 
 def test_train_long_windows():
