@@ -127,6 +127,13 @@ def select_landmarks(h: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, w: t
     dt = dtype_code(h.dtype)
     if v.dtype != h.dtype:
         raise TypeError("h and v must share a dtype")
+    # the kernels read rows in 16-byte vectors: other widths are zero-padded (zero columns
+    # leave every row norm, and so every score, unchanged)
+    vec = 16 // h.element_size()
+    if h.shape[1] % vec:
+        h = torch.nn.functional.pad(h, (0, (-h.shape[1]) % vec))
+    if v.shape[2] % vec:
+        v = torch.nn.functional.pad(v, (0, (-v.shape[2]) % vec))
     T, hidden = h.shape
     _, G, D = v.shape
     H = alpha.shape[0]

@@ -109,8 +109,10 @@ double oracle_canon_sqrt64(double x) {
 
 /* ------------------------------------------------------------------- norms */
 double oracle_row_sumsq(const void* row, int dtype, int n) {
+    /* 16-byte vectors of vw elements; a row that is not whole vectors is summed as if
+       zero-padded to them (the zeros add exactly nothing: the operator pads such rows) */
     int vw = dtype == DSALT_DTYPE_F32 ? 4 : 8;
-    int nch = n / vw;
+    int nch = (n + vw - 1) / vw;
     int g = 1;
     while (g < nch && g < 64) g <<= 1;
     double a[64], b[64];
@@ -118,7 +120,8 @@ double oracle_row_sumsq(const void* row, int dtype, int n) {
         double acc = 0.0;
         for (int ch = l; ch < nch; ch += g)
             for (int e = 0; e < vw; ++e) {
-                double x = load_elem(row, dtype, (int64_t)ch * vw + e);
+                int64_t i = (int64_t)ch * vw + e;
+                double x = i < n ? load_elem(row, dtype, i) : 0.0;
                 acc = acc + x * x;
             }
         a[l] = acc;

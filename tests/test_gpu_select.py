@@ -60,6 +60,21 @@ def test_block_select_bit_exact(dt, D):
     np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
 
 
+@pytest.mark.parametrize("dt,hidden,D", [(torch.bfloat16, 100, 100), (torch.float16, 1000, 20), (torch.float32, 98, 30)])
+def test_row_widths_off_the_vector_size(dt, hidden, D):
+    # hidden / head_dim widths that are not whole 16-byte vectors: the operator zero-pads the
+    # rows (zero columns change no norm), indices, z and scores stay bit-exact with the oracle
+    # on the unpadded rows
+    h, v, alpha, w, cu = _case([300, 517], hidden, 2, D, 4, dt, 60, seed=8)
+    for mode in (ops.SELECT_GLOBAL, ops.SELECT_BLOCK):
+        res, ref = _run(h, v, alpha, w, cu, 24, mode, 100, ops.STATS_SEQUENCE)
+        if mode == ops.SELECT_GLOBAL:
+            for a_, b_ in zip(res, ref):
+                np.testing.assert_array_equal(a_.cpu().numpy(), b_)
+        else:
+            np.testing.assert_array_equal(res.cpu().numpy(), ref)
+
+
 def test_padding_when_few_candidates():
     h, v, alpha, w, cu = _case([90], 64, 1, 64, 2, torch.bfloat16, 200, seed=3)
     w[:] = 80  # only positions >= 80 are candidates: 10 of them

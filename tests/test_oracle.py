@@ -101,13 +101,16 @@ def test_canon_sqrt_close_to_sqrt():
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("n", [64, 128, 256, 1024, 96])
+@pytest.mark.parametrize("n", [64, 128, 256, 1024, 96, 98, 100, 13])
 def test_norms_match_fp64_norm(dt, n):
+    # widths that are not whole 16-byte vectors (98, 100, 13) too: summed as the zero-padded row
     g = torch.Generator().manual_seed(n)
     h = (torch.randn(50, n, generator=g) * 3).to(dt)
     v = torch.randn(50, 2, 64, generator=g).to(dt)
     from tests.helpers import bits, oracle_dtype
     nx, nv = OS.norms(bits(h), bits(v), oracle_dtype(dt))
+    hp = torch.nn.functional.pad(h, (0, (-n) % (16 // h.element_size())))
+    assert np.array_equal(OS.norms(bits(hp), bits(v), oracle_dtype(dt))[0], nx)
     exact = np.linalg.norm(h.double().numpy(), axis=1)
     ref = torch.tensor(exact).to(torch.float32).to(dt).to(torch.float64).numpy()
     ulp = {torch.float32: 2.0 ** -23, torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}[dt]
