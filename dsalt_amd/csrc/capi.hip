@@ -552,9 +552,8 @@ int dsalt_export_probs(const dsalt_probs_args* a, dsalt_stream_t stream) {
 
 int dsalt_cross_entropy_rows(const dsalt_ce_args* a, dsalt_stream_t stream) {
     if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
-    if (a->rows < 0 || a->n_cols < 8 || a->n_cols % 8)
-        return fail(DSALT_ERR_INVALID, "rows >= 0 and n_cols a positive multiple of 8 required (got %d, %d)", a->rows,
-                    a->n_cols);
+    if (a->rows < 0 || a->n_cols < 1)
+        return fail(DSALT_ERR_INVALID, "rows >= 0 and n_cols >= 1 required (got %d, %d)", a->rows, a->n_cols);
     if (a->dtype < 0 || a->dtype > 2) return fail(DSALT_ERR_INVALID, "unknown dtype %d", a->dtype);
     if (a->reduction < 0 || a->reduction > 2) return fail(DSALT_ERR_INVALID, "reduction must be 0, 1 or 2");
     if (a->rows == 0) return DSALT_OK;
@@ -592,8 +591,8 @@ int dsalt_cross_entropy_rows(const dsalt_ce_args* a, dsalt_stream_t stream) {
 
 int dsalt_silu_mul(const dsalt_silu_mul_args* a, dsalt_stream_t stream) {
     if (!a) return fail(DSALT_ERR_INVALID, "null argument struct");
-    if (a->rows < 0 || a->cols < 0 || a->cols % 8)
-        return fail(DSALT_ERR_INVALID, "rows >= 0 and cols a multiple of 8 required (got %d x %d)", a->rows, a->cols);
+    if (a->rows < 0 || a->cols < 0)
+        return fail(DSALT_ERR_INVALID, "rows >= 0 and cols >= 0 required (got %d x %d)", a->rows, a->cols);
     if (a->dtype < 0 || a->dtype > 2) return fail(DSALT_ERR_INVALID, "unknown dtype %d", a->dtype);
     if (a->rows == 0 || a->cols == 0) return DSALT_OK;
     const int64_t es = (int64_t)esize(a->dtype);

@@ -1,5 +1,6 @@
 // Row cross-entropy for the fused linear cross-entropy: one block per row of logits.
-// Pass 1 streams the row once (8 elements per thread per step) for the running max and
+// Pass 1 streams the row once (8 elements per thread per step, then the last V mod 8
+// elements one per thread: any vocabulary size, rows 16-byte aligned) for the running max and
 // the sum of exponentials (rescaled once per 8-element step), the label-smoothing sum and
 // the first index of the largest logit; the block combines them.  Pass 2 writes the
 // gradient with respect to the logits in place.  Formulas (float32):
@@ -56,6 +57,7 @@ __global__ __launch_bounds__(kCeThreads) void ce_kernel(CeParams p) {
     T* X = (T*)p.x + (int64_t)r * p.x_st;
     const int64_t y = p.target[r];
     const int V = p.n_cols;
+    const int V8 = V & ~7;  // whole 8-element vectors; the tail V8 .. V-1 one element per thread
     const bool has_w = p.ce_weight != nullptr;
     const float eps = p.label_smoothing / (float)V;
     if (y == p.ignore_index) {
@@ -63,7 +65,8 @@ __global__ __launch_bounds__(kCeThreads) void ce_kernel(CeParams p) {
             vec8 zero;
 #pragma unroll
             for (int e = 0; e < 8; ++e) zero[e] = from_float<T>(0.f);
-            for (int c = tid * 8; c < V; c += kCeThreads * 8) *(vec8*)(X + c) = zero;
+            for (int c = tid * 8; c < V8; c += kCeThreads * 8) *(vec8*)(X + c) = zero;
+            for (int c = V8 + tid; c < V; c += kCeThreads) X[c] = from_float<T>(0.f);
         }
         if (tid == 0) {
             p.loss[r] = 0.f;
@@ -74,7 +77,7 @@ __global__ __launch_bounds__(kCeThreads) void ce_kernel(CeParams p) {
         return;
     }
     RowStats s = {-INFINITY, 0.f, 0.f, -INFINITY, 0x7fffffff};
-    for (int c = tid * 8; c < V; c += kCeThreads * 8) {
+    for (int c = tid * 8; c < V8; c += kCeThreads * 8) {
         const vec8 v = *(const vec8*)(X + c);
         float xv[8];
         float m8 = -INFINITY;
@@ -102,6 +105,19 @@ __global__ __launch_bounds__(kCeThreads) void ce_kernel(CeParams p) {
         }
         s.d += d8;
         s.sx += sx8;
+    }
+    for (int c = V8 + tid; c < V; c += kCeThreads) {  // the tail: indices past every vector's
+        const float xv = capped(to_float(X[c]), p.softcap);
+        if (xv > s.bv) {
+            s.bv = xv;
+            s.bi = c;
+        }
+        if (xv > s.m) {
+            s.d = s.m == -INFINITY ? 0.f : s.d * __expf(s.m - xv);
+            s.m = xv;
+        }
+        s.d += __expf(xv - s.m);
+        s.sx += has_w ? xv * p.ce_weight[c] : xv;
     }
     // combine: lanes of a wave, then the waves
 #pragma unroll
@@ -132,35 +148,37 @@ __global__ __launch_bounds__(kCeThreads) void ce_kernel(CeParams p) {
     const bool mean = p.reduction == 1;
     if (p.grads) {
         const float inv_d = 1.f / d;
-        for (int c = tid * 8; c < V; c += kCeThreads * 8) {
+        // gradient of logit c (x0 as stored)
+        auto grad = [&](float x0, int c) {
+            const float th = p.softcap > 0.f ? tanhf(x0 / p.softcap) : 0.f;
+            const float xv = p.softcap > 0.f ? p.softcap * th : x0;
+            const float sm = __expf(xv - m) * inv_d;
+            const bool is_y = c == y;
+            float g;
+            if (!has_w) {
+                g = sm * (1.f + 2.f * zs * lse) - eps - (is_y ? 1.f - ls : 0.f);
+                if (mean) g = g / p.n_non_ignore;
+            } else {
+                float go = (1.f - ls) * (sm - (is_y ? 1.f : 0.f)) * wy;
+                float gs = eps * (sm * p.weight_sum - p.ce_weight[c]);
+                float gz = 2.f * zs * lse * sm;
+                if (mean) {
+                    go = go / p.sum_non_ignore_weight;
+                    gs = gs / p.sum_non_ignore_weight;
+                    gz = gz / p.n_non_ignore;
+                }
+                g = go + gs + gz;
+            }
+            if (p.softcap > 0.f) g *= 1.f - th * th;
+            return from_float<T>(g * scale_tok);
+        };
+        for (int c = tid * 8; c < V8; c += kCeThreads * 8) {
             vec8 v = *(const vec8*)(X + c);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float x0 = to_float(v[e]);
-                const float th = p.softcap > 0.f ? tanhf(x0 / p.softcap) : 0.f;
-                const float xv = p.softcap > 0.f ? p.softcap * th : x0;
-                const float sm = __expf(xv - m) * inv_d;
-                const bool is_y = c + e == y;
-                float g;
-                if (!has_w) {
-                    g = sm * (1.f + 2.f * zs * lse) - eps - (is_y ? 1.f - ls : 0.f);
-                    if (mean) g = g / p.n_non_ignore;
-                } else {
-                    float go = (1.f - ls) * (sm - (is_y ? 1.f : 0.f)) * wy;
-                    float gs = eps * (sm * p.weight_sum - p.ce_weight[c + e]);
-                    float gz = 2.f * zs * lse * sm;
-                    if (mean) {
-                        go = go / p.sum_non_ignore_weight;
-                        gs = gs / p.sum_non_ignore_weight;
-                        gz = gz / p.n_non_ignore;
-                    }
-                    g = go + gs + gz;
-                }
-                if (p.softcap > 0.f) g *= 1.f - th * th;
-                v[e] = from_float<T>(g * scale_tok);
-            }
+            for (int e = 0; e < 8; ++e) v[e] = grad(to_float(v[e]), c + e);
             *(vec8*)(X + c) = v;
         }
+        for (int c = V8 + tid; c < V; c += kCeThreads) X[c] = grad(to_float(X[c]), c);
     }
     if (tid == 0) {
         float loss = wy * (lse - xy);

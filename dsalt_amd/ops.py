@@ -515,6 +515,19 @@ def export_probs(q, k, w, cu_seqlens, lmk_idx, lse, lmk_bias=None, *, seq=0, row
 _REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
 
 
+def _aligned_rows(t: torch.Tensor) -> bool:
+    """Rows of the 2-D tensor start on 16-byte boundaries (what the kernels' vector loads need)."""
+    return t.data_ptr() % 16 == 0 and (t.shape[0] <= 1 or (t.stride(0) * t.element_size()) % 16 == 0)
+
+
+def _padded_rows(t: torch.Tensor) -> torch.Tensor:
+    """A copy of the 2-D tensor whose rows start on 16-byte boundaries (row stride rounded up)."""
+    vec = 16 // t.element_size()
+    buf = torch.empty((t.shape[0], -(-t.shape[1] // vec) * vec), dtype=t.dtype, device=t.device)
+    buf[:, :t.shape[1]].copy_(t)
+    return buf[:, :t.shape[1]]
+
+
 def cross_entropy_rows(logits, target, *, ce_weight=None, ignore_index=-100, n_non_ignore=None,
                        sum_non_ignore_weight=None, weight_sum=None, lse_square_scale=0.0, label_smoothing=0.0,
                        softcap=None, reduction="mean", want_grad=True, token_scaling=False, want_z=False,
@@ -526,6 +539,17 @@ def cross_entropy_rows(logits, target, *, ce_weight=None, ignore_index=-100, n_n
     dev = _gpu(logits, target, ce_weight)
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("logits must be [rows, V] with unit column stride")
+    if not _aligned_rows(logits):  # e.g. an odd vocabulary: run on a padded copy, gradient copied back
+        buf = _padded_rows(logits)
+        res = cross_entropy_rows(buf, target, ce_weight=ce_weight, ignore_index=ignore_index,
+                                 n_non_ignore=n_non_ignore, sum_non_ignore_weight=sum_non_ignore_weight,
+                                 weight_sum=weight_sum, lse_square_scale=lse_square_scale,
+                                 label_smoothing=label_smoothing, softcap=softcap, reduction=reduction,
+                                 want_grad=want_grad, token_scaling=token_scaling, want_z=want_z,
+                                 want_accuracy=want_accuracy, want_predicted=want_predicted)
+        if want_grad:
+            logits.copy_(buf)
+        return res
     rows, V = logits.shape
     tgt = target.detach().to(torch.int64).contiguous()
     cw = ce_weight.detach().to(torch.float32).contiguous() if ce_weight is not None else None
@@ -569,6 +593,9 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = No
         raise ValueError("gate and up must be [rows, cols] of one dtype with unit column stride")
     if out is None:
         out = torch.empty(gate.shape, dtype=gate.dtype, device=dev)
+    if gate.shape[0] and not (_aligned_rows(gate) and _aligned_rows(up) and _aligned_rows(out)):
+        o = silu_mul(_padded_rows(gate), _padded_rows(up), _padded_rows(out))  # rows off 16-byte boundaries
+        return out.copy_(o)
     a = SiluMulArgs(gate.shape[0], gate.shape[1], dtype_code(gate.dtype), gate.data_ptr(), gate.stride(0),
                     up.data_ptr(), up.stride(0), out.data_ptr(), out.stride(0))
     L = _lib.load()

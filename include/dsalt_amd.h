@@ -270,7 +270,7 @@ int    dsalt_export_probs(const dsalt_probs_args* a, dsalt_stream_t stream);
  * predicted tokens), plus the token scaling of its driver (:420-446): every output of a
  * row times the row's probability of its target.  n_non_ignore / sum_non_ignore_weight /
  * weight_sum are the batch totals the "mean" reduction divides by.  Targets must be
- * ignore_index or in [0, n_cols); n_cols a multiple of 8; rows 16-byte aligned.  The
+ * ignore_index or in [0, n_cols); any n_cols >= 1; rows 16-byte aligned.  The
  * GEMMs around it (logits, grad_input, grad_weight) are the caller's. */
 typedef struct dsalt_ce_args {
     int32_t rows;
@@ -302,7 +302,7 @@ int    dsalt_cross_entropy_rows(const dsalt_ce_args* a, dsalt_stream_t stream);
  * F.silu(gate_proj(x)) * up_proj(x) of SwiGLUFFN.forward,
  * dsalt/modules/dsalt_transformer.py:20-21 (silu in float32 as g / (1 + exp(-g))
  * rounded to the tensor type, the product rounded to the tensor type).  rows x cols
- * with cols a multiple of 8; every row 16-byte aligned.  Needs no workspace. */
+ * of any width; every row 16-byte aligned.  Needs no workspace. */
 typedef struct dsalt_silu_mul_args {
     int32_t rows;
     int32_t cols;

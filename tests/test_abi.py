@@ -266,8 +266,8 @@ def test_rope_validation(field, value):
     assert lib.dsalt_last_error()
 
 
-@pytest.mark.parametrize("field,value", [("cols", 12), ("dtype", 3), ("up", None), ("out", (1 << 20) + 2),
-                                         ("gate_stride", 8), ("out_stride", 36)])
+@pytest.mark.parametrize("field,value", [("cols", -1), ("cols", 40), ("dtype", 3), ("up", None),
+                                         ("out", (1 << 20) + 2), ("gate_stride", 8), ("out_stride", 36)])
 def test_silu_mul_validation(field, value):
     lib = _lib.load()
     a = _lib.SiluMulArgs(64, 32, 1, 1 << 20, 64, (1 << 20) + 64, 64, 1 << 21, 32)
@@ -290,9 +290,9 @@ def test_export_probs_validation(field, value):
     assert lib.dsalt_export_probs(ctypes.byref(a), None) == 1
 
 
-@pytest.mark.parametrize("field,value", [("n_cols", 100), ("dtype", 4), ("reduction", 3), ("logits", (1 << 20) + 8),
-                                         ("logits_stride", 64), ("target", None), ("label_smoothing", 1.5),
-                                         ("softcap", -1.0)])
+@pytest.mark.parametrize("field,value", [("n_cols", 0), ("n_cols", 130), ("dtype", 4), ("reduction", 3),
+                                         ("logits", (1 << 20) + 8), ("logits_stride", 64), ("logits_stride", 100),
+                                         ("target", None), ("label_smoothing", 1.5), ("softcap", -1.0)])
 def test_cross_entropy_validation(field, value):
     lib = _lib.load()
     a = _lib.CeArgs()

@@ -150,6 +150,58 @@ def test_silu_mul_on_fused_gate_up_matches_torch(dt):
     assert torch.equal(out, ref), float((out.float() - ref.float()).abs().max())
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("F_", [1, 7, 100, 11001])
+def test_silu_mul_any_width(dt, F_):
+    # widths off the 8-column vectors: rows on 16-byte boundaries run the kernel's tail; the
+    # halves of an odd-width fused buffer and odd-width contiguous rows run on padded copies
+    g = torch.Generator().manual_seed(F_)
+    T = 129
+    gu = (torch.randn(T, 2 * F_, generator=g) * 4).to(dt).to(DEV)
+    vec = 16 // gu.element_size()
+    pad = -(-F_ // vec) * vec
+    aligned = [torch.zeros(T, pad, dtype=dt, device=DEV)[:, :F_] for _ in range(3)]
+    aligned[0].copy_(gu[:, :F_])
+    aligned[1].copy_(gu[:, F_:])
+    cases = ((gu[:, :F_], gu[:, F_:], None), (gu[:, :F_].contiguous(), gu[:, F_:].contiguous(), None),
+             (aligned[0], aligned[1], aligned[2]))
+    for gate, up, out in cases:
+        res = ops.silu_mul(gate, up, out)
+        ref = torch.nn.functional.silu(gate.contiguous()) * up.contiguous()
+        torch.cuda.synchronize()
+        assert torch.equal(res, ref), float((res.float() - ref.float()).abs().max())
+
+
+@pytest.mark.parametrize("V,aligned", [(2, False), (17, True), (1001, False), (50257, True), (50257, False)])
+def test_row_kernel_any_vocabulary(V, aligned):
+    # vocabularies off the 8-column vectors: aligned rows (row stride rounded up) run the
+    # kernel's tail, contiguous odd rows a padded copy with the gradient copied back
+    from oracle import cross_entropy as OCE
+    g = torch.Generator().manual_seed(V)
+    N = 70
+    x = torch.randn(N, V, generator=g) * 3
+    t = torch.randint(0, V, (N,), generator=g)
+    t[::7] = -100
+    t[1] = V - 1  # a target in the tail
+    cw = torch.rand(V, generator=g) + 0.2
+    for w_, opts in ((None, dict(label_smoothing=0.1, lse_square_scale=1e-3)), (cw, dict(label_smoothing=0.05)),
+                     (None, dict(softcap=15.0))):
+        if aligned:
+            logits = torch.zeros(N, -(-V // 4) * 4, device=DEV)[:, :V]
+            logits.copy_(x)
+        else:
+            logits = x.to(DEV)
+        loss, z, acc, pred = ops.cross_entropy_rows(logits, t.to(DEV), ce_weight=None if w_ is None else w_.to(DEV),
+                                                    want_z=True, want_accuracy=True, want_predicted=True, **opts)
+        torch.cuda.synchronize()
+        rl, rz, rg, am, _ = OCE.ce_rows(x.double().numpy(), t.numpy(), None if w_ is None else w_.double().numpy(),
+                                        -100, opts.get("lse_square_scale", 0.0), opts.get("label_smoothing", 0.0),
+                                        "mean", opts.get("softcap"), False)
+        assert rel_err(f64(loss), rl) < 1e-5 and rel_err(f64(logits), rg) < 1e-5, (V, aligned, opts)
+        keep = (t != -100).numpy()
+        assert np.array_equal(pred.cpu().numpy()[keep], am[keep])
+
+
 # ------------------------------------------------------------------ fused linear cross-entropy
 @pytest.mark.parametrize("opts", [dict(), dict(label_smoothing=0.1, lse_square_scale=1e-3), dict(softcap=20.0),
                                   dict(ce_weight=True, label_smoothing=0.05, reduction="sum"),
@@ -195,11 +247,12 @@ def test_row_kernel_token_scaling_matches_oracle():
     assert rel_err(f64(loss), rl) < 1e-5 and rel_err(f64(logits), rg) < 1e-5
 
 
-@pytest.mark.parametrize("dt,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
-def test_fused_linear_cross_entropy_matches_autograd(dt, tol):
+@pytest.mark.parametrize("dt,tol,V", [(torch.float32, 1e-5, 5000), (torch.bfloat16, 2e-2, 5000),
+                                      (torch.float32, 1e-5, 5003)])
+def test_fused_linear_cross_entropy_matches_autograd(dt, tol, V):
     from dsalt_amd.kernels.cross_entropy import LigerFusedLinearCrossEntropyFunction
     g = torch.Generator().manual_seed(92)
-    BT, H, V = 700, 256, 5000
+    BT, H = 700, 256
     x = (torch.randn(BT, H, generator=g)).to(dt).to(DEV).requires_grad_(True)
     w = (torch.randn(V, H, generator=g) * 0.05).to(dt).to(DEV).requires_grad_(True)
     b = (torch.randn(V, generator=g) * 0.1).to(dt).to(DEV).requires_grad_(True)
