@@ -1,8 +1,9 @@
 """Edge cases of the operator on the GPU against the oracle: empty and one-token sequences in a
 packed batch (also with block-causal blocks that are not multiples of 64 rows), no landmarks,
 the largest landmark sets (512 slots and the wide kernels' 2048), every landmark slot empty,
-the GQA ratio of the 3B decoder, and windows covering whole sequences.  Indices bit-exact; outputs and
-gradients relative max|a-b| / max|b| within 1e-5 (fp32) or 2e-2 (bf16)."""
+the GQA ratio of the 3B decoder, windows covering whole sequences, and rows more than 2 GiB past
+the tensors' base.  Indices bit-exact; outputs and gradients relative max|a-b| / max|b| within 1e-5
+(fp32) or 2e-2 (bf16)."""
 from __future__ import annotations
 
 import math
@@ -131,3 +132,50 @@ def test_all_landmark_slots_empty():
     rdq, _, _, _ = OA.attention_bwd(f64(x["q"]), f64(x["k"]), f64(x["v"]), x["w"].numpy(), x["cu"].numpy(),
                                     idx.cpu().numpy(), 1 / 8.0, f64(x["do"]))
     assert rel_err(f64(dq), rdq) < 1e-5
+
+
+def test_rows_past_2gib_offsets():
+    """A packed batch whose second sequence starts 600000 tokens in (its q, k, v rows 2.3 GiB
+    past the tensors' base) against the same sequence alone: indices, outputs, LSE and dQ
+    bit-identical, dK / dV bit-identical on every row that is no landmark; landmark rows sum
+    their fp32 row-chunk partials over as many chunks as the longest sequence needs, so
+    they may differ in the last bits (within 2e-3).  The block-causal forward likewise."""
+    H, D, dt, L1, L2, K = 16, 128, torch.bfloat16, 600_000, 2048, 64
+    g = torch.Generator(device=DEV).manual_seed(5)
+    T = L1 + L2
+
+    def rnd(*s):
+        return torch.randn(*s, generator=g, device=DEV).to(dt)
+
+    q, k, v, do, h = rnd(T, H, D), rnd(T, H, D), rnd(T, H, D), rnd(T, H, D), rnd(T, 256)
+    w = torch.randint(1, 257, (T,), generator=g, device=DEV, dtype=torch.int32)
+    alpha = torch.rand(H, generator=g, device=DEV)
+    cu = torch.tensor([0, L1, T], dtype=torch.int32, device=DEV)
+    cu2 = torch.tensor([0, L2], dtype=torch.int32, device=DEV)
+    assert L1 * H * D * q.element_size() > 2 ** 31
+
+    def run(sl, cu_, maxlen, mode):
+        idx = ops.select_landmarks(h[sl], v[sl], alpha, w[sl], cu_, K, max_seqlen=maxlen, select_mode=mode,
+                                   block_size=512, stats_scope=ops.STATS_SEQUENCE)
+        out, lse = ops.attention_forward(q[sl], k[sl], v[sl], w[sl], cu_, idx, None, max_seqlen=maxlen,
+                                         select_mode=mode, block_size=512)
+        if mode == ops.SELECT_BLOCK:
+            return idx, out, lse
+        return (idx, out, lse) + ops.attention_backward(do[sl], q[sl], k[sl], v[sl], out, lse, w[sl], cu_, idx,
+                                                        max_seqlen=maxlen, want_dbias=False)[:3]
+
+    for mode in (ops.SELECT_GLOBAL, ops.SELECT_BLOCK):
+        a = run(slice(0, T), cu, L1, mode)
+        b = run(slice(L1, T), cu2, L2, mode)
+        torch.cuda.synchronize()
+        assert torch.equal(a[0][:, 1, :b[0].shape[2]], b[0][:, 0]), "indices"
+        for name, x, y in zip(("out", "lse", "dq"), a[1:4], b[1:4]):
+            assert torch.equal(x[L1:], y), name
+        if mode == ops.SELECT_BLOCK:
+            continue
+        lm = torch.zeros(L2, dtype=torch.bool, device=DEV)
+        ix = b[0][:, 0].reshape(-1)
+        lm[ix[ix >= 0].long()] = True
+        for name, x, y in (("dk", a[4][L1:], b[4]), ("dv", a[5][L1:], b[5])):
+            assert torch.equal(x[~lm], y[~lm]), name
+            assert float((x[lm].float() - y[lm].float()).abs().max() / y.float().abs().max()) < 2e-3, name
