@@ -9,7 +9,8 @@ max|a-b| / max|b| within 1e-5 (fp32) or 2e-2 (16-bit); log-sum-exps within 1e-4 
 gradients of global sets through the landmark-row / other-row class and per-row bounds of the
 other gradient tests.  A second sweep draws configurations of the training operator (soft window
 edge, landmark log-weights, continuous windows up to past the sequence ends) and checks them
-as tests/test_gpu_train.py does.
+as tests/test_gpu_train.py does; a third draws selection-only configurations (indices, z and
+scores bit-exact), a fourth the autograd operator over head_dims 16-128.
 """
 from __future__ import annotations
 
@@ -143,3 +144,99 @@ def test_random_training_configuration(seed):
     print("case", {k: (str(v) if k == "dt" else v) for k, v in c.items()}, flush=True)
     TT._check(c["lens"], c["H"], c["D"], c["K"], c["wlo"], c["whi"], c["dt"], seed=60_000 + seed, tau=c["tau"],
               edge=c["edge"], integer_every=c["integer_every"], variant=c["variant"])
+
+
+def draw_select(seed: int) -> dict:
+    """Selection-only configuration of case `seed`: widths that are not whole 16-byte vectors,
+    duplicated rows (exact score ties), heavy-tailed norms, alpha at 0 and 1, both statistics
+    scopes, block sizes from 1 row."""
+    r = np.random.default_rng(110_000 + seed)
+    S = int(r.integers(1, 5))
+    lens = [0 if r.random() < 0.1 else 1 if r.random() < 0.1 else int(r.integers(2, 3000)) for _ in range(S)]
+    lens[0] = max(lens[0], 2)
+    G = int(r.choice([1, 2, 4, 8]))
+    return dict(lens=lens, G=G, H=G * int(r.choice([1, 2, 3])), D=int(r.choice([32, 64, 80, 128])),
+                hidden=int(r.choice([64, 96, 100, 256, 1000, 2048])),
+                dt=[torch.float32, torch.bfloat16, torch.float16][int(r.choice(3, p=[0.3, 0.5, 0.2]))],
+                mode=int(r.random() < 0.5), bs=int(r.choice([1, 17, 37, 64, 100, 128, 256, 512, 1024])),
+                K=int(r.choice([int(r.integers(1, 64)), int(r.integers(64, 600)), int(r.integers(600, 2049))],
+                               p=[0.45, 0.4, 0.15])),
+                wmax=int(r.integers(1, 1500)), scope=int(r.integers(0, 2)), ties=bool(r.random() < 0.3),
+                heavy=bool(r.random() < 0.3), alphas=r.random(8))
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_selection_configuration(seed):
+    """Landmark indices (and, for global sets, z and scores) bit-exact with the oracle."""
+    c = draw_select(seed)
+    print("case", {k: (str(v) if k in ("dt", "alphas") else v) for k, v in c.items()}, flush=True)
+    g = torch.Generator().manual_seed(111_000 + seed)
+    T, G, H = sum(c["lens"]), c["G"], c["H"]
+    h = torch.randn(T, c["hidden"], generator=g)
+    v = torch.randn(T, G, c["D"], generator=g)
+    if c["heavy"]:
+        h = h * torch.exp(0.5 * torch.randn(T, 1, generator=g))
+        v = v * torch.exp(torch.randn(T, G, 1, generator=g))
+    if c["ties"]:
+        src, dst = torch.randint(0, T, (T // 4,), generator=g), torch.randint(0, T, (T // 4,), generator=g)
+        h[dst], v[dst] = h[src], v[src]
+    h, v = h.to(c["dt"]), v.to(c["dt"])
+    alpha = torch.rand(H, generator=g)
+    for j in range(H):
+        u = c["alphas"][j % 8]
+        alpha[j] = 0.0 if u < 0.1 else 1.0 if u < 0.2 else alpha[j]
+    w = torch.randint(1, c["wmax"] + 1, (T,), generator=g, dtype=torch.int32)
+    cu = torch.tensor([0] + list(np.cumsum(c["lens"])), dtype=torch.int32)
+    mode, want = c["mode"], c["mode"] == 0
+    res = ops.select_landmarks(*(t.to(DEV) for t in (h, v, alpha, w, cu)), c["K"], max_seqlen=max(c["lens"]),
+                               select_mode=mode, block_size=c["bs"], stats_scope=c["scope"], want_scores=want)
+    ref = OS.select(bits(h), bits(v), alpha.numpy(), w.numpy(), cu.numpy(), c["K"], oracle_dtype(c["dt"]),
+                    mode=mode, block_size=c["bs"], stats_scope=c["scope"], want_scores=want)
+    for a, b in zip(res if want else (res,), ref if want else (ref,)):
+        np.testing.assert_array_equal(a.cpu().numpy(), b)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_autograd_operator_configuration(seed):
+    """The autograd operator (unsorted caller sets, landmark bias, head_dims 16-128 run
+    zero-padded to the compiled 64 / 128): output and the gradients of q, k, v and the bias
+    against the oracle."""
+    from dsalt_amd import kernels as KK
+    r = np.random.default_rng(70_000 + seed)
+    g = torch.Generator().manual_seed(71_000 + seed)
+    S = int(r.integers(1, 5))
+    lens = [0 if r.random() < 0.1 else 1 if r.random() < 0.1 else int(r.integers(2, 600)) for _ in range(S)]
+    lens[0] = max(lens[0], 16)
+    G = int(r.choice([1, 2, 4]))
+    H = G * int(r.choice([1, 2]))
+    D = int(r.choice([16, 32, 48, 64, 72, 80, 96, 100, 112, 128]))
+    dt = [torch.float32, torch.bfloat16, torch.float16][int(r.choice(3, p=[0.3, 0.5, 0.2]))]
+    K = int(r.integers(0, 80))
+    wmax = int(r.integers(1, 400))
+    print("case", dict(lens=lens, H=H, G=G, D=D, dt=str(dt), K=K, wmax=wmax), flush=True)
+    T = sum(lens)
+    q, k, v = (torch.randn(T, n, D, generator=g).to(dt) for n in (H, G, G))
+    w = torch.randint(1, wmax + 1, (T,), generator=g).float()
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    idx = torch.full((H, S, K), -1, dtype=torch.int64)
+    for hh in range(H):
+        for s, L in enumerate(lens):
+            c = torch.randperm(L, generator=g)[:max(K - int(r.integers(0, 3)), 0)]
+            idx[hh, s, :len(c)] = c
+    bias = torch.randn(idx.shape, generator=g) * 0.3
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    bd = bias.to(DEV).requires_grad_(True)
+    out = KK.dsalt_triton_attention(qd, kd, vd, idx.to(DEV), bd, w.to(DEV), cu.to(DEV))
+    do = torch.randn(out.shape, generator=g)
+    out.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    scale = 1.0 / math.sqrt(D)
+    idx4, b4 = idx.numpy()[:, :, None], bias.double().numpy()[:, :, None]
+    wi = w.clamp(min=1).long().numpy()
+    ro, _ = OA.attention_fwd(f64(q), f64(k), f64(v), wi, cu.numpy(), idx4, scale, lmk_bias=b4)
+    assert rel_err(f64(out), ro) < TOL[dt], "out"
+    rg = OA.attention_bwd(f64(q), f64(k), f64(v), wi, cu.numpy(), idx4, scale, f64(do.to(dt)), lmk_bias=b4,
+                          out=f64(out.to(dt)))
+    check_grads(("autograd", seed), (qd.grad, kd.grad, vd.grad), rg[:3], idx, cu, TOL[dt])
+    if K:
+        assert rel_err(f64(bd.grad), rg[3][:, :, 0]) < TOL[dt], "d_bias"
