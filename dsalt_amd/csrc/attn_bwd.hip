@@ -952,8 +952,11 @@ template <typename T, int D>
 constexpr int lmk_waves(int k_lmk) { return (sizeof(T) == 2 && D == 64 && k_lmk > 64) ? 8 : 4; }
 
 // LK: sets of more than kSetSlots landmarks (the set's positions in a larger LDS copy).
+// (16-bit head_dim 128 in four-wave blocks is held to three waves per SIMD: 166 VGPRs, no
+// spills, from 170 at two)
 template <typename T, int D, int NW, bool LK = false>
-__global__ __launch_bounds__(64 * NW, (NW == 8 && sizeof(T) == 2 && D == 64) ? 4 : 2) void bwd_lmk_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * NW, (NW == 8 && sizeof(T) == 2 && D == 64) ? 4
+                                      : (NW == 4 && sizeof(T) == 2 && D == 128) ? 3 : 2) void bwd_lmk_kernel(AttnParams p) {
     constexpr int NT = 64 * NW;
     constexpr int kLmkGroup = 16 * NW;
     constexpr int BQ = BwdShape<T, D>::BL;
