@@ -201,8 +201,13 @@ __device__ __forceinline__ void band_edge(const AttnParams& p, const RowGroup& R
 //
 // NW = 8: eight waves, one row group each, over two plan tiles (128 rows): every staged chunk
 // serves twice the rows (head_dim 128, where the chunks' staging is most of the time).
+// (the 16-bit head_dim-128 training forward is held to four waves per SIMD: 128 VGPRs, no
+// spills, from 132 at three)
 template <typename T, int D, int BN, int RG, bool TR, bool MS = false, int NW = 4>
-__global__ __launch_bounds__(64 * NW, (sizeof(T) == 2 && D == 64 && RG == 2 && BN == 32) ? 4 : 2) void fwd_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * NW, ((sizeof(T) == 2 && D == 64 && RG == 2 && BN == 32) ||
+                                       (sizeof(T) == 2 && D == 128 && RG == 1 && BN == 32 && NW == 4 && TR))
+                                          ? 4
+                                          : 2) void fwd_kernel(AttnParams p) {
     static_assert(!MS || (RG == 1 && !TR), "several sets per block: one row group, inference");
     static_assert(NW == 4 || (NW == 8 && RG == 1 && !MS), "eight waves: one row group each, one set per block");
     constexpr int NT = 64 * NW;
