@@ -171,6 +171,15 @@ def topk_violations(idx, scores, w, cu, k):
 # Rows below the floor (gradients that cancel to almost nothing, such as the first row's dq)
 # are held by the class bound only.
 ROW_FLOOR = 0.25
+# fp32 gradients: class bound FP32_TOL, row bound FP32_ROW_TOL.  dS = P (dP - delta) cancels in
+# rows that see few keys with |delta| far above |dq| / (scale |k|) (up to 25-fold at head_dim 128:
+# a query one token into its sequence, one of its two keys dominant), and such a row's dq then
+# carries that factor times the rounding of its fp32 dot products dP = dO . v (128 terms: 1.5e-5
+# absolute at the 99.99th percentile, in the kernels' order as in plain sequential order).  The
+# worst row over 368 random fp32 configurations of the sweep was 1.8e-5 off; a float32
+# computation on the CPU lands in the same range on other rows of the same cases.
+FP32_TOL = 1e-5
+FP32_ROW_TOL = 4e-5
 
 
 def landmark_rows(idx, cu, T: int) -> np.ndarray:
@@ -217,11 +226,13 @@ def grad_errors(a, b, lmk=None, floor: float = ROW_FLOOR) -> dict:
     return out
 
 
-def assert_grad_close(what, a, b, tol: float, lmk=None, floor: float = ROW_FLOOR) -> dict:
-    """Raises AssertionError (with every figure) unless both bounds above hold."""
+def assert_grad_close(what, a, b, tol: float, lmk=None, floor: float = ROW_FLOOR, row_tol: float | None = None) -> dict:
+    """Raises AssertionError (with every figure) unless both bounds above hold: the class bound
+    within tol, the row bound within row_tol (default tol)."""
     e = grad_errors(a, b, lmk, floor)
-    bad = {k: v for k, v in e.items() if (k.endswith("_class") or k.endswith("_row")) and not v < tol}
-    assert not bad, (what, tol, e)
+    rt = tol if row_tol is None else row_tol
+    bad = {k: v for k, v in e.items() if (k.endswith("_class") and not v < tol) or (k.endswith("_row") and not v < rt)}
+    assert not bad, (what, tol, rt, e)
     return e
 
 
@@ -230,7 +241,8 @@ def check_grads(what, got, ref, idx, cu, tol: float) -> None:
     landmark rows: the union of its query heads' sets) through ``assert_grad_close``.
     The reference's backward takes delta = rowsum(O dO) from the stored output
     (dsalt/kernels/dsalt_triton_bwd.py:17-49), so ``ref`` is the oracle fed the output the
-    kernels stored: rows whose dP - delta nearly cancels then compare like for like.
+    kernels stored: rows whose dP - delta nearly cancels then compare like for like.  With the
+    fp32 tolerance (tol <= FP32_TOL) the row bound is FP32_ROW_TOL.
 
     got: tensors or arrays (dq, dk, dv); ref: float64 arrays of the same shapes."""
     got = [f64(t) if isinstance(t, torch.Tensor) else np.asarray(t, np.float64) for t in got]
@@ -241,9 +253,10 @@ def check_grads(what, got, ref, idx, cu, tol: float) -> None:
     G = got[1].shape[1]
     rep = H // G
     lm = landmark_rows(idx, cu, T)
+    rt = FP32_ROW_TOL if tol <= FP32_TOL else tol
     for h in range(H):
-        assert_grad_close((what, "dq", h), got[0][:, h], ref[0][:, h], tol)
+        assert_grad_close((what, "dq", h), got[0][:, h], ref[0][:, h], tol, row_tol=rt)
     for g in range(G):
         lg = lm[:, g * rep:(g + 1) * rep].any(1)
         for name, a, b in (("dk", got[1], ref[1]), ("dv", got[2], ref[2])):
-            assert_grad_close((what, name, g), a[:, g], b[:, g], tol, lg)
+            assert_grad_close((what, name, g), a[:, g], b[:, g], tol, lg, row_tol=rt)

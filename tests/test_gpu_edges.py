@@ -1,5 +1,6 @@
 """Edge cases of the operator on the GPU against the oracle: empty and one-token sequences in a
-packed batch (also with block-causal blocks that are not multiples of 64 rows), no landmarks,
+packed batch (also with block-causal blocks that are not multiples of 64 rows), a batch of
+one-token sequences only (whose dq and dk vanish: bounded absolutely), no landmarks,
 the largest landmark sets (512 slots and the wide kernels' 2048), every landmark slot empty,
 the GQA ratio of the 3B decoder, windows covering whole sequences, and rows more than 2 GiB past
 the tensors' base.  Indices bit-exact; outputs and gradients relative max|a-b| / max|b| within 1e-5
@@ -70,6 +71,36 @@ def _run(x, K, mode=ops.SELECT_GLOBAL, block=64, backward=True):
 def test_empty_and_single_token_sequences(dt):
     _run(_case([100, 0, 1, 0, 130], 2, 2, 64, 8, 40, dt, seed=200), 8)
 
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_only_one_token_sequences(dt):
+    """A batch of one-token and empty sequences only: each query sees its own key alone (P = 1,
+    no landmark candidates), so out = v, dv = dO summed over the group's query heads, and dq = dk
+    = 0 exactly.  The kernels' dq and dk hold the rounding of dP - delta only: bounded absolutely
+    by tol x scale x max|dO . v| x max|k| (a relative bound against the oracle's zeros means
+    nothing)."""
+    x = _case([1, 1, 0, 1], 4, 2, 64, 8, 30, dt, seed=211)
+    d = {k: v.to(DEV) for k, v in x.items()}
+    idx = ops.select_landmarks(d["h"], d["v"], d["alpha"], d["w"], d["cu"], 8, max_seqlen=1,
+                               stats_scope=ops.STATS_SEQUENCE)
+    assert torch.all(idx == -1)
+    scale = 1.0 / 8.0
+    out, lse = ops.attention_forward(d["q"], d["k"], d["v"], d["w"], d["cu"], idx, None, scale=scale, max_seqlen=1)
+    ro, rl = OA.attention_fwd(f64(x["q"]), f64(x["k"]), f64(x["v"]), x["w"].numpy(), x["cu"].numpy(),
+                              idx.cpu().numpy(), scale)
+    rep = 2
+    assert np.array_equal(ro, np.repeat(f64(x["v"]), rep, axis=1))
+    assert rel_err(f64(out), ro) < TOL[dt]
+    assert np.abs(f64(lse) - rl).max() < TOL[dt] * np.abs(rl).max()
+    dq, dk, dv, _ = ops.attention_backward(d["do"], d["q"], d["k"], d["v"], out, lse, d["w"], d["cu"], idx,
+                                           scale=scale, max_seqlen=1, want_dbias=False)
+    do, v, k = f64(x["do"]), f64(x["v"]), f64(x["k"])
+    rdv = do.reshape(do.shape[0], 2, rep, -1).sum(2)
+    assert rel_err(f64(dv), rdv) < TOL[dt]
+    dp = np.abs(np.einsum("thd,thd->th", do, np.repeat(v, rep, axis=1))).max()
+    bound = TOL[dt] * scale * dp * np.abs(k).max()
+    assert np.abs(f64(dq)).max() <= bound and np.abs(f64(dk)).max() <= bound, (np.abs(f64(dq)).max(), bound)
 
 def test_empty_sequences_block_causal():
     _run(_case([0, 300, 0, 1, 70], 2, 2, 64, 8, 40, torch.bfloat16, seed=201), 8, mode=ops.SELECT_BLOCK,

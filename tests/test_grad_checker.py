@@ -12,6 +12,8 @@ gradients of one head of the benchmark workloads at their full length:
   * planted mistakes must fail: every non-landmark dK row 5 % too large, every dQ row 5 % too
     large, every landmark dV row 5 % too large, one ordinary dK row of median norm 50 % too
     large (which the single all-rows bound accepts).
+The fp32 bounds (class 1e-5, row FP32_ROW_TOL) likewise: gradients computed in float32 pass,
+one ordinary dq row 1e-4 off fails.
 """
 from __future__ import annotations
 
@@ -24,7 +26,8 @@ import torch
 from dsalt_amd import ops
 from dsalt_amd.workloads import WORKLOADS, generate
 from oracle import attention as OA
-from tests.helpers import assert_grad_close, f64, landmark_rows, oracle_select_by_group, rel_err
+from tests.helpers import (FP32_ROW_TOL, FP32_TOL, assert_grad_close, f64, landmark_rows, oracle_select_by_group,
+                           rel_err)
 
 TOL = 2e-2
 
@@ -100,3 +103,44 @@ def test_one_ordinary_row_wrong_fails_where_the_single_bound_passes(grads):
     if name == "fwdbwd_bf16_h16_l32768":
         # the single bound over all rows does not see it at the headline shape
         assert rel_err(dk, b) < TOL
+
+
+# ------------------------------------------------------------------ fp32 bounds
+@pytest.fixture(scope="module")
+def fp32_case():
+    """Three ragged sequences, one head of head_dim 128, windows up to 441, three landmarks per
+    sequence: float64 gradients and gradients computed in float32 (dense masked softmax in torch,
+    delta from the float32 output, as the GPU tests feed the oracle the stored output)."""
+    g = torch.Generator().manual_seed(935)
+    lens = [279, 589, 151]
+    T, D = sum(lens), 128
+    q, k, v, do = (torch.randn(T, 1, D, generator=g) for _ in range(4))
+    w = torch.randint(1, 442, (T,), generator=g, dtype=torch.int32).numpy()
+    cu = np.array([0] + list(np.cumsum(lens)))
+    idx = np.stack([np.sort(torch.randperm(n, generator=g)[:3].numpy()) for n in lens])[None, :, None, :]
+    mask = torch.from_numpy(OA.dense_mask_kernel(w, cu, idx))[0]
+    scale = 1.0 / math.sqrt(D)
+    q2, k2, v2, do2 = q[:, 0], k[:, 0], v[:, 0], do[:, 0]
+    p = torch.softmax(torch.where(mask, q2 @ k2.T * scale, torch.tensor(-math.inf)), dim=1)
+    out = p @ v2
+    ds = p * (do2 @ v2.T - (out * do2).sum(1, keepdim=True))
+    f32 = [(ds @ k2 * scale).double().numpy(), (ds.T @ q2 * scale).double().numpy(), (p.T @ do2).double().numpy()]
+    exact = OA.attention_bwd(f64(q), f64(k), f64(v), w, cu, idx, scale, f64(do), out=f64(out)[:, None])[:3]
+    lmk = landmark_rows(idx, cu, T)[:, 0]
+    return f32, [e[:, 0] for e in exact], lmk
+
+
+def test_fp32_arithmetic_passes_the_fp32_bounds(fp32_case):
+    f32, exact, lmk = fp32_case
+    for name, a, b in zip(("dq", "dk", "dv"), f32, exact):
+        assert_grad_close(name, a, b, FP32_TOL, lmk if name != "dq" else None, row_tol=FP32_ROW_TOL)
+
+
+def test_fp32_one_ordinary_row_wrong_fails(fp32_case):
+    f32, exact, lmk = fp32_case
+    rn = np.linalg.norm(exact[0], axis=1)
+    j = np.argsort(rn)[len(rn) // 2]  # a row of median norm, 1e-4 off
+    dq = f32[0].copy()
+    dq[j] *= 1 + 1e-4
+    with pytest.raises(AssertionError):
+        assert_grad_close("dq", dq, exact[0], FP32_TOL, row_tol=FP32_ROW_TOL)
