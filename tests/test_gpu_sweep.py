@@ -10,7 +10,9 @@ gradients of global sets through the landmark-row / other-row class and per-row 
 other gradient tests.  A second sweep draws configurations of the training operator (soft window
 edge, landmark log-weights, continuous windows up to past the sequence ends) and checks them
 as tests/test_gpu_train.py does; a third draws selection-only configurations (indices, z and
-scores bit-exact), a fourth the autograd operator over head_dims 16-128.
+scores bit-exact), a fourth the autograd operator over head_dims 16-128, and two more the
+probability export (against the oracle's dense matrix), plan reuse (bit for bit) and the landmark
+gather (exact), over given landmark sets of any block size.
 """
 from __future__ import annotations
 
@@ -240,3 +242,109 @@ def test_random_autograd_operator_configuration(seed):
     check_grads(("autograd", seed), (qd.grad, kd.grad, vd.grad), rg[:3], idx, cu, TOL[dt])
     if K:
         assert rel_err(f64(bd.grad), rg[3][:, :, 0]) < TOL[dt], "d_bias"
+
+
+def random_sets(g: torch.Generator, H: int, lens: list, mode: int, bs: int, K: int) -> torch.Tensor:
+    """[H, S, n_sets, K] int32 landmark sets: each set up to K distinct positions of its sequence
+    (block-causal: below the set's first row), ascending, some sets a slot or two short, -1 padded."""
+    ns = ops.n_sets(mode, max(max(lens), 1), bs)
+    idx = torch.full((H, len(lens), ns, K), -1, dtype=torch.int32)
+    for h in range(H):
+        for s, L in enumerate(lens):
+            for b in range(ns):
+                hi = L if mode == ops.SELECT_GLOBAL else min(L, b * bs)
+                n = min(max(K - int(torch.randint(0, 3, (1,), generator=g)), 0), hi)
+                if n > 0:
+                    idx[h, s, b, :n] = torch.randperm(hi, generator=g)[:n].sort().values.to(torch.int32)
+    return idx
+
+
+def draw_api(seed: int) -> dict:
+    """Configuration of the operator's other entry points (probability export, plan reuse,
+    landmark gather, the allocation-free forward): global or block-causal sets of any block
+    size, 0 to 300 landmarks, any tiling variant bits, given landmark sets and biases."""
+    r = np.random.default_rng(90_000 + seed)
+    S = int(r.integers(1, 5))
+    lens = [0 if r.random() < 0.1 else 1 if r.random() < 0.1 else int(r.integers(2, 700)) for _ in range(S)]
+    lens[0] = max(lens[0], 16)
+    G = int(r.choice([1, 2, 4]))
+    mode = seed % 2  # global and block-causal sets alternate
+    bs = int(r.choice([17, 64, 100, 128, 256, 512])) if mode else 512
+    K = int(r.integers(0, 300))
+    if mode and bs % 64:
+        K = min(K, SET_SLOTS // (63 // bs + 2))
+    return dict(lens=lens, G=G, H=G * int(r.choice([1, 2, 4])), D=int(r.choice([64, 128])),
+                dt=[torch.float32, torch.bfloat16, torch.float16][int(r.integers(0, 3))], mode=mode, bs=bs, K=K,
+                wmax=int(r.integers(1, 600)), variant=int(r.integers(0, 64)), seed=seed)
+
+
+def api_inputs(c: dict) -> dict:
+    g = torch.Generator().manual_seed(91_000 + c["seed"])
+    T, H, G, D, dt = sum(c["lens"]), c["H"], c["G"], c["D"], c["dt"]
+    x = {"q": torch.randn(T, H, D, generator=g).to(dt), "k": torch.randn(T, G, D, generator=g).to(dt),
+         "v": torch.randn(T, G, D, generator=g).to(dt), "do": torch.randn(T, H, D, generator=g).to(dt),
+         "w": torch.randint(1, c["wmax"] + 1, (T,), generator=g, dtype=torch.int32),
+         "cu": torch.tensor([0] + list(np.cumsum(c["lens"])), dtype=torch.int32)}
+    x["idx"] = random_sets(g, H, c["lens"], c["mode"], c["bs"], c["K"])
+    x["bias"] = torch.randn(x["idx"].shape, generator=g) * 0.5
+    return x
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_probability_export_configuration(seed):
+    """The exported probabilities of every sequence, densified, against the oracle's dense
+    attention matrix (relative max|a-b| / max|b|, 1e-5 fp32 / 2e-2 16-bit)."""
+    from dsalt_amd.kernels.attention_probs import SparseAttentionProbs
+    c = draw_api(seed)
+    print("case", {k: (str(v) if k == "dt" else v) for k, v in c.items()}, flush=True)
+    x = api_inputs(c)
+    mode, bs, maxlen = c["mode"], c["bs"], max(c["lens"])
+    scale = 1.0 / math.sqrt(c["D"])
+    d = {k: v.to(DEV) for k, v in x.items()}
+    _, lse = ops.attention_forward(d["q"], d["k"], d["v"], d["w"], d["cu"], d["idx"], d["bias"], scale=scale,
+                                   max_seqlen=maxlen, select_mode=mode, block_size=bs, variant=c["variant"])
+    for s, L in enumerate(c["lens"]):
+        if L == 0:
+            continue
+        p_win, p_lmk = ops.export_probs(d["q"], d["k"], d["w"], d["cu"], d["idx"], lse, d["bias"], seq=s, scale=scale,
+                                        max_seqlen=maxlen, select_mode=mode, block_size=bs)
+        sp = SparseAttentionProbs(p_win, p_lmk, d["idx"][:, s].long() if c["K"] else None, bs if mode else 0)
+        ref = OA.attention_probs(f64(x["q"]), f64(x["k"]), x["w"].numpy(), x["cu"].numpy(), x["idx"].numpy(), scale,
+                                 seq=s, lmk_bias=x["bias"].double().numpy(), block_size=bs if mode else None)
+        assert rel_err(f64(sp.to_dense()), ref) < TOL[c["dt"]], ("sequence", s)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_plan_and_gather_configuration(seed):
+    """A row plan made once and passed in gives the forward (and, for global sets, the backward)
+    bit for bit; gathered landmark rows equal the rows at the sets' positions (zero for -1)."""
+    c = draw_api(seed)
+    print("case", {k: (str(v) if k == "dt" else v) for k, v in c.items()}, flush=True)
+    x = api_inputs(c)
+    mode, bs, maxlen, var = c["mode"], c["bs"], max(c["lens"]), c["variant"]
+    d = {k: v.to(DEV) for k, v in x.items()}
+    fa = (d["q"], d["k"], d["v"], d["w"], d["cu"], d["idx"], None)
+    out, lse = ops.attention_forward(*fa, max_seqlen=maxlen, select_mode=mode, block_size=bs, variant=var)
+    plan = ops.new_plan(d["q"], d["k"], d["cu"], d["idx"], max_seqlen=maxlen, select_mode=mode, block_size=bs)
+    o2, l2 = ops.attention_forward(*fa, max_seqlen=maxlen, select_mode=mode, block_size=bs, plan=plan, variant=var)
+    assert torch.equal(o2, out) and torch.equal(l2, lse)
+    if mode == ops.SELECT_GLOBAL:
+        ba = (d["do"], d["q"], d["k"], d["v"], out, lse, d["w"], d["cu"], d["idx"])
+        a = ops.attention_backward(*ba, max_seqlen=maxlen, want_dbias=False, variant=var)
+        b = ops.attention_backward(*ba, max_seqlen=maxlen, want_dbias=False, plan=plan, variant=var)
+        for u, w_ in zip(a[:3], b[:3]):
+            assert torch.equal(u, w_)
+    lk, lv = ops.gather_landmarks(d["k"], d["v"], d["cu"], d["idx"], max_seqlen=maxlen, select_mode=mode,
+                                  block_size=bs, n_heads=c["H"])
+    rep = c["H"] // c["G"]
+    cu = x["cu"].numpy()
+    for name, got, src in (("k", lk, x["k"]), ("v", lv, x["v"])):
+        got = got.cpu()
+        for h in range(c["H"]):
+            for s, L in enumerate(c["lens"]):
+                pos = x["idx"][h, s].long()
+                ok = (pos >= 0) & (pos < L)
+                rows = src[int(cu[s]) + pos.clamp(0, max(L - 1, 0)), h // rep] if L else torch.zeros(
+                    pos.shape + (c["D"],), dtype=src.dtype)
+                ref = torch.where(ok[..., None], rows, torch.zeros((), dtype=src.dtype))
+                assert torch.equal(got[h, s], ref), (name, h, s)

@@ -1,7 +1,8 @@
 """dsalt_fwd_noalloc: the forward with its row plan in the library's static device scratch
 (no allocation, no workspace), called through the C ABI.  Its outputs must equal
 dsalt_fwd's bit for bit (the same kernels), on two calls in a row, the second with a
-smaller input; sizes beyond the scratch are rejected before anything runs."""
+smaller input, and on random configurations (block-causal sets, biases, tiling variants); sizes
+beyond the scratch are rejected before anything runs."""
 from __future__ import annotations
 
 import ctypes
@@ -50,3 +51,26 @@ def test_noalloc_rejects_plans_beyond_the_scratch():
     assert L.dsalt_plan_bytes(ctypes.byref(a.p)) > _lib.FWD_NOALLOC_MAX_PLAN_BYTES
     assert L.dsalt_fwd_noalloc(ctypes.byref(a), None) == 3
     assert b"scratch" in L.dsalt_last_error()
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_noalloc_random_configurations(seed):
+    """Random configurations of the other entry points' sweep (global or block-causal sets of
+    any block size, landmark biases, any tiling variant bits): the allocation-free forward equals
+    dsalt_fwd bit for bit."""
+    from tests.test_gpu_sweep import api_inputs, draw_api
+    c = draw_api(seed)
+    print("case", {k: (str(v) if k == "dt" else v) for k, v in c.items()}, flush=True)
+    x = api_inputs(c)
+    mode, bs, maxlen = c["mode"], c["bs"], max(c["lens"])
+    d = [x[n].to(DEV) for n in ("q", "k", "v", "w", "cu", "idx", "bias")]
+    ref_out, ref_lse = ops.attention_forward(*d, max_seqlen=maxlen, select_mode=mode, block_size=bs,
+                                             variant=c["variant"])
+    L = _lib.load()
+    a, out, lse, keep = ops._fwd_args(*d, None, maxlen, mode, bs)
+    a.variant = c["variant"]
+    assert L.dsalt_plan_bytes(ctypes.byref(a.p)) <= _lib.FWD_NOALLOC_MAX_PLAN_BYTES
+    a.workspace, a.workspace_bytes = None, 0
+    _lib.check("dsalt_fwd_noalloc", L.dsalt_fwd_noalloc(ctypes.byref(a), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_out) and torch.equal(lse, ref_lse)
