@@ -61,6 +61,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="fwdbwd_bf16_h16_l32768")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seqlen", type=int, default=0, metavar="L",
+                    help="run the operator workload with sequences of L tokens instead of its own length "
+                         "(the line then carries no traffic record, which is measured at the workload's length)")
     ap.add_argument("--variant", default="auto",
                     help="tile variant bits (DSALT_VARIANT_*) of the attention kernels, or 'auto': the autotune's "
                          "winner for the workload's shape (timed before the warmup, outside the timed region)")
@@ -437,6 +440,9 @@ def main():
     from dsalt_amd import _lib, ops
     from dsalt_amd.workloads import MODEL_WORKLOADS, WORKLOADS, generate
 
+    if args.seqlen and (args.workload in MODEL_WORKLOADS or args.workload not in WORKLOADS):
+        print(f"--seqlen applies to the operator workloads only (not {args.workload})", file=sys.stderr)
+        sys.exit(2)
     if args.workload in MODEL_WORKLOADS:
         return model_bench(args, MODEL_WORKLOADS[args.workload])
     if args.workload == "ce_qwen3b_l32768":
@@ -444,6 +450,10 @@ def main():
     if args.workload.startswith("probs_"):
         return probs_bench(args, WORKLOADS[args.workload[len("probs_"):]])
     wl = WORKLOADS[args.workload]
+    own_len = wl.seqlen
+    if args.seqlen and args.seqlen != wl.seqlen:
+        import dataclasses
+        wl = dataclasses.replace(wl, seqlen=args.seqlen)
     lib = _lib.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -580,7 +590,7 @@ def main():
             with open(tpath) as f:
                 rec = json.load(f)
             # only a record measured on the current kernel sources counts
-            if rec.get("_sources") == kernel_source_sha():
+            if rec.get("_sources") == kernel_source_sha() and wl.seqlen == own_len:
                 traffic = (rec.get(dom) or {}).get("bytes")
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -612,7 +622,7 @@ def main():
                           f"host cpu_count {r['cpu_count']})")}
 
     line = {
-        "metric": METRIC,
+        "metric": METRIC if wl.seqlen == 32768 else METRIC.replace("@L=32K", f"@L={wl.seqlen}"),
         "value": round(T * args.steps / elapsed, 1),
         "unit": "tokens/s",
         "n_gpus": 1,

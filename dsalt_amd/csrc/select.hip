@@ -11,7 +11,10 @@
 //               rounds them to fp32 and then to the input dtype.
 //   sel_sums    one 256-thread block per (range, signal): fp64 S1, S2 by 256
 //               strided partials and a halving tree; in the global variant the
-//               same block turns them into mean / unbiased std.
+//               same block turns them into mean / unbiased std (global sets of up
+//               to 32768 tokens without z or scores for the caller: each top-k
+//               part computes them itself, in the same order, and sel_sums is
+//               not launched).
 //   sel_stats   (block-causal) mean / std per prefix by adding whole-block sums
 //               in block order.
 //   sel_z       (global) z = fp32((a - mean)/std) in fp64, one thread per
@@ -787,6 +790,16 @@ __device__ __forceinline__ KeyFn global_key_of(const SelectParams& p, const floa
     return key;
 }
 
+// Each global top-k part reads its whole range's norms to compute the statistics itself, which
+// saves the sel_sums launch but costs parts x length reads, growing with the square of the
+// length: past kPartStatsMaxLen tokens per sequence sel_sums computes them once per range, in the
+// same order (selection of H16, 32768 tokens: 50.4 us in the parts, 51.6 through sel_sums;
+// 65536 tokens: 89.3 against 84.0 us).
+constexpr int kPartStatsMaxLen = 32768;
+inline bool parts_own_stats(const SelectParams& p) {
+    return !p.z_x && !p.z_v && !p.scores && p.max_seqlen <= kPartStatsMaxLen;
+}
+
 __device__ __forceinline__ int global_range(const SelectParams& p, int s) {
     return p.stats_scope == DSALT_STATS_PACKED ? 0 : s;
 }
@@ -1354,8 +1367,8 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
         else
             DSALT_LAUNCH("sel_norms", sel_norms_kernel<float>, grid, dim3(256), shm, stream, p, nx, nv, nullptr, blocks);
         // the global top-k parts compute the statistics they need themselves (the same order)
-        // unless z or scores are written for the caller
-        const bool global_parts_only = global && !p.z_x && !p.z_v && !p.scores;
+        // unless z or scores are written for the caller, or the sequences are long
+        const bool global_parts_only = global && parts_own_stats(p);
         if (!global_parts_only)
             DSALT_LAUNCH("sel_sums", sel_sums_kernel, dim3(nranges, nsig), dim3(256), 0, stream, p, nx, nv, sums,
                          global ? stats : nullptr);
@@ -1411,7 +1424,7 @@ hipError_t select_launch(const SelectParams& p, void* ws, hipStream_t stream, in
     const size_t kb = align256(sizeof(unsigned long long) * (size_t)nsets_total * t.nparts * t.kpad);
     unsigned long long* ka = (unsigned long long*)w;
     unsigned long long* kb2 = (unsigned long long*)(w + kb);
-    const bool stats_written = p.z_x || p.z_v || p.scores;
+    const bool stats_written = !parts_own_stats(p);
     DSALT_LAUNCH("sel_part", sel_part_kernel, dim3(nsets_total * t.nparts), dim3(kSortThreads), 0, stream, p, nx, nv,
                  stats_written ? stats : nullptr, t.psize, t.nparts, t.kpad, ka);
     // keys per merge block <= kMergeMax

@@ -1,5 +1,6 @@
-"""The benchmark's own contract on the CPU: one GPU only, kernel labels of profiler names, and
-the HBM-traffic record built from counter runs (scaled by a plain copy of known size)."""
+"""The benchmark's own contract on the CPU: one GPU only, a sequence-length override for the
+operator workloads only, kernel labels of profiler names, and the HBM-traffic record built from
+counter runs (scaled by a plain copy of known size)."""
 from __future__ import annotations
 
 import csv
@@ -20,6 +21,13 @@ def test_refuses_more_than_one_gpu():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stdout + r.stderr
+
+
+def test_sequence_length_only_for_operator_workloads():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--workload", "ce_qwen3b_l32768",
+                        "--seqlen", "1024"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2
+    assert "operator workloads only" in r.stderr
 
 
 @pytest.mark.parametrize("name,label", [

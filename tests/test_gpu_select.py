@@ -52,6 +52,18 @@ def test_global_select_bit_exact(dt, scope):
     np.testing.assert_array_equal(sc.cpu().numpy(), rsc)
 
 
+@pytest.mark.parametrize("scope", [ops.STATS_PACKED, ops.STATS_SEQUENCE])
+@pytest.mark.parametrize("want", [False, True])
+def test_global_select_long_sequences(scope, want):
+    """Sequences longer than 32768 tokens take their statistics from one sel_sums pass instead
+    of every top-k part (with or without z and scores for the caller): indices, z and scores
+    bit-exact, next to a short sequence of the same batch."""
+    h, v, alpha, w, cu = _case([70001, 3000], 256, 2, 64, 4, torch.bfloat16, 300, seed=11)
+    res, ref = _run(h, v, alpha, w, cu, 128, ops.SELECT_GLOBAL, 512, scope, want=want)
+    for a, b in zip(res if want else (res,), ref if want else (ref,)):
+        np.testing.assert_array_equal(a.cpu().numpy(), b)
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("D", [64, 128])
 def test_block_select_bit_exact(dt, D):
