@@ -64,6 +64,9 @@ def parse():
     ap.add_argument("--seqlen", type=int, default=0, metavar="L",
                     help="run the operator workload with sequences of L tokens instead of its own length "
                          "(the line then carries no traffic record, which is measured at the workload's length)")
+    ap.add_argument("--batch", type=int, default=0, metavar="B",
+                    help="run the operator workload with B sequences instead of its own batch (no traffic record "
+                         "on the line either)")
     ap.add_argument("--variant", default="auto",
                     help="tile variant bits (DSALT_VARIANT_*) of the attention kernels, or 'auto': the autotune's "
                          "winner for the workload's shape (timed before the warmup, outside the timed region)")
@@ -440,8 +443,8 @@ def main():
     from dsalt_amd import _lib, ops
     from dsalt_amd.workloads import MODEL_WORKLOADS, WORKLOADS, generate
 
-    if args.seqlen and (args.workload in MODEL_WORKLOADS or args.workload not in WORKLOADS):
-        print(f"--seqlen applies to the operator workloads only (not {args.workload})", file=sys.stderr)
+    if (args.seqlen or args.batch) and (args.workload in MODEL_WORKLOADS or args.workload not in WORKLOADS):
+        print(f"--seqlen and --batch apply to the operator workloads only (not {args.workload})", file=sys.stderr)
         sys.exit(2)
     if args.workload in MODEL_WORKLOADS:
         return model_bench(args, MODEL_WORKLOADS[args.workload])
@@ -450,10 +453,10 @@ def main():
     if args.workload.startswith("probs_"):
         return probs_bench(args, WORKLOADS[args.workload[len("probs_"):]])
     wl = WORKLOADS[args.workload]
-    own_len = wl.seqlen
-    if args.seqlen and args.seqlen != wl.seqlen:
+    own_shape = (wl.batch, wl.seqlen)
+    if (args.seqlen and args.seqlen != wl.seqlen) or (args.batch and args.batch != wl.batch):
         import dataclasses
-        wl = dataclasses.replace(wl, seqlen=args.seqlen)
+        wl = dataclasses.replace(wl, seqlen=args.seqlen or wl.seqlen, batch=args.batch or wl.batch)
     lib = _lib.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -590,7 +593,7 @@ def main():
             with open(tpath) as f:
                 rec = json.load(f)
             # only a record measured on the current kernel sources counts
-            if rec.get("_sources") == kernel_source_sha() and wl.seqlen == own_len:
+            if rec.get("_sources") == kernel_source_sha() and (wl.batch, wl.seqlen) == own_shape:
                 traffic = (rec.get(dom) or {}).get("bytes")
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,

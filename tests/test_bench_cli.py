@@ -1,5 +1,5 @@
 """The benchmark's own contract on the CPU: one GPU only, a sequence-length override for the
-operator workloads only, kernel labels of profiler names, and the HBM-traffic record built from
+operator workloads only (and a batch override), kernel labels of profiler names, and the HBM-traffic record built from
 counter runs (scaled by a plain copy of known size)."""
 from __future__ import annotations
 
@@ -28,6 +28,9 @@ def test_sequence_length_only_for_operator_workloads():
                         "--seqlen", "1024"], capture_output=True, text=True, timeout=300)
     assert r.returncode == 2
     assert "operator workloads only" in r.stderr
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--workload", "prefill_qwen3b_l32768",
+                        "--batch", "2"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2 and "operator workloads only" in r.stderr
 
 
 @pytest.mark.parametrize("name,label", [
