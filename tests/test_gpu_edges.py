@@ -72,7 +72,6 @@ def test_empty_and_single_token_sequences(dt):
     _run(_case([100, 0, 1, 0, 130], 2, 2, 64, 8, 40, dt, seed=200), 8)
 
 
-
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 def test_only_one_token_sequences(dt):
     """A batch of one-token and empty sequences only: each query sees its own key alone (P = 1,
@@ -102,6 +101,7 @@ def test_only_one_token_sequences(dt):
     bound = TOL[dt] * scale * dp * np.abs(k).max()
     assert np.abs(f64(dq)).max() <= bound and np.abs(f64(dk)).max() <= bound, (np.abs(f64(dq)).max(), bound)
 
+
 def test_empty_sequences_block_causal():
     _run(_case([0, 300, 0, 1, 70], 2, 2, 64, 8, 40, torch.bfloat16, seed=201), 8, mode=ops.SELECT_BLOCK,
          block=64, backward=False)
@@ -121,6 +121,14 @@ def test_block_causal_tiles_whose_sets_are_all_empty(D, dt):
     x = _case([400, 60], 4, 2, D, 29, 600, dt, seed=210)
     x["w"][:200] = 600
     _run(x, 29, mode=ops.SELECT_BLOCK, block=17, backward=False)
+
+
+def test_many_sequences_landmark_sums():
+    """64 sequences x 8 heads x 128 slots x head_dim 64: 16384 blocks of landmark partial sums,
+    40 % of the slots empty."""
+    r = np.random.default_rng(212)
+    lens = [int(n) for n in r.integers(40, 400, 64)]
+    _run(_case(lens, 8, 8, 64, 128, 300, torch.bfloat16, seed=212), 128)
 
 
 def test_no_landmarks():
