@@ -203,6 +203,9 @@ __device__ __forceinline__ void band_edge(const AttnParams& p, const RowGroup& R
 // serves twice the rows (head_dim 128, where the chunks' staging is most of the time).
 // (the 16-bit head_dim-128 training forward is held to four waves per SIMD: 128 VGPRs, no
 // spills, from 132 at three)
+// (head, sequence) pairs from which each XCD walks its pairs one at a time (fwd_kernel)
+constexpr int kPairOrderMin = 256;
+
 template <typename T, int D, int BN, int RG, bool TR, bool MS = false, int NW = 4>
 __global__ __launch_bounds__(64 * NW, ((sizeof(T) == 2 && D == 64 && RG == 2 && BN == 32) ||
                                        (sizeof(T) == 2 && D == 128 && RG == 1 && BN == 32 && NW == 4 && TR))
@@ -230,10 +233,20 @@ __global__ __launch_bounds__(64 * NW, ((sizeof(T) == 2 && D == 64 && RG == 2 && 
     // tile-major order, the last tiles of every sequence first (their rows see the most
     // landmarks: the longest blocks start first and short ones fill the end of the grid);
     // blocks reach the XCDs round-robin, so where 8 divides heads x sequences each XCD keeps
-    // the same (head, sequence) pairs, and their K/V rows in its L2, throughout
+    // the same (head, sequence) pairs, and their K/V rows in its L2, throughout.  With many
+    // pairs that order puts every block an XCD runs at once on another pair, and a pair's next
+    // tile hundreds of blocks later: there each XCD walks its pairs one at a time instead, all
+    // tiles of a pair (the last first) before the next, so neighbouring tiles share K/V in L2.
     const int nhs = p.n_heads * p.num_seqs;
-    const int hs = blockIdx.x % nhs;
-    const int b = nblk - 1 - (int)blockIdx.x / nhs;
+    int hs, b;
+    if (nhs % 8 == 0 && nhs >= kPairOrderMin) {
+        const int x = (int)blockIdx.x % 8, j = (int)blockIdx.x / 8;
+        hs = (j / nblk) * 8 + x;
+        b = nblk - 1 - j % nblk;
+    } else {
+        hs = (int)blockIdx.x % nhs;
+        b = nblk - 1 - (int)blockIdx.x / nhs;
+    }
     const int h = hs % p.n_heads;
     const int s = hs / p.n_heads;
     int st, len;

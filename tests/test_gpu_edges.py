@@ -125,10 +125,20 @@ def test_block_causal_tiles_whose_sets_are_all_empty(D, dt):
 
 def test_many_sequences_landmark_sums():
     """64 sequences x 8 heads x 128 slots x head_dim 64: 16384 blocks of landmark partial sums,
-    40 % of the slots empty."""
+    40 % of the slots empty; 512 (head, sequence) pairs in the forward's per-XCD pair order."""
     r = np.random.default_rng(212)
     lens = [int(n) for n in r.integers(40, 400, 64)]
     _run(_case(lens, 8, 8, 64, 128, 300, torch.bfloat16, seed=212), 128)
+
+
+@pytest.mark.parametrize("D,block", [(128, 50), (64, 64)])
+def test_many_sequences_block_causal(D, block):
+    """32 sequences x 8 heads (256 (head, sequence) pairs: each XCD walks its pairs' tiles in
+    turn), block-causal sets, one of them with tiles over several sets."""
+    r = np.random.default_rng(213)
+    lens = [int(n) for n in r.integers(40, 500, 32)]
+    _run(_case(lens, 8, 8, D, 24, 200, torch.bfloat16, seed=213), 24, mode=ops.SELECT_BLOCK, block=block,
+         backward=False)
 
 
 def test_no_landmarks():
